@@ -1,0 +1,132 @@
+/*
+ * mignon_hip.h -- C ABI of the MI355X (gfx950) batched INT8 engine for mignon-ai's Hybrid NCA model.
+ *
+ * The reference engine is Go (internal/quant over internal/kernels); this ABI is what its cgo binding
+ * would call. Each entry point names the reference interface it replaces. Conventions:
+ *   - Every function returns MG_OK (0) or a negative MG_ERR_* code; mg_last_error() gives the message
+ *     (thread-local). Go panics cannot cross cgo, so the reference's panics become error codes too.
+ *   - Handles own their device memory and one HIP stream; calls on one handle are serialised (the
+ *     reference serialises a model and its sessions on one mutex, internal/quant/model.go:67,123).
+ *   - Array arguments are host pointers unless MG_PTR_DEVICE is passed in `flags`; then every array of
+ *     that call is a device pointer and the work is only enqueued on the handle's stream (call
+ *     mg_model_sync to wait). Host-pointer calls return when their outputs are written.
+ *   - Optional outputs may be NULL.
+ */
+#ifndef MIGNON_HIP_H
+#define MIGNON_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MG_OK 0
+#define MG_ERR_INVALID (-1)     /* bad argument or shape (the reference panics or returns nil) */
+#define MG_ERR_FORMAT (-2)      /* damaged or unsupported model file (quant.Decode's errors) */
+#define MG_ERR_DEVICE (-3)      /* HIP runtime error */
+#define MG_ERR_NOMEM (-4)       /* device allocation failed */
+#define MG_ERR_UNSUPPORTED (-5) /* valid model the engine does not run (e.g. head width not compiled) */
+
+#define MG_PTR_DEVICE 1 /* all array arguments of the call are device pointers; the call is asynchronous */
+
+typedef struct mg_model mg_model;
+typedef struct mg_sessions mg_sessions;
+
+typedef struct {
+    int vocab_size;    /* quant.Model.VocabSize  (internal/quant/model.go:71-74) */
+    int state_size;    /* quant.Model.StateSize  (internal/quant/model.go:76-79) */
+    int hidden_size;   /* quant.Model.HiddenSize (internal/quant/model.go:81-84) */
+    int num_blocks;    /* quant.Model.NumBlocks  (internal/quant/model.go:86-89) */
+    int attn_heads;    /* metadata attn_heads (internal/checkpoint/checkpoint.go:29) */
+    int attn_window;   /* metadata attn_window (internal/checkpoint/checkpoint.go:30) */
+    int max_context;   /* quant.Model.maxContext after NewModel's defaulting (internal/quant/model.go:91-95) */
+    int tied_embed;
+    int norm_ring;     /* quant.Model.normRing (internal/quant/stream.go:37-47) */
+    int attn_cache;    /* quant.Model.attnCache (internal/quant/attention.go:46-52) */
+    long long num_params; /* quant.Model.NumParams (internal/quant/checkpoint.go:91-104) */
+} mg_model_info_t;
+
+/* Thread-local message of the last failed call on this thread. */
+const char* mg_last_error(void);
+
+/* Decodes an INT8 model file (binary mignon.model/1 or legacy JSON) and uploads it to the current HIP
+ * device. Replaces quant.Decode + quant.NewModel (internal/quant/checkpoint.go:162-212,
+ * internal/quant/model.go:90-118) and pkg/model.Decode for INT8 files (pkg/model/model.go:59-117).
+ * max_context <= 0 takes the file's metadata context_size; below 64 it becomes 128 as in NewModel. */
+int mg_model_load(const uint8_t* data, size_t n, int max_context, mg_model** out);
+
+/* Decodes and validates a model file without touching the GPU (quant.Decode's checks,
+ * internal/quant/checkpoint.go:162-225) and reports what mg_model_load would build. */
+int mg_model_file_info(const uint8_t* data, size_t n, int max_context, mg_model_info_t* info);
+
+/* quant.Model accessors (internal/quant/model.go:71-89, internal/quant/checkpoint.go:91-104). */
+int mg_model_info(const mg_model* m, mg_model_info_t* info);
+
+/* Replaces the handle's stream (NULL restores the library's own stream). */
+int mg_model_set_stream(mg_model* m, void* hip_stream);
+void* mg_model_stream(const mg_model* m);
+int mg_model_sync(mg_model* m);
+void mg_model_free(mg_model* m);
+
+/* quant.Model.Call / Forward (internal/quant/model.go:120-137): next-token logits after the last
+ * token, window truncated to max_context. logits: host double[V]. Returns V, or 0 for empty input. */
+int mg_model_call(mg_model* m, const int32_t* ids, int n, double* logits);
+
+/* Teacher-forced batch: B sequences of T tokens, every position's next-token distribution at once.
+ * Position t of sequence b gives the logits Call(ids[b][0..t]) gives (internal/quant/stream.go:11-17;
+ * beyond max_context the positions follow a streaming session, internal/quant/session.go:41-56).
+ *   logits  [B][T][V] fp32
+ *   logprob [B][T]    fp32: log-softmax of target ids[b][t+1] under position t (eval.logProb,
+ *                     internal/eval/suite.go:200-208); NaN for t = T-1 and for out-of-range targets
+ *   probs   [B][T][V] fp32 softmax probabilities
+ *   bits    [B]       fp32: bits per token over the sequence's targets (eval nll.score +
+ *                     tokenizer.BitsPerByte with tokens for bytes, internal/eval/eval.go:25-48) */
+int mg_forward_batch(mg_model* m, const int32_t* ids, int B, int T, float* logits, float* logprob, float* probs,
+                     float* bits, int flags);
+
+/* n streaming sessions (quant.Model.NewSession, internal/quant/session.go:20-28): window =
+ * min(max_context, context) when context > 0. State lives in device memory, constant per session. */
+int mg_sessions_create(mg_model* m, int n, int context, mg_sessions** out);
+
+/* quantSession.Prefill for every session at once (internal/quant/session.go:30-39): prompts
+ * [n][max_len] with lengths lens[n] (1..max_len); prompts longer than the window keep their last
+ * window tokens. Outputs describe the next token after each prompt:
+ *   logits [n][V] fp32, argmax [n] (first maximum, internal/generate/greedy.go:89-102),
+ *   prob [n] double = 1 / sum exp(l - max). */
+int mg_sessions_prefill(mg_sessions* s, const int32_t* prompts, const int32_t* lens, int max_len, float* logits,
+                        int32_t* argmax, double* prob, int flags);
+
+/* quantSession.Append for every session (internal/quant/session.go:41-56): ids [n]. */
+int mg_sessions_step(mg_sessions* s, const int32_t* ids, float* logits, int32_t* argmax, double* prob, int flags);
+
+/* generate.greedyLoop for every session without stop tokens (internal/generate/greedy.go:63-87):
+ * Prefill(prompt), then max_tokens tokens, each the first-maximum argmax with its probability, with
+ * Append after every token but the last. out_ids [n][max_tokens], out_probs [n][max_tokens]. */
+int mg_sessions_decode_greedy(mg_sessions* s, const int32_t* prompts, const int32_t* lens, int max_len,
+                              int max_tokens, int32_t* out_ids, double* out_probs, int flags);
+
+/* quantSession.StateBytes (internal/quant/session.go:65-68, formula internal/quant/stream.go:87-101). */
+long long mg_sessions_state_bytes(const mg_sessions* s);
+/* Device bytes actually held per session. */
+long long mg_sessions_device_bytes(const mg_sessions* s);
+int mg_sessions_count(const mg_sessions* s);
+void mg_sessions_free(mg_sessions* s);
+
+/* Standalone INT8 GEMM (kernels.MatVecInt8 per row, internal/kernels/int8.go:31-41, on integer
+ * activations): acc[m][n] = sum_k A[m][k]*W[n][k] exactly in int32, C[m][n] = float(acc)*scale[n].
+ * A [M][K], W [N][K] (one row per output channel), scale [N], C [M][N], acc [M][N] (optional).
+ * stream: HIP stream for MG_PTR_DEVICE calls (NULL = default stream). */
+int mg_gemm_i8(const int8_t* A, int M, int K, const int8_t* W, int N, const float* scale, float* C, int32_t* acc,
+               int flags, void* stream);
+
+/* quant.NewTensorF32 (internal/quant/tensor.go:12-42) on the GPU: scale = max|w|/127, q = clamp(round
+ * half away from zero (w/scale), +-127); an all-zero tensor gets scale 1. */
+int mg_quantize_f32(const float* w, long long n, int8_t* q, float* scale, int flags, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MIGNON_HIP_H */

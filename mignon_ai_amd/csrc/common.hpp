@@ -1,0 +1,150 @@
+// Device helpers shared by the gfx950 kernels.
+//
+// Numerics follow the reference INT8 engine (W8A32: int8 weights with one fp32 scale per tensor, fp32
+// activations). Everything here is built with -ffp-contract=off, so a*b+c rounds twice unless fmaf is
+// written, exactly like the reference's Go code (which has no implicit FMA on amd64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mg {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int WAVE = 64;
+
+// Limb expansion of fp32 activations for int8 MFMA. A row segment x with scale s = amax/127 is held as
+// three int8 digits q0, q1, q2 in [-127, 127] with x ~= s*(q0 + q1/254 + q2/254^2); each digit plane is
+// multiplied by the int8 weights with exact int32 accumulation and the three sums are combined in fp32.
+// Representation error is at most s*(0.5/64516 + 2^-23*127), about 1.2e-7*amax.
+constexpr float kLimbBase = 254.0f;
+constexpr float kInvLimb1 = 1.0f / 254.0f;
+constexpr float kInvLimb2 = 1.0f / 64516.0f;
+// Chunks whose largest magnitude is below this are stored as zero (127/amax would overflow).
+constexpr float kTinyAmax = 1e-30f;
+
+struct Limbs {
+    int8_t q0, q1, q2;
+};
+
+__device__ __forceinline__ float clamp127(float v) { return fminf(fmaxf(v, -127.0f), 127.0f); }
+
+// inv = 127/amax (0 when the chunk is zero). Integer-valued inputs with amax = 127 give inv = 1, so
+// their first digit is the input itself and the other two are zero.
+__device__ __forceinline__ Limbs split_limbs(float x, float inv) {
+    float y = x * inv;
+    float q0 = clamp127(rintf(y));
+    float y1 = (y - q0) * kLimbBase;
+    float q1 = clamp127(rintf(y1));
+    float y2 = (y1 - q1) * kLimbBase;
+    float q2 = clamp127(rintf(y2));
+    return Limbs{(int8_t)q0, (int8_t)q1, (int8_t)q2};
+}
+
+__device__ __forceinline__ void limb_scale(float amax, float& scale, float& inv) {
+    if (amax < kTinyAmax) {
+        scale = 0.0f;
+        inv = 0.0f;
+    } else {
+        scale = amax / 127.0f;
+        inv = 127.0f / amax;
+    }
+}
+
+// quant.sigmoidClamped (internal/quant/stream.go:127-136): 1/(1 + float32(exp(float64(-x)))),
+// saturated beyond |x| > 15.
+__device__ __forceinline__ float sigmoid_clamped(float x) {
+    if (x > 15.0f) return 1.0f;
+    if (x < -15.0f) return 0.0f;
+    return 1.0f / (1.0f + (float)exp((double)(-x)));
+}
+
+// One element of the reference's vectorised e^x (vecExpASM_F32, internal/kernels/vec_amd64.s:281-430):
+// clamp to [-88, 88], k = nearest-even(x*log2e), two-constant ln2 reduction with FMA, degree-5
+// polynomial as an FMA chain, 2^k from exponent bits. Bit-identical to the reference on IEEE FMA.
+__device__ __forceinline__ float fast_exp_ref(float x) {
+    const float invLn2 = __uint_as_float(0x3fb8aa3bu), ln2Hi = __uint_as_float(0x3f317200u),
+                ln2Lo = __uint_as_float(0x35bfbe8eu);
+    const float c2 = 0.5f, c3 = __uint_as_float(0x3e2aaaabu), c4 = __uint_as_float(0x3d2aaaabu),
+                c5 = __uint_as_float(0x3c088889u);
+    x = (x < 88.0f) ? x : 88.0f;
+    x = (x > -88.0f) ? x : -88.0f;
+    float k = rintf(x * invLn2);
+    float r = fmaf(-k, ln2Hi, x);
+    r = fmaf(-k, ln2Lo, r);
+    float p = fmaf(r, c5, c4);
+    p = fmaf(r, p, c3);
+    p = fmaf(r, p, c2);
+    p = fmaf(r, p, 1.0f);
+    p = fmaf(r, p, 1.0f);
+    int ki = (int)k + 127;
+    return p * __uint_as_float((uint32_t)ki << 23);
+}
+
+// Horizontal reduction of the reference's 8-lane AVX2 accumulators (vec_amd64.s:38-44): lanes i and
+// i+4, then pairs (0,2), (1,3), then the two results.
+__device__ __forceinline__ float hreduce8(const float v[8]) {
+    float f0 = v[0] + v[4], f1 = v[1] + v[5], f2 = v[2] + v[6], f3 = v[3] + v[7];
+    float g0 = f0 + f2, g1 = f1 + f3;
+    return g0 + g1;
+}
+
+// kernels.DotF32 as dotProductASM_F32 computes it (internal/kernels/vec_amd64.s:4-63), sequentially in
+// one lane: two 8-lane FMA accumulators over 16-chunks, an 8-chunk into the first, the tree, then the
+// unfused scalar tail. x may live in registers (compile-time indexing after unrolling), y anywhere.
+template <int N, class X, class Y>
+__device__ __forceinline__ float dot_f32_ref(const X& x, const Y& y) {
+    float a0[8], a1[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) { a0[j] = 0.0f; a1[j] = 0.0f; }
+    int i = 0;
+#pragma unroll
+    for (; i + 16 <= N; i += 16) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            a0[j] = fmaf(x[i + j], y[i + j], a0[j]);
+            a1[j] = fmaf(x[i + 8 + j], y[i + 8 + j], a1[j]);
+        }
+    }
+    if (i + 8 <= N) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) a0[j] = fmaf(x[i + j], y[i + j], a0[j]);
+        i += 8;
+    }
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = a0[j] + a1[j];
+    float s = hreduce8(v);
+#pragma unroll
+    for (; i < N; i++) {
+        float p = x[i] * y[i];
+        s = s + p;
+    }
+    return s;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__host__ __device__ constexpr int round_up(int a, int b) { return (a + b - 1) / b * b; }
+
+// Grid mapping that keeps consecutive tiles on one XCD: the dispatcher places workgroup b on XCD b % 8,
+// so tile t goes to XCD t / per_xcd. Tiles sharing an activation row block are consecutive, which makes
+// the weight sweep over one row block hit the same XCD's L2.
+__device__ __forceinline__ int xcd_tile(int b, int total) {
+    int per = (total + 7) / 8;
+    return (b % 8) * per + b / 8;
+}
+__host__ __forceinline__ int xcd_grid(int total) { return 8 * ((total + 7) / 8); }
+
+}  // namespace mg

@@ -1,0 +1,939 @@
+// Host side of the engine: device model layout, the batched teacher-forced forward, streaming sessions
+// and the C ABI (include/mignon_hip.h).
+//
+// Execution is step-major: every token in flight advances through one rule step together (the float
+// engine's order, internal/ca/forward.go:99-142), which the reference states is equivalent to its
+// position-major streaming order (internal/quant/stream.go:11-17). Per block step:
+//   row kernel      RMSNorm(cur; gamma) -> n (fp32) and limb-expanded n
+//   GEMM LATCH      lambda = sigmoid_clamped(n . W_select^T * s + base)
+//   scan            g_t = lambda*g_{t-1} + (1-lambda)*n_t; x = [n_t | n_{t-dil} | g_t] limb-expanded
+//   GEMM GLU        h = (x.W1v*s + b1v) * sigmoid_clamped(x.W1g*s + b1g), limb-expanded per 64 units
+//   GEMM HIGHWAY    cur = (1-g)*cur + g*o, o = h.W2^T*s + b2
+// then the attention sublayer (row kernel, QKV GEMM, windowed attention, Out GEMM into cur) and the
+// tied head (row kernel, logits GEMM with fused softmax statistics).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/mignon_hip.h"
+#include "common.hpp"
+#include "gemm.hpp"
+#include "kernels.hpp"
+#include "model_file.hpp"
+
+namespace mg {
+namespace {
+
+thread_local std::string g_last_error;
+
+struct Error : std::runtime_error {
+    int code;
+    Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+void hip_check(hipError_t e, const char* what) {
+    if (e == hipSuccess) return;
+    if (e == hipErrorOutOfMemory) throw Error(MG_ERR_NOMEM, std::string(what) + ": out of device memory");
+    if (e == hipErrorInvalidValue) throw Error(MG_ERR_INVALID, std::string(what) + ": invalid launch arguments");
+    throw Error(MG_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+#define HIPCHECK(x) hip_check((x), #x)
+
+void require(bool ok, const std::string& msg) {
+    if (!ok) throw Error(MG_ERR_INVALID, msg);
+}
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t n = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    ~DevBuf() { release(); }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+    }
+    void ensure(size_t bytes) {
+        if (bytes <= n) return;
+        release();
+        if (bytes == 0) return;
+        hipError_t e = hipMalloc(&p, bytes);
+        if (e != hipSuccess) {
+            p = nullptr;
+            (void)hipGetLastError();
+            throw Error(MG_ERR_NOMEM, "device allocation of " + std::to_string(bytes) + " bytes failed");
+        }
+        n = bytes;
+    }
+    template <class T>
+    T* as() const { return (T*)p; }
+};
+
+struct DevBlock {
+    int steps = 1, dil_base = 2, init_dil = 1;
+    int8_t* w1 = nullptr; float* b1 = nullptr; float s1 = 0;  // [2Hp][3Dp] value/gate rows paired by 16
+    int8_t* w2 = nullptr; float* b2 = nullptr; float s2 = 0;  // [2Dp][Hp] value/gate rows paired by 16
+    int8_t* wsel = nullptr; float ssel = 0;                   // [NpD][Dp]
+    float* gamma = nullptr;                                   // [Dp] or null (no normalisation)
+    bool attn = false;
+    float* anorm = nullptr;
+    int8_t* qkv = nullptr; float sqkv = 0;                    // [Np3][Dp]
+    int8_t* wo = nullptr; float so = 0;                       // [NpD][Dp]
+    // ca.StepDilation (internal/ca/layout.go:22-30)
+    int dilation(int step) const {
+        int d = init_dil;
+        for (int s = 0; s < step && d < 32; s++) d *= dil_base;
+        return std::min(d, 32);
+    }
+};
+
+// Workspace for a batch of tokens in flight.
+struct Workspace {
+    int cap_tokens = 0;
+    DevBuf cur, bin, nf, lam, nl, ns, xl, xs, hl, hs, qkv, att, stats, lse, tlog, logprob, argmax, prob, ids, tgt,
+        rowmap, lens, tmp;
+};
+
+}  // namespace
+}  // namespace mg
+
+struct mg_model {
+    int device = 0;
+    int V = 0, D = 0, H = 0, Dp = 0, Hp = 0, heads = 0, window = 0, max_context = 0, ring = 1, cap = 0;
+    int NpD = 0, Np3 = 0, Vp = 0, nattn = 0, nbs = 0;
+    bool tied = true;
+    long long num_params = 0;
+    std::vector<std::unique_ptr<mg::DevBuf>> bufs;
+    int8_t* emb = nullptr;
+    float emb_scale = 0;
+    std::vector<mg::DevBlock> blocks;
+    int8_t* headw = nullptr;
+    float head_scale = 0;
+    float* headb = nullptr;
+    float* final_norm = nullptr;
+    float* latch_base = nullptr;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    mg::Workspace ws;
+    std::mutex mu;
+};
+
+struct mg_sessions {
+    mg_model* m = nullptr;
+    int n = 0, window = 0;
+    mg::DevBuf norm_ring, g, kring, vring, pos, next_ids, out_ids, out_probs, logits, argmax, prob;
+};
+
+namespace mg {
+namespace {
+
+template <class T>
+T* upload(mg_model* m, const std::vector<T>& h) {
+    m->bufs.emplace_back(new DevBuf());
+    DevBuf& b = *m->bufs.back();
+    b.ensure(std::max<size_t>(h.size() * sizeof(T), 16));
+    if (!h.empty()) HIPCHECK(hipMemcpy(b.p, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice));
+    return b.as<T>();
+}
+
+// quant.Model.normRing (internal/quant/stream.go:37-47)
+int norm_ring_of(const std::vector<DevBlock>& blocks) {
+    int longest = 0;
+    for (auto& b : blocks)
+        for (int s = 0; s < b.steps; s++) longest = std::max(longest, b.dilation(s));
+    return longest + 1;
+}
+
+std::vector<float> latch_base_logits(int D) {
+    // ca.ComputeDecayLatchConstants + ca.ComputeSelectiveLatchBaseLogits (internal/ca/layout.go:60-85,
+    // internal/ca/latch.go:9-25): sigmoid(base_d) = 2^(-1/T_d), T_d geometric from 1.5 to 64 tokens.
+    std::vector<float> base(D);
+    for (int d = 0; d < D; d++) {
+        double td = D == 1 ? 1.5 : 1.5 * std::pow(std::pow(64.0 / 1.5, 1.0 / (double)(D - 1)), (double)d);
+        float decay = (float)std::pow(2.0, -1.0 / td);
+        double lam = (double)decay;
+        base[d] = lam <= 0.0 ? -15.0f : lam >= 1.0 ? 15.0f : (float)std::log(lam / (1.0 - lam));
+    }
+    return base;
+}
+
+// Head widths with a compiled attention kernel (kernels.hip, DH_SWITCH).
+bool attention_width_supported(int dh) {
+    static const int widths[] = {1, 2, 4, 8, 12, 16, 20, 24, 32, 40, 48, 64, 80, 96, 128};
+    for (int w : widths)
+        if (w == dh) return true;
+    return false;
+}
+
+void build_device_model(mg_model* m, const HostModel& hm, int max_context) {
+    const int V = hm.V, D = hm.D, H = hm.H;
+    m->V = V; m->D = D; m->H = H;
+    m->Dp = round_up(D, 64);
+    m->Hp = round_up(H, 64);
+    m->NpD = round_up(m->Dp, GEMM_BN);
+    m->Np3 = round_up(3 * D, GEMM_BN);
+    m->Vp = round_up(V, GEMM_BN);
+    m->tied = hm.tied;
+    m->heads = hm.attn_heads;
+    m->window = hm.attn_window;
+    int ctx = max_context > 0 ? max_context : hm.context_size;
+    m->max_context = ctx < 64 ? 128 : ctx;  // quant.NewModel (internal/quant/model.go:91-95)
+    m->cap = m->window > 0 ? m->window : m->max_context;
+    m->num_params = hm.num_params;
+    const int Dp = m->Dp, Hp = m->Hp;
+
+    m->emb = upload(m, hm.embed);
+    m->emb_scale = hm.embed_scale;
+    m->latch_base = nullptr;
+    {
+        std::vector<float> base = latch_base_logits(D);
+        base.resize(m->NpD, 0.0f);
+        m->latch_base = upload(m, base);
+    }
+    m->blocks.resize(hm.blocks.size());
+    m->nattn = 0;
+    m->nbs = 0;
+    for (size_t b = 0; b < hm.blocks.size(); b++) {
+        const HostBlock& hb = hm.blocks[b];
+        DevBlock& db = m->blocks[b];
+        db.steps = hb.steps;
+        db.dil_base = hb.dilation_base;
+        db.init_dil = hb.initial_dilation;
+        m->nbs += hb.steps;
+        // W1: rows regrouped in blocks of 32 = 16 value rows + the 16 matching gate rows; each input
+        // segment (n, left, g) padded from D to Dp columns.
+        std::vector<int8_t> w1((size_t)2 * Hp * 3 * Dp, 0);
+        std::vector<float> b1((size_t)2 * Hp, 0.0f);
+        for (int r = 0; r < 2 * Hp; r++) {
+            int blk = r / 32, i = r % 32, j = 16 * blk + (i % 16);
+            if (j >= H) continue;
+            int src = i < 16 ? j : H + j;
+            for (int seg = 0; seg < 3; seg++)
+                std::memcpy(&w1[(size_t)r * 3 * Dp + seg * Dp], &hb.w1[(size_t)src * 3 * D + seg * D], D);
+            b1[r] = hb.b1[src];
+        }
+        db.w1 = upload(m, w1); db.b1 = upload(m, b1); db.s1 = hb.s1;
+        // W2: same pairing (16 delta rows + 16 highway-gate rows), hidden columns padded to Hp.
+        std::vector<int8_t> w2((size_t)2 * Dp * Hp, 0);
+        std::vector<float> b2((size_t)2 * Dp, 0.0f);
+        for (int r = 0; r < 2 * Dp; r++) {
+            int blk = r / 32, i = r % 32, c = 16 * blk + (i % 16);
+            if (c >= D) continue;
+            int src = i < 16 ? c : D + c;
+            std::memcpy(&w2[(size_t)r * Hp], &hb.w2[(size_t)src * H], H);
+            b2[r] = hb.b2[src];
+        }
+        db.w2 = upload(m, w2); db.b2 = upload(m, b2); db.s2 = hb.s2;
+        std::vector<int8_t> ws((size_t)m->NpD * Dp, 0);
+        for (int r = 0; r < D; r++) std::memcpy(&ws[(size_t)r * Dp], &hb.wsel[(size_t)r * D], D);
+        db.wsel = upload(m, ws); db.ssel = hb.ssel;
+        if ((int)hb.gamma.size() == D) {
+            std::vector<float> g(hb.gamma);
+            g.resize(Dp, 0.0f);
+            db.gamma = upload(m, g);
+        }
+        db.attn = hb.has_attn;
+        if (hb.has_attn) {
+            m->nattn++;
+            std::vector<float> an(hb.attn_norm);
+            an.resize(Dp, 0.0f);
+            db.anorm = upload(m, an);
+            std::vector<int8_t> q((size_t)m->Np3 * Dp, 0);
+            for (int r = 0; r < 3 * D; r++) std::memcpy(&q[(size_t)r * Dp], &hb.qkv[(size_t)r * D], D);
+            db.qkv = upload(m, q); db.sqkv = hb.sqkv;
+            std::vector<int8_t> o((size_t)m->NpD * Dp, 0);
+            for (int r = 0; r < D; r++) std::memcpy(&o[(size_t)r * Dp], &hb.wo[(size_t)r * D], D);
+            db.wo = upload(m, o); db.so = hb.so;
+        }
+    }
+    m->ring = norm_ring_of(m->blocks);
+    const std::vector<int8_t>& hw = hm.tied ? hm.embed : hm.head_w;
+    std::vector<int8_t> head((size_t)m->Vp * Dp, 0);
+    for (int r = 0; r < V; r++) std::memcpy(&head[(size_t)r * Dp], &hw[(size_t)r * D], D);
+    m->headw = upload(m, head);
+    m->head_scale = hm.tied ? hm.embed_scale : hm.head_scale;
+    std::vector<float> hb(m->Vp, 0.0f);
+    for (size_t v = 0; v < hm.head_b.size() && v < (size_t)V; v++) hb[v] = hm.head_b[v];
+    m->headb = upload(m, hb);
+    if ((int)hm.final_norm.size() == D) {
+        std::vector<float> fn(hm.final_norm);
+        fn.resize(Dp, 0.0f);
+        m->final_norm = upload(m, fn);
+    }
+    if (m->nattn > 0) {
+        if (m->heads <= 0 || D % m->heads) throw Error(MG_ERR_FORMAT, "model file: attention heads must divide the state size");
+        int dh = D / m->heads;
+        if (!attention_width_supported(dh))
+            throw Error(MG_ERR_UNSUPPORTED, "attention head width " + std::to_string(dh) + " is not compiled");
+        if (m->cap > 256) throw Error(MG_ERR_UNSUPPORTED, "attention cache above 256 positions is not supported");
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Workspace sizing: every per-token buffer for up to `tokens` rows.
+// ------------------------------------------------------------------------------------------------
+void ensure_ws(mg_model* m, int tokens) {
+    Workspace& w = m->ws;
+    if (tokens <= w.cap_tokens) return;
+    size_t M = (size_t)tokens;
+    const size_t Dp = m->Dp, Hp = m->Hp, D = m->D;
+    w.cur.ensure(M * Dp * 4);
+    w.bin.ensure(M * Dp * 4);
+    w.nf.ensure(M * Dp * 4);
+    w.lam.ensure(M * Dp * 4);
+    w.nl.ensure(M * 3 * Dp);
+    w.ns.ensure(M * 4);
+    w.xl.ensure(M * 9 * Dp);
+    w.xs.ensure(M * 4);
+    w.hl.ensure(M * 3 * Hp);
+    w.hs.ensure(M * (Hp / 64) * 4);
+    if (m->nattn) {
+        w.qkv.ensure(M * 3 * D * 4);
+        w.att.ensure(M * Dp * 4);
+    }
+    w.stats.ensure(M * (m->Vp / GEMM_BN) * 12);
+    w.lse.ensure(M * 4);
+    w.tlog.ensure(M * 4);
+    w.logprob.ensure(M * 4);
+    w.argmax.ensure(M * 4);
+    w.prob.ensure(M * 8);
+    w.ids.ensure(M * 4);
+    w.tgt.ensure(M * 4);
+    w.rowmap.ensure(M * 4);
+    w.lens.ensure(M * 4);
+    w.cap_tokens = tokens;
+}
+
+GemmArgs lx3_args(const int8_t* A, long long ld, const float* As, int as_ld, int kc_steps, const int8_t* W, int Np,
+                  int Kp, int M, int nvalid, float wscale) {
+    GemmArgs g;
+    g.A = A; g.a_row = 3 * ld; g.a_limb = ld;
+    g.As = As; g.as_ld = as_ld; g.kc_steps = kc_steps;
+    g.W = W; g.ldw = Kp; g.Np = Np; g.Kp = Kp; g.M = M; g.nvalid = nvalid; g.wscale = wscale;
+    return g;
+}
+
+void gemm(int nl, int epi, const GemmArgs& g, hipStream_t s) { HIPCHECK(launch_gemm(nl, epi, g, s)); }
+
+// Row kernel helper: mode + optional norm, writes n (fp32) and the limb-expanded copy into ws.nl/ns.
+void row_call(mg_model* m, int M, int mode, const int32_t* ids, const float* src, int lds, const int32_t* row_map,
+              const float* gamma, float* nout, bool limbs, hipStream_t s) {
+    Workspace& w = m->ws;
+    RowArgs r;
+    r.M = M; r.D = m->D; r.Dp = m->Dp; r.mode = mode;
+    r.ids = ids; r.emb = m->emb; r.emb_scale = m->emb_scale; r.V = m->V;
+    r.cur = w.cur.as<float>(); r.block_in = w.bin.as<float>();
+    r.src = src; r.lds = lds; r.row_map = row_map; r.gamma = gamma; r.nout = nout;
+    if (limbs) {
+        r.limbs = w.nl.as<int8_t>(); r.l_row = 3LL * m->Dp; r.l_limb = m->Dp; r.lscale = w.ns.as<float>();
+    }
+    HIPCHECK(launch_row(r, s));
+}
+
+__global__ void targets_kernel(int M, int T, const int32_t* ids, int32_t* tgt) {
+    int m = blockIdx.x * blockDim.x + threadIdx.x;
+    if (m >= M) return;
+    tgt[m] = (m % T) < T - 1 ? ids[m + 1] : -1;
+}
+
+__global__ void last_rows_kernel(int B, int T, const int32_t* lens, int32_t* rowmap) {
+    int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b < B) rowmap[b] = b * T + lens[b] - 1;
+}
+
+// Prompt windowing (quantSession.Prefill keeps the last `window` tokens, internal/quant/session.go:30-39)
+// into a [S][Tw] token matrix padded with id 0; lengths are clamped to 1..max_len.
+__global__ void window_ids_kernel(int S, int max_len, int window, int Tw, const int32_t* in, const int32_t* lens_in,
+                                  int32_t* out, int32_t* lens_out) {
+    int s = blockIdx.x;
+    int len = min(max(lens_in[s], 1), max_len);
+    int L = min(len, window), off = len - L;
+    for (int t = threadIdx.x; t < Tw; t += blockDim.x) out[(long long)s * Tw + t] = t < L ? in[(long long)s * max_len + off + t] : 0;
+    if (threadIdx.x == 0) lens_out[s] = L;
+}
+
+// ------------------------------------------------------------------------------------------------
+// The model body over M rows. Batched mode (sess == null): rows are B sequences of T positions.
+// Prefill export (sess != null, step == false): also writes the session state at each sequence's last
+// position. Step mode (step == true): one position per session against its device-resident state.
+// On return ws.cur holds the final cell state of every row.
+// ------------------------------------------------------------------------------------------------
+struct BodyCtx {
+    int B = 0, T = 1;
+    const int32_t* ids = nullptr;
+    mg_sessions* sess = nullptr;
+    bool step = false;
+    const int32_t* lens = nullptr;  // prefill export lengths (device)
+};
+
+void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
+    Workspace& w = m->ws;
+    const int M = c.B * c.T;
+    const int Dp = m->Dp, Hp = m->Hp, D = m->D;
+    int bs = 0, ab = 0;
+    for (size_t b = 0; b < m->blocks.size(); b++) {
+        const DevBlock& blk = m->blocks[b];
+        const int mode = b == 0 ? ROW_EMBED : ROW_RESID;
+        if (blk.steps == 0) row_call(m, M, mode, c.ids, nullptr, 0, nullptr, nullptr, nullptr, false, s);
+        for (int st = 0; st < blk.steps; st++, bs++) {
+            const int dil = blk.dilation(st);
+            // n = RMSNorm(cur; gamma) (stream.go:166-171), fused with the embedding / residual at step 0
+            row_call(m, M, st == 0 ? mode : ROW_SRC, c.ids, nullptr, 0, nullptr, blk.gamma, w.nf.as<float>(), true, s);
+            // lambda = sigmoid_clamped(n.W_sel*s + base) (stream.go:195-205)
+            GemmArgs g = lx3_args(w.nl.as<int8_t>(), Dp, w.ns.as<float>(), 1, Dp / 64, blk.wsel, m->NpD, Dp, M, D, blk.ssel);
+            g.bias = m->latch_base; g.out = w.lam.as<float>(); g.ldo = Dp;
+            gemm(3, EPI_LATCH, g, s);
+            if (c.step) {
+                LatchStepArgs la;
+                la.S = M; la.D = D; la.Dp = Dp; la.dil = dil; la.ring = m->ring;
+                la.pos = c.sess->pos.as<int32_t>(); la.lam = w.lam.as<float>(); la.nf = w.nf.as<float>();
+                la.g = c.sess->g.as<float>() + (size_t)bs * c.B * Dp;
+                la.norm_ring = c.sess->norm_ring.as<float>() + (size_t)bs * c.B * m->ring * Dp;
+                la.xl = w.xl.as<int8_t>(); la.xs = w.xs.as<float>();
+                HIPCHECK(launch_latch_step(la, s));
+            } else {
+                ScanArgs sa;
+                sa.B = c.B; sa.T = c.T; sa.D = D; sa.Dp = Dp; sa.dil = dil;
+                sa.lam = w.lam.as<float>(); sa.nf = w.nf.as<float>(); sa.xl = w.xl.as<int8_t>(); sa.xs = w.xs.as<float>();
+                if (c.sess) {
+                    sa.lens = c.lens;
+                    sa.g_out = c.sess->g.as<float>() + (size_t)bs * c.B * Dp;
+                    HIPCHECK(launch_export_ring(c.B, c.T, Dp, m->ring, c.lens, w.nf.as<float>(),
+                                                c.sess->norm_ring.as<float>() + (size_t)bs * c.B * m->ring * Dp, s));
+                }
+                HIPCHECK(launch_scan(sa, s));
+            }
+            // h = GLU(x) (stream.go:214-220), limb-expanded with one scale per 64 hidden units
+            g = lx3_args(w.xl.as<int8_t>(), 3LL * Dp, w.xs.as<float>(), 1, 3 * Dp / 64, blk.w1, 2 * Hp, 3 * Dp, M, 2 * Hp, blk.s1);
+            g.bias = blk.b1; g.hl = w.hl.as<int8_t>(); g.hl_row = 3LL * Hp; g.hl_limb = Hp;
+            g.hs = w.hs.as<float>(); g.hs_ld = Hp / 64;
+            gemm(3, EPI_GLU, g, s);
+            // cur = highway(cur, W2 h) (stream.go:222-229)
+            g = lx3_args(w.hl.as<int8_t>(), Hp, w.hs.as<float>(), Hp / 64, 1, blk.w2, 2 * Dp, Hp, M, D, blk.s2);
+            g.bias = blk.b2; g.cur = w.cur.as<float>(); g.ldcur = Dp;
+            gemm(3, EPI_HIGHWAY, g, s);
+        }
+        if (blk.attn) {
+            // attendPosition (internal/quant/attention.go:69-104)
+            row_call(m, M, ROW_SRC, nullptr, nullptr, 0, nullptr, blk.anorm, nullptr, true, s);
+            GemmArgs g = lx3_args(w.nl.as<int8_t>(), Dp, w.ns.as<float>(), 1, Dp / 64, blk.qkv, m->Np3, Dp, M, 3 * D, blk.sqkv);
+            g.out = w.qkv.as<float>(); g.ldo = 3 * D;
+            gemm(3, EPI_F32, g, s);
+            if (c.step) {
+                AttnStepArgs aa;
+                aa.S = M; aa.D = D; aa.Dp = Dp; aa.heads = m->heads; aa.window = m->window; aa.cap = m->cap;
+                aa.pos = c.sess->pos.as<int32_t>(); aa.qkv = w.qkv.as<float>();
+                aa.kring = c.sess->kring.as<float>() + (size_t)ab * c.B * m->cap * D;
+                aa.vring = c.sess->vring.as<float>() + (size_t)ab * c.B * m->cap * D;
+                aa.att = w.att.as<float>();
+                HIPCHECK(launch_attention_step(aa, s));
+            } else {
+                if (c.sess)
+                    HIPCHECK(launch_export_kv(c.B, c.T, D, m->cap, c.lens, w.qkv.as<float>(),
+                                              c.sess->kring.as<float>() + (size_t)ab * c.B * m->cap * D,
+                                              c.sess->vring.as<float>() + (size_t)ab * c.B * m->cap * D, s));
+                AttnArgs aa;
+                aa.B = c.B; aa.T = c.T; aa.D = D; aa.Dp = Dp; aa.heads = m->heads; aa.window = m->window; aa.cap = m->cap;
+                aa.qkv = w.qkv.as<float>(); aa.att = w.att.as<float>();
+                HIPCHECK(launch_attention(aa, s));
+            }
+            row_call(m, M, ROW_SRC, nullptr, w.att.as<float>(), Dp, nullptr, nullptr, nullptr, true, s);
+            g = lx3_args(w.nl.as<int8_t>(), Dp, w.ns.as<float>(), 1, Dp / 64, blk.wo, m->NpD, Dp, M, D, blk.so);
+            g.cur = w.cur.as<float>(); g.ldcur = Dp;
+            gemm(3, EPI_RESID, g, s);
+            ab++;
+        }
+    }
+    if (m->blocks.empty()) row_call(m, M, ROW_EMBED, c.ids, nullptr, 0, nullptr, nullptr, nullptr, false, s);
+}
+
+// Head over M rows of ws.cur (optionally gathered through row_map): final RMSNorm, logits GEMM with
+// per-tile softmax statistics, then the per-row combination.
+void run_head(mg_model* m, int M, const int32_t* row_map, const int32_t* tgt, float* logits_out, HeadCombineArgs hc,
+              hipStream_t s) {
+    Workspace& w = m->ws;
+    // headLogits (internal/quant/stream.go:232-248)
+    row_call(m, M, ROW_SRC, nullptr, nullptr, 0, row_map, m->final_norm, nullptr, true, s);
+    GemmArgs g = lx3_args(w.nl.as<int8_t>(), m->Dp, w.ns.as<float>(), 1, m->Dp / 64, m->headw, m->Vp, m->Dp, M, m->V, m->head_scale);
+    g.bias = m->headb; g.out = logits_out; g.ldo = m->V;
+    g.stats = w.stats.as<float>(); g.stats_ld = m->Vp / GEMM_BN;
+    g.tgt = tgt; g.tlog = w.tlog.as<float>();
+    gemm(3, EPI_LOGITS, g, s);
+    hc.M = M; hc.ntiles = m->Vp / GEMM_BN; hc.stats = w.stats.as<float>(); hc.V = m->V;
+    hc.tgt = tgt; hc.tlog = w.tlog.as<float>();
+    HIPCHECK(launch_head_combine(hc, s));
+}
+
+struct Guard {
+    mg_model* m;
+    std::lock_guard<std::mutex> lk;
+    explicit Guard(mg_model* mm) : m(mm), lk(mm->mu) { HIPCHECK(hipSetDevice(mm->device)); }
+};
+
+// Host<->device staging for calls given host pointers.
+struct Staging {
+    std::vector<std::unique_ptr<DevBuf>> bufs;
+    template <class T>
+    T* in(const T* host, size_t n, hipStream_t s) {
+        bufs.emplace_back(new DevBuf());
+        bufs.back()->ensure(std::max<size_t>(n * sizeof(T), 16));
+        if (n) HIPCHECK(hipMemcpyAsync(bufs.back()->p, host, n * sizeof(T), hipMemcpyHostToDevice, s));
+        return bufs.back()->as<T>();
+    }
+    template <class T>
+    T* out(size_t n) {
+        bufs.emplace_back(new DevBuf());
+        bufs.back()->ensure(std::max<size_t>(n * sizeof(T), 16));
+        return bufs.back()->as<T>();
+    }
+};
+
+template <class F>
+int guarded(F&& f) {
+    try {
+        return f();
+    } catch (const Error& e) {
+        g_last_error = e.what();
+        return e.code;
+    } catch (const FormatError& e) {
+        g_last_error = e.what();
+        return MG_ERR_FORMAT;
+    } catch (const std::bad_alloc&) {
+        g_last_error = "host allocation failed";
+        return MG_ERR_NOMEM;
+    } catch (const std::exception& e) {
+        g_last_error = e.what();
+        return MG_ERR_FORMAT;
+    }
+}
+
+constexpr long long kMaxChunkTokens = 1 << 19;  // tokens per workspace pass of a teacher-forced batch
+
+}  // namespace
+}  // namespace mg
+
+using namespace mg;
+
+extern "C" {
+
+const char* mg_last_error(void) { return g_last_error.c_str(); }
+
+int mg_model_load(const uint8_t* data, size_t n, int max_context, mg_model** out) {
+    return guarded([&] {
+        require(data != nullptr && out != nullptr, "mg_model_load: null argument");
+        *out = nullptr;
+        HostModel hm = decode_model_file(data, n);
+        validate_for_engine(hm);
+        std::unique_ptr<mg_model> m(new mg_model());
+        HIPCHECK(hipGetDevice(&m->device));
+        build_device_model(m.get(), hm, max_context);
+        HIPCHECK(hipStreamCreateWithFlags(&m->own_stream, hipStreamNonBlocking));
+        m->stream = m->own_stream;
+        HIPCHECK(hipDeviceSynchronize());
+        *out = m.release();
+        return MG_OK;
+    });
+}
+
+int mg_model_file_info(const uint8_t* data, size_t n, int max_context, mg_model_info_t* info) {
+    return guarded([&] {
+        require(data != nullptr && info != nullptr, "mg_model_file_info: null argument");
+        HostModel hm = decode_model_file(data, n);
+        validate_for_engine(hm);
+        std::vector<DevBlock> blocks(hm.blocks.size());
+        for (size_t b = 0; b < hm.blocks.size(); b++) {
+            blocks[b].steps = hm.blocks[b].steps;
+            blocks[b].dil_base = hm.blocks[b].dilation_base;
+            blocks[b].init_dil = hm.blocks[b].initial_dilation;
+        }
+        int ctx = max_context > 0 ? max_context : hm.context_size;
+        ctx = ctx < 64 ? 128 : ctx;
+        info->vocab_size = hm.V; info->state_size = hm.D; info->hidden_size = hm.H;
+        info->num_blocks = (int)hm.blocks.size(); info->attn_heads = hm.attn_heads; info->attn_window = hm.attn_window;
+        info->max_context = ctx; info->tied_embed = hm.tied ? 1 : 0;
+        info->norm_ring = norm_ring_of(blocks);
+        info->attn_cache = hm.attn_window > 0 ? hm.attn_window : ctx;
+        info->num_params = hm.num_params;
+        return MG_OK;
+    });
+}
+
+int mg_model_info(const mg_model* m, mg_model_info_t* info) {
+    return guarded([&] {
+        require(m && info, "mg_model_info: null argument");
+        info->vocab_size = m->V; info->state_size = m->D; info->hidden_size = m->H;
+        info->num_blocks = (int)m->blocks.size(); info->attn_heads = m->heads; info->attn_window = m->window;
+        info->max_context = m->max_context; info->tied_embed = m->tied ? 1 : 0;
+        info->norm_ring = m->ring; info->attn_cache = m->cap; info->num_params = m->num_params;
+        return MG_OK;
+    });
+}
+
+int mg_model_set_stream(mg_model* m, void* stream) {
+    return guarded([&] {
+        require(m != nullptr, "mg_model_set_stream: null model");
+        std::lock_guard<std::mutex> lk(m->mu);
+        m->stream = stream ? (hipStream_t)stream : m->own_stream;
+        return MG_OK;
+    });
+}
+
+void* mg_model_stream(const mg_model* m) { return m ? (void*)m->stream : nullptr; }
+
+int mg_model_sync(mg_model* m) {
+    return guarded([&] {
+        require(m != nullptr, "mg_model_sync: null model");
+        Guard g(m);
+        HIPCHECK(hipStreamSynchronize(m->stream));
+        return MG_OK;
+    });
+}
+
+void mg_model_free(mg_model* m) {
+    if (!m) return;
+    (void)hipSetDevice(m->device);
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    if (m->own_stream) (void)hipStreamDestroy(m->own_stream);
+    delete m;
+}
+
+int mg_forward_batch(mg_model* m, const int32_t* ids, int B, int T, float* logits, float* logprob, float* probs,
+                     float* bits, int flags) {
+    return guarded([&] {
+        require(m && ids, "mg_forward_batch: null argument");
+        require(B >= 0 && T >= 0, "mg_forward_batch: negative shape");
+        if (B == 0 || T == 0) return MG_OK;
+        Guard gd(m);
+        hipStream_t s = m->stream;
+        const bool dev = flags & MG_PTR_DEVICE;
+        const int V = m->V;
+        int chunk = (int)std::max<long long>(1, std::min<long long>(B, kMaxChunkTokens / std::max(T, 1)));
+        ensure_ws(m, chunk * T);
+        Workspace& w = m->ws;
+        Staging st;
+        for (int b0 = 0; b0 < B; b0 += chunk) {
+            const int Bc = std::min(chunk, B - b0);
+            const int M = Bc * T;
+            const size_t row0 = (size_t)b0 * T;
+            int32_t* ids_d = w.ids.as<int32_t>();
+            if (dev) HIPCHECK(hipMemcpyAsync(ids_d, ids + row0, (size_t)M * 4, hipMemcpyDeviceToDevice, s));
+            else HIPCHECK(hipMemcpyAsync(ids_d, ids + row0, (size_t)M * 4, hipMemcpyHostToDevice, s));
+            hipLaunchKernelGGL(targets_kernel, dim3((M + 255) / 256), dim3(256), 0, s, M, T, ids_d, w.tgt.as<int32_t>());
+            HIPCHECK(hipGetLastError());
+            BodyCtx c;
+            c.B = Bc; c.T = T; c.ids = ids_d;
+            run_body(m, c, s);
+            float* lg = nullptr;
+            if (logits) lg = dev ? logits + row0 * V : st.out<float>((size_t)M * V);
+            HeadCombineArgs hc;
+            hc.lse = w.lse.as<float>();
+            hc.logprob = w.logprob.as<float>();
+            run_head(m, M, nullptr, w.tgt.as<int32_t>(), lg, hc, s);
+            if (logprob) {
+                if (dev) HIPCHECK(hipMemcpyAsync(logprob + row0, w.logprob.p, (size_t)M * 4, hipMemcpyDeviceToDevice, s));
+                else HIPCHECK(hipMemcpyAsync(logprob + row0, w.logprob.p, (size_t)M * 4, hipMemcpyDeviceToHost, s));
+            }
+            if (bits) {
+                float* bd = dev ? bits + b0 : st.out<float>((size_t)Bc);
+                HIPCHECK(launch_bits(Bc, T, w.logprob.as<float>(), ids_d, V, bd, s));
+                if (!dev) HIPCHECK(hipMemcpyAsync(bits + b0, bd, (size_t)Bc * 4, hipMemcpyDeviceToHost, s));
+            }
+            if (probs) {
+                float* pd = dev ? probs + row0 * V : st.out<float>((size_t)M * V);
+                GemmArgs g = lx3_args(w.nl.as<int8_t>(), m->Dp, w.ns.as<float>(), 1, m->Dp / 64, m->headw, m->Vp, m->Dp, M, V, m->head_scale);
+                g.bias = m->headb; g.out = pd; g.ldo = V; g.lse = w.lse.as<float>();
+                gemm(3, EPI_PROBS, g, s);
+                if (!dev) HIPCHECK(hipMemcpyAsync(probs + row0 * V, pd, (size_t)M * V * 4, hipMemcpyDeviceToHost, s));
+            }
+            if (logits && !dev) HIPCHECK(hipMemcpyAsync(logits + row0 * V, lg, (size_t)M * V * 4, hipMemcpyDeviceToHost, s));
+            if (!dev) {
+                HIPCHECK(hipStreamSynchronize(s));
+                st.bufs.clear();
+            }
+        }
+        return MG_OK;
+    });
+}
+
+int mg_model_call(mg_model* m, const int32_t* ids, int n, double* logits) {
+    return guarded([&] {
+        require(m && logits, "mg_model_call: null argument");
+        if (n <= 0) return 0;
+        if (n > m->max_context) {  // quant.Model.prefill keeps the most recent maxContext tokens
+            ids += n - m->max_context;
+            n = m->max_context;
+        }
+        std::vector<float> all((size_t)n * m->V);
+        int rc = mg_forward_batch(m, ids, 1, n, all.data(), nullptr, nullptr, nullptr, 0);
+        if (rc != MG_OK) return rc;
+        for (int v = 0; v < m->V; v++) logits[v] = (double)all[(size_t)(n - 1) * m->V + v];
+        return m->V;
+    });
+}
+
+int mg_sessions_create(mg_model* m, int n, int context, mg_sessions** out) {
+    return guarded([&] {
+        require(m && out, "mg_sessions_create: null argument");
+        require(n > 0, "mg_sessions_create: n must be positive");
+        *out = nullptr;
+        Guard gd(m);
+        std::unique_ptr<mg_sessions> s(new mg_sessions());
+        s->m = m;
+        s->n = n;
+        s->window = (context > 0 && context < m->max_context) ? context : m->max_context;
+        const size_t Dp = m->Dp, D = m->D;
+        s->norm_ring.ensure(std::max<size_t>(16, (size_t)m->nbs * n * m->ring * Dp * 4));
+        s->g.ensure(std::max<size_t>(16, (size_t)m->nbs * n * Dp * 4));
+        s->kring.ensure(std::max<size_t>(16, (size_t)m->nattn * n * m->cap * D * 4));
+        s->vring.ensure(std::max<size_t>(16, (size_t)m->nattn * n * m->cap * D * 4));
+        s->pos.ensure((size_t)n * 4);
+        s->next_ids.ensure((size_t)n * 4);
+        HIPCHECK(launch_fill_f32(s->norm_ring.as<float>(), (long long)(s->norm_ring.n / 4), 0.0f, m->stream));
+        HIPCHECK(launch_fill_f32(s->g.as<float>(), (long long)(s->g.n / 4), 0.0f, m->stream));
+        HIPCHECK(launch_fill_f32(s->kring.as<float>(), (long long)(s->kring.n / 4), 0.0f, m->stream));
+        HIPCHECK(launch_fill_f32(s->vring.as<float>(), (long long)(s->vring.n / 4), 0.0f, m->stream));
+        HIPCHECK(launch_fill_i32(s->pos.as<int32_t>(), n, 0, m->stream));
+        HIPCHECK(hipStreamSynchronize(m->stream));
+        *out = s.release();
+        return MG_OK;
+    });
+}
+
+namespace {
+
+// Batched prefill on device-resident windowed prompts; leaves the head statistics in ws.
+void prefill_device(mg_sessions* s, const int32_t* prompts_d, const int32_t* lens_d, int max_len, float* logits_d,
+                    HeadCombineArgs hc, hipStream_t st) {
+    mg_model* m = s->m;
+    const int S = s->n;
+    const int Tw = std::min(max_len, s->window);
+    ensure_ws(m, S * Tw);
+    Workspace& w = m->ws;
+    w.tmp.ensure((size_t)S * Tw * 4);
+    int32_t* ids_w = w.tmp.as<int32_t>();
+    int32_t* lens_w = w.lens.as<int32_t>();
+    hipLaunchKernelGGL(window_ids_kernel, dim3(S), dim3(128), 0, st, S, max_len, s->window, Tw, prompts_d, lens_d, ids_w, lens_w);
+    HIPCHECK(hipGetLastError());
+    BodyCtx c;
+    c.B = S; c.T = Tw; c.ids = ids_w; c.sess = s; c.lens = lens_w;
+    run_body(m, c, st);
+    hipLaunchKernelGGL(last_rows_kernel, dim3((S + 255) / 256), dim3(256), 0, st, S, Tw, lens_w, w.rowmap.as<int32_t>());
+    HIPCHECK(hipGetLastError());
+    run_head(m, S, w.rowmap.as<int32_t>(), nullptr, logits_d, hc, st);
+    HIPCHECK(launch_set_pos(S, lens_w, s->pos.as<int32_t>(), 0, st));
+}
+
+void step_device(mg_sessions* s, const int32_t* ids_d, float* logits_d, HeadCombineArgs hc, hipStream_t st) {
+    mg_model* m = s->m;
+    const int S = s->n;
+    ensure_ws(m, S);
+    BodyCtx c;
+    c.B = S; c.T = 1; c.ids = ids_d; c.sess = s; c.step = true;
+    run_body(m, c, st);
+    run_head(m, S, nullptr, nullptr, logits_d, hc, st);
+    HIPCHECK(launch_set_pos(S, nullptr, s->pos.as<int32_t>(), 1, st));
+}
+
+}  // namespace
+
+int mg_sessions_prefill(mg_sessions* s, const int32_t* prompts, const int32_t* lens, int max_len, float* logits,
+                        int32_t* argmax, double* prob, int flags) {
+    return guarded([&] {
+        require(s && prompts && lens, "mg_sessions_prefill: null argument");
+        require(max_len > 0, "mg_sessions_prefill: max_len must be positive");
+        mg_model* m = s->m;
+        Guard gd(m);
+        hipStream_t st = m->stream;
+        const bool dev = flags & MG_PTR_DEVICE;
+        const int S = s->n;
+        if (!dev)
+            for (int i = 0; i < S; i++)
+                require(lens[i] >= 1 && lens[i] <= max_len, "mg_sessions_prefill: lengths must be in 1..max_len");
+        Staging sg;
+        const int32_t* p_d = dev ? prompts : sg.in(prompts, (size_t)S * max_len, st);
+        const int32_t* l_d = dev ? lens : sg.in(lens, (size_t)S, st);
+        float* lg = logits ? (dev ? logits : sg.out<float>((size_t)S * m->V)) : nullptr;
+        HeadCombineArgs hc;
+        hc.argmax = argmax ? (dev ? argmax : sg.out<int32_t>(S)) : nullptr;
+        hc.prob = prob ? (dev ? prob : sg.out<double>(S)) : nullptr;
+        prefill_device(s, p_d, l_d, max_len, lg, hc, st);
+        if (!dev) {
+            if (logits) HIPCHECK(hipMemcpyAsync(logits, lg, (size_t)S * m->V * 4, hipMemcpyDeviceToHost, st));
+            if (argmax) HIPCHECK(hipMemcpyAsync(argmax, hc.argmax, (size_t)S * 4, hipMemcpyDeviceToHost, st));
+            if (prob) HIPCHECK(hipMemcpyAsync(prob, hc.prob, (size_t)S * 8, hipMemcpyDeviceToHost, st));
+            HIPCHECK(hipStreamSynchronize(st));
+        }
+        return MG_OK;
+    });
+}
+
+int mg_sessions_step(mg_sessions* s, const int32_t* ids, float* logits, int32_t* argmax, double* prob, int flags) {
+    return guarded([&] {
+        require(s && ids, "mg_sessions_step: null argument");
+        mg_model* m = s->m;
+        Guard gd(m);
+        hipStream_t st = m->stream;
+        const bool dev = flags & MG_PTR_DEVICE;
+        const int S = s->n;
+        Staging sg;
+        const int32_t* i_d = dev ? ids : sg.in(ids, (size_t)S, st);
+        float* lg = logits ? (dev ? logits : sg.out<float>((size_t)S * m->V)) : nullptr;
+        HeadCombineArgs hc;
+        hc.argmax = argmax ? (dev ? argmax : sg.out<int32_t>(S)) : nullptr;
+        hc.prob = prob ? (dev ? prob : sg.out<double>(S)) : nullptr;
+        step_device(s, i_d, lg, hc, st);
+        if (!dev) {
+            if (logits) HIPCHECK(hipMemcpyAsync(logits, lg, (size_t)S * m->V * 4, hipMemcpyDeviceToHost, st));
+            if (argmax) HIPCHECK(hipMemcpyAsync(argmax, hc.argmax, (size_t)S * 4, hipMemcpyDeviceToHost, st));
+            if (prob) HIPCHECK(hipMemcpyAsync(prob, hc.prob, (size_t)S * 8, hipMemcpyDeviceToHost, st));
+            HIPCHECK(hipStreamSynchronize(st));
+        }
+        return MG_OK;
+    });
+}
+
+int mg_sessions_decode_greedy(mg_sessions* s, const int32_t* prompts, const int32_t* lens, int max_len,
+                              int max_tokens, int32_t* out_ids, double* out_probs, int flags) {
+    return guarded([&] {
+        require(s && prompts && lens && out_ids, "mg_sessions_decode_greedy: null argument");
+        require(max_len > 0 && max_tokens >= 0, "mg_sessions_decode_greedy: bad lengths");
+        if (max_tokens == 0) return MG_OK;
+        mg_model* m = s->m;
+        Guard gd(m);
+        hipStream_t st = m->stream;
+        const bool dev = flags & MG_PTR_DEVICE;
+        const int S = s->n;
+        if (!dev)
+            for (int i = 0; i < S; i++)
+                require(lens[i] >= 1 && lens[i] <= max_len, "mg_sessions_decode_greedy: lengths must be in 1..max_len");
+        Staging sg;
+        const int32_t* p_d = dev ? prompts : sg.in(prompts, (size_t)S * max_len, st);
+        const int32_t* l_d = dev ? lens : sg.in(lens, (size_t)S, st);
+        int32_t* oi = dev ? out_ids : sg.out<int32_t>((size_t)S * max_tokens);
+        double* op = out_probs ? (dev ? out_probs : sg.out<double>((size_t)S * max_tokens)) : nullptr;
+        HeadCombineArgs hc;
+        hc.next_ids = s->next_ids.as<int32_t>();
+        hc.out_ids = oi; hc.out_probs = op; hc.out_ld = max_tokens; hc.out_col = 0;
+        prefill_device(s, p_d, l_d, max_len, nullptr, hc, st);
+        for (int k = 1; k < max_tokens; k++) {
+            hc.out_col = k;
+            step_device(s, s->next_ids.as<int32_t>(), nullptr, hc, st);
+        }
+        if (!dev) {
+            HIPCHECK(hipMemcpyAsync(out_ids, oi, (size_t)S * max_tokens * 4, hipMemcpyDeviceToHost, st));
+            if (out_probs) HIPCHECK(hipMemcpyAsync(out_probs, op, (size_t)S * max_tokens * 8, hipMemcpyDeviceToHost, st));
+            HIPCHECK(hipStreamSynchronize(st));
+        }
+        return MG_OK;
+    });
+}
+
+long long mg_sessions_state_bytes(const mg_sessions* s) {
+    if (!s) return -1;
+    // quantSeqState.bytes (internal/quant/stream.go:87-101): CA caches at 8 bytes per element, attention
+    // rings and score scratch at 4.
+    const mg_model* m = s->m;
+    long long n = 3LL * m->D + (long long)m->nbs * ((long long)m->ring * m->D + m->D);
+    long long n32 = m->nattn > 0 ? 2LL * m->cap : 0;
+    n32 += (long long)m->nattn * 2 * m->cap * m->D;
+    return n * 8 + n32 * 4;
+}
+
+long long mg_sessions_device_bytes(const mg_sessions* s) {
+    if (!s) return -1;
+    const mg_model* m = s->m;
+    return (long long)m->nbs * (m->ring + 1) * m->Dp * 4 + (long long)m->nattn * 2 * m->cap * m->D * 4 + 8;
+}
+
+int mg_sessions_count(const mg_sessions* s) { return s ? s->n : -1; }
+
+void mg_sessions_free(mg_sessions* s) {
+    if (!s) return;
+    (void)hipSetDevice(s->m->device);
+    (void)hipStreamSynchronize(s->m->stream);
+    delete s;
+}
+
+int mg_gemm_i8(const int8_t* A, int M, int K, const int8_t* W, int N, const float* scale, float* C, int32_t* acc,
+               int flags, void* stream) {
+    return guarded([&] {
+        require(A && W && scale && (C || acc), "mg_gemm_i8: null argument");
+        require(M >= 0 && K > 0 && N > 0, "mg_gemm_i8: bad shape");
+        if (M == 0) return MG_OK;
+        hipStream_t st = (hipStream_t)stream;
+        const bool dev = flags & MG_PTR_DEVICE;
+        const int Kp = round_up(K, GEMM_BK), Np = round_up(N, GEMM_BN);
+        Staging sg;
+        // Operands in the kernel's padded layout when K or N is not a multiple of the tile; otherwise
+        // device operands are used in place.
+        const int8_t* a_d = A;
+        const int8_t* w_d = W;
+        if (!dev || Kp != K) {
+            int8_t* ap = sg.out<int8_t>((size_t)M * Kp);
+            if (Kp != K) HIPCHECK(hipMemsetAsync(ap, 0, (size_t)M * Kp, st));
+            HIPCHECK(hipMemcpy2DAsync(ap, Kp, A, K, K, M, dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, st));
+            a_d = ap;
+        }
+        if (!dev || Kp != K || Np != N) {
+            int8_t* wp = sg.out<int8_t>((size_t)Np * Kp);
+            HIPCHECK(hipMemsetAsync(wp, 0, (size_t)Np * Kp, st));
+            HIPCHECK(hipMemcpy2DAsync(wp, Kp, W, K, K, N, dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, st));
+            w_d = wp;
+        }
+        const float* s_d = dev ? scale : sg.in(scale, (size_t)N, st);
+        float* c_d = C ? (dev ? C : sg.out<float>((size_t)M * N)) : nullptr;
+        int32_t* i_d = acc ? (dev ? acc : sg.out<int32_t>((size_t)M * N)) : nullptr;
+        if (!c_d) c_d = sg.out<float>((size_t)M * N);
+        GemmArgs g;
+        g.A = a_d; g.a_row = Kp; g.a_limb = 0;
+        g.W = w_d; g.ldw = Kp; g.Np = Np; g.Kp = Kp; g.M = M; g.nvalid = N;
+        g.wscale_n = s_d; g.out = c_d; g.ldo = N; g.out_i32 = i_d;
+        HIPCHECK(launch_gemm(1, EPI_C2, g, st));
+        if (dev && !sg.bufs.empty()) HIPCHECK(hipStreamSynchronize(st));  // padded copies die on return
+        if (!dev) {
+            if (C) HIPCHECK(hipMemcpyAsync(C, c_d, (size_t)M * N * 4, hipMemcpyDeviceToHost, st));
+            if (acc) HIPCHECK(hipMemcpyAsync(acc, i_d, (size_t)M * N * 4, hipMemcpyDeviceToHost, st));
+            HIPCHECK(hipStreamSynchronize(st));
+        }
+        return MG_OK;
+    });
+}
+
+int mg_quantize_f32(const float* w, long long n, int8_t* q, float* scale, int flags, void* stream) {
+    return guarded([&] {
+        require(w && q && scale, "mg_quantize_f32: null argument");
+        require(n >= 0, "mg_quantize_f32: negative length");
+        hipStream_t st = (hipStream_t)stream;
+        const bool dev = flags & MG_PTR_DEVICE;
+        if (n == 0) {  // NewTensorF32 of an empty slice: empty tensor, scale 0
+            if (dev) HIPCHECK(hipMemsetAsync(scale, 0, 4, st));
+            else *scale = 0.0f;
+            return MG_OK;
+        }
+        Staging sg;
+        const float* w_d = dev ? w : sg.in(w, (size_t)n, st);
+        int8_t* q_d = dev ? q : sg.out<int8_t>((size_t)n);
+        float* s_d = dev ? scale : sg.out<float>(1);
+        float* tmp = sg.out<float>(4);
+        HIPCHECK(launch_quantize(w_d, n, q_d, s_d, tmp, st));
+        if (!dev) {
+            HIPCHECK(hipMemcpyAsync(q, q_d, (size_t)n, hipMemcpyDeviceToHost, st));
+            HIPCHECK(hipMemcpyAsync(scale, s_d, 4, hipMemcpyDeviceToHost, st));
+            HIPCHECK(hipStreamSynchronize(st));
+        } else {
+            HIPCHECK(hipStreamSynchronize(st));  // the temporaries above are released on return
+        }
+        return MG_OK;
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,616 @@
+// Non-GEMM kernels of the INT8 engine for gfx950: per-row embedding / residual / RMSNorm / limb
+// expansion, the selective-latch scan, windowed attention, head statistics and the quantiser.
+//
+// Arithmetic follows the reference INT8 engine (internal/quant/stream.go, internal/quant/attention.go,
+// internal/nn) with the same rounding points; the reduction orders of the reference's AVX2 kernels are
+// reproduced where a result depends on them (RMSNorm's sum of squares, attention dot products, softmax
+// sums, the P.V accumulation), so these stages are bit-identical to the reference given equal inputs.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mg {
+
+namespace {
+
+// ------------------------------------------------------------------------------------------------
+// Row kernel: one wavefront per token row; lane holds elements d = lane + 64*i.
+// ------------------------------------------------------------------------------------------------
+template <int NS>
+__global__ __launch_bounds__(64) void row_kernel(RowArgs a) {
+    __shared__ float xsh[NS * 64];
+    const int m = blockIdx.x;
+    const int lane = threadIdx.x;
+    const int D = a.D, Dp = a.Dp;
+    float x[NS];
+    if (a.mode == ROW_EMBED) {
+        // quant.Model.appendPosition: clamp the id, dequantise the embedding (stream.go:144-152)
+        int id = a.ids[m];
+        if (id < 0 || id >= a.V) id = 0;
+        const int8_t* e = a.emb + (long long)id * D;
+#pragma unroll
+        for (int i = 0; i < NS; i++) {
+            int d = lane + 64 * i;
+            float v = d < D ? (float)e[d] * a.emb_scale : 0.0f;
+            x[i] = v;
+            if (d < Dp) {
+                a.cur[(long long)m * Dp + d] = v;
+                a.block_in[(long long)m * Dp + d] = v;
+            }
+        }
+    } else if (a.mode == ROW_RESID) {
+        // inter-block residual: blockIn += cur; cur = blockIn (stream.go:157-163)
+#pragma unroll
+        for (int i = 0; i < NS; i++) {
+            int d = lane + 64 * i;
+            float v = 0.0f;
+            if (d < Dp) {
+                long long o = (long long)m * Dp + d;
+                v = a.block_in[o] + a.cur[o];
+                a.block_in[o] = v;
+                a.cur[o] = v;
+            }
+            x[i] = v;
+        }
+    } else {
+        const float* src = a.src ? a.src : a.cur;
+        int lds = a.src ? a.lds : Dp;
+        long long r = a.row_map ? a.row_map[m] : m;
+#pragma unroll
+        for (int i = 0; i < NS; i++) {
+            int d = lane + 64 * i;
+            x[i] = d < D ? src[r * lds + d] : 0.0f;
+        }
+    }
+
+    float y[NS];
+    if (a.gamma) {
+        // nn.RMSNormForwardF32 (internal/nn/rmsnorm.go:14-32) with DotF32's AVX2 accumulation:
+        // 16 partial sums (two 8-lane registers) over 16-element chunks, an 8-chunk into the first.
+#pragma unroll
+        for (int i = 0; i < NS; i++) xsh[lane + 64 * i] = x[i];
+        __syncthreads();
+        float part = 0.0f;
+        const int c16 = D / 16;
+        if (lane < 16) {
+            for (int c = 0; c < c16; c++) {
+                float v = xsh[16 * c + lane];
+                part = fmaf(v, v, part);
+            }
+            if (lane < 8 && D - 16 * c16 >= 8) {
+                float v = xsh[16 * c16 + lane];
+                part = fmaf(v, v, part);
+            }
+        }
+        float v8[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v8[j] = __shfl(part, j, 64) + __shfl(part, j + 8, 64);
+        float ss = hreduce8(v8);
+        for (int e = (D / 8) * 8; e < D; e++) {
+            float t = xsh[e];
+            float p = t * t;
+            ss = ss + p;
+        }
+        float rms = (float)sqrt((double)(ss / (float)D + 1e-5f));
+        float inv = 1.0f / rms;
+#pragma unroll
+        for (int i = 0; i < NS; i++) {
+            int d = lane + 64 * i;
+            float hat = x[i] * inv;
+            y[i] = d < D ? hat * a.gamma[d] : 0.0f;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NS; i++) y[i] = x[i];
+    }
+
+    if (a.nout) {
+#pragma unroll
+        for (int i = 0; i < NS; i++) {
+            int d = lane + 64 * i;
+            if (d < Dp) a.nout[(long long)m * Dp + d] = y[i];
+        }
+    }
+    if (a.limbs) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NS; i++) mx = fmaxf(mx, fabsf(y[i]));
+        mx = wave_max(mx);
+        float s, inv;
+        limb_scale(mx, s, inv);
+        int8_t* row = a.limbs + (long long)m * a.l_row;
+#pragma unroll
+        for (int i = 0; i < NS; i++) {
+            int d = lane + 64 * i;
+            if (d < Dp) {
+                Limbs L = split_limbs(y[i], inv);
+                row[d] = L.q0;
+                row[a.l_limb + d] = L.q1;
+                row[2 * a.l_limb + d] = L.q2;
+            }
+        }
+        if (lane == 0) a.lscale[m] = s;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Latch scan: one workgroup per sequence, one thread per channel, sequential over positions.
+// quant.Model.updateLatch (stream.go:195-205): g = lam*g + (1-lam)*n; the rule input
+// [n | left | g] (stream.go:180-184, ca.AssembleNeighborhood) is limb-expanded with one scale per row.
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void scan_kernel(ScanArgs a) {
+    __shared__ float red[2][16];
+    const int b = blockIdx.x;
+    const int d = threadIdx.x;
+    const int lane = d & 63, w = d >> 6, nw = blockDim.x >> 6;
+    const int D = a.D, Dp = a.Dp, T = a.T;
+    const long long xrow = 3LL * 3 * Dp, xlimb = 3LL * Dp;
+    const int last = a.lens ? a.lens[b] - 1 : -1;
+    float g = 0.0f;
+    for (int t = 0; t < T; t++) {
+        const long long m = (long long)b * T + t;
+        float n = 0.0f, left = 0.0f;
+        if (d < D) {
+            n = a.nf[m * Dp + d];
+            float lam = a.lam[m * Dp + d];
+            if (t >= a.dil) left = a.nf[(m - a.dil) * Dp + d];
+            float p1 = lam * g;
+            float p2 = (1.0f - lam) * n;
+            g = p1 + p2;
+        }
+        float mx = fmaxf(fabsf(n), fmaxf(fabsf(left), fabsf(g)));
+        mx = wave_max(mx);
+        if (lane == 0) red[t & 1][w] = mx;
+        __syncthreads();
+        mx = red[t & 1][0];
+        for (int i = 1; i < nw; i++) mx = fmaxf(mx, red[t & 1][i]);
+        float s, inv;
+        limb_scale(mx, s, inv);
+        int8_t* row = a.xl + m * xrow;
+        Limbs L0 = split_limbs(n, inv), L1 = split_limbs(left, inv), L2 = split_limbs(g, inv);
+        row[d] = L0.q0; row[xlimb + d] = L0.q1; row[2 * xlimb + d] = L0.q2;
+        row[Dp + d] = L1.q0; row[xlimb + Dp + d] = L1.q1; row[2 * xlimb + Dp + d] = L1.q2;
+        row[2 * Dp + d] = L2.q0; row[xlimb + 2 * Dp + d] = L2.q1; row[2 * xlimb + 2 * Dp + d] = L2.q2;
+        if (d == 0) a.xs[m] = s;
+        if (t == last && a.g_out) a.g_out[(long long)b * Dp + d] = g;
+    }
+}
+
+__global__ __launch_bounds__(1024) void latch_step_kernel(LatchStepArgs a) {
+    __shared__ float red[16];
+    const int s_ = blockIdx.x;
+    const int d = threadIdx.x;
+    const int lane = d & 63, w = d >> 6, nw = blockDim.x >> 6;
+    const int D = a.D, Dp = a.Dp;
+    const int pos = a.pos[s_];
+    float n = 0.0f, left = 0.0f, g = 0.0f;
+    if (d < D) {
+        n = a.nf[(long long)s_ * Dp + d];
+        float lam = a.lam[(long long)s_ * Dp + d];
+        g = a.g[(long long)s_ * Dp + d];
+        float p1 = lam * g;
+        float p2 = (1.0f - lam) * n;
+        g = p1 + p2;
+        a.g[(long long)s_ * Dp + d] = g;
+        float* ring = a.norm_ring + (long long)s_ * a.ring * Dp;
+        ring[(long long)(pos % a.ring) * Dp + d] = n;
+        if (pos >= a.dil) left = ring[(long long)((pos - a.dil) % a.ring) * Dp + d];
+    }
+    float mx = fmaxf(fabsf(n), fmaxf(fabsf(left), fabsf(g)));
+    mx = wave_max(mx);
+    if (lane == 0) red[w] = mx;
+    __syncthreads();
+    mx = red[0];
+    for (int i = 1; i < nw; i++) mx = fmaxf(mx, red[i]);
+    float sc, inv;
+    limb_scale(mx, sc, inv);
+    const long long xlimb = 3LL * Dp;
+    int8_t* row = a.xl + (long long)s_ * 3 * xlimb;
+    Limbs L0 = split_limbs(n, inv), L1 = split_limbs(left, inv), L2 = split_limbs(g, inv);
+    row[d] = L0.q0; row[xlimb + d] = L0.q1; row[2 * xlimb + d] = L0.q2;
+    row[Dp + d] = L1.q0; row[xlimb + Dp + d] = L1.q1; row[2 * xlimb + Dp + d] = L1.q2;
+    row[2 * Dp + d] = L2.q0; row[xlimb + 2 * Dp + d] = L2.q1; row[2 * xlimb + 2 * Dp + d] = L2.q2;
+    if (d == 0) a.xs[s_] = sc;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Attention (quant.Model.attendPosition, internal/quant/attention.go:69-104)
+// ------------------------------------------------------------------------------------------------
+
+// nn.WindowStart (internal/nn/attention.go:54-60)
+__device__ __forceinline__ int window_start(int i, int window) {
+    return (window > 0 && i - window + 1 > 0) ? i - window + 1 : 0;
+}
+
+// AddScaledF32 on AVX2 (vec_amd64.s:65-123): element i is fused when it lies in a 16- or 8-chunk,
+// the last DH % 8 elements take an unfused multiply and add.
+template <int DH>
+__device__ __forceinline__ float axpy_ref(int i, float alpha, float x, float y) {
+    constexpr int fused = (DH / 8) * 8;
+    if (i < fused) return fmaf(alpha, x, y);
+    float p = x * alpha;
+    return p + y;
+}
+
+constexpr int ATT_QT = 64;  // queries per workgroup (one per lane)
+
+// One workgroup per (sequence, 64-query tile, head). Keys of the tile's whole window are staged in LDS,
+// each lane scores its query against them (DotF32 order), runs the reference softmax, then the values
+// replace the keys in LDS for the P.V accumulation.
+template <int DH>
+__global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
+    extern __shared__ float smem[];
+    const int nqt = (a.T + ATT_QT - 1) / ATT_QT;
+    const int b = blockIdx.x / nqt, qt = blockIdx.x % nqt;
+    const int h = blockIdx.y;
+    const int lane = threadIdx.x;
+    const int T = a.T, D = a.D, cap = a.cap;
+    const int t0 = qt * ATT_QT;
+    const int t1 = min(t0 + ATT_QT, T);
+    const int r0 = max(window_start(t0, a.window), max(t0 - cap + 1, 0));
+    const int rows = t1 - r0;
+    float* kv = smem;                    // [rows][DH]
+    float* sc = smem + (ATT_QT + cap - 1) * DH;  // [cap][64]
+    const long long base = (long long)b * T;
+    const int ld = 3 * D;
+
+    for (int e = lane; e < rows * DH; e += 64) {
+        int r = e / DH, i = e % DH;
+        kv[e] = a.qkv[(base + r0 + r) * ld + D + h * DH + i];
+    }
+    __syncthreads();
+
+    const int t = t0 + lane;
+    const bool active = t < t1;
+    float q[DH];
+    int lo = 0, span = 0;
+    float inv = 0.0f;
+    if (active) {
+#pragma unroll
+        for (int i = 0; i < DH; i++) q[i] = a.qkv[(base + t) * ld + h * DH + i];
+        lo = max(window_start(t, a.window), t - cap + 1);
+        span = t - lo + 1;
+        const float scale = (float)(1.0 / sqrt((double)DH));
+        float mx = -3.40282347e38f;
+        for (int jj = 0; jj < span; jj++) {
+            const float* k = kv + (lo + jj - r0) * DH;
+            float s = dot_f32_ref<DH>(q, k) * scale;
+            sc[jj * 64 + lane] = s;
+            if (s > mx) mx = s;
+        }
+        // nn.SoftmaxInPlaceF32 (internal/nn/head.go:151-172)
+        float sum = 0.0f;
+        for (int jj = 0; jj < span; jj++) {
+            float e = fast_exp_ref(sc[jj * 64 + lane] - mx);
+            sc[jj * 64 + lane] = e;
+            sum += e;
+        }
+        inv = 1.0f / sum;
+    }
+    __syncthreads();
+    for (int e = lane; e < rows * DH; e += 64) {
+        int r = e / DH, i = e % DH;
+        kv[e] = a.qkv[(base + r0 + r) * ld + 2 * D + h * DH + i];
+    }
+    __syncthreads();
+    if (!active) return;
+    float o[DH];
+#pragma unroll
+    for (int i = 0; i < DH; i++) o[i] = 0.0f;
+    for (int jj = 0; jj < span; jj++) {
+        float p = sc[jj * 64 + lane] * inv;
+        const float* v = kv + (lo + jj - r0) * DH;
+#pragma unroll
+        for (int i = 0; i < DH; i++) o[i] = axpy_ref<DH>(i, p, v[i], o[i]);
+    }
+    float* dst = a.att + (base + t) * a.Dp + h * DH;
+#pragma unroll
+    for (int i = 0; i < DH; i++) dst[i] = o[i];
+}
+
+// One wavefront per (session, head): lane j scores key j of the ring, lane i accumulates output i.
+template <int DH>
+__global__ __launch_bounds__(64) void attention_step_kernel(AttnStepArgs a) {
+    __shared__ float es[256];
+    __shared__ float qs[DH];
+    __shared__ float inv_sh;
+    const int s_ = blockIdx.x / a.heads, h = blockIdx.x % a.heads;
+    const int lane = threadIdx.x;
+    const int D = a.D, cap = a.cap;
+    const int pos = a.pos[s_];
+    const int lo = max(window_start(pos, a.window), pos - cap + 1);
+    const int span = pos - lo + 1;
+    const float* qkv = a.qkv + (long long)s_ * 3 * D;
+    const float* kr = a.kring + (long long)s_ * cap * D;
+    const float* vr = a.vring + (long long)s_ * cap * D;
+    for (int i = lane; i < DH; i += 64) qs[i] = qkv[h * DH + i];
+    __syncthreads();
+    float q[DH];
+#pragma unroll
+    for (int i = 0; i < DH; i++) q[i] = qs[i];
+    const float scale = (float)(1.0 / sqrt((double)DH));
+    float mx = -3.40282347e38f;
+    for (int jj = lane; jj < span; jj += 64) {
+        int j = lo + jj;
+        const float* k = (j == pos) ? qkv + D + h * DH : kr + (long long)(j % cap) * D + h * DH;
+        float s = dot_f32_ref<DH>(q, k) * scale;
+        es[jj] = s;
+        mx = fmaxf(mx, s);
+    }
+    mx = wave_max(mx);
+    for (int jj = lane; jj < span; jj += 64) es[jj] = fast_exp_ref(es[jj] - mx);
+    __syncthreads();
+    if (lane == 0) {
+        float sum = 0.0f;
+        for (int jj = 0; jj < span; jj++) sum += es[jj];
+        inv_sh = 1.0f / sum;
+    }
+    __syncthreads();
+    const float inv = inv_sh;
+    for (int i = lane; i < DH; i += 64) {
+        float o = 0.0f;
+        for (int jj = 0; jj < span; jj++) {
+            int j = lo + jj;
+            float p = es[jj] * inv;
+            float v = (j == pos) ? qkv[2 * D + h * DH + i] : vr[(long long)(j % cap) * D + h * DH + i];
+            o = axpy_ref<DH>(i, p, v, o);
+        }
+        a.att[(long long)s_ * a.Dp + h * DH + i] = o;
+    }
+    // record this position's key and value (slot pos % cap; the evicted key is outside the window)
+    float* kw = a.kring + (long long)s_ * cap * D + (long long)(pos % cap) * D + h * DH;
+    float* vw = a.vring + (long long)s_ * cap * D + (long long)(pos % cap) * D + h * DH;
+    for (int i = lane; i < DH; i += 64) {
+        kw[i] = qkv[D + h * DH + i];
+        vw[i] = qkv[2 * D + h * DH + i];
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Head statistics, log-probs, bits
+// ------------------------------------------------------------------------------------------------
+__global__ void head_combine_kernel(HeadCombineArgs a) {
+    const int m = blockIdx.x * blockDim.x + threadIdx.x;
+    if (m >= a.M) return;
+    const float* st = a.stats + (long long)m * a.ntiles * 3;
+    float bm = -INFINITY, bs = 0.0f;
+    int bi = 0x7fffffff;
+    for (int t = 0; t < a.ntiles; t++) {
+        float om = st[3 * t], os = st[3 * t + 1];
+        int oi = __float_as_int(st[3 * t + 2]);
+        if (om == -INFINITY) continue;
+        float nm = fmaxf(bm, om);
+        float ns = (bm == -INFINITY ? 0.0f : bs * __expf(bm - nm)) + os * __expf(om - nm);
+        int ni = (om > bm) ? oi : (bm > om) ? bi : min(bi, oi);
+        bm = nm; bs = ns; bi = ni;
+    }
+    float lse = bm + logf(bs);
+    if (a.lse) a.lse[m] = lse;
+    if (a.argmax) a.argmax[m] = bi;
+    double p = 1.0 / (double)bs;
+    if (a.prob) a.prob[m] = p;
+    if (a.logprob) {
+        int tg = a.tgt ? a.tgt[m] : -1;
+        a.logprob[m] = (tg >= 0 && tg < a.V) ? a.tlog[m] - lse : __int_as_float(0x7fc00000);
+    }
+    if (a.next_ids) a.next_ids[m] = bi;
+    if (a.out_ids) a.out_ids[(long long)m * a.out_ld + a.out_col] = bi;
+    if (a.out_probs) a.out_probs[(long long)m * a.out_ld + a.out_col] = p;
+}
+
+// eval's nll.score accumulates nats in float64 target by target (internal/eval/eval.go:25-48);
+// tokenizer.BitsPerByte divides by ln 2 and the count (internal/tokenizer/bytes.go:5-11), with the
+// token count in place of bytes. Position t's logits predict ids[t+1].
+__global__ void bits_kernel(int B, int T, const float* logprob, const int32_t* ids, int V, float* bits) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= B) return;
+    double nats = 0.0;
+    int n = 0;
+    for (int t = 0; t + 1 < T; t++) {
+        int tg = ids[(long long)b * T + t + 1];
+        if (tg < 0 || tg >= V) continue;
+        nats -= (double)logprob[(long long)b * T + t];
+        n++;
+    }
+    bits[b] = n ? (float)(nats / (0.6931471805599453 * n)) : 0.0f;
+}
+
+// ------------------------------------------------------------------------------------------------
+// quant.NewTensorF32 (internal/quant/tensor.go:12-42)
+// ------------------------------------------------------------------------------------------------
+__global__ void absmax_kernel(const float* w, long long n, unsigned* out) {
+    float m = 0.0f;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x)
+        m = fmaxf(m, fabsf(w[i]));
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0) atomicMax(out, __float_as_uint(m));
+}
+
+__global__ void quantize_kernel(const float* w, long long n, int8_t* q, const unsigned* amax_bits, float* scale_out) {
+    const float maxAbs = __uint_as_float(*amax_bits);
+    const float s = maxAbs / 127.0f;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
+        float v = 0.0f;
+        if (maxAbs != 0.0f) {
+            v = roundf(w[i] / s);  // round half away from zero, like math.Round
+            v = fminf(fmaxf(v, -127.0f), 127.0f);
+        }
+        q[i] = (int8_t)v;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = maxAbs == 0.0f ? 1.0f : s;
+}
+
+// ------------------------------------------------------------------------------------------------
+// session state export and small helpers
+// ------------------------------------------------------------------------------------------------
+__global__ void export_ring_kernel(int B, int T, int Dp, int ring, const int32_t* lens, const float* nf, float* nr) {
+    const int b = blockIdx.x;
+    const int len = lens[b];
+    const int p0 = max(0, len - ring);
+    for (int p = p0; p < len; p++)
+        for (int d = threadIdx.x; d < Dp; d += blockDim.x)
+            nr[((long long)b * ring + p % ring) * Dp + d] = nf[((long long)b * T + p) * Dp + d];
+}
+
+__global__ void export_kv_kernel(int B, int T, int D, int cap, const int32_t* lens, const float* qkv, float* kr,
+                                 float* vr) {
+    const int b = blockIdx.x;
+    const int len = lens[b];
+    const int p0 = max(0, len - cap);
+    for (int p = p0; p < len; p++)
+        for (int d = threadIdx.x; d < D; d += blockDim.x) {
+            const float* row = qkv + ((long long)b * T + p) * 3 * D;
+            kr[((long long)b * cap + p % cap) * D + d] = row[D + d];
+            vr[((long long)b * cap + p % cap) * D + d] = row[2 * D + d];
+        }
+}
+
+__global__ void set_pos_kernel(int S, const int32_t* lens, int32_t* pos, int add) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < S) pos[i] = (lens ? lens[i] : pos[i]) + add;
+}
+
+__global__ void fill_i32_kernel(int32_t* p, int n, int v) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+__global__ void fill_f32_kernel(float* p, long long n, float v) {
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+template <int DH>
+hipError_t attn_t(const AttnArgs& a, hipStream_t s) {
+    const int nqt = (a.T + ATT_QT - 1) / ATT_QT;
+    size_t lds = (size_t)((ATT_QT + a.cap - 1) * DH + a.cap * 64) * sizeof(float);
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(attention_kernel<DH>, dim3(a.B * nqt, a.heads), dim3(64), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int DH>
+hipError_t attn_step_t(const AttnStepArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(attention_step_kernel<DH>, dim3(a.S * a.heads), dim3(64), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_row(const RowArgs& a, hipStream_t s) {
+    if (a.M <= 0) return hipSuccess;
+    const int ns = a.Dp / 64;
+    if (a.Dp % 64 || ns < 1 || ns > 16) return hipErrorInvalidValue;
+#define ROW_CASE(N) \
+    case N: hipLaunchKernelGGL(row_kernel<N>, dim3(a.M), dim3(64), 0, s, a); break;
+    switch (ns) {
+        ROW_CASE(1) ROW_CASE(2) ROW_CASE(3) ROW_CASE(4) ROW_CASE(5) ROW_CASE(6) ROW_CASE(7) ROW_CASE(8)
+        ROW_CASE(9) ROW_CASE(10) ROW_CASE(11) ROW_CASE(12) ROW_CASE(13) ROW_CASE(14) ROW_CASE(15) ROW_CASE(16)
+    }
+#undef ROW_CASE
+    return hipGetLastError();
+}
+
+hipError_t launch_scan(const ScanArgs& a, hipStream_t s) {
+    if (a.B <= 0) return hipSuccess;
+    if (a.Dp % 64 || a.Dp > 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(scan_kernel, dim3(a.B), dim3(a.Dp), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_latch_step(const LatchStepArgs& a, hipStream_t s) {
+    if (a.S <= 0) return hipSuccess;
+    if (a.Dp % 64 || a.Dp > 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(latch_step_kernel, dim3(a.S), dim3(a.Dp), 0, s, a);
+    return hipGetLastError();
+}
+
+#define DH_SWITCH(dh, FN, ...)                \
+    switch (dh) {                             \
+        case 1: return FN<1>(__VA_ARGS__);     \
+        case 2: return FN<2>(__VA_ARGS__);     \
+        case 4: return FN<4>(__VA_ARGS__);     \
+        case 8: return FN<8>(__VA_ARGS__);     \
+        case 12: return FN<12>(__VA_ARGS__);   \
+        case 20: return FN<20>(__VA_ARGS__);   \
+        case 40: return FN<40>(__VA_ARGS__);   \
+        case 80: return FN<80>(__VA_ARGS__);   \
+        case 16: return FN<16>(__VA_ARGS__);   \
+        case 24: return FN<24>(__VA_ARGS__);   \
+        case 32: return FN<32>(__VA_ARGS__);   \
+        case 48: return FN<48>(__VA_ARGS__);   \
+        case 64: return FN<64>(__VA_ARGS__);   \
+        case 96: return FN<96>(__VA_ARGS__);   \
+        case 128: return FN<128>(__VA_ARGS__); \
+        default: return hipErrorInvalidValue; \
+    }
+
+hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
+    if (a.B <= 0 || a.T <= 0) return hipSuccess;
+    if (a.heads <= 0 || a.D % a.heads || a.cap <= 0 || a.cap > 256) return hipErrorInvalidValue;
+    DH_SWITCH(a.D / a.heads, attn_t, a, s)
+}
+
+hipError_t launch_attention_step(const AttnStepArgs& a, hipStream_t s) {
+    if (a.S <= 0) return hipSuccess;
+    if (a.heads <= 0 || a.D % a.heads || a.cap <= 0 || a.cap > 256) return hipErrorInvalidValue;
+    DH_SWITCH(a.D / a.heads, attn_step_t, a, s)
+}
+
+hipError_t launch_head_combine(const HeadCombineArgs& a, hipStream_t s) {
+    if (a.M <= 0) return hipSuccess;
+    hipLaunchKernelGGL(head_combine_kernel, dim3((a.M + 255) / 256), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_bits(int B, int T, const float* logprob, const int32_t* ids, int V, float* bits, hipStream_t s) {
+    if (B <= 0) return hipSuccess;
+    hipLaunchKernelGGL(bits_kernel, dim3((B + 255) / 256), dim3(256), 0, s, B, T, logprob, ids, V, bits);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize(const float* w, long long n, int8_t* q, float* scale, float* amax_tmp, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    unsigned* am = (unsigned*)amax_tmp;
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, s, (int32_t*)am, 1, 0);
+    long long blocks = (n + 255) / 256;
+    int g = (int)(blocks < 4096 ? blocks : 4096);
+    hipLaunchKernelGGL(absmax_kernel, dim3(g), dim3(256), 0, s, w, n, am);
+    hipLaunchKernelGGL(quantize_kernel, dim3(g), dim3(256), 0, s, w, n, q, am, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_export_ring(int B, int T, int Dp, int ring, const int32_t* lens, const float* nf, float* norm_ring,
+                              hipStream_t s) {
+    if (B <= 0) return hipSuccess;
+    hipLaunchKernelGGL(export_ring_kernel, dim3(B), dim3(256), 0, s, B, T, Dp, ring, lens, nf, norm_ring);
+    return hipGetLastError();
+}
+
+hipError_t launch_export_kv(int B, int T, int D, int cap, const int32_t* lens, const float* qkv, float* kring,
+                            float* vring, hipStream_t s) {
+    if (B <= 0) return hipSuccess;
+    hipLaunchKernelGGL(export_kv_kernel, dim3(B), dim3(256), 0, s, B, T, D, cap, lens, qkv, kring, vring);
+    return hipGetLastError();
+}
+
+hipError_t launch_set_pos(int S, const int32_t* lens, int32_t* pos, int add, hipStream_t s) {
+    if (S <= 0) return hipSuccess;
+    hipLaunchKernelGGL(set_pos_kernel, dim3((S + 255) / 256), dim3(256), 0, s, S, lens, pos, add);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_i32(int32_t* p, int n, int v, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_i32_kernel, dim3((n + 255) / 256), dim3(256), 0, s, p, n, v);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_f32(float* p, long long n, float v, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    long long blocks = (n + 255) / 256;
+    int g = (int)(blocks < 8192 ? blocks : 8192);
+    hipLaunchKernelGGL(fill_f32_kernel, dim3(g), dim3(256), 0, s, p, n, v);
+    return hipGetLastError();
+}
+
+}  // namespace mg

@@ -1,0 +1,109 @@
+// Launchers for the engine's non-GEMM kernels (see kernels.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mg {
+
+enum RowMode : int { ROW_SRC = 0, ROW_EMBED = 1, ROW_RESID = 2 };
+
+struct RowArgs {
+    int M = 0, D = 0, Dp = 0;
+    int mode = ROW_SRC;
+    const int32_t* ids = nullptr;      // ROW_EMBED
+    const int8_t* emb = nullptr;       // [V][D]
+    float emb_scale = 0;
+    int V = 0;
+    float* cur = nullptr;              // [M][Dp] (ROW_EMBED, ROW_RESID, and ROW_SRC when src is null)
+    float* block_in = nullptr;         // [M][Dp]
+    const float* src = nullptr;        // ROW_SRC source rows (row stride lds), or null for cur
+    int lds = 0;
+    const int32_t* row_map = nullptr;  // ROW_SRC: output row m reads source row row_map[m]
+    const float* gamma = nullptr;      // RMSNorm scales, or null (copy)
+    float* nout = nullptr;             // normalised rows [M][Dp], or null
+    int8_t* limbs = nullptr;           // limb-expanded rows: row m, limb l at limbs + m*l_row + l*l_limb
+    long long l_row = 0, l_limb = 0;
+    float* lscale = nullptr;           // [M]
+};
+hipError_t launch_row(const RowArgs& a, hipStream_t s);
+
+// Selective latch over whole sequences plus the rule input [n | left | g] (teacher-forced forward).
+struct ScanArgs {
+    int B = 0, T = 0, D = 0, Dp = 0, dil = 1;
+    const float* lam = nullptr;  // [B*T][Dp]
+    const float* nf = nullptr;   // [B*T][Dp]
+    int8_t* xl = nullptr;        // [B*T][3][3*Dp]
+    float* xs = nullptr;         // [B*T]
+    const int32_t* lens = nullptr;  // per-sequence length (export position lens[b]-1) or null
+    float* g_out = nullptr;         // exported latch state [B][Dp] or null
+};
+hipError_t launch_scan(const ScanArgs& a, hipStream_t s);
+
+// One streaming position per session: latch update, norm ring write and the rule input.
+struct LatchStepArgs {
+    int S = 0, D = 0, Dp = 0, dil = 1, ring = 1;
+    const int32_t* pos = nullptr;  // [S]
+    const float* lam = nullptr;    // [S][Dp]
+    const float* nf = nullptr;     // [S][Dp]
+    float* g = nullptr;            // latch state [S][Dp]
+    float* norm_ring = nullptr;    // [S][ring][Dp]
+    int8_t* xl = nullptr;          // [S][3][3*Dp]
+    float* xs = nullptr;           // [S]
+};
+hipError_t launch_latch_step(const LatchStepArgs& a, hipStream_t s);
+
+// Windowed causal attention over whole sequences (teacher-forced forward).
+struct AttnArgs {
+    int B = 0, T = 0, D = 0, Dp = 0, heads = 0, window = 0, cap = 0;
+    const float* qkv = nullptr;  // [B*T][3D]
+    float* att = nullptr;        // [B*T][Dp]
+};
+hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
+
+// Attention for one streaming position per session over its key/value ring.
+struct AttnStepArgs {
+    int S = 0, D = 0, Dp = 0, heads = 0, window = 0, cap = 0;
+    const int32_t* pos = nullptr;  // [S]
+    const float* qkv = nullptr;    // [S][3D]
+    float* kring = nullptr;        // [S][cap][D]
+    float* vring = nullptr;        // [S][cap][D]
+    float* att = nullptr;          // [S][Dp]
+};
+hipError_t launch_attention_step(const AttnStepArgs& a, hipStream_t s);
+
+// Per-row combination of the head GEMM's per-tile statistics.
+struct HeadCombineArgs {
+    int M = 0, ntiles = 0;
+    const float* stats = nullptr;  // [M][ntiles][3]
+    float* lse = nullptr;          // [M] or null
+    int32_t* argmax = nullptr;     // [M] or null
+    double* prob = nullptr;        // [M] or null: 1 / sum exp(l - max)
+    const float* tlog = nullptr;   // [M] target logits (with tgt)
+    const int32_t* tgt = nullptr;  // [M] target ids (invalid: < 0 or >= V)
+    int V = 0;
+    float* logprob = nullptr;      // [M] or null
+    // greedy decode bookkeeping (optional)
+    int32_t* next_ids = nullptr;   // [M]
+    int32_t* out_ids = nullptr;    // [M][out_ld] at column out_col
+    double* out_probs = nullptr;
+    int out_ld = 0, out_col = 0;
+};
+hipError_t launch_head_combine(const HeadCombineArgs& a, hipStream_t s);
+
+// Per-sequence bits per token from per-position log-probs (targets t = 1..T-1).
+hipError_t launch_bits(int B, int T, const float* logprob, const int32_t* ids, int V, float* bits, hipStream_t s);
+
+// Per-tensor symmetric quantiser (quant.NewTensorF32).
+hipError_t launch_quantize(const float* w, long long n, int8_t* q, float* scale, float* amax_tmp, hipStream_t s);
+
+// Session state export after a batched prefill.
+hipError_t launch_export_ring(int B, int T, int Dp, int ring, const int32_t* lens, const float* nf, float* norm_ring,
+                              hipStream_t s);
+hipError_t launch_export_kv(int B, int T, int D, int cap, const int32_t* lens, const float* qkv, float* kring,
+                            float* vring, hipStream_t s);
+hipError_t launch_set_pos(int S, const int32_t* lens, int32_t* pos, int add, hipStream_t s);
+hipError_t launch_fill_i32(int32_t* p, int n, int v, hipStream_t s);
+hipError_t launch_fill_f32(float* p, long long n, float v, hipStream_t s);
+
+}  // namespace mg

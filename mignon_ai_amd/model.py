@@ -1,0 +1,221 @@
+"""Python host API over the C ABI, mirroring the reference's Go interfaces for this path:
+
+  Model        quant.Model      (internal/quant/model.go:60-137): info accessors, call/forward (LogitsFn),
+                                new_session (infer.SessionProvider, internal/infer/infer.go:17-20)
+  Session      infer.Session    (internal/infer/infer.go:8-15) as quantSession implements it
+                                (internal/quant/session.go:11-68)
+  Sessions     the batched form: n sessions advancing together on the GPU
+  forward_batch                 every position of B sequences at once (teacher-forced scoring)
+
+Arrays are numpy on the host; the *_device methods take torch CUDA tensors and only enqueue work on
+the model's stream.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from ._lib import MG_PTR_DEVICE, ModelInfo, check, lib, ptr
+
+
+def _i32(a):
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+class Model:
+    def __init__(self, data: bytes, max_context: int = 0):
+        buf = (ctypes.c_uint8 * len(data)).from_buffer_copy(data)
+        h = ctypes.c_void_p()
+        check(lib().mg_model_load(buf, len(data), int(max_context), ctypes.byref(h)))
+        self._h = h
+        self.info = ModelInfo()
+        check(lib().mg_model_info(self._h, ctypes.byref(self.info)))
+
+    @classmethod
+    def load(cls, path: str, max_context: int = 0) -> "Model":
+        with open(path, "rb") as f:
+            return cls(f.read(), max_context)
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().mg_model_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def handle(self):
+        return self._h
+
+    # quant.Model accessors
+    def vocab_size(self) -> int:
+        return self.info.vocab_size
+
+    def state_size(self) -> int:
+        return self.info.state_size
+
+    def hidden_size(self) -> int:
+        return self.info.hidden_size
+
+    def num_blocks(self) -> int:
+        return self.info.num_blocks
+
+    def num_params(self) -> int:
+        return self.info.num_params
+
+    @property
+    def max_context(self) -> int:
+        return self.info.max_context
+
+    def set_stream(self, stream_ptr: int | None):
+        check(lib().mg_model_set_stream(self._h, stream_ptr))
+
+    def sync(self):
+        check(lib().mg_model_sync(self._h))
+
+    # quant.Model.Call / Forward (LogitsFn)
+    def call(self, ids):
+        ids = _i32(ids)
+        out = np.empty(self.vocab_size(), np.float64)
+        n = check(lib().mg_model_call(self._h, ptr(ids), len(ids), ptr(out)))
+        return out if n else None
+
+    forward = call
+
+    def forward_batch(self, ids2d, logits=True, logprob=False, probs=False, bits=False):
+        ids = _i32(ids2d)
+        B, T = ids.shape
+        V = self.vocab_size()
+        out = {}
+        lg = np.empty((B, T, V), np.float32) if logits else None
+        lp = np.empty((B, T), np.float32) if logprob else None
+        pr = np.empty((B, T, V), np.float32) if probs else None
+        bt = np.empty(B, np.float32) if bits else None
+        check(lib().mg_forward_batch(self._h, ptr(ids), B, T, ptr(lg), ptr(lp), ptr(pr), ptr(bt), 0))
+        for k, v in (("logits", lg), ("logprob", lp), ("probs", pr), ("bits", bt)):
+            if v is not None:
+                out[k] = v
+        return out
+
+    def forward_batch_device(self, ids, logits=None, logprob=None, probs=None, bits=None):
+        B, T = ids.shape
+        check(lib().mg_forward_batch(self._h, ptr(ids), B, T, ptr(logits), ptr(logprob), ptr(probs), ptr(bits),
+                                     MG_PTR_DEVICE))
+
+    def new_session(self, context_size: int = 0) -> "Session":
+        return Session(self, context_size)
+
+    def sessions(self, n: int, context_size: int = 0) -> "Sessions":
+        return Sessions(self, n, context_size)
+
+
+class Sessions:
+    def __init__(self, model: Model, n: int, context_size: int = 0):
+        self.model = model
+        h = ctypes.c_void_p()
+        check(lib().mg_sessions_create(model.handle, int(n), int(context_size), ctypes.byref(h)))
+        self._h = h
+        self.n = n
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().mg_sessions_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def state_bytes(self) -> int:
+        return lib().mg_sessions_state_bytes(self._h)
+
+    def device_bytes(self) -> int:
+        return lib().mg_sessions_device_bytes(self._h)
+
+    def prefill(self, prompts2d, lens=None, logits=True):
+        p = _i32(prompts2d)
+        n, L = p.shape
+        lens = _i32(lens if lens is not None else np.full(n, L))
+        V = self.model.vocab_size()
+        lg = np.empty((n, V), np.float32) if logits else None
+        am = np.empty(n, np.int32)
+        pb = np.empty(n, np.float64)
+        check(lib().mg_sessions_prefill(self._h, ptr(p), ptr(lens), L, ptr(lg), ptr(am), ptr(pb), 0))
+        return lg, am, pb
+
+    def step(self, ids, logits=True):
+        ids = _i32(ids)
+        V = self.model.vocab_size()
+        lg = np.empty((self.n, V), np.float32) if logits else None
+        am = np.empty(self.n, np.int32)
+        pb = np.empty(self.n, np.float64)
+        check(lib().mg_sessions_step(self._h, ptr(ids), ptr(lg), ptr(am), ptr(pb), 0))
+        return lg, am, pb
+
+    def decode_greedy(self, prompts2d, max_tokens, lens=None):
+        p = _i32(prompts2d)
+        n, L = p.shape
+        lens = _i32(lens if lens is not None else np.full(n, L))
+        ids = np.empty((n, max_tokens), np.int32)
+        probs = np.empty((n, max_tokens), np.float64)
+        check(lib().mg_sessions_decode_greedy(self._h, ptr(p), ptr(lens), L, int(max_tokens), ptr(ids), ptr(probs), 0))
+        return ids, probs
+
+    def decode_greedy_device(self, prompts, lens, max_tokens, out_ids, out_probs):
+        n, L = prompts.shape
+        check(lib().mg_sessions_decode_greedy(self._h, ptr(prompts), ptr(lens), L, int(max_tokens), ptr(out_ids),
+                                              ptr(out_probs), MG_PTR_DEVICE))
+
+
+class Session:
+    """One streaming session with quantSession's semantics (internal/quant/session.go:30-56): Prefill
+    resets and keeps the last `window` tokens, an empty Prefill returns None and leaves the state, Append
+    streams on (a never-prefilled session starts from an empty state, as the reference's re-prefill of a
+    single held token does)."""
+
+    def __init__(self, model: Model, context_size: int = 0):
+        self._s = Sessions(model, 1, context_size)
+        self.V = model.vocab_size()
+
+    def prefill(self, tokens):
+        tokens = _i32(tokens)
+        if len(tokens) == 0:
+            return None
+        lg, _, _ = self._s.prefill(tokens[None, :])
+        return lg[0].astype(np.float64)
+
+    def append(self, token):
+        lg, _, _ = self._s.step(np.array([token], np.int32))
+        return lg[0].astype(np.float64)
+
+    def state_bytes(self) -> int:
+        return self._s.state_bytes()
+
+
+def gemm_i8(A, W, scale, want_acc=False):
+    """mg_gemm_i8 on host arrays: A [M][K] int8, W [N][K] int8, scale [N] -> C [M][N] (and int32 acc)."""
+    A = np.ascontiguousarray(A, np.int8)
+    W = np.ascontiguousarray(W, np.int8)
+    s = np.ascontiguousarray(scale, np.float32)
+    M, K = A.shape
+    N = W.shape[0]
+    C = np.empty((M, N), np.float32)
+    acc = np.empty((M, N), np.int32) if want_acc else None
+    check(lib().mg_gemm_i8(ptr(A), M, K, ptr(W), N, ptr(s), ptr(C), ptr(acc), 0, None))
+    return (C, acc) if want_acc else C
+
+
+def gemm_i8_device(A, W, scale, C, acc=None, stream=None):
+    M, K = A.shape
+    N = W.shape[0]
+    check(lib().mg_gemm_i8(ptr(A), M, K, ptr(W), N, ptr(scale), ptr(C), ptr(acc), MG_PTR_DEVICE, stream))
+
+
+def quantize_f32(w):
+    """mg_quantize_f32 on a host array -> (int8 data, fp32 scale): quant.NewTensorF32 on the GPU."""
+    w = np.ascontiguousarray(w, np.float32).ravel()
+    q = np.empty(w.shape, np.int8)
+    s = np.zeros(1, np.float32)
+    check(lib().mg_quantize_f32(ptr(w), len(w), ptr(q), ptr(s), 0, None))
+    return q, np.float32(s[0])

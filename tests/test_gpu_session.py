@@ -1,0 +1,78 @@
+"""Streaming sessions and batched greedy decode through the C ABI."""
+import numpy as np
+import pytest
+
+from helpers import EQUIV_CASES, assert_close, equiv_model_bytes, model_bytes, oracle_model
+from mignon_ai_amd import Model, synth
+
+pytestmark = pytest.mark.gpu
+
+WINDOW, TOKENS, PREFILL = 12, 40, 5  # internal/quant/session_test.go:9-13
+
+
+@pytest.mark.parametrize("case", list(EQUIV_CASES))
+def test_session_matches_oracle(case):
+    """TestQuantSessionMatchesCall's sequence (internal/quant/session_test.go:18-52) on the GPU engine,
+    each output checked against the oracle's session."""
+    data = equiv_model_bytes(case)
+    gm = Model(data)
+    om = oracle_model(data)
+    rng = np.random.default_rng(9)
+    toks = rng.integers(0, 16, TOKENS).astype(np.int32)
+    gs = gm.new_session(WINDOW)
+    os_ = om.new_session(WINDOW)
+    assert_close(gs.prefill(toks[:PREFILL]), os_.prefill(toks[:PREFILL]), what="prefill")
+    for i in range(PREFILL, TOKENS):
+        assert_close(gs.append(toks[i]), os_.append(toks[i]), what=f"append {i}")
+    long = toks[:2 * WINDOW]
+    assert_close(gs.prefill(long), os_.prefill(long), what="long prefill")
+    assert gs.state_bytes() == os_.state_bytes()
+
+
+def test_batched_sessions_match_forward():
+    """Session Prefill + Append per position equals the teacher-forced batch (both on the GPU)."""
+    data = model_bytes("c3")
+    spec = synth.CONFIGS["c3"]["spec"]
+    gm = Model(data)
+    S, P, G = 16, 8, 24
+    ids = synth.token_ids(4, "c3:sess", (S, P + G), spec.V)
+    full = gm.forward_batch(ids)["logits"]
+    ss = gm.sessions(S)
+    lg, am, pb = ss.prefill(ids[:, :P])
+    assert_close(lg, full[:, P - 1], what="prefill")
+    assert np.array_equal(am, lg.argmax(-1))
+    for t in range(P, P + G):
+        lg, am, pb = ss.step(ids[:, t])
+        assert_close(lg, full[:, t], what=f"step {t}")
+
+
+def test_ragged_prefill():
+    data = model_bytes("c3")
+    spec = synth.CONFIGS["c3"]["spec"]
+    gm = Model(data)
+    om = oracle_model(data)
+    lens = np.array([1, 5, 32, 17], np.int32)
+    ids = synth.token_ids(5, "c3:ragged", (4, 32), spec.V)
+    ss = gm.sessions(4)
+    lg, am, pb = ss.prefill(ids, lens)
+    for i, L in enumerate(lens):
+        assert_close(lg[i], om.call(ids[i, :L]), what=f"session {i}")
+    nxt = synth.token_ids(6, "c3:ragged2", (4,), spec.V)
+    lg2, _, _ = ss.step(nxt)
+    for i, L in enumerate(lens):
+        assert_close(lg2[i], om.call(np.concatenate([ids[i, :L], nxt[i:i + 1]])), what=f"session {i} step")
+
+
+def test_greedy_decode_matches_oracle():
+    """Config-4 shape, a subset of sessions: greedy tokens identical to the oracle's greedyLoop."""
+    data = model_bytes("c4")
+    spec = synth.CONFIGS["c4"]["spec"]
+    gm = Model(data)
+    om = oracle_model(data)
+    S, P, G = 8, 32, 64
+    prompts = synth.token_ids(3, "c4:prompts", (S, P), spec.V)
+    ss = gm.sessions(S)
+    ids, probs = ss.decode_greedy(prompts, G)
+    rid, rprob = om.greedy(prompts, G)
+    assert np.array_equal(ids, rid)
+    assert np.allclose(probs, rprob, rtol=1e-4)
