@@ -1,0 +1,306 @@
+#!/usr/bin/env python3
+"""Benchmark of the batched INT8 engine on one MI355X.
+
+    python bench.py [--config c5] [--steps K] [--warmup W] [--gpus 1]
+
+Prints one JSON line. A step is one pass of the hot path over one batch of seeded synthetic input that
+is already resident in HBM:
+  c5 (default)  16384 x 128-token teacher-forced scoring of the D384/H1024/4-block model: full softmax
+                probabilities [16384, 128, 8192] fp32 and per-sequence bits per token
+  c3            1024 x 128 tokens of the D128 model: logits + per-token log-probs
+  c4            4096 sessions: 32-token prefill + 64 greedy tokens (value counts generated tokens)
+  c2            the standalone INT8 GEMM 262144 x 384 x 512 (value counts rows = tokens)
+  c1            64 x 128 tokens of the tiny model: logits
+
+roofline: the kernel class with the largest share of the timed region, its algorithmic work per launch
+(int8 MACs x 2 for GEMMs, compulsory bytes for memory-bound kernels) over its average launch time, both
+measured live with HIP events on the model's stream. cpu_baseline: the CPU restatement of the reference
+engine (oracle/, AVX2 dot kernels) timed on this host on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "INT8 tokens/sec (batched forward + decode); % of int8-MFMA / HBM roofline"
+PEAK_MFMA_TOPS = 5000.0   # MI355X dense int8 MFMA, TOP/s
+PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, GB/s
+
+
+def per_token_macs(spec):
+    """int8-weight MACs per token, per GEMM class (reference layout, internal/ca/layout.go:96-162)."""
+    D, H, V = spec.D, spec.H, spec.V
+    bsteps = sum(b.steps for b in spec.blocks)
+    nattn = len(spec.blocks) if spec.heads > 0 else 0
+    return {
+        "gemm_glu": bsteps * 3 * D * 2 * H,
+        "gemm_highway": bsteps * H * 2 * D,
+        "gemm_latch": bsteps * D * D,
+        "gemm_qkv": nattn * D * 3 * D,
+        "gemm_out": nattn * D * D,
+        "gemm_logits": D * V,
+        "gemm_probs": D * V,
+    }
+
+
+def cpu_threads():
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def roofline_for(prof, work_per_step, steps):
+    """Dominant kernel class by time; work_per_step maps class -> (bound, algorithmic units per step)."""
+    total = {k: v[1] for k, v in prof.items()}
+    cands = [k for k in total if k in work_per_step]
+    if not cands:
+        return None, None
+    dom = max(cands, key=lambda k: total[k])
+    launches, ms = prof[dom]
+    bound, units = work_per_step[dom]
+    per_launch = units * steps / launches
+    avg_s = ms / launches / 1e3
+    if bound == "mfma":
+        achieved = per_launch / avg_s / 1e12
+        r = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_TOPS, "unit": "TFLOP/s",
+             "frac": round(achieved / PEAK_MFMA_TOPS, 4), "traffic": None}
+    else:
+        achieved = per_launch / avg_s / 1e9
+        r = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+             "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None}
+    r["kernel"] = dom
+    r["per_launch"] = per_launch
+    r["avg_launch_ms"] = round(ms / launches, 4)
+    return dom, r
+
+
+def timed(step, warmup, steps, torch, before=None):
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    if before:
+        before()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return ev0.elapsed_time(ev1) / steps, wall
+
+
+def cpu_baseline_forward(data, spec, T, seconds, seed):
+    from oracle import oracle as O
+    om = O.OracleModel(O.read_model(data))
+    thr = cpu_threads()
+    # a first batch sizes the sample so that it takes about `seconds`
+    probe = synth_ids(seed, "cpu-probe", (thr, min(T, 32)), spec.V)
+    t0 = time.perf_counter()
+    om.forward_all(probe, nthreads=thr)
+    rate = probe.size / max(time.perf_counter() - t0, 1e-6)
+    nseq = int(max(thr, min(4096, rate * seconds / T)))
+    ids = synth_ids(seed, "cpu-sample", (nseq, T), spec.V)
+    t0 = time.perf_counter()
+    om.forward_all(ids, nthreads=thr)
+    dt = time.perf_counter() - t0
+    return {"value": round(ids.size / dt, 1), "unit": "tokens/s", "cores": thr, "kind": "port",
+            "sample": f"{nseq} sequences x {T} tokens, teacher-forced (session route: every position's logits), "
+                      f"{dt:.1f} s; C++ restatement of the reference Go engine with AVX2 dot kernels"}
+
+
+def cpu_baseline_decode(data, spec, P, G, seconds, seed):
+    from oracle import oracle as O
+    om = O.OracleModel(O.read_model(data))
+    thr = cpu_threads()
+    probe = synth_ids(seed, "cpu-probe", (thr, P), spec.V)
+    t0 = time.perf_counter()
+    om.greedy(probe, 4, nthreads=thr)
+    rate = thr * (P + 4) / max(time.perf_counter() - t0, 1e-6)  # positions per second
+    nses = int(max(thr, min(4096, rate * seconds / (P + G))))
+    prompts = synth_ids(seed, "cpu-sample", (nses, P), spec.V)
+    t0 = time.perf_counter()
+    om.greedy(prompts, G, nthreads=thr)
+    dt = time.perf_counter() - t0
+    return {"value": round(nses * G / dt, 1), "unit": "generated tokens/s", "cores": thr, "kind": "port",
+            "sample": f"{nses} sessions x ({P}-token prefill + {G} greedy tokens), {dt:.1f} s; C++ restatement "
+                      f"of the reference Go engine with AVX2 dot kernels"}
+
+
+def cpu_baseline_gemm(A, W, s, seconds):
+    from oracle import oracle as O
+    thr = cpu_threads()
+    rows = max(thr, 256)
+    t0 = time.perf_counter()
+    O.gemm_i8_ref(A[:rows], W, s, nthreads=thr)
+    rate = rows / max(time.perf_counter() - t0, 1e-6)
+    n = int(min(len(A), max(rows, rate * seconds)))
+    t0 = time.perf_counter()
+    O.gemm_i8_ref(A[:n], W, s, nthreads=thr)
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 1), "unit": "rows/s", "cores": thr, "kind": "port",
+            "sample": f"{n} of {len(A)} rows, {dt:.1f} s; MatVecInt8 per row (DotInt8F32, AVX2) as the reference"}
+
+
+def synth_ids(seed, tag, shape, V):
+    from mignon_ai_amd import synth
+    return synth.token_ids(seed, tag, shape, V)
+
+
+def run(args):
+    import torch
+
+    from mignon_ai_amd import Model, gemm_i8_device, mgnn, quantize_f32, synth
+
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a GPU")
+    torch.cuda.set_device(0)
+    # Everything runs on one non-default stream: the engine's launches, its HIP-event kernel timing and
+    # the torch events bracketing the timed region.
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    name = args.config
+    out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic"}
+    cpu = None
+
+    if name == "c2":
+        c = synth.C2
+        M, K, N = c["M"], c["K"], c["N"]
+        A = (synth.u64_stream(args.seed, "A", M * K) % np.uint64(255)).astype(np.int64) - 127
+        W = (synth.u64_stream(args.seed, "W", N * K) % np.uint64(255)).astype(np.int64) - 127
+        A = A.astype(np.int8).reshape(M, K)
+        W = W.astype(np.int8).reshape(N, K)
+        s = (1e-3 + 9e-3 * synth.uniform(args.seed, "s", N)).astype(np.float32)
+        dA, dW, ds = (torch.from_numpy(x).cuda() for x in (A, W, s))
+        dC = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        stream = torch.cuda.current_stream().cuda_stream
+
+        def step():
+            gemm_i8_device(dA, dW, ds, dC, None, stream)
+
+        ms, wall = timed(step, args.warmup, args.steps, torch)
+        bytes_ = M * K + N * K + 4 * N + 4 * M * N
+        gbs = bytes_ / (ms / 1e3) / 1e9
+        out.update(value=round(M / (ms / 1e3), 1), unit="tokens/s", ms_per_step=round(ms, 4),
+                   config={"workload": "c2: INT8 GEMM A[262144x384] x W[512x384]^T, int32 accumulate, "
+                                       "per-channel fp32 scale, fp32 out", "M": M, "K": K, "N": N})
+        out["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                           "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "kernel": "gemm_i8",
+                           "per_launch": bytes_, "avg_launch_ms": round(ms, 4)}
+        if not args.no_cpu_baseline:
+            cpu = cpu_baseline_gemm(A, W, s, args.cpu_seconds)
+        out["wall_s"] = round(wall, 3)
+    else:
+        cfg = synth.CONFIGS[name]
+        spec = cfg["spec"]
+        data = mgnn.build_model_file(spec, args.seed, quantize_f32)
+        m = Model(data)
+        m.set_stream(torch.cuda.current_stream().cuda_stream)
+        macs = per_token_macs(spec)
+        if name in ("c1", "c3", "c5"):
+            B, T = cfg["B"], cfg["T"]
+            ids = torch.from_numpy(synth.token_ids(args.seed, name + ":ids", (B, T), spec.V)).cuda()
+            kw = {}
+            if name == "c5":
+                kw["probs"] = torch.empty((B, T, spec.V), dtype=torch.float32, device="cuda")
+                kw["bits"] = torch.empty(B, dtype=torch.float32, device="cuda")
+                outputs = "full softmax probabilities [B,T,V] fp32 + bits/token per sequence"
+            elif name == "c3":
+                kw["logits"] = torch.empty((B, T, spec.V), dtype=torch.float32, device="cuda")
+                kw["logprob"] = torch.empty((B, T), dtype=torch.float32, device="cuda")
+                outputs = "logits [B,T,V] fp32 + per-token log-probs"
+            else:
+                kw["logits"] = torch.empty((B, T, spec.V), dtype=torch.float32, device="cuda")
+                outputs = "logits [B,T,V] fp32"
+
+            def step():
+                m.forward_batch_device(ids, **kw)
+
+            tokens = B * T
+            work = {k: ("mfma", 2 * v * tokens) for k, v in macs.items() if v}
+            if "probs" not in kw:
+                work.pop("gemm_probs", None)
+            ms, wall = timed(step, args.warmup, args.steps, torch, before=lambda: m.profile(True))
+            prof = m.profile_read()
+            m.profile(False)
+            value = tokens / (ms / 1e3)
+            out.update(value=round(value, 1), unit="tokens/s", ms_per_step=round(ms, 4))
+            out["config"] = {"workload": f"{name}: {B} sequences x {T} tokens, D{spec.D} H{spec.H} "
+                                         f"{len(spec.blocks)} blocks heads {spec.heads} window {spec.window} "
+                                         f"V{spec.V}; {outputs}", "B": B, "T": T, "params": spec.n_params}
+            if not args.no_cpu_baseline:
+                cpu = cpu_baseline_forward(data, spec, T, args.cpu_seconds, args.seed)
+        else:  # c4
+            S, P, G = cfg["B"], cfg["P"], cfg["G"]
+            prompts = torch.from_numpy(synth.token_ids(args.seed, "c4:prompts", (S, P), spec.V)).cuda()
+            lens = torch.full((S,), P, dtype=torch.int32, device="cuda")
+            oid = torch.empty((S, G), dtype=torch.int32, device="cuda")
+            opb = torch.empty((S, G), dtype=torch.float64, device="cuda")
+            sess = m.sessions(S)
+
+            def step():
+                sess.decode_greedy_device(prompts, lens, G, oid, opb)
+
+            positions = S * (P + G - 1)
+            work = {k: ("mfma", 2 * v * positions) for k, v in macs.items() if v and k != "gemm_probs"}
+            # K/V ring reads of the decode steps: sum over appended positions of the attended span
+            span = sum(min(p + 1, spec.window) for p in range(P, P + G - 1))
+            work["attention_step"] = ("hbm", S * len(spec.blocks) * 2 * span * spec.D * 4)
+            ms, wall = timed(step, args.warmup, args.steps, torch, before=lambda: m.profile(True))
+            prof = m.profile_read()
+            m.profile(False)
+            value = S * G / (ms / 1e3)
+            out.update(value=round(value, 1), unit="generated tokens/s", ms_per_step=round(ms, 4))
+            out["config"] = {"workload": f"c4: {S} sessions, {P}-token prefill + {G} greedy tokens, D{spec.D} "
+                                         f"H{spec.H} {len(spec.blocks)} blocks heads {spec.heads} window "
+                                         f"{spec.window} V{spec.V}", "sessions": S, "prompt": P, "generated": G,
+                             "params": spec.n_params}
+            if not args.no_cpu_baseline:
+                cpu = cpu_baseline_decode(data, spec, P, G, args.cpu_seconds, args.seed)
+        dom, roof = roofline_for(prof, work, args.steps)
+        out["roofline"] = roof
+        total_macs = sum(v for k, v in macs.items() if k != "gemm_probs")
+        tok = (cfg["B"] * cfg["T"]) if name != "c4" else cfg["B"] * (cfg["P"] + cfg["G"] - 1)
+        path_tops = 2 * total_macs * tok / (ms / 1e3) / 1e12
+        out["path_roofline"] = {"bound": "mfma", "achieved": round(path_tops, 2), "peak": PEAK_MFMA_TOPS,
+                                "unit": "TFLOP/s", "frac": round(path_tops / PEAK_MFMA_TOPS, 4),
+                                "note": "whole step: algorithmic int8 MACs x 2 (one pass of every weight "
+                                        "GEMM; the probability head's recompute not counted)"}
+        out["kernels_ms_per_step"] = {k: round(v[1] / args.steps, 3) for k, v in sorted(prof.items(),
+                                                                                      key=lambda kv: -kv[1][1])}
+        out["wall_s"] = round(wall, 3)
+    out["cpu_baseline"] = cpu
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", default="c5", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the path shards by sequence with no "
+                                   "exchange step, so N>1 is not run (see the sharding note in DESIGN.md)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    out = run(args)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

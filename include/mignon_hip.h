@@ -67,6 +67,17 @@ int mg_model_info(const mg_model* m, mg_model_info_t* info);
 /* Replaces the handle's stream (NULL restores the library's own stream). */
 int mg_model_set_stream(mg_model* m, void* hip_stream);
 void* mg_model_stream(const mg_model* m);
+
+/* Kernel timing (no reference counterpart; measurement support). While on, every kernel launch of the
+ * handle is bracketed by HIP events on its stream; mg_model_profile_read waits for the stream and
+ * returns per-class launch counts and summed durations (at most max entries; returns the class count). */
+typedef struct {
+    char name[32];
+    long long launches;
+    double total_ms;
+} mg_kernel_time_t;
+int mg_model_profile(mg_model* m, int on);
+int mg_model_profile_read(mg_model* m, mg_kernel_time_t* out, int max);
 int mg_model_sync(mg_model* m);
 void mg_model_free(mg_model* m);
 

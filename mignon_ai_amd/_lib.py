@@ -34,6 +34,10 @@ class ModelInfo(ctypes.Structure):
                 ("norm_ring", _int), ("attn_cache", _int), ("num_params", _ll)]
 
 
+class KernelTime(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 32), ("launches", _ll), ("total_ms", ctypes.c_double)]
+
+
 # name -> (restype, argtypes); the exported set of include/mignon_hip.h
 SIGNATURES = {
     "mg_last_error": (ctypes.c_char_p, []),
@@ -43,6 +47,8 @@ SIGNATURES = {
     "mg_model_set_stream": (_int, [_vp, _vp]),
     "mg_model_stream": (_vp, [_vp]),
     "mg_model_sync": (_int, [_vp]),
+    "mg_model_profile": (_int, [_vp, _int]),
+    "mg_model_profile_read": (_int, [_vp, _vp, _int]),
     "mg_model_free": (None, [_vp]),
     "mg_model_call": (_int, [_vp, _vp, _int, _vp]),
     "mg_forward_batch": (_int, [_vp, _vp, _int, _int, _vp, _vp, _vp, _vp, _int]),

@@ -96,6 +96,54 @@ struct DevBlock {
     }
 };
 
+// Kernel classes timed by the optional profiler (HIP events around every launch on the launch stream).
+enum KClass : int {
+    K_ROW = 0, K_GEMM_LATCH, K_SCAN, K_LATCH_STEP, K_GEMM_GLU, K_GEMM_HIGHWAY, K_GEMM_QKV, K_ATTN, K_ATTN_STEP,
+    K_GEMM_OUT, K_GEMM_LOGITS, K_HEAD_COMBINE, K_GEMM_PROBS, K_BITS, K_EXPORT, K_GEMM_I8, K_NCLASS
+};
+const char* const kClassNames[K_NCLASS] = {
+    "row_norm_pack", "gemm_latch", "latch_scan", "latch_step", "gemm_glu", "gemm_highway", "gemm_qkv",
+    "attention", "attention_step", "gemm_out", "gemm_logits", "head_combine", "gemm_probs", "bits",
+    "state_export", "gemm_i8"};
+
+struct Profile {
+    bool on = false;
+    std::vector<hipEvent_t> pool;
+    size_t used = 0;
+    std::vector<std::pair<int, size_t>> recs;  // class, index of the start event (end = start + 1)
+    ~Profile() {
+        for (hipEvent_t e : pool) (void)hipEventDestroy(e);
+    }
+    hipEvent_t next() {
+        if (used == pool.size()) {
+            hipEvent_t e;
+            if (hipEventCreate(&e) != hipSuccess) throw Error(MG_ERR_DEVICE, "hipEventCreate failed");
+            pool.push_back(e);
+        }
+        return pool[used++];
+    }
+};
+
+// Records start/end events around the launches in its scope when the model's profiler is on.
+struct ProfScope {
+    Profile* p;
+    hipStream_t s;
+    int cls;
+    size_t start = 0;
+    ProfScope(Profile& pr, int c, hipStream_t st) : p(pr.on ? &pr : nullptr), s(st), cls(c) {
+        if (p) {
+            start = p->used;
+            (void)hipEventRecord(p->next(), s);
+        }
+    }
+    ~ProfScope() {
+        if (p) {
+            (void)hipEventRecord(p->next(), s);
+            p->recs.emplace_back(cls, start);
+        }
+    }
+};
+
 // Workspace for a batch of tokens in flight.
 struct Workspace {
     int cap_tokens = 0;
@@ -124,6 +172,7 @@ struct mg_model {
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     mg::Workspace ws;
+    mg::Profile prof;
     std::mutex mu;
 };
 
@@ -322,7 +371,23 @@ GemmArgs lx3_args(const int8_t* A, long long ld, const float* As, int as_ld, int
     return g;
 }
 
-void gemm(int nl, int epi, const GemmArgs& g, hipStream_t s) { HIPCHECK(launch_gemm(nl, epi, g, s)); }
+int gemm_class(int epi) {
+    switch (epi) {
+        case EPI_LATCH: return K_GEMM_LATCH;
+        case EPI_GLU: return K_GEMM_GLU;
+        case EPI_HIGHWAY: return K_GEMM_HIGHWAY;
+        case EPI_F32: return K_GEMM_QKV;
+        case EPI_RESID: return K_GEMM_OUT;
+        case EPI_LOGITS: return K_GEMM_LOGITS;
+        case EPI_PROBS: return K_GEMM_PROBS;
+        default: return K_GEMM_I8;
+    }
+}
+
+void gemm(mg_model* m, int nl, int epi, const GemmArgs& g, hipStream_t s) {
+    ProfScope ps(m->prof, gemm_class(epi), s);
+    HIPCHECK(launch_gemm(nl, epi, g, s));
+}
 
 // Row kernel helper: mode + optional norm, writes n (fp32) and the limb-expanded copy into ws.nl/ns.
 void row_call(mg_model* m, int M, int mode, const int32_t* ids, const float* src, int lds, const int32_t* row_map,
@@ -336,6 +401,7 @@ void row_call(mg_model* m, int M, int mode, const int32_t* ids, const float* src
     if (limbs) {
         r.limbs = w.nl.as<int8_t>(); r.l_row = 3LL * m->Dp; r.l_limb = m->Dp; r.lscale = w.ns.as<float>();
     }
+    ProfScope ps(m->prof, K_ROW, s);
     HIPCHECK(launch_row(r, s));
 }
 
@@ -391,7 +457,7 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
             // lambda = sigmoid_clamped(n.W_sel*s + base) (stream.go:195-205)
             GemmArgs g = lx3_args(w.nl.as<int8_t>(), Dp, w.ns.as<float>(), 1, Dp / 64, blk.wsel, m->NpD, Dp, M, D, blk.ssel);
             g.bias = m->latch_base; g.out = w.lam.as<float>(); g.ldo = Dp;
-            gemm(3, EPI_LATCH, g, s);
+            gemm(m, 3, EPI_LATCH, g, s);
             if (c.step) {
                 LatchStepArgs la;
                 la.S = M; la.D = D; la.Dp = Dp; la.dil = dil; la.ring = m->ring;
@@ -399,6 +465,7 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                 la.g = c.sess->g.as<float>() + (size_t)bs * c.B * Dp;
                 la.norm_ring = c.sess->norm_ring.as<float>() + (size_t)bs * c.B * m->ring * Dp;
                 la.xl = w.xl.as<int8_t>(); la.xs = w.xs.as<float>();
+                ProfScope ps(m->prof, K_LATCH_STEP, s);
                 HIPCHECK(launch_latch_step(la, s));
             } else {
                 ScanArgs sa;
@@ -407,27 +474,29 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                 if (c.sess) {
                     sa.lens = c.lens;
                     sa.g_out = c.sess->g.as<float>() + (size_t)bs * c.B * Dp;
+                    ProfScope ps(m->prof, K_EXPORT, s);
                     HIPCHECK(launch_export_ring(c.B, c.T, Dp, m->ring, c.lens, w.nf.as<float>(),
                                                 c.sess->norm_ring.as<float>() + (size_t)bs * c.B * m->ring * Dp, s));
                 }
+                ProfScope ps(m->prof, K_SCAN, s);
                 HIPCHECK(launch_scan(sa, s));
             }
             // h = GLU(x) (stream.go:214-220), limb-expanded with one scale per 64 hidden units
             g = lx3_args(w.xl.as<int8_t>(), 3LL * Dp, w.xs.as<float>(), 1, 3 * Dp / 64, blk.w1, 2 * Hp, 3 * Dp, M, 2 * Hp, blk.s1);
             g.bias = blk.b1; g.hl = w.hl.as<int8_t>(); g.hl_row = 3LL * Hp; g.hl_limb = Hp;
             g.hs = w.hs.as<float>(); g.hs_ld = Hp / 64;
-            gemm(3, EPI_GLU, g, s);
+            gemm(m, 3, EPI_GLU, g, s);
             // cur = highway(cur, W2 h) (stream.go:222-229)
             g = lx3_args(w.hl.as<int8_t>(), Hp, w.hs.as<float>(), Hp / 64, 1, blk.w2, 2 * Dp, Hp, M, D, blk.s2);
             g.bias = blk.b2; g.cur = w.cur.as<float>(); g.ldcur = Dp;
-            gemm(3, EPI_HIGHWAY, g, s);
+            gemm(m, 3, EPI_HIGHWAY, g, s);
         }
         if (blk.attn) {
             // attendPosition (internal/quant/attention.go:69-104)
             row_call(m, M, ROW_SRC, nullptr, nullptr, 0, nullptr, blk.anorm, nullptr, true, s);
             GemmArgs g = lx3_args(w.nl.as<int8_t>(), Dp, w.ns.as<float>(), 1, Dp / 64, blk.qkv, m->Np3, Dp, M, 3 * D, blk.sqkv);
             g.out = w.qkv.as<float>(); g.ldo = 3 * D;
-            gemm(3, EPI_F32, g, s);
+            gemm(m, 3, EPI_F32, g, s);
             if (c.step) {
                 AttnStepArgs aa;
                 aa.S = M; aa.D = D; aa.Dp = Dp; aa.heads = m->heads; aa.window = m->window; aa.cap = m->cap;
@@ -435,21 +504,25 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                 aa.kring = c.sess->kring.as<float>() + (size_t)ab * c.B * m->cap * D;
                 aa.vring = c.sess->vring.as<float>() + (size_t)ab * c.B * m->cap * D;
                 aa.att = w.att.as<float>();
+                ProfScope ps(m->prof, K_ATTN_STEP, s);
                 HIPCHECK(launch_attention_step(aa, s));
             } else {
-                if (c.sess)
+                if (c.sess) {
+                    ProfScope ps(m->prof, K_EXPORT, s);
                     HIPCHECK(launch_export_kv(c.B, c.T, D, m->cap, c.lens, w.qkv.as<float>(),
                                               c.sess->kring.as<float>() + (size_t)ab * c.B * m->cap * D,
                                               c.sess->vring.as<float>() + (size_t)ab * c.B * m->cap * D, s));
+                }
                 AttnArgs aa;
                 aa.B = c.B; aa.T = c.T; aa.D = D; aa.Dp = Dp; aa.heads = m->heads; aa.window = m->window; aa.cap = m->cap;
                 aa.qkv = w.qkv.as<float>(); aa.att = w.att.as<float>();
+                ProfScope ps(m->prof, K_ATTN, s);
                 HIPCHECK(launch_attention(aa, s));
             }
             row_call(m, M, ROW_SRC, nullptr, w.att.as<float>(), Dp, nullptr, nullptr, nullptr, true, s);
             g = lx3_args(w.nl.as<int8_t>(), Dp, w.ns.as<float>(), 1, Dp / 64, blk.wo, m->NpD, Dp, M, D, blk.so);
             g.cur = w.cur.as<float>(); g.ldcur = Dp;
-            gemm(3, EPI_RESID, g, s);
+            gemm(m, 3, EPI_RESID, g, s);
             ab++;
         }
     }
@@ -467,9 +540,10 @@ void run_head(mg_model* m, int M, const int32_t* row_map, const int32_t* tgt, fl
     g.bias = m->headb; g.out = logits_out; g.ldo = m->V;
     g.stats = w.stats.as<float>(); g.stats_ld = m->Vp / GEMM_BN;
     g.tgt = tgt; g.tlog = w.tlog.as<float>();
-    gemm(3, EPI_LOGITS, g, s);
+    gemm(m, 3, EPI_LOGITS, g, s);
     hc.M = M; hc.ntiles = m->Vp / GEMM_BN; hc.stats = w.stats.as<float>(); hc.V = m->V;
     hc.tgt = tgt; hc.tlog = w.tlog.as<float>();
+    ProfScope ps(m->prof, K_HEAD_COMBINE, s);
     HIPCHECK(launch_head_combine(hc, s));
 }
 
@@ -589,6 +663,47 @@ int mg_model_set_stream(mg_model* m, void* stream) {
 
 void* mg_model_stream(const mg_model* m) { return m ? (void*)m->stream : nullptr; }
 
+int mg_model_profile(mg_model* m, int on) {
+    return guarded([&] {
+        require(m != nullptr, "mg_model_profile: null model");
+        Guard g(m);
+        if (on) {
+            m->prof.used = 0;
+            m->prof.recs.clear();
+        }
+        m->prof.on = on != 0;
+        return MG_OK;
+    });
+}
+
+int mg_model_profile_read(mg_model* m, mg_kernel_time_t* out, int max) {
+    return guarded([&] {
+        require(m != nullptr && (out != nullptr || max == 0), "mg_model_profile_read: null argument");
+        Guard g(m);
+        HIPCHECK(hipStreamSynchronize(m->stream));
+        double ms[K_NCLASS] = {0};
+        long long n[K_NCLASS] = {0};
+        for (auto& r : m->prof.recs) {
+            float t = 0;
+            HIPCHECK(hipEventElapsedTime(&t, m->prof.pool[r.second], m->prof.pool[r.second + 1]));
+            ms[r.first] += t;
+            n[r.first]++;
+        }
+        int k = 0;
+        for (int c = 0; c < K_NCLASS; c++) {
+            if (!n[c]) continue;
+            if (k < max) {
+                std::memset(out[k].name, 0, sizeof(out[k].name));
+                std::strncpy(out[k].name, kClassNames[c], sizeof(out[k].name) - 1);
+                out[k].launches = n[c];
+                out[k].total_ms = ms[c];
+            }
+            k++;
+        }
+        return k;
+    });
+}
+
 int mg_model_sync(mg_model* m) {
     return guarded([&] {
         require(m != nullptr, "mg_model_sync: null model");
@@ -644,6 +759,7 @@ int mg_forward_batch(mg_model* m, const int32_t* ids, int B, int T, float* logit
             }
             if (bits) {
                 float* bd = dev ? bits + b0 : st.out<float>((size_t)Bc);
+                ProfScope ps(m->prof, K_BITS, s);
                 HIPCHECK(launch_bits(Bc, T, w.logprob.as<float>(), ids_d, V, bd, s));
                 if (!dev) HIPCHECK(hipMemcpyAsync(bits + b0, bd, (size_t)Bc * 4, hipMemcpyDeviceToHost, s));
             }
@@ -651,7 +767,7 @@ int mg_forward_batch(mg_model* m, const int32_t* ids, int B, int T, float* logit
                 float* pd = dev ? probs + row0 * V : st.out<float>((size_t)M * V);
                 GemmArgs g = lx3_args(w.nl.as<int8_t>(), m->Dp, w.ns.as<float>(), 1, m->Dp / 64, m->headw, m->Vp, m->Dp, M, V, m->head_scale);
                 g.bias = m->headb; g.out = pd; g.ldo = V; g.lse = w.lse.as<float>();
-                gemm(3, EPI_PROBS, g, s);
+                gemm(m, 3, EPI_PROBS, g, s);
                 if (!dev) HIPCHECK(hipMemcpyAsync(probs + row0 * V, pd, (size_t)M * V * 4, hipMemcpyDeviceToHost, s));
             }
             if (logits && !dev) HIPCHECK(hipMemcpyAsync(logits + row0 * V, lg, (size_t)M * V * 4, hipMemcpyDeviceToHost, s));

@@ -233,11 +233,17 @@ __device__ __forceinline__ float axpy_ref(int i, float alpha, float x, float y) 
 
 constexpr int ATT_QT = 64;  // queries per workgroup (one per lane)
 
+// LDS row stride of the staged keys/values: odd, so that lanes reading consecutive rows (consecutive
+// queries look at consecutive keys) hit different banks.
+template <int DH>
+constexpr int att_stride() { return DH + 1; }
+
 // One workgroup per (sequence, 64-query tile, head). Keys of the tile's whole window are staged in LDS,
 // each lane scores its query against them (DotF32 order), runs the reference softmax, then the values
 // replace the keys in LDS for the P.V accumulation.
 template <int DH>
 __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
+    constexpr int DS = att_stride<DH>();
     extern __shared__ float smem[];
     const int nqt = (a.T + ATT_QT - 1) / ATT_QT;
     const int b = blockIdx.x / nqt, qt = blockIdx.x % nqt;
@@ -248,14 +254,14 @@ __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
     const int t1 = min(t0 + ATT_QT, T);
     const int r0 = max(window_start(t0, a.window), max(t0 - cap + 1, 0));
     const int rows = t1 - r0;
-    float* kv = smem;                    // [rows][DH]
-    float* sc = smem + (ATT_QT + cap - 1) * DH;  // [cap][64]
+    float* kv = smem;                            // [rows][DS]
+    float* sc = smem + (ATT_QT + cap - 1) * DS;  // [cap][64]
     const long long base = (long long)b * T;
     const int ld = 3 * D;
 
     for (int e = lane; e < rows * DH; e += 64) {
         int r = e / DH, i = e % DH;
-        kv[e] = a.qkv[(base + r0 + r) * ld + D + h * DH + i];
+        kv[r * DS + i] = a.qkv[(base + r0 + r) * ld + D + h * DH + i];
     }
     __syncthreads();
 
@@ -272,7 +278,7 @@ __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
         const float scale = (float)(1.0 / sqrt((double)DH));
         float mx = -3.40282347e38f;
         for (int jj = 0; jj < span; jj++) {
-            const float* k = kv + (lo + jj - r0) * DH;
+            const float* k = kv + (lo + jj - r0) * DS;
             float s = dot_f32_ref<DH>(q, k) * scale;
             sc[jj * 64 + lane] = s;
             if (s > mx) mx = s;
@@ -289,7 +295,7 @@ __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
     __syncthreads();
     for (int e = lane; e < rows * DH; e += 64) {
         int r = e / DH, i = e % DH;
-        kv[e] = a.qkv[(base + r0 + r) * ld + 2 * D + h * DH + i];
+        kv[r * DS + i] = a.qkv[(base + r0 + r) * ld + 2 * D + h * DH + i];
     }
     __syncthreads();
     if (!active) return;
@@ -298,7 +304,7 @@ __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
     for (int i = 0; i < DH; i++) o[i] = 0.0f;
     for (int jj = 0; jj < span; jj++) {
         float p = sc[jj * 64 + lane] * inv;
-        const float* v = kv + (lo + jj - r0) * DH;
+        const float* v = kv + (lo + jj - r0) * DS;
 #pragma unroll
         for (int i = 0; i < DH; i++) o[i] = axpy_ref<DH>(i, p, v[i], o[i]);
     }
@@ -482,7 +488,7 @@ __global__ void fill_f32_kernel(float* p, long long n, float v) {
 template <int DH>
 hipError_t attn_t(const AttnArgs& a, hipStream_t s) {
     const int nqt = (a.T + ATT_QT - 1) / ATT_QT;
-    size_t lds = (size_t)((ATT_QT + a.cap - 1) * DH + a.cap * 64) * sizeof(float);
+    size_t lds = (size_t)((ATT_QT + a.cap - 1) * att_stride<DH>() + a.cap * 64) * sizeof(float);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     hipLaunchKernelGGL(attention_kernel<DH>, dim3(a.B * nqt, a.heads), dim3(64), lds, s, a);
     return hipGetLastError();

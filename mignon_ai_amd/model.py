@@ -75,6 +75,17 @@ class Model:
     def sync(self):
         check(lib().mg_model_sync(self._h))
 
+    def profile(self, on: bool):
+        """Start (clearing earlier records) or stop per-kernel HIP-event timing on the model's stream."""
+        check(lib().mg_model_profile(self._h, 1 if on else 0))
+
+    def profile_read(self) -> dict:
+        """{kernel class: (launches, total ms)} of the launches recorded while profiling was on."""
+        from ._lib import KernelTime
+        buf = (KernelTime * 32)()
+        n = check(lib().mg_model_profile_read(self._h, buf, 32))
+        return {buf[i].name.decode(): (buf[i].launches, buf[i].total_ms) for i in range(min(n, 32))}
+
     # quant.Model.Call / Forward (LogitsFn)
     def call(self, ids):
         ids = _i32(ids)

@@ -20,6 +20,8 @@
 #include <thread>
 #include <vector>
 
+#include <immintrin.h>
+
 namespace {
 
 // ---------------------------------------------------------------------------------------------
@@ -39,7 +41,7 @@ inline float hreduce8(const float v[8]) {
 // kernels.DotF32 on an AVX2 machine: dotProductASM_F32 (internal/kernels/vec_amd64.s:4-63).
 // Two 8-lane FMA accumulators over 16-element chunks, one more 8-chunk into acc0, the reduction
 // tree, then the scalar tail with an unfused multiply and add.
-float dot_f32(const float* x, const float* y, int n) {
+float dot_f32_scalar(const float* x, const float* y, int n) {
     float a0[8] = {0}, a1[8] = {0};
     int i = 0;
     for (; n - i >= 16; i += 16) {
@@ -65,7 +67,7 @@ float dot_f32(const float* x, const float* y, int n) {
 // kernels.DotInt8F32 on an AVX2 machine: dotInt8ASM_F32 (internal/kernels/vec_amd64.s:603-679).
 // Four 8-lane accumulators (Y0, Y1, Y4, Y5) over 32-element chunks, 8-chunks into Y0, then
 // (Y0+Y1)+(Y4+Y5), the reduction tree and the unfused scalar tail.
-float dot_i8_f32(const float* x, const int8_t* w, int n) {
+float dot_i8_f32_scalar(const float* x, const int8_t* w, int n) {
     float a0[8] = {0}, a1[8] = {0}, a4[8] = {0}, a5[8] = {0};
     int i = 0;
     for (; n - i >= 32; i += 32) {
@@ -91,6 +93,65 @@ float dot_i8_f32(const float* x, const int8_t* w, int n) {
         s = s + p;
     }
     return s;
+}
+
+// The same two kernels with AVX2/FMA intrinsics, issued as the reference's assembly issues them
+// (VPMOVSXBD/VCVTDQ2PS/VFMADD231PS per 8 lanes, VADDPS between accumulators). Each lane runs the same
+// FMA chain as the scalar restatement above, so the bits are identical; this path exists so that the
+// CPU baseline runs at the reference's vector width. Chosen at run time when the CPU has AVX2 and FMA.
+__attribute__((target("avx2,fma"))) float dot_f32_avx2(const float* x, const float* y, int n) {
+    __m256 a0 = _mm256_setzero_ps(), a1 = _mm256_setzero_ps();
+    int i = 0;
+    for (; n - i >= 16; i += 16) {
+        a0 = _mm256_fmadd_ps(_mm256_loadu_ps(x + i), _mm256_loadu_ps(y + i), a0);
+        a1 = _mm256_fmadd_ps(_mm256_loadu_ps(x + i + 8), _mm256_loadu_ps(y + i + 8), a1);
+    }
+    if (n - i >= 8) {
+        a0 = _mm256_fmadd_ps(_mm256_loadu_ps(x + i), _mm256_loadu_ps(y + i), a0);
+        i += 8;
+    }
+    float v[8];
+    _mm256_storeu_ps(v, _mm256_add_ps(a0, a1));
+    float s = hreduce8(v);
+    for (; i < n; i++) {
+        float p = x[i] * y[i];
+        s = s + p;
+    }
+    return s;
+}
+
+__attribute__((target("avx2,fma"))) inline __m256 widen8(const int8_t* w) {
+    return _mm256_cvtepi32_ps(_mm256_cvtepi8_epi32(_mm_loadl_epi64((const __m128i*)w)));
+}
+
+__attribute__((target("avx2,fma"))) float dot_i8_f32_avx2(const float* x, const int8_t* w, int n) {
+    __m256 a0 = _mm256_setzero_ps(), a1 = _mm256_setzero_ps(), a4 = _mm256_setzero_ps(), a5 = _mm256_setzero_ps();
+    int i = 0;
+    for (; n - i >= 32; i += 32) {
+        a0 = _mm256_fmadd_ps(widen8(w + i), _mm256_loadu_ps(x + i), a0);
+        a1 = _mm256_fmadd_ps(widen8(w + i + 8), _mm256_loadu_ps(x + i + 8), a1);
+        a4 = _mm256_fmadd_ps(widen8(w + i + 16), _mm256_loadu_ps(x + i + 16), a4);
+        a5 = _mm256_fmadd_ps(widen8(w + i + 24), _mm256_loadu_ps(x + i + 24), a5);
+    }
+    for (; n - i >= 8; i += 8) a0 = _mm256_fmadd_ps(widen8(w + i), _mm256_loadu_ps(x + i), a0);
+    float v[8];
+    _mm256_storeu_ps(v, _mm256_add_ps(_mm256_add_ps(a0, a1), _mm256_add_ps(a4, a5)));
+    float s = hreduce8(v);
+    for (; i < n; i++) {
+        float p = (float)w[i] * x[i];
+        s = s + p;
+    }
+    return s;
+}
+
+const bool g_avx2 = __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
+int g_force_scalar = 0;
+
+inline float dot_f32(const float* x, const float* y, int n) {
+    return (g_avx2 && !g_force_scalar) ? dot_f32_avx2(x, y, n) : dot_f32_scalar(x, y, n);
+}
+inline float dot_i8_f32(const float* x, const int8_t* w, int n) {
+    return (g_avx2 && !g_force_scalar) ? dot_i8_f32_avx2(x, w, n) : dot_i8_f32_scalar(x, w, n);
 }
 
 // kernels.MatVecInt8 (internal/kernels/int8.go:31-41): y[r] = Dot(x, W[r])*scale, then += bias[r]
@@ -618,6 +679,10 @@ int or_greedy(OrModel* m, const int* prompts, int B, int P, int max_tokens, int 
     return 0;
 }
 
+// 1 selects the scalar restatement of the dot kernels even on AVX2 machines (tests compare both).
+void or_force_scalar(int on) { g_force_scalar = on; }
+int or_has_avx2(void) { return g_avx2 ? 1 : 0; }
+
 // Single-kernel entry points for the kernel-level pins.
 float or_dot_f32(const float* x, const float* y, int n) { return dot_f32(x, y, n); }
 float or_dot_i8_f32(const float* x, const int8_t* w, int n) { return dot_i8_f32(x, w, n); }
@@ -681,6 +746,18 @@ int or_gemm_i8_exact(const int8_t* A, int M, int K, const int8_t* W, int N, cons
         }
     });
     return overflow.load() ? -1 : 0;
+}
+
+// Config-2 GEMM the way the reference computes it: kernels.MatVecInt8 per activation row, the int8
+// activations converted to float32 first (DotInt8F32 then one multiply by the channel scale). Used as
+// the timed CPU baseline of the standalone GEMM.
+int or_gemm_i8_ref(const int8_t* A, int M, int K, const int8_t* W, int N, const float* s, float* C, int nthreads) {
+    parallel_for(M, nthreads, [&](int, int m) {
+        std::vector<float> x(K);
+        for (int k = 0; k < K; k++) x[k] = (float)A[(size_t)m * K + k];
+        for (int n = 0; n < N; n++) C[(size_t)m * N + n] = dot_i8_f32(x.data(), W + (size_t)n * K, K) * s[n];
+    });
+    return 0;
 }
 
 }  // extern "C"

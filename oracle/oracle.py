@@ -65,6 +65,8 @@ def lib():
             "or_forward_all": (ctypes.c_int, [v, _i32p, ctypes.c_int, ctypes.c_int, _f32p, ctypes.c_int]),
             "or_greedy": (ctypes.c_int, [v, _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _i32p,
                                          _f64p, ctypes.c_int]),
+            "or_force_scalar": (None, [ctypes.c_int]),
+            "or_has_avx2": (ctypes.c_int, []),
             "or_dot_f32": (ctypes.c_float, [_f32p, _f32p, ctypes.c_int]),
             "or_dot_i8_f32": (ctypes.c_float, [_f32p, _i8p, ctypes.c_int]),
             "or_fast_exp": (ctypes.c_float, [ctypes.c_float]),
@@ -76,6 +78,8 @@ def lib():
                                     _f32p]),
             "or_latch_base": (None, [ctypes.c_int, _f32p]),
             "or_quantize": (None, [_f32p, ctypes.c_longlong, _i8p, _f32p]),
+            "or_gemm_i8_ref": (ctypes.c_int, [_i8p, ctypes.c_int, ctypes.c_int, _i8p, ctypes.c_int, _f32p, _f32p,
+                                              ctypes.c_int]),
             "or_gemm_i8_exact": (ctypes.c_int, [_i8p, ctypes.c_int, ctypes.c_int, _i8p, ctypes.c_int, _f32p, _f32p,
                                                 _i32p, ctypes.c_int]),
         }
@@ -98,6 +102,15 @@ def _c(a, dtype):
 # ------------------------------------------------------------------------------------------------
 # kernel-level entry points
 # ------------------------------------------------------------------------------------------------
+
+def force_scalar(on: bool):
+    """Use the scalar restatement of the dot kernels instead of the AVX2 path (identical bits)."""
+    lib().or_force_scalar(1 if on else 0)
+
+
+def has_avx2() -> bool:
+    return bool(lib().or_has_avx2())
+
 
 def dot_f32(x, y) -> np.float32:
     x, y = _c(x, np.float32), _c(y, np.float32)
@@ -173,6 +186,16 @@ def gemm_i8_exact(A, W, scale, want_acc=True, nthreads=8):
     if rc != 0:
         raise OverflowError("int32 accumulator overflow")
     return C, acc
+
+
+def gemm_i8_ref(A, W, scale, nthreads=8):
+    """Reference method for config 2: MatVecInt8 per row on float32-converted int8 activations."""
+    A, W, s = _c(A, np.int8), _c(W, np.int8), _c(scale, np.float32)
+    M, K = A.shape
+    N = W.shape[0]
+    C = np.empty((M, N), np.float32)
+    lib().or_gemm_i8_ref(_p(A, _i8p), M, K, _p(W, _i8p), N, _p(s, _f32p), _p(C, _f32p), nthreads)
+    return C
 
 
 # ------------------------------------------------------------------------------------------------

@@ -189,3 +189,21 @@ def test_latch_base_closed_form():
         b = O.latch_base(D).astype(np.float64)
         T = np.full(D, 1.5) if D == 1 else 1.5 * (64 / 1.5) ** (np.arange(D) / (D - 1))
         assert np.allclose(1 / (1 + np.exp(-b)), 2.0 ** (-1 / T), rtol=1e-6)
+
+
+def test_avx2_dot_paths_match_scalar_restatement():
+    """The oracle's AVX2 dot kernels (used for speed) give the scalar restatement's exact bits."""
+    if not O.has_avx2():
+        pytest.skip("host has no AVX2/FMA")
+    rng = np.random.default_rng(12)
+    try:
+        for n in list(range(0, 70)) + [96, 127, 128, 384, 1000, 1152]:
+            x = (rng.standard_normal(n) * rng.choice([1e-3, 1, 1e3])).astype(np.float32)
+            y = rng.standard_normal(n).astype(np.float32)
+            w = rng.integers(-128, 128, n).astype(np.int8)
+            O.force_scalar(False)
+            a, b = O.dot_f32(x, y), O.dot_i8_f32(x, w)
+            O.force_scalar(True)
+            assert bits(a) == bits(O.dot_f32(x, y)) and bits(b) == bits(O.dot_i8_f32(x, w)), n
+    finally:
+        O.force_scalar(False)
