@@ -60,6 +60,16 @@ __device__ __forceinline__ float sigmoid_clamped(float x) {
     return 1.0f / (1.0f + (float)exp((double)(-x)));
 }
 
+// sigmoidClamped evaluated with the hardware exponential and reciprocal (v_exp_f32, v_rcp_f32): used in
+// GEMM epilogues, where the reference's float64 exp and a correctly rounded division per output would
+// cost as much VALU time as the matrix work. For |x| <= 15 the relative error is below 2e-6 (the
+// argument rounding of x*log2(e) dominates), far inside the engine's 1e-4 output tolerance.
+__device__ __forceinline__ float sigmoid_clamped_f32(float x) {
+    if (x > 15.0f) return 1.0f;
+    if (x < -15.0f) return 0.0f;
+    return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
+
 // One element of the reference's vectorised e^x (vecExpASM_F32, internal/kernels/vec_amd64.s:281-430):
 // clamp to [-88, 88], k = nearest-even(x*log2e), two-constant ln2 reduction with FMA, degree-5
 // polynomial as an FMA chain, 2^k from exponent bits. Bit-identical to the reference on IEEE FMA.

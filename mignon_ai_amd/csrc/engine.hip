@@ -147,7 +147,7 @@ struct ProfScope {
 // Workspace for a batch of tokens in flight.
 struct Workspace {
     int cap_tokens = 0;
-    DevBuf cur, bin, nf, lam, nl, ns, xl, xs, hl, hs, qkv, att, stats, lse, tlog, logprob, argmax, prob, ids, tgt,
+    DevBuf cur, bin, nf, lam, nl, ns, xl, xs, h, hl, hs, qkv, att, stats, lse, tlog, logprob, argmax, prob, ids, tgt,
         rowmap, lens, tmp;
 };
 
@@ -194,6 +194,14 @@ T* upload(mg_model* m, const std::vector<T>& h) {
     return b.as<T>();
 }
 
+// Row-major [Np][Kp] int8 weights -> the GEMM's fragment layout (gemm.hpp).
+std::vector<int8_t> frag_pack(const std::vector<int8_t>& w, int Np, int Kp) {
+    std::vector<int8_t> out((size_t)Np * Kp);
+    for (int n = 0; n < Np; n++)
+        for (int k = 0; k < Kp; k++) out[frag_off_w(n, k, Np)] = w[(size_t)n * Kp + k];
+    return out;
+}
+
 // quant.Model.normRing (internal/quant/stream.go:37-47)
 int norm_ring_of(const std::vector<DevBlock>& blocks) {
     int longest = 0;
@@ -228,9 +236,9 @@ void build_device_model(mg_model* m, const HostModel& hm, int max_context) {
     m->V = V; m->D = D; m->H = H;
     m->Dp = round_up(D, 64);
     m->Hp = round_up(H, 64);
-    m->NpD = round_up(m->Dp, GEMM_BN);
-    m->Np3 = round_up(3 * D, GEMM_BN);
-    m->Vp = round_up(V, GEMM_BN);
+    m->NpD = round_up(m->Dp, LX_BN);
+    m->Np3 = round_up(3 * D, LX_BN);
+    m->Vp = round_up(V, LX_BN);
     m->tied = hm.tied;
     m->heads = hm.attn_heads;
     m->window = hm.attn_window;
@@ -270,7 +278,7 @@ void build_device_model(mg_model* m, const HostModel& hm, int max_context) {
                 std::memcpy(&w1[(size_t)r * 3 * Dp + seg * Dp], &hb.w1[(size_t)src * 3 * D + seg * D], D);
             b1[r] = hb.b1[src];
         }
-        db.w1 = upload(m, w1); db.b1 = upload(m, b1); db.s1 = hb.s1;
+        db.w1 = upload(m, frag_pack(w1, 2 * Hp, 3 * Dp)); db.b1 = upload(m, b1); db.s1 = hb.s1;
         // W2: same pairing (16 delta rows + 16 highway-gate rows), hidden columns padded to Hp.
         std::vector<int8_t> w2((size_t)2 * Dp * Hp, 0);
         std::vector<float> b2((size_t)2 * Dp, 0.0f);
@@ -281,10 +289,10 @@ void build_device_model(mg_model* m, const HostModel& hm, int max_context) {
             std::memcpy(&w2[(size_t)r * Hp], &hb.w2[(size_t)src * H], H);
             b2[r] = hb.b2[src];
         }
-        db.w2 = upload(m, w2); db.b2 = upload(m, b2); db.s2 = hb.s2;
+        db.w2 = upload(m, frag_pack(w2, 2 * Dp, Hp)); db.b2 = upload(m, b2); db.s2 = hb.s2;
         std::vector<int8_t> ws((size_t)m->NpD * Dp, 0);
         for (int r = 0; r < D; r++) std::memcpy(&ws[(size_t)r * Dp], &hb.wsel[(size_t)r * D], D);
-        db.wsel = upload(m, ws); db.ssel = hb.ssel;
+        db.wsel = upload(m, frag_pack(ws, m->NpD, Dp)); db.ssel = hb.ssel;
         if ((int)hb.gamma.size() == D) {
             std::vector<float> g(hb.gamma);
             g.resize(Dp, 0.0f);
@@ -298,17 +306,17 @@ void build_device_model(mg_model* m, const HostModel& hm, int max_context) {
             db.anorm = upload(m, an);
             std::vector<int8_t> q((size_t)m->Np3 * Dp, 0);
             for (int r = 0; r < 3 * D; r++) std::memcpy(&q[(size_t)r * Dp], &hb.qkv[(size_t)r * D], D);
-            db.qkv = upload(m, q); db.sqkv = hb.sqkv;
+            db.qkv = upload(m, frag_pack(q, m->Np3, Dp)); db.sqkv = hb.sqkv;
             std::vector<int8_t> o((size_t)m->NpD * Dp, 0);
             for (int r = 0; r < D; r++) std::memcpy(&o[(size_t)r * Dp], &hb.wo[(size_t)r * D], D);
-            db.wo = upload(m, o); db.so = hb.so;
+            db.wo = upload(m, frag_pack(o, m->NpD, Dp)); db.so = hb.so;
         }
     }
     m->ring = norm_ring_of(m->blocks);
     const std::vector<int8_t>& hw = hm.tied ? hm.embed : hm.head_w;
     std::vector<int8_t> head((size_t)m->Vp * Dp, 0);
     for (int r = 0; r < V; r++) std::memcpy(&head[(size_t)r * Dp], &hw[(size_t)r * D], D);
-    m->headw = upload(m, head);
+    m->headw = upload(m, frag_pack(head, m->Vp, Dp));
     m->head_scale = hm.tied ? hm.embed_scale : hm.head_scale;
     std::vector<float> hb(m->Vp, 0.0f);
     for (size_t v = 0; v < hm.head_b.size() && v < (size_t)V; v++) hb[v] = hm.head_b[v];
@@ -334,22 +342,24 @@ void ensure_ws(mg_model* m, int tokens) {
     Workspace& w = m->ws;
     if (tokens <= w.cap_tokens) return;
     size_t M = (size_t)tokens;
+    const size_t Mp = (size_t)round_up(tokens, LX_ROWS);  // limb operands are read in whole row tiles
     const size_t Dp = m->Dp, Hp = m->Hp, D = m->D;
     w.cur.ensure(M * Dp * 4);
     w.bin.ensure(M * Dp * 4);
     w.nf.ensure(M * Dp * 4);
     w.lam.ensure(M * Dp * 4);
-    w.nl.ensure(M * 3 * Dp);
-    w.ns.ensure(M * 4);
-    w.xl.ensure(M * 9 * Dp);
-    w.xs.ensure(M * 4);
-    w.hl.ensure(M * 3 * Hp);
-    w.hs.ensure(M * (Hp / 64) * 4);
+    w.nl.ensure(Mp * 3 * Dp);
+    w.ns.ensure(Mp * 4);
+    w.xl.ensure(Mp * 9 * Dp);
+    w.xs.ensure(Mp * 4);
+    w.h.ensure(M * Hp * 4);
+    w.hl.ensure(Mp * 3 * Hp);
+    w.hs.ensure(Mp * 4);
     if (m->nattn) {
         w.qkv.ensure(M * 3 * D * 4);
         w.att.ensure(M * Dp * 4);
     }
-    w.stats.ensure(M * (m->Vp / GEMM_BN) * 12);
+    w.stats.ensure(M * (m->Vp / LX_BN) * 12);
     w.lse.ensure(M * 4);
     w.tlog.ensure(M * 4);
     w.logprob.ensure(M * 4);
@@ -362,12 +372,10 @@ void ensure_ws(mg_model* m, int tokens) {
     w.cap_tokens = tokens;
 }
 
-GemmArgs lx3_args(const int8_t* A, long long ld, const float* As, int as_ld, int kc_steps, const int8_t* W, int Np,
-                  int Kp, int M, int nvalid, float wscale) {
+GemmArgs lx_args(const int8_t* A, const float* As, const int8_t* W, int Np, int Kp, int M, int nvalid, float wscale) {
     GemmArgs g;
-    g.A = A; g.a_row = 3 * ld; g.a_limb = ld;
-    g.As = As; g.as_ld = as_ld; g.kc_steps = kc_steps;
-    g.W = W; g.ldw = Kp; g.Np = Np; g.Kp = Kp; g.M = M; g.nvalid = nvalid; g.wscale = wscale;
+    g.A = A; g.As = As;
+    g.W = W; g.Np = Np; g.Kp = Kp; g.M = M; g.nvalid = nvalid; g.wscale = wscale;
     return g;
 }
 
@@ -384,9 +392,9 @@ int gemm_class(int epi) {
     }
 }
 
-void gemm(mg_model* m, int nl, int epi, const GemmArgs& g, hipStream_t s) {
+void gemm(mg_model* m, int epi, const GemmArgs& g, hipStream_t s) {
     ProfScope ps(m->prof, gemm_class(epi), s);
-    HIPCHECK(launch_gemm(nl, epi, g, s));
+    HIPCHECK(launch_gemm_lx(epi, g, s));
 }
 
 // Row kernel helper: mode + optional norm, writes n (fp32) and the limb-expanded copy into ws.nl/ns.
@@ -399,7 +407,7 @@ void row_call(mg_model* m, int M, int mode, const int32_t* ids, const float* src
     r.cur = w.cur.as<float>(); r.block_in = w.bin.as<float>();
     r.src = src; r.lds = lds; r.row_map = row_map; r.gamma = gamma; r.nout = nout;
     if (limbs) {
-        r.limbs = w.nl.as<int8_t>(); r.l_row = 3LL * m->Dp; r.l_limb = m->Dp; r.lscale = w.ns.as<float>();
+        r.limbs = w.nl.as<int8_t>(); r.lscale = w.ns.as<float>();
     }
     ProfScope ps(m->prof, K_ROW, s);
     HIPCHECK(launch_row(r, s));
@@ -455,9 +463,9 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
             // n = RMSNorm(cur; gamma) (stream.go:166-171), fused with the embedding / residual at step 0
             row_call(m, M, st == 0 ? mode : ROW_SRC, c.ids, nullptr, 0, nullptr, blk.gamma, w.nf.as<float>(), true, s);
             // lambda = sigmoid_clamped(n.W_sel*s + base) (stream.go:195-205)
-            GemmArgs g = lx3_args(w.nl.as<int8_t>(), Dp, w.ns.as<float>(), 1, Dp / 64, blk.wsel, m->NpD, Dp, M, D, blk.ssel);
+            GemmArgs g = lx_args(w.nl.as<int8_t>(), w.ns.as<float>(), blk.wsel, m->NpD, Dp, M, D, blk.ssel);
             g.bias = m->latch_base; g.out = w.lam.as<float>(); g.ldo = Dp;
-            gemm(m, 3, EPI_LATCH, g, s);
+            gemm(m, EPI_LATCH, g, s);
             if (c.step) {
                 LatchStepArgs la;
                 la.S = M; la.D = D; la.Dp = Dp; la.dil = dil; la.ring = m->ring;
@@ -481,22 +489,28 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                 ProfScope ps(m->prof, K_SCAN, s);
                 HIPCHECK(launch_scan(sa, s));
             }
-            // h = GLU(x) (stream.go:214-220), limb-expanded with one scale per 64 hidden units
-            g = lx3_args(w.xl.as<int8_t>(), 3LL * Dp, w.xs.as<float>(), 1, 3 * Dp / 64, blk.w1, 2 * Hp, 3 * Dp, M, 2 * Hp, blk.s1);
-            g.bias = blk.b1; g.hl = w.hl.as<int8_t>(); g.hl_row = 3LL * Hp; g.hl_limb = Hp;
-            g.hs = w.hs.as<float>(); g.hs_ld = Hp / 64;
-            gemm(m, 3, EPI_GLU, g, s);
+            // h = GLU(x) (stream.go:214-220) in fp32, then limb-expanded with one scale per row
+            g = lx_args(w.xl.as<int8_t>(), w.xs.as<float>(), blk.w1, 2 * Hp, 3 * Dp, M, m->H, blk.s1);
+            g.bias = blk.b1; g.out = w.h.as<float>(); g.ldo = Hp;
+            gemm(m, EPI_GLU, g, s);
+            {
+                RowArgs r;
+                r.M = M; r.D = m->H; r.Dp = Hp; r.mode = ROW_SRC; r.src = w.h.as<float>(); r.lds = Hp;
+                r.limbs = w.hl.as<int8_t>(); r.lscale = w.hs.as<float>();
+                ProfScope ps(m->prof, K_ROW, s);
+                HIPCHECK(launch_row(r, s));
+            }
             // cur = highway(cur, W2 h) (stream.go:222-229)
-            g = lx3_args(w.hl.as<int8_t>(), Hp, w.hs.as<float>(), Hp / 64, 1, blk.w2, 2 * Dp, Hp, M, D, blk.s2);
+            g = lx_args(w.hl.as<int8_t>(), w.hs.as<float>(), blk.w2, 2 * Dp, Hp, M, D, blk.s2);
             g.bias = blk.b2; g.cur = w.cur.as<float>(); g.ldcur = Dp;
-            gemm(m, 3, EPI_HIGHWAY, g, s);
+            gemm(m, EPI_HIGHWAY, g, s);
         }
         if (blk.attn) {
             // attendPosition (internal/quant/attention.go:69-104)
             row_call(m, M, ROW_SRC, nullptr, nullptr, 0, nullptr, blk.anorm, nullptr, true, s);
-            GemmArgs g = lx3_args(w.nl.as<int8_t>(), Dp, w.ns.as<float>(), 1, Dp / 64, blk.qkv, m->Np3, Dp, M, 3 * D, blk.sqkv);
+            GemmArgs g = lx_args(w.nl.as<int8_t>(), w.ns.as<float>(), blk.qkv, m->Np3, Dp, M, 3 * D, blk.sqkv);
             g.out = w.qkv.as<float>(); g.ldo = 3 * D;
-            gemm(m, 3, EPI_F32, g, s);
+            gemm(m, EPI_F32, g, s);
             if (c.step) {
                 AttnStepArgs aa;
                 aa.S = M; aa.D = D; aa.Dp = Dp; aa.heads = m->heads; aa.window = m->window; aa.cap = m->cap;
@@ -520,9 +534,9 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                 HIPCHECK(launch_attention(aa, s));
             }
             row_call(m, M, ROW_SRC, nullptr, w.att.as<float>(), Dp, nullptr, nullptr, nullptr, true, s);
-            g = lx3_args(w.nl.as<int8_t>(), Dp, w.ns.as<float>(), 1, Dp / 64, blk.wo, m->NpD, Dp, M, D, blk.so);
+            g = lx_args(w.nl.as<int8_t>(), w.ns.as<float>(), blk.wo, m->NpD, Dp, M, D, blk.so);
             g.cur = w.cur.as<float>(); g.ldcur = Dp;
-            gemm(m, 3, EPI_RESID, g, s);
+            gemm(m, EPI_RESID, g, s);
             ab++;
         }
     }
@@ -536,12 +550,12 @@ void run_head(mg_model* m, int M, const int32_t* row_map, const int32_t* tgt, fl
     Workspace& w = m->ws;
     // headLogits (internal/quant/stream.go:232-248)
     row_call(m, M, ROW_SRC, nullptr, nullptr, 0, row_map, m->final_norm, nullptr, true, s);
-    GemmArgs g = lx3_args(w.nl.as<int8_t>(), m->Dp, w.ns.as<float>(), 1, m->Dp / 64, m->headw, m->Vp, m->Dp, M, m->V, m->head_scale);
+    GemmArgs g = lx_args(w.nl.as<int8_t>(), w.ns.as<float>(), m->headw, m->Vp, m->Dp, M, m->V, m->head_scale);
     g.bias = m->headb; g.out = logits_out; g.ldo = m->V;
-    g.stats = w.stats.as<float>(); g.stats_ld = m->Vp / GEMM_BN;
+    g.stats = w.stats.as<float>(); g.stats_ld = m->Vp / LX_BN;
     g.tgt = tgt; g.tlog = w.tlog.as<float>();
-    gemm(m, 3, EPI_LOGITS, g, s);
-    hc.M = M; hc.ntiles = m->Vp / GEMM_BN; hc.stats = w.stats.as<float>(); hc.V = m->V;
+    gemm(m, EPI_LOGITS, g, s);
+    hc.M = M; hc.ntiles = m->Vp / LX_BN; hc.stats = w.stats.as<float>(); hc.V = m->V;
     hc.tgt = tgt; hc.tlog = w.tlog.as<float>();
     ProfScope ps(m->prof, K_HEAD_COMBINE, s);
     HIPCHECK(launch_head_combine(hc, s));
@@ -765,9 +779,9 @@ int mg_forward_batch(mg_model* m, const int32_t* ids, int B, int T, float* logit
             }
             if (probs) {
                 float* pd = dev ? probs + row0 * V : st.out<float>((size_t)M * V);
-                GemmArgs g = lx3_args(w.nl.as<int8_t>(), m->Dp, w.ns.as<float>(), 1, m->Dp / 64, m->headw, m->Vp, m->Dp, M, V, m->head_scale);
+                GemmArgs g = lx_args(w.nl.as<int8_t>(), w.ns.as<float>(), m->headw, m->Vp, m->Dp, M, V, m->head_scale);
                 g.bias = m->headb; g.out = pd; g.ldo = V; g.lse = w.lse.as<float>();
-                gemm(m, 3, EPI_PROBS, g, s);
+                gemm(m, EPI_PROBS, g, s);
                 if (!dev) HIPCHECK(hipMemcpyAsync(probs + row0 * V, pd, (size_t)M * V * 4, hipMemcpyDeviceToHost, s));
             }
             if (logits && !dev) HIPCHECK(hipMemcpyAsync(logits + row0 * V, lg, (size_t)M * V * 4, hipMemcpyDeviceToHost, s));
@@ -1010,10 +1024,10 @@ int mg_gemm_i8(const int8_t* A, int M, int K, const int8_t* W, int N, const floa
         int32_t* i_d = acc ? (dev ? acc : sg.out<int32_t>((size_t)M * N)) : nullptr;
         if (!c_d) c_d = sg.out<float>((size_t)M * N);
         GemmArgs g;
-        g.A = a_d; g.a_row = Kp; g.a_limb = 0;
+        g.A = a_d; g.a_row = Kp;
         g.W = w_d; g.ldw = Kp; g.Np = Np; g.Kp = Kp; g.M = M; g.nvalid = N;
         g.wscale_n = s_d; g.out = c_d; g.ldo = N; g.out_i32 = i_d;
-        HIPCHECK(launch_gemm(1, EPI_C2, g, st));
+        HIPCHECK(launch_gemm_c2(g, st));
         if (dev && !sg.bufs.empty()) HIPCHECK(hipStreamSynchronize(st));  // padded copies die on return
         if (!dev) {
             if (C) HIPCHECK(hipMemcpyAsync(C, c_d, (size_t)M * N * 4, hipMemcpyDeviceToHost, st));

@@ -1,5 +1,5 @@
-// Int8 MFMA GEMM of the engine: C[m][n] = sum_k A[m][k] * W[n][k], A token-major, W in the reference
-// layout (one row per output channel, K contiguous: kernels.MatVecInt8, internal/kernels/int8.go:31-41).
+// Int8 MFMA GEMMs of the engine: C[m][n] = sum_k A[m][k] * W[n][k], A token-major, W one row per output
+// channel with K contiguous (kernels.MatVecInt8's layout, internal/kernels/int8.go:31-41).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -11,45 +11,55 @@ enum Epi : int {
     EPI_C2 = 0,       // standalone int8 GEMM: C = float(acc)*scale[n], optional int32 acc
     EPI_F32 = 1,      // y = acc*s                                  (attention QKV)
     EPI_LATCH = 2,    // lambda = sigmoid_clamped(acc*s + base[n])  (latch selector)
-    EPI_GLU = 3,      // h = (acc_v*s + b_v) * sigmoid_clamped(acc_g*s + b_g) -> limb-expanded h
+    EPI_GLU = 3,      // h = (acc_v*s + b_v) * sigmoid_clamped(acc_g*s + b_g), fp32
     EPI_HIGHWAY = 4,  // cur = (1-g)*cur + g*(acc_v*s + b_v), g = sigmoid_clamped(acc_g*s + b_g)
     EPI_RESID = 5,    // cur += acc*s                               (attention output projection)
     EPI_LOGITS = 6,   // l = acc*s + b: optional store, per-tile (max, sum exp, first argmax), target logit
     EPI_PROBS = 7,    // p = exp(acc*s + b - lse[m])
 };
 
-// Tile shape: 128 output channels x 64 tokens per workgroup, K in steps of 64.
+// ------------------------------------------------------------------------------------------------
+// Fragment layout. Operands of v_mfma_i32_16x16x64_i8 are 16 rows x 64 bytes, lane L holding row
+// (L & 15) and bytes [16*(L >> 4), +16). Both GEMM operands are stored as such 1 KiB fragments so that
+// every fragment is one coalesced 16-byte-per-lane load:
+//   weights      [K/64][Np/16][1 KiB]          (all channel tiles of one K step are contiguous)
+//   activations  [Mp/16][K/64][3 limbs][1 KiB]  (Mp = M rounded up to LX_ROWS)
+// ------------------------------------------------------------------------------------------------
+__host__ __device__ inline long long frag_off_a(int m, int k, int limb, int kc) {
+    return ((((long long)(m >> 4) * kc + (k >> 6)) * 3 + limb) << 10) + (((m & 15) + 16 * ((k >> 4) & 3)) << 4) + (k & 15);
+}
+__host__ __device__ inline long long frag_off_w(int n, int k, int np) {
+    return ((((long long)(k >> 6) * (np >> 4)) + (n >> 4)) << 10) + (((n & 15) + 16 * ((k >> 4) & 3)) << 4) + (k & 15);
+}
+
+// Tile of the limb-expanded GEMM: 128 channels x 64 tokens per workgroup (4 waves x 16 tokens).
+constexpr int LX_BN = 128;
+constexpr int LX_BM = 64;
+// Activation buffers in the fragment layout are allocated in whole 128-row blocks.
+constexpr int LX_ROWS = 128;
+// Tile of the plain int8 GEMM (config 2): 128 channels x 64 tokens.
 constexpr int GEMM_BN = 128;
 constexpr int GEMM_BM = 64;
 constexpr int GEMM_BK = 64;
 
 struct GemmArgs {
-    // A (tokens): row m, limb l at A + m*a_row + l*a_limb; int8, Kp bytes valid per limb row.
+    // Limb-expanded A (fragment layout) with one scale per token row; or plain row-major int8 A (c2).
     const int8_t* A = nullptr;
-    long long a_row = 0;
-    long long a_limb = 0;
-    // Limb scales: As[m*as_ld + c] for K chunk c of kc_steps*64 columns (limb-expanded A only).
-    const float* As = nullptr;
-    int as_ld = 1;
-    int kc_steps = 1;
-    // W (channels): row n at W + n*ldw, Np rows (multiple of 128), Kp columns (multiple of 64).
+    long long a_row = 0;              // c2: row stride
+    const float* As = nullptr;        // per-row limb scale
+    // W: fragment layout (limb-expanded path) or row-major [Np][ldw] (c2).
     const int8_t* W = nullptr;
     int ldw = 0;
     int M = 0, Np = 0, Kp = 0;
-    int nvalid = 0;  // output channels that exist (the rest are padding)
+    int nvalid = 0;                   // output channels that exist (the rest are padding)
     float wscale = 1.0f;
     const float* wscale_n = nullptr;  // per-channel scale (EPI_C2)
-    const float* bias = nullptr;      // per W row (after any reordering)
+    const float* bias = nullptr;      // per W row (after any reordering), Np entries
     float* out = nullptr;             // fp32 output, row stride ldo
     long long ldo = 0;
     int32_t* out_i32 = nullptr;       // EPI_C2 raw accumulators (row stride ldo)
     float* cur = nullptr;             // EPI_HIGHWAY / EPI_RESID state, row stride ldcur
     int ldcur = 0;
-    int8_t* hl = nullptr;             // EPI_GLU limb output: row m, limb l at hl + m*hl_row + l*hl_limb
-    long long hl_row = 0;
-    long long hl_limb = 0;
-    float* hs = nullptr;              // EPI_GLU limb scales [m][hs_ld], one per 64 outputs
-    int hs_ld = 0;
     float* stats = nullptr;           // EPI_LOGITS: [m][stats_ld][3] = max, sum exp(l - max), argmax
     int stats_ld = 0;
     const int32_t* tgt = nullptr;     // EPI_LOGITS: target id per row (or null)
@@ -57,7 +67,9 @@ struct GemmArgs {
     const float* lse = nullptr;       // EPI_PROBS: log-sum-exp per row
 };
 
-// nl = number of A limbs (1: plain int8 A; 3: limb-expanded fp32 activations).
-hipError_t launch_gemm(int nl, int epi, const GemmArgs& a, hipStream_t stream);
+// Limb-expanded GEMM (epilogues EPI_F32 .. EPI_PROBS).
+hipError_t launch_gemm_lx(int epi, const GemmArgs& a, hipStream_t stream);
+// Plain int8 GEMM of config 2 (EPI_C2).
+hipError_t launch_gemm_c2(const GemmArgs& a, hipStream_t stream);
 
 }  // namespace mg

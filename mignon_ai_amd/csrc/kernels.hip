@@ -6,6 +6,7 @@
 // reproduced where a result depends on them (RMSNorm's sum of squares, attention dot products, softmax
 // sums, the P.V accumulation), so these stages are bit-identical to the reference given equal inputs.
 #include "common.hpp"
+#include "gemm.hpp"
 #include "kernels.hpp"
 
 namespace mg {
@@ -13,122 +14,160 @@ namespace mg {
 namespace {
 
 // ------------------------------------------------------------------------------------------------
-// Row kernel: one wavefront per token row; lane holds elements d = lane + 64*i.
+// Row kernel: one workgroup per 16-token tile (one fragment row block of the GEMM operand layout); each
+// of the 4 waves processes 4 token rows, lane holding elements d = lane + 64*i. Limb bytes are staged
+// in LDS in fragment order and the tile's 3*Dp*16 bytes (contiguous in the layout) are written with
+// 16-byte stores.
 // ------------------------------------------------------------------------------------------------
+constexpr int ROW_TILE = 16;
+
 template <int NS>
-__global__ __launch_bounds__(64) void row_kernel(RowArgs a) {
-    __shared__ float xsh[NS * 64];
-    const int m = blockIdx.x;
-    const int lane = threadIdx.x;
+__global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
+    __shared__ float xsh[4][NS * 64];
+    extern __shared__ __align__(16) int8_t stage[];  // [Dp/64][3][1 KiB] when limbs are written
+    const int w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
     const int D = a.D, Dp = a.Dp;
-    float x[NS];
-    if (a.mode == ROW_EMBED) {
-        // quant.Model.appendPosition: clamp the id, dequantise the embedding (stream.go:144-152)
-        int id = a.ids[m];
-        if (id < 0 || id >= a.V) id = 0;
-        const int8_t* e = a.emb + (long long)id * D;
+    const int m_base = blockIdx.x * ROW_TILE;
+    for (int rr = w; rr < ROW_TILE; rr += 4) {
+        const int m = m_base + rr;
+        const bool valid = m < a.M;
+        float x[NS];
+        if (!valid) {
 #pragma unroll
-        for (int i = 0; i < NS; i++) {
-            int d = lane + 64 * i;
-            float v = d < D ? (float)e[d] * a.emb_scale : 0.0f;
-            x[i] = v;
-            if (d < Dp) {
-                a.cur[(long long)m * Dp + d] = v;
-                a.block_in[(long long)m * Dp + d] = v;
+            for (int i = 0; i < NS; i++) x[i] = 0.0f;
+        } else if (a.mode == ROW_EMBED) {
+            // quant.Model.appendPosition: clamp the id, dequantise the embedding (stream.go:144-152)
+            int id = a.ids[m];
+            if (id < 0 || id >= a.V) id = 0;
+            const int8_t* e = a.emb + (long long)id * D;
+#pragma unroll
+            for (int i = 0; i < NS; i++) {
+                int d = lane + 64 * i;
+                float v = d < D ? (float)e[d] * a.emb_scale : 0.0f;
+                x[i] = v;
+                if (d < Dp) {
+                    a.cur[(long long)m * Dp + d] = v;
+                    a.block_in[(long long)m * Dp + d] = v;
+                }
+            }
+        } else if (a.mode == ROW_RESID) {
+            // inter-block residual: blockIn += cur; cur = blockIn (stream.go:157-163)
+#pragma unroll
+            for (int i = 0; i < NS; i++) {
+                int d = lane + 64 * i;
+                float v = 0.0f;
+                if (d < Dp) {
+                    long long o = (long long)m * Dp + d;
+                    v = a.block_in[o] + a.cur[o];
+                    a.block_in[o] = v;
+                    a.cur[o] = v;
+                }
+                x[i] = v;
+            }
+        } else {
+            const float* src = a.src ? a.src : a.cur;
+            int lds = a.src ? a.lds : Dp;
+            long long r = a.row_map ? a.row_map[m] : m;
+#pragma unroll
+            for (int i = 0; i < NS; i++) {
+                int d = lane + 64 * i;
+                x[i] = d < D ? src[r * lds + d] : 0.0f;
             }
         }
-    } else if (a.mode == ROW_RESID) {
-        // inter-block residual: blockIn += cur; cur = blockIn (stream.go:157-163)
-#pragma unroll
-        for (int i = 0; i < NS; i++) {
-            int d = lane + 64 * i;
-            float v = 0.0f;
-            if (d < Dp) {
-                long long o = (long long)m * Dp + d;
-                v = a.block_in[o] + a.cur[o];
-                a.block_in[o] = v;
-                a.cur[o] = v;
-            }
-            x[i] = v;
-        }
-    } else {
-        const float* src = a.src ? a.src : a.cur;
-        int lds = a.src ? a.lds : Dp;
-        long long r = a.row_map ? a.row_map[m] : m;
-#pragma unroll
-        for (int i = 0; i < NS; i++) {
-            int d = lane + 64 * i;
-            x[i] = d < D ? src[r * lds + d] : 0.0f;
-        }
-    }
 
-    float y[NS];
-    if (a.gamma) {
-        // nn.RMSNormForwardF32 (internal/nn/rmsnorm.go:14-32) with DotF32's AVX2 accumulation:
-        // 16 partial sums (two 8-lane registers) over 16-element chunks, an 8-chunk into the first.
+        float y[NS];
+        if (a.gamma && valid) {
+            // nn.RMSNormForwardF32 (internal/nn/rmsnorm.go:14-32) with DotF32's AVX2 accumulation:
+            // 16 partial sums (two 8-lane registers) over 16-element chunks, an 8-chunk into the first.
+            float* xs = xsh[w];
 #pragma unroll
-        for (int i = 0; i < NS; i++) xsh[lane + 64 * i] = x[i];
-        __syncthreads();
-        float part = 0.0f;
-        const int c16 = D / 16;
-        if (lane < 16) {
-            for (int c = 0; c < c16; c++) {
-                float v = xsh[16 * c + lane];
-                part = fmaf(v, v, part);
+            for (int i = 0; i < NS; i++) xs[lane + 64 * i] = x[i];
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes have landed
+            __builtin_amdgcn_wave_barrier();
+            float part = 0.0f;
+            const int c16 = D / 16;
+            if (lane < 16) {
+                for (int c = 0; c < c16; c++) {
+                    float v = xs[16 * c + lane];
+                    part = fmaf(v, v, part);
+                }
+                if (lane < 8 && D - 16 * c16 >= 8) {
+                    float v = xs[16 * c16 + lane];
+                    part = fmaf(v, v, part);
+                }
             }
-            if (lane < 8 && D - 16 * c16 >= 8) {
-                float v = xsh[16 * c16 + lane];
-                part = fmaf(v, v, part);
+            float v8[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v8[j] = __shfl(part, j, 64) + __shfl(part, j + 8, 64);
+            float ss = hreduce8(v8);
+            for (int e = (D / 8) * 8; e < D; e++) {
+                float t = xs[e];
+                float p = t * t;
+                ss = ss + p;
             }
-        }
-        float v8[8];
+            float rms = (float)sqrt((double)(ss / (float)D + 1e-5f));
+            float inv = 1.0f / rms;
 #pragma unroll
-        for (int j = 0; j < 8; j++) v8[j] = __shfl(part, j, 64) + __shfl(part, j + 8, 64);
-        float ss = hreduce8(v8);
-        for (int e = (D / 8) * 8; e < D; e++) {
-            float t = xsh[e];
-            float p = t * t;
-            ss = ss + p;
-        }
-        float rms = (float)sqrt((double)(ss / (float)D + 1e-5f));
-        float inv = 1.0f / rms;
+            for (int i = 0; i < NS; i++) {
+                int d = lane + 64 * i;
+                float hat = x[i] * inv;
+                y[i] = d < D ? hat * a.gamma[d] : 0.0f;
+            }
+            __builtin_amdgcn_wave_barrier();  // xs is rewritten by this wave's next row
+        } else {
 #pragma unroll
-        for (int i = 0; i < NS; i++) {
-            int d = lane + 64 * i;
-            float hat = x[i] * inv;
-            y[i] = d < D ? hat * a.gamma[d] : 0.0f;
+            for (int i = 0; i < NS; i++) y[i] = x[i];
         }
-    } else {
-#pragma unroll
-        for (int i = 0; i < NS; i++) y[i] = x[i];
-    }
 
-    if (a.nout) {
+        if (a.nout && valid) {
 #pragma unroll
-        for (int i = 0; i < NS; i++) {
-            int d = lane + 64 * i;
-            if (d < Dp) a.nout[(long long)m * Dp + d] = y[i];
+            for (int i = 0; i < NS; i++) {
+                int d = lane + 64 * i;
+                if (d < Dp) a.nout[(long long)m * Dp + d] = y[i];
+            }
+        }
+        if (a.limbs) {
+            float mx = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NS; i++) mx = fmaxf(mx, fabsf(y[i]));
+            mx = wave_max(mx);
+            float sc, inv;
+            limb_scale(mx, sc, inv);
+            // fragment position of element d = lane + 64 i: K step i, lane (rr + 16 (lane>>4)), byte lane&15
+            const int fo = (rr + 16 * (lane >> 4)) * 16 + (lane & 15);
+#pragma unroll
+            for (int i = 0; i < NS; i++) {
+                if (lane + 64 * i < Dp) {
+                    Limbs L = split_limbs(y[i], inv);
+                    stage[(i * 3 + 0) * 1024 + fo] = L.q0;
+                    stage[(i * 3 + 1) * 1024 + fo] = L.q1;
+                    stage[(i * 3 + 2) * 1024 + fo] = L.q2;
+                }
+            }
+            if (lane == 0 && valid) a.lscale[m] = sc;
         }
     }
     if (a.limbs) {
-        float mx = 0.0f;
+        __syncthreads();
+        const int bytes = 3 * Dp * ROW_TILE;  // Dp/64 K steps x 3 limbs x 1 KiB
+        int8_t* dst = a.limbs + (long long)blockIdx.x * bytes;
+        for (int o = threadIdx.x * 16; o < bytes; o += 256 * 16) *(v4i*)(dst + o) = *(const v4i*)(stage + o);
+    }
+}
+
+// Rule input [n | left | g] of token m, channel d, limb-expanded with row scale 1/inv into the GEMM
+// fragment layout (K = 3*Dp; segment s occupies columns [s*Dp, (s+1)*Dp)).
+__device__ __forceinline__ void store_x_limbs(int8_t* xl, int m, int d, int Dp, int kc, float n, float left, float g,
+                                              float inv) {
+    const float v[3] = {n, left, g};
 #pragma unroll
-        for (int i = 0; i < NS; i++) mx = fmaxf(mx, fabsf(y[i]));
-        mx = wave_max(mx);
-        float s, inv;
-        limb_scale(mx, s, inv);
-        int8_t* row = a.limbs + (long long)m * a.l_row;
-#pragma unroll
-        for (int i = 0; i < NS; i++) {
-            int d = lane + 64 * i;
-            if (d < Dp) {
-                Limbs L = split_limbs(y[i], inv);
-                row[d] = L.q0;
-                row[a.l_limb + d] = L.q1;
-                row[2 * a.l_limb + d] = L.q2;
-            }
-        }
-        if (lane == 0) a.lscale[m] = s;
+    for (int sg = 0; sg < 3; sg++) {
+        Limbs L = split_limbs(v[sg], inv);
+        const int k = sg * Dp + d;
+        xl[frag_off_a(m, k, 0, kc)] = L.q0;
+        xl[frag_off_a(m, k, 1, kc)] = L.q1;
+        xl[frag_off_a(m, k, 2, kc)] = L.q2;
     }
 }
 
@@ -139,11 +178,15 @@ __global__ __launch_bounds__(64) void row_kernel(RowArgs a) {
 // ------------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void scan_kernel(ScanArgs a) {
     __shared__ float red[2][16];
+    // When sequences start on 16-token tile boundaries, a tile's x limbs (3*Dp/64 K steps x 3 limbs x
+    // 1 KiB) are staged here and written with 16-byte stores; otherwise bytes go straight out.
+    extern __shared__ __align__(16) int8_t stage[];
     const int b = blockIdx.x;
     const int d = threadIdx.x;
     const int lane = d & 63, w = d >> 6, nw = blockDim.x >> 6;
     const int D = a.D, Dp = a.Dp, T = a.T;
-    const long long xrow = 3LL * 3 * Dp, xlimb = 3LL * Dp;
+    const int kc = 3 * Dp / 64;
+    const bool staged = (T % 16) == 0;
     const int last = a.lens ? a.lens[b] - 1 : -1;
     float g = 0.0f;
     for (int t = 0; t < T; t++) {
@@ -165,11 +208,28 @@ __global__ __launch_bounds__(1024) void scan_kernel(ScanArgs a) {
         for (int i = 1; i < nw; i++) mx = fmaxf(mx, red[t & 1][i]);
         float s, inv;
         limb_scale(mx, s, inv);
-        int8_t* row = a.xl + m * xrow;
-        Limbs L0 = split_limbs(n, inv), L1 = split_limbs(left, inv), L2 = split_limbs(g, inv);
-        row[d] = L0.q0; row[xlimb + d] = L0.q1; row[2 * xlimb + d] = L0.q2;
-        row[Dp + d] = L1.q0; row[xlimb + Dp + d] = L1.q1; row[2 * xlimb + Dp + d] = L1.q2;
-        row[2 * Dp + d] = L2.q0; row[xlimb + 2 * Dp + d] = L2.q1; row[2 * xlimb + 2 * Dp + d] = L2.q2;
+        if (staged) {
+            const float v[3] = {n, left, g};
+            const int rr = (int)(m & 15);
+#pragma unroll
+            for (int sg = 0; sg < 3; sg++) {
+                Limbs L = split_limbs(v[sg], inv);
+                const int k = sg * Dp + d;
+                const int o = (k >> 6) * 3 * 1024 + ((rr + 16 * ((k >> 4) & 3)) << 4) + (k & 15);
+                stage[o] = L.q0;
+                stage[o + 1024] = L.q1;
+                stage[o + 2048] = L.q2;
+            }
+            if (rr == 15) {
+                __syncthreads();
+                const int bytes = kc * 3 * 1024;
+                int8_t* dst = a.xl + (m >> 4) * (long long)bytes;
+                for (int o = d * 16; o < bytes; o += blockDim.x * 16) *(v4i*)(dst + o) = *(const v4i*)(stage + o);
+                __syncthreads();
+            }
+        } else {
+            store_x_limbs(a.xl, (int)m, d, Dp, kc, n, left, g, inv);
+        }
         if (d == 0) a.xs[m] = s;
         if (t == last && a.g_out) a.g_out[(long long)b * Dp + d] = g;
     }
@@ -203,12 +263,7 @@ __global__ __launch_bounds__(1024) void latch_step_kernel(LatchStepArgs a) {
     for (int i = 1; i < nw; i++) mx = fmaxf(mx, red[i]);
     float sc, inv;
     limb_scale(mx, sc, inv);
-    const long long xlimb = 3LL * Dp;
-    int8_t* row = a.xl + (long long)s_ * 3 * xlimb;
-    Limbs L0 = split_limbs(n, inv), L1 = split_limbs(left, inv), L2 = split_limbs(g, inv);
-    row[d] = L0.q0; row[xlimb + d] = L0.q1; row[2 * xlimb + d] = L0.q2;
-    row[Dp + d] = L1.q0; row[xlimb + Dp + d] = L1.q1; row[2 * xlimb + Dp + d] = L1.q2;
-    row[2 * Dp + d] = L2.q0; row[xlimb + 2 * Dp + d] = L2.q1; row[2 * xlimb + 2 * Dp + d] = L2.q2;
+    store_x_limbs(a.xl, s_, d, Dp, 3 * Dp / 64, n, left, g, inv);
     if (d == 0) a.xs[s_] = sc;
 }
 
@@ -233,10 +288,74 @@ __device__ __forceinline__ float axpy_ref(int i, float alpha, float x, float y) 
 
 constexpr int ATT_QT = 64;  // queries per workgroup (one per lane)
 
-// LDS row stride of the staged keys/values: odd, so that lanes reading consecutive rows (consecutive
-// queries look at consecutive keys) hit different banks.
+// Copies `rows` rows of DH floats (global row stride ld) into LDS rows of stride DS, 16 bytes per lane
+// per step when the width allows it, with several loads in flight.
+template <int DH, int DS>
+__device__ __forceinline__ void stage_rows(float* kv, const float* src, int ld, int rows, int lane) {
+    if constexpr (DH % 4 == 0) {
+        constexpr int C4 = DH / 4;
+        const int n4 = rows * C4;
+#pragma unroll 4
+        for (int e = lane; e < n4; e += 64) {
+            const int r = e / C4, c = e % C4;
+            *(float4*)(kv + r * DS + 4 * c) = *(const float4*)(src + (long long)r * ld + 4 * c);
+        }
+    } else {
+        for (int e = lane; e < rows * DH; e += 64) {
+            const int r = e / DH, i = e % DH;
+            kv[r * DS + i] = src[(long long)r * ld + i];
+        }
+    }
+}
+
+// LDS row stride of the staged keys/values. Lanes read consecutive rows (consecutive queries look at
+// consecutive keys). Widths that are a multiple of 4 take 16-byte rows padded by 4 floats, read with
+// 128-bit loads (consecutive rows land 4 banks apart); other widths take an odd stride and scalar reads.
 template <int DH>
-constexpr int att_stride() { return DH + 1; }
+constexpr bool att_vec() { return DH % 4 == 0; }
+template <int DH>
+constexpr int att_stride() { return att_vec<DH>() ? DH + 4 : DH + 1; }
+
+// DotF32 (dotProductASM_F32 order, see dot_f32_ref) of a register vector with an LDS row, the row
+// read 16 bytes at a time.
+template <int DH>
+__device__ __forceinline__ float dot_ref_lds4(const float (&q)[DH], const float* row) {
+    const float4* r4 = (const float4*)row;
+    float a0[8], a1[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) { a0[j] = 0.0f; a1[j] = 0.0f; }
+    int i = 0;
+#pragma unroll
+    for (; i + 16 <= DH; i += 16) {
+        float4 k0 = r4[i / 4], k1 = r4[i / 4 + 1], k2 = r4[i / 4 + 2], k3 = r4[i / 4 + 3];
+        a0[0] = fmaf(q[i + 0], k0.x, a0[0]); a0[1] = fmaf(q[i + 1], k0.y, a0[1]);
+        a0[2] = fmaf(q[i + 2], k0.z, a0[2]); a0[3] = fmaf(q[i + 3], k0.w, a0[3]);
+        a0[4] = fmaf(q[i + 4], k1.x, a0[4]); a0[5] = fmaf(q[i + 5], k1.y, a0[5]);
+        a0[6] = fmaf(q[i + 6], k1.z, a0[6]); a0[7] = fmaf(q[i + 7], k1.w, a0[7]);
+        a1[0] = fmaf(q[i + 8], k2.x, a1[0]); a1[1] = fmaf(q[i + 9], k2.y, a1[1]);
+        a1[2] = fmaf(q[i + 10], k2.z, a1[2]); a1[3] = fmaf(q[i + 11], k2.w, a1[3]);
+        a1[4] = fmaf(q[i + 12], k3.x, a1[4]); a1[5] = fmaf(q[i + 13], k3.y, a1[5]);
+        a1[6] = fmaf(q[i + 14], k3.z, a1[6]); a1[7] = fmaf(q[i + 15], k3.w, a1[7]);
+    }
+    if (i + 8 <= DH) {
+        float4 k0 = r4[i / 4], k1 = r4[i / 4 + 1];
+        a0[0] = fmaf(q[i + 0], k0.x, a0[0]); a0[1] = fmaf(q[i + 1], k0.y, a0[1]);
+        a0[2] = fmaf(q[i + 2], k0.z, a0[2]); a0[3] = fmaf(q[i + 3], k0.w, a0[3]);
+        a0[4] = fmaf(q[i + 4], k1.x, a0[4]); a0[5] = fmaf(q[i + 5], k1.y, a0[5]);
+        a0[6] = fmaf(q[i + 6], k1.z, a0[6]); a0[7] = fmaf(q[i + 7], k1.w, a0[7]);
+        i += 8;
+    }
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = a0[j] + a1[j];
+    float s = hreduce8(v);
+#pragma unroll
+    for (; i < DH; i++) {
+        float p = q[i] * row[i];
+        s = s + p;
+    }
+    return s;
+}
 
 // One workgroup per (sequence, 64-query tile, head). Keys of the tile's whole window are staged in LDS,
 // each lane scores its query against them (DotF32 order), runs the reference softmax, then the values
@@ -244,7 +363,7 @@ constexpr int att_stride() { return DH + 1; }
 template <int DH>
 __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
     constexpr int DS = att_stride<DH>();
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];
     const int nqt = (a.T + ATT_QT - 1) / ATT_QT;
     const int b = blockIdx.x / nqt, qt = blockIdx.x % nqt;
     const int h = blockIdx.y;
@@ -259,10 +378,7 @@ __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
     const long long base = (long long)b * T;
     const int ld = 3 * D;
 
-    for (int e = lane; e < rows * DH; e += 64) {
-        int r = e / DH, i = e % DH;
-        kv[r * DS + i] = a.qkv[(base + r0 + r) * ld + D + h * DH + i];
-    }
+    stage_rows<DH, DS>(kv, a.qkv + (base + r0) * ld + D + h * DH, ld, rows, lane);
     __syncthreads();
 
     const int t = t0 + lane;
@@ -271,15 +387,26 @@ __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
     int lo = 0, span = 0;
     float inv = 0.0f;
     if (active) {
+        const float* qp = a.qkv + (base + t) * ld + h * DH;
+        if constexpr (att_vec<DH>()) {
 #pragma unroll
-        for (int i = 0; i < DH; i++) q[i] = a.qkv[(base + t) * ld + h * DH + i];
+            for (int i = 0; i < DH; i += 4) {
+                float4 v = *(const float4*)(qp + i);
+                q[i] = v.x; q[i + 1] = v.y; q[i + 2] = v.z; q[i + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < DH; i++) q[i] = qp[i];
+        }
         lo = max(window_start(t, a.window), t - cap + 1);
         span = t - lo + 1;
         const float scale = (float)(1.0 / sqrt((double)DH));
         float mx = -3.40282347e38f;
         for (int jj = 0; jj < span; jj++) {
             const float* k = kv + (lo + jj - r0) * DS;
-            float s = dot_f32_ref<DH>(q, k) * scale;
+            float s;
+            if constexpr (att_vec<DH>()) s = dot_ref_lds4<DH>(q, k) * scale;
+            else s = dot_f32_ref<DH>(q, k) * scale;
             sc[jj * 64 + lane] = s;
             if (s > mx) mx = s;
         }
@@ -293,10 +420,7 @@ __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
         inv = 1.0f / sum;
     }
     __syncthreads();
-    for (int e = lane; e < rows * DH; e += 64) {
-        int r = e / DH, i = e % DH;
-        kv[r * DS + i] = a.qkv[(base + r0 + r) * ld + 2 * D + h * DH + i];
-    }
+    stage_rows<DH, DS>(kv, a.qkv + (base + r0) * ld + 2 * D + h * DH, ld, rows, lane);
     __syncthreads();
     if (!active) return;
     float o[DH];
@@ -305,12 +429,29 @@ __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
     for (int jj = 0; jj < span; jj++) {
         float p = sc[jj * 64 + lane] * inv;
         const float* v = kv + (lo + jj - r0) * DS;
+        if constexpr (att_vec<DH>()) {
+            const float4* v4 = (const float4*)v;
 #pragma unroll
-        for (int i = 0; i < DH; i++) o[i] = axpy_ref<DH>(i, p, v[i], o[i]);
+            for (int i = 0; i < DH; i += 4) {
+                float4 vv = v4[i / 4];
+                o[i] = axpy_ref<DH>(i, p, vv.x, o[i]);
+                o[i + 1] = axpy_ref<DH>(i + 1, p, vv.y, o[i + 1]);
+                o[i + 2] = axpy_ref<DH>(i + 2, p, vv.z, o[i + 2]);
+                o[i + 3] = axpy_ref<DH>(i + 3, p, vv.w, o[i + 3]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < DH; i++) o[i] = axpy_ref<DH>(i, p, v[i], o[i]);
+        }
     }
     float* dst = a.att + (base + t) * a.Dp + h * DH;
+    if constexpr (att_vec<DH>()) {
 #pragma unroll
-    for (int i = 0; i < DH; i++) dst[i] = o[i];
+        for (int i = 0; i < DH; i += 4) *(float4*)(dst + i) = make_float4(o[i], o[i + 1], o[i + 2], o[i + 3]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < DH; i++) dst[i] = o[i];
+    }
 }
 
 // One wavefront per (session, head): lane j scores key j of the ring, lane i accumulates output i.
@@ -505,12 +646,16 @@ hipError_t attn_step_t(const AttnStepArgs& a, hipStream_t s) {
 hipError_t launch_row(const RowArgs& a, hipStream_t s) {
     if (a.M <= 0) return hipSuccess;
     const int ns = a.Dp / 64;
-    if (a.Dp % 64 || ns < 1 || ns > 16) return hipErrorInvalidValue;
+    if (a.Dp % 64 || ns < 1 || ns > 32) return hipErrorInvalidValue;
+    const int tiles = (a.M + ROW_TILE - 1) / ROW_TILE;
+    const size_t stage = a.limbs ? (size_t)3 * a.Dp * ROW_TILE : 0;
 #define ROW_CASE(N) \
-    case N: hipLaunchKernelGGL(row_kernel<N>, dim3(a.M), dim3(64), 0, s, a); break;
+    case N: hipLaunchKernelGGL(row_kernel<N>, dim3(tiles), dim3(256), stage, s, a); break;
     switch (ns) {
         ROW_CASE(1) ROW_CASE(2) ROW_CASE(3) ROW_CASE(4) ROW_CASE(5) ROW_CASE(6) ROW_CASE(7) ROW_CASE(8)
         ROW_CASE(9) ROW_CASE(10) ROW_CASE(11) ROW_CASE(12) ROW_CASE(13) ROW_CASE(14) ROW_CASE(15) ROW_CASE(16)
+        ROW_CASE(17) ROW_CASE(18) ROW_CASE(19) ROW_CASE(20) ROW_CASE(21) ROW_CASE(22) ROW_CASE(23) ROW_CASE(24)
+        ROW_CASE(25) ROW_CASE(26) ROW_CASE(27) ROW_CASE(28) ROW_CASE(29) ROW_CASE(30) ROW_CASE(31) ROW_CASE(32)
     }
 #undef ROW_CASE
     return hipGetLastError();
@@ -519,7 +664,8 @@ hipError_t launch_row(const RowArgs& a, hipStream_t s) {
 hipError_t launch_scan(const ScanArgs& a, hipStream_t s) {
     if (a.B <= 0) return hipSuccess;
     if (a.Dp % 64 || a.Dp > 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(scan_kernel, dim3(a.B), dim3(a.Dp), 0, s, a);
+    const size_t stage = (a.T % 16) == 0 ? (size_t)9 * a.Dp * 16 : 0;
+    hipLaunchKernelGGL(scan_kernel, dim3(a.B), dim3(a.Dp), stage, s, a);
     return hipGetLastError();
 }
 

@@ -22,8 +22,7 @@ struct RowArgs {
     const int32_t* row_map = nullptr;  // ROW_SRC: output row m reads source row row_map[m]
     const float* gamma = nullptr;      // RMSNorm scales, or null (copy)
     float* nout = nullptr;             // normalised rows [M][Dp], or null
-    int8_t* limbs = nullptr;           // limb-expanded rows: row m, limb l at limbs + m*l_row + l*l_limb
-    long long l_row = 0, l_limb = 0;
+    int8_t* limbs = nullptr;           // limb-expanded rows in the GEMM fragment layout (K = Dp)
     float* lscale = nullptr;           // [M]
 };
 hipError_t launch_row(const RowArgs& a, hipStream_t s);
@@ -33,7 +32,7 @@ struct ScanArgs {
     int B = 0, T = 0, D = 0, Dp = 0, dil = 1;
     const float* lam = nullptr;  // [B*T][Dp]
     const float* nf = nullptr;   // [B*T][Dp]
-    int8_t* xl = nullptr;        // [B*T][3][3*Dp]
+    int8_t* xl = nullptr;        // [n | left | g] limb-expanded, fragment layout, K = 3*Dp
     float* xs = nullptr;         // [B*T]
     const int32_t* lens = nullptr;  // per-sequence length (export position lens[b]-1) or null
     float* g_out = nullptr;         // exported latch state [B][Dp] or null
@@ -48,7 +47,7 @@ struct LatchStepArgs {
     const float* nf = nullptr;     // [S][Dp]
     float* g = nullptr;            // latch state [S][Dp]
     float* norm_ring = nullptr;    // [S][ring][Dp]
-    int8_t* xl = nullptr;          // [S][3][3*Dp]
+    int8_t* xl = nullptr;          // fragment layout, K = 3*Dp
     float* xs = nullptr;           // [S]
 };
 hipError_t launch_latch_step(const LatchStepArgs& a, hipStream_t s);

@@ -208,7 +208,7 @@ inline void validate_for_engine(const HostModel& m) {
         if (!ok) throw FormatError("model file: " + what);
     };
     need(m.V > 0 && m.D > 0 && m.H > 0, "vocab, state and hidden sizes must be positive");
-    need(m.D <= 1024 && m.H <= 8192, "state size above 1024 or hidden size above 8192 is not supported");
+    need(m.D <= 1024 && m.H <= 2048, "state size above 1024 or hidden size above 2048 is not supported");
     need(m.embed.size() == (size_t)m.V * m.D, "embed has the wrong size");
     for (size_t b = 0; b < m.blocks.size(); b++) {
         const HostBlock& hb = m.blocks[b];
