@@ -136,6 +136,16 @@ int mg_gemm_i8(const int8_t* A, int M, int K, const int8_t* W, int N, const floa
  * half away from zero (w/scale), +-127); an all-zero tensor gets scale 1. */
 int mg_quantize_f32(const float* w, long long n, int8_t* q, float* scale, int flags, void* stream);
 
+/* Engine tuning, no reference counterpart. Selects the limb-expanded GEMM kernel for every model of
+ * the process: MG_GEMM_AUTO (default) uses the weight-stationary kernel (weights held in LDS, many
+ * token tiles streamed through them) for large batches whose weight slab fits in LDS and the streaming
+ * kernel otherwise; MG_GEMM_STREAM and MG_GEMM_SLAB force one of them where it applies. Both give the
+ * same results. Returns the previous selection, or MG_ERR_INVALID. */
+#define MG_GEMM_AUTO 0
+#define MG_GEMM_STREAM 1
+#define MG_GEMM_SLAB 2
+int mg_gemm_select(int kind);
+
 #ifdef __cplusplus
 }
 #endif

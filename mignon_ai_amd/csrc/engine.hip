@@ -318,8 +318,10 @@ void build_device_model(mg_model* m, const HostModel& hm, int max_context) {
     for (int r = 0; r < V; r++) std::memcpy(&head[(size_t)r * Dp], &hw[(size_t)r * D], D);
     m->headw = upload(m, frag_pack(head, m->Vp, Dp));
     m->head_scale = hm.tied ? hm.embed_scale : hm.head_scale;
-    std::vector<float> hb(m->Vp, 0.0f);
-    for (size_t v = 0; v < hm.head_b.size() && v < (size_t)V; v++) hb[v] = hm.head_b[v];
+    // vocabulary padding: bias -inf (with zero weight rows) makes its logits -inf, so the head's
+    // epilogues need no per-channel validity test
+    std::vector<float> hb(m->Vp, -INFINITY);
+    for (int v = 0; v < V; v++) hb[v] = (size_t)v < hm.head_b.size() ? hm.head_b[v] : 0.0f;
     m->headb = upload(m, hb);
     if ((int)hm.final_norm.size() == D) {
         std::vector<float> fn(hm.final_norm);
@@ -1064,6 +1066,15 @@ int mg_quantize_f32(const float* w, long long n, int8_t* q, float* scale, int fl
         }
         return MG_OK;
     });
+}
+
+int mg_gemm_select(int kind) {
+    const int prev = select_gemm_kernel(kind);
+    if (prev < 0) {
+        g_last_error = "mg_gemm_select: unknown kernel selection " + std::to_string(kind);
+        return MG_ERR_INVALID;
+    }
+    return prev;
 }
 
 }  // extern "C"

@@ -15,6 +15,10 @@
 //
 // Plain int8 GEMM (gemm_c2_kernel, config 2): row-major operands, 4 waves in a 2 x 2 grid, both
 // operands staged through LDS with an 80-byte row stride (conflict-free 16-byte fragment reads).
+#include <algorithm>
+#include <atomic>
+#include <type_traits>
+
 #include "common.hpp"
 #include "gemm.hpp"
 
@@ -27,6 +31,234 @@ __device__ __forceinline__ void store4(float* dst, const float v[4], int nvalid_
         *(float4*)dst = make_float4(v[0], v[1], v[2], v[3]);
     } else {
         for (int r = 0; r < 4 && r < nvalid_here; r++) dst[r] = v[r];
+    }
+}
+
+// Epilogue of one wave's 16-token x 128-channel tile (first token mt0, channel tile n_tile).
+//
+// The three digit-plane sums of tile ti, register r combine into the fp32 dot product
+// x.w = s*(P0 + P1/254 + P2/254^2) times the weight scale; s*wscale is one factor per token, and a
+// bias is added with the same FMA. Token of this lane: mt0 + (L & 15); channel of (ti, r):
+// n0 + 16ti + 4*(L >> 4) + r. Kept lean: for K = 384 the epilogue's VALU work is comparable to the
+// MFMA work of the whole tile.
+__device__ __forceinline__ float limb_dot(const v4i (&acc)[3][8], int ti, int r) {
+    return fmaf((float)acc[2][ti][r], kInvLimb2, fmaf((float)acc[1][ti][r], kInvLimb1, (float)acc[0][ti][r]));
+}
+
+// sigmoidClamped from 2^x and the hardware reciprocal (see sigmoid_clamped_f32); exactly 0 and 1 beyond
+// |x| > 15 as in the reference.
+__device__ __forceinline__ float sigmoid_epi(float x) {
+    const float e = __builtin_amdgcn_exp2f(x * -1.4426950408889634f);
+    const float v = __builtin_amdgcn_rcpf(1.0f + e);
+    return fabsf(x) > 15.0f ? (x > 0.0f ? 1.0f : 0.0f) : v;
+}
+
+// Per-token values the epilogue needs, loaded when the tile starts so that their latency hides behind
+// the tile's MFMAs.
+// (Only loads here: any arithmetic on a loaded value would make the compiler wait for it at once.)
+struct EpiRow {
+    float s = 0.0f;   // activation scale (times the weight scale in the epilogue)
+    int tgt = -1;     // EPI_LOGITS: target id
+    float lse = 0.0f; // EPI_PROBS: log-sum-exp
+};
+
+template <int EPI>
+__device__ __forceinline__ EpiRow epi_row(const GemmArgs& g, int m) {
+    EpiRow e;
+    const int mm = min(m, g.M - 1);  // rows past M are never stored; their values are not used
+    e.s = g.As[mm];
+    if constexpr (EPI == EPI_LOGITS) {
+        if (g.tgt) e.tgt = g.tgt[mm];
+    }
+    if constexpr (EPI == EPI_PROBS) e.lse = g.lse[mm];
+    return e;
+}
+
+// bias_t: the bias of this tile's 128 channels (global memory, or the workgroup's LDS copy).
+template <int EPI>
+__device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[3][8], int mt0, int n0, int n_tile,
+                                            int lane, const EpiRow& row, const float* bias_t) {
+    const int g4 = lane >> 4;
+    const int m = mt0 + (lane & 15);
+    const bool mok = m < g.M;
+    const float sw = row.s * g.wscale;
+    const int nb = n0 + 4 * g4;
+    const bool vec = (g.ldo & 3) == 0;
+
+    if constexpr (EPI == EPI_F32 || EPI == EPI_LATCH) {
+        if (!mok) return;
+        float* orow = g.out + (long long)m * g.ldo;
+#pragma unroll
+        for (int ti = 0; ti < 8; ti++) {
+            const int n = nb + ti * 16;
+            const int nv = g.nvalid - n;
+            if (nv <= 0) continue;
+            float v[4];
+            if constexpr (EPI == EPI_LATCH) {
+                const float4 b = *(const float4*)(bias_t + 4 * g4 + ti * 16);
+                const float bb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int r = 0; r < 4; r++) v[r] = sigmoid_epi(fmaf(limb_dot(acc, ti, r), sw, bb[r]));
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++) v[r] = limb_dot(acc, ti, r) * sw;
+            }
+            store4(orow + n, v, nv, vec);
+        }
+    } else if constexpr (EPI == EPI_RESID) {
+        // cur += x.w: all eight row segments are loaded before any is needed (one memory latency)
+        if (!mok) return;
+        float* crow = g.cur + (long long)m * g.ldcur;
+        const bool cvec = (g.ldcur & 3) == 0;
+        float c[8][4];
+#pragma unroll
+        for (int ti = 0; ti < 8; ti++) {
+            const int n = nb + ti * 16;
+            const int nv = g.nvalid - n;
+            if (nv >= 4 && cvec) {
+                const float4 t = *(const float4*)(crow + n);
+                c[ti][0] = t.x; c[ti][1] = t.y; c[ti][2] = t.z; c[ti][3] = t.w;
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++) c[ti][r] = r < nv ? crow[n + r] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int ti = 0; ti < 8; ti++) {
+            const int n = nb + ti * 16;
+            const int nv = g.nvalid - n;
+            if (nv <= 0) continue;
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) v[r] = c[ti][r] + limb_dot(acc, ti, r) * sw;
+            store4(crow + n, v, nv, cvec);
+        }
+    } else if constexpr (EPI == EPI_PROBS) {
+        // p = exp(l - lse) = 2^(x.w*log2e + (b - lse)*log2e)
+        if (!mok) return;
+        const float l2e = 1.4426950408889634f;
+        const float swl = sw * l2e, lsel = row.lse * l2e;
+        float* orow = g.out + (long long)m * g.ldo;
+#pragma unroll
+        for (int ti = 0; ti < 8; ti++) {
+            const int n = nb + ti * 16;
+            const int nv = g.nvalid - n;
+            if (nv <= 0) continue;
+            const float4 b = *(const float4*)(bias_t + 4 * g4 + ti * 16);
+            const float bb[4] = {b.x, b.y, b.z, b.w};
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) v[r] = __builtin_amdgcn_exp2f(fmaf(limb_dot(acc, ti, r), swl, fmaf(bb[r], l2e, -lsel)));
+            store4(orow + n, v, nv, vec);
+        }
+    } else if constexpr (EPI == EPI_GLU || EPI == EPI_HIGHWAY) {
+        // W rows are reordered in blocks of 32: 16 value rows then the 16 matching gate rows, so tile
+        // pair (2p, 2p+1) holds value and gate of output channel n0/2 + 16p + 4*(L >> 4) + r.
+        if (!mok) return;
+        float c[4][4];
+        float* crow = nullptr;
+        const bool cvec = (g.ldcur & 3) == 0;
+        if constexpr (EPI == EPI_HIGHWAY) {
+            // the four cur segments this lane updates, loaded together
+            crow = g.cur + (long long)m * g.ldcur;
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                const int ch = n0 / 2 + p * 16 + 4 * g4;
+                const int nv = g.nvalid - ch;
+                if (nv >= 4 && cvec) {
+                    const float4 t = *(const float4*)(crow + ch);
+                    c[p][0] = t.x; c[p][1] = t.y; c[p][2] = t.z; c[p][3] = t.w;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) c[p][r] = r < nv ? crow[ch + r] : 0.0f;
+                }
+            }
+        }
+        float* orow = g.out + (long long)m * g.ldo;
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const int ch = n0 / 2 + p * 16 + 4 * g4;
+            const int nv = g.nvalid - ch;
+            if (nv <= 0) continue;
+            const int rv = 32 * p + 4 * g4;  // value rows rv..rv+3, gate rows rv+16.. within the tile
+            const float4 bv = *(const float4*)(bias_t + rv), bg = *(const float4*)(bias_t + rv + 16);
+            const float bvv[4] = {bv.x, bv.y, bv.z, bv.w}, bgg[4] = {bg.x, bg.y, bg.z, bg.w};
+            float ov[4], gt[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                ov[r] = fmaf(limb_dot(acc, 2 * p, r), sw, bvv[r]);
+                gt[r] = sigmoid_epi(fmaf(limb_dot(acc, 2 * p + 1, r), sw, bgg[r]));
+            }
+            float v[4];
+            if constexpr (EPI == EPI_GLU) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) v[r] = ov[r] * gt[r];  // mlpHidden *= sigmoid(gate) (stream.go:218-220)
+                store4(orow + ch, v, nv, vec);
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float a = (1.0f - gt[r]) * c[p][r];  // highway (stream.go:226-229)
+                    const float b = gt[r] * ov[r];
+                    v[r] = a + b;
+                }
+                store4(crow + ch, v, nv, cvec);
+            }
+        }
+    } else if constexpr (EPI == EPI_LOGITS) {
+        // Logits of this lane's 32 channels (vocabulary padding has bias -inf and zero weights, so its
+        // logits are -inf), four at a time: running max with its first index, and the sum of
+        // exp(l - max) rescaled whenever the max rises.
+        const float l2e = 1.4426950408889634f;
+        float bmax = -INFINITY, bsum = 0.0f;
+        int bidx = 0x7fffffff;
+        const int t = row.tgt - nb;  // the target's position among this lane's channels
+        float* orow = g.out ? g.out + (long long)m * g.ldo : nullptr;
+#pragma unroll
+        for (int ti = 0; ti < 8; ti++) {
+            const int n = nb + ti * 16;
+            const float4 b = *(const float4*)(bias_t + 4 * g4 + ti * 16);
+            const float bb[4] = {b.x, b.y, b.z, b.w};
+            float y[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) y[r] = fmaf(limb_dot(acc, ti, r), sw, bb[r]);
+            if (orow && mok) {
+                const int nv = g.nvalid - n;
+                if (nv > 0) store4(orow + n, y, nv, vec);
+            }
+            float mx = bmax;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {  // channels rise with (ti, r): ties keep the first index
+                const bool up = y[r] > mx;
+                mx = up ? y[r] : mx;
+                bidx = up ? n + r : bidx;
+            }
+            const float ml = mx == -INFINITY ? 0.0f : mx * l2e;
+            const float rescale = bmax == mx ? 1.0f : __builtin_amdgcn_exp2f(fmaf(bmax, l2e, -ml));
+            float s = bsum * rescale;
+#pragma unroll
+            for (int r = 0; r < 4; r++) s += __builtin_amdgcn_exp2f(fmaf(y[r], l2e, -ml));
+            bsum = s;
+            bmax = mx;
+            if (mok && t >= ti * 16 && t < ti * 16 + 4) {
+                const int r = t & 3;
+                g.tlog[m] = r == 0 ? y[0] : r == 1 ? y[1] : r == 2 ? y[2] : y[3];
+            }
+        }
+        // the four lane groups interleave channels: combine, the smaller index wins ties
+#pragma unroll
+        for (int o = 16; o <= 32; o <<= 1) {
+            float om = __shfl_xor(bmax, o, 64), os = __shfl_xor(bsum, o, 64);
+            int oi = __shfl_xor(bidx, o, 64);
+            float nm = fmaxf(bmax, om);
+            float ns = (bmax == -INFINITY ? 0.0f : bsum * __expf(bmax - nm)) +
+                       (om == -INFINITY ? 0.0f : os * __expf(om - nm));
+            int ni = (om > bmax) ? oi : (bmax > om) ? bidx : min(bidx, oi);
+            bmax = nm; bsum = ns; bidx = ni;
+        }
+        if (mok && g4 == 0) {
+            float* dst = g.stats + ((long long)m * g.stats_ld + n_tile) * 3;
+            dst[0] = bmax; dst[1] = bsum; dst[2] = __int_as_float(bidx);
+        }
     }
 }
 
@@ -48,7 +280,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int n_tile = t % nt;
     const int n0 = n_tile * LX_BN;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int g4 = lane >> 4;
     const int kc = g.Kp >> 6;
 
     // weight tile of K step ks: 8 KiB contiguous at wbase + ks*wstep
@@ -63,6 +294,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int l = 0; l < 3; l++)
 #pragma unroll
         for (int ti = 0; ti < 8; ti++) acc[l][ti] = v4i{0, 0, 0, 0};
+    const EpiRow row = epi_row<EPI>(g, m0 + w * 16 + (lane & 15));
 
     v4i wreg0, wreg1, acur[3], anext[3];
     wreg0 = *(const v4i*)(wbase);
@@ -110,134 +342,128 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         __syncthreads();
     }
 
-    // ------------------------------------------------------------------------------------------
-    // Epilogue: combine the three digit planes of tile ti, register r, into the fp32 dot product
-    // (x.w = s*(P0 + P1/254 + P2/254^2)) times the weight scale.
-    // Token of this lane: m0 + 16w + (L & 15); channel of (ti, r): n0 + 16ti + 4*(L >> 4) + r.
-    // ------------------------------------------------------------------------------------------
-    const int m = m0 + w * 16 + (lane & 15);
-    const bool mok = m < g.M;
-    float y[8][4];
-    {
-        const float s = mok ? g.As[m] : 0.0f;
-#pragma unroll
-        for (int ti = 0; ti < 8; ti++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                float v = fmaf((float)acc[2][ti][r], kInvLimb2, fmaf((float)acc[1][ti][r], kInvLimb1, (float)acc[0][ti][r]));
-                y[ti][r] = (s * v) * g.wscale;
-            }
-    }
-    const int nb = n0 + 4 * g4;
+    lx_epilogue<EPI>(g, acc, m0 + w * 16, n0, n_tile, lane, row, g.bias ? g.bias + n0 : nullptr);
+}
 
-    if constexpr (EPI == EPI_F32 || EPI == EPI_LATCH || EPI == EPI_RESID || EPI == EPI_PROBS) {
-        if (!mok) return;
-        float lse_m = 0.0f;
-        if constexpr (EPI == EPI_PROBS) lse_m = g.lse[m];
+// ------------------------------------------------------------------------------------------------
+// Weight-stationary limb-expanded GEMM
+// ------------------------------------------------------------------------------------------------
+// A workgroup of 8 waves copies one 128-channel weight slab (all K steps, kc*8 KiB) and its bias into
+// LDS once, then streams a run of token tiles through it: wave w takes 16-token tiles t_begin + w,
+// + 8, ... of the run. After the slab load there is no barrier: each wave reads weight fragments from
+// the read-only slab and its own activation fragments straight from global memory, two K steps ahead
+// (three register sets, rotated by unrolling the K loop by three). The prefetch runs across tiles: the
+// last two K steps of a tile fetch the first two steps of the wave's next tile, before the epilogue's
+// stores. REM = kc % 3 fixes at compile time where those land. Two waves per SIMD: one wave's epilogue
+// overlaps the other's MFMAs.
+//
+// Block b -> (XCD b % 8, slot b / 8); slot -> (channel slab slot % nt, run (slot / nt)*8 + XCD), so all
+// slabs of a run execute on one XCD and its activations are fetched from HBM into that XCD's L2 once.
+template <int EPI, int REM>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_slab_kernel(GemmArgs g,
+                                                                                                   int run_tiles,
+                                                                                                   int n_runs) {
+    extern __shared__ __align__(16) int8_t slab[];
+    const int nt = g.Np / LX_BN;
+    const int slot = blockIdx.x >> 3;
+    const int n_tile = slot % nt;
+    const int run = (slot / nt) * 8 + (blockIdx.x & 7);
+    if (run >= n_runs) return;
+    const int n0 = n_tile * LX_BN;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int kc = g.Kp >> 6;
+    float* bias_s = (float*)(slab + kc * 8192);
+
+    {
+        // slab[ks][ti][1 KiB] <- W fragments (ks, n0/16 + ti): 8 KiB contiguous per K step
+        const int8_t* src = g.W + (long long)(n0 >> 4) * 1024;
+        const long long wstep = (long long)(g.Np >> 4) * 1024;
+        const int chunks = kc * 512;  // 16-byte chunks, 512 per K step
+#pragma unroll 4
+        for (int c = tid; c < chunks; c += 512)
+            *(v4i*)(slab + ((long long)c << 4)) = *(const v4i*)(src + (c >> 9) * wstep + ((c & 511) << 4));
+        if (tid < LX_BN) bias_s[tid] = g.bias ? g.bias[n0 + tid] : 0.0f;
+    }
+    __syncthreads();
+
+    const int mtiles = (g.M + 15) >> 4;
+    const int t_begin = run * run_tiles;
+    const int t_end = min(t_begin + run_tiles, mtiles);
+    int tile = t_begin + w;
+    if (tile >= t_end) return;
+    const int8_t* wlane = slab + lane * 16;
+    const long long astep = 3 * 1024;  // one K step of one tile: three limb fragments
+    const long long tstep = (long long)kc * astep;
+
+    const int8_t* ap = g.A + (long long)tile * tstep + lane * 16;
+    v4i a0[3], a1[3], a2[3];
 #pragma unroll
-        for (int ti = 0; ti < 8; ti++) {
-            const int n = nb + ti * 16;
-            const int nv = g.nvalid - n;
-            if (nv <= 0) continue;
-            float v[4];
-            float4 b = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if constexpr (EPI == EPI_LATCH || EPI == EPI_PROBS) b = *(const float4*)(g.bias + n);
-            const float bb[4] = {b.x, b.y, b.z, b.w};
+    for (int l = 0; l < 3; l++) a0[l] = *(const v4i*)(ap + l * 1024);
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                float yy = y[ti][r];
-                if constexpr (EPI == EPI_LATCH) yy = sigmoid_clamped_f32(yy + bb[r]);
-                if constexpr (EPI == EPI_PROBS) {
-                    yy = yy + bb[r];
-                    yy = __expf(yy - lse_m);
-                }
-                v[r] = yy;
+    for (int l = 0; l < 3; l++) a1[l] = *(const v4i*)(ap + astep + l * 1024);  // kc >= 2
+
+    for (;;) {
+        const EpiRow row = epi_row<EPI>(g, tile * 16 + (lane & 15));
+        // the next tile's fragments (this tile's again when there is none: harmless, in bounds)
+        const int next = tile + 8;
+        const int8_t* np = next < t_end ? ap + 8 * tstep : ap;
+        v4i acc[3][8];
+#pragma unroll
+        for (int l = 0; l < 3; l++)
+#pragma unroll
+            for (int ti = 0; ti < 8; ti++) acc[l][ti] = v4i{0, 0, 0, 0};
+        // One K step: multiply step ks held in `cur`; with PF, first prefetch step ks+2 (of this tile, or
+        // of the next) into `nxt`. Every path issues the same loads in the same order, so the compiler's
+        // in-order load counting lets each step wait only for the loads two steps back.
+        auto step = [&](int ks, v4i (&cur)[3], v4i (&nxt)[3], auto pf) {
+            if constexpr (decltype(pf)::value) {
+                const int8_t* src = ks + 2 < kc ? ap + (ks + 2) * astep : np + (ks + 2 - kc) * astep;
+#pragma unroll
+                for (int l = 0; l < 3; l++) nxt[l] = *(const v4i*)(src + l * 1024);
             }
-            if constexpr (EPI == EPI_RESID) {
-                float* dst = g.cur + (long long)m * g.ldcur + n;
-                for (int r = 0; r < 4 && r < nv; r++) dst[r] = dst[r] + v[r];
-            } else {
-                store4(g.out + (long long)m * g.ldo + n, v, nv, (g.ldo & 3) == 0);
-            }
+            v4i wf[8];
+            const int8_t* wp = wlane + ks * 8192;
+#pragma unroll
+            for (int ti = 0; ti < 8; ti++) wf[ti] = *(const v4i*)(wp + ti * 1024);
+#pragma unroll
+            for (int ti = 0; ti < 8; ti++)
+#pragma unroll
+                for (int l = 0; l < 3; l++)
+                    acc[l][ti] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[ti], cur[l], acc[l][ti], 0, 0, 0);
+            // order: the step's global prefetches, its eight LDS reads, then the MFMAs
+            if constexpr (decltype(pf)::value) __builtin_amdgcn_sched_group_barrier(0x020, 3, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 24, 0);
+        };
+        constexpr std::true_type PF{};
+        constexpr std::false_type NOPF{};
+        int ks = 0;
+        for (; ks + 3 <= kc; ks += 3) {
+            step(ks, a0, a2, PF);
+            step(ks + 1, a1, a0, PF);
+            step(ks + 2, a2, a1, PF);
         }
-    } else if constexpr (EPI == EPI_GLU || EPI == EPI_HIGHWAY) {
-        // W rows are reordered in blocks of 32: 16 value rows then the 16 matching gate rows, so tile
-        // pair (2p, 2p+1) holds value and gate of output channel n0/2 + 16p + 4*(L >> 4) + r.
-        if (!mok) return;
+        if constexpr (REM == 1) step(ks, a0, a2, PF);
+        if constexpr (REM == 2) {
+            // a0 (after this step) and a2 are free for the next tile's first two steps
+            step(ks, a0, a2, NOPF);
 #pragma unroll
-        for (int p = 0; p < 4; p++) {
-            const int ch = n0 / 2 + p * 16 + 4 * g4;
-            const int row_v = n0 + 32 * p + 4 * g4, row_g = row_v + 16;
-            if (ch >= g.nvalid) continue;
-            const float4 bv = *(const float4*)(g.bias + row_v), bg = *(const float4*)(g.bias + row_g);
-            const float bvv[4] = {bv.x, bv.y, bv.z, bv.w}, bgg[4] = {bg.x, bg.y, bg.z, bg.w};
-            float v[4];
-            if constexpr (EPI == EPI_GLU) {
+            for (int l = 0; l < 3; l++) a0[l] = *(const v4i*)(np + l * 1024);
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    float ov = y[2 * p][r] + bvv[r];
-                    float og = y[2 * p + 1][r] + bgg[r];
-                    v[r] = ov * sigmoid_clamped_f32(og);  // mlpHidden *= sigmoid(gate) (stream.go:218-220)
-                }
-                store4(g.out + (long long)m * g.ldo + ch, v, g.nvalid - ch, (g.ldo & 3) == 0);
-            } else {
-                float* dst = g.cur + (long long)m * g.ldcur + ch;
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    if (ch + r >= g.nvalid) continue;
-                    float ov = y[2 * p][r] + bvv[r];
-                    float gate = sigmoid_clamped_f32(y[2 * p + 1][r] + bgg[r]);
-                    float c = dst[r];
-                    float a = (1.0f - gate) * c;  // highway (stream.go:226-229)
-                    float b = gate * ov;
-                    dst[r] = a + b;
-                }
-            }
+            for (int l = 0; l < 3; l++) a2[l] = *(const v4i*)(np + astep + l * 1024);
+            step(ks + 1, a1, a0, NOPF);
         }
-    } else if constexpr (EPI == EPI_LOGITS) {
-        const int target = (mok && g.tgt) ? g.tgt[m] : -1;
-        // logits of this lane's 32 channels, then (max, first argmax, sum exp) in two passes
-        float bmax = -INFINITY;
-        int bidx = 0x7fffffff;
+        lx_epilogue<EPI>(g, acc, tile * 16, n0, n_tile, lane, row, bias_s);
+        if (next >= t_end) break;
+        tile = next;
+        ap = np;
+        // where the next tile's steps 0 and 1 arrived: (a0, a1), (a1, a2) or (a0, a2) for REM 0, 1, 2
+        if constexpr (REM == 1) {
 #pragma unroll
-        for (int ti = 0; ti < 8; ti++) {
-            const int n = nb + ti * 16;
-            const int nv = g.nvalid - n;
-            const float4 b = *(const float4*)(g.bias + n);
-            const float bb[4] = {b.x, b.y, b.z, b.w};
+            for (int l = 0; l < 3; l++) { a0[l] = a1[l]; a1[l] = a2[l]; }
+        } else if constexpr (REM == 2) {
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                float yy = y[ti][r] + bb[r];
-                if (r >= nv) yy = -INFINITY;
-                y[ti][r] = yy;
-                if (yy > bmax) {  // channels rise with (ti, r): ties keep the first index
-                    bmax = yy;
-                    bidx = n + r;
-                }
-                if (n + r == target) g.tlog[m] = yy;
-            }
-            if (mok && g.out && nv > 0) store4(g.out + (long long)m * g.ldo + n, y[ti], nv, (g.ldo & 3) == 0);
-        }
-        float bsum = 0.0f;
-#pragma unroll
-        for (int ti = 0; ti < 8; ti++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) bsum += __expf(y[ti][r] - bmax);
-        if (bmax == -INFINITY) bsum = 0.0f;  // every channel of this lane is vocabulary padding
-        // the four lane groups interleave channels: combine, the smaller index wins ties
-#pragma unroll
-        for (int o = 16; o <= 32; o <<= 1) {
-            float om = __shfl_xor(bmax, o, 64), os = __shfl_xor(bsum, o, 64);
-            int oi = __shfl_xor(bidx, o, 64);
-            float nm = fmaxf(bmax, om);
-            float ns = (bmax == -INFINITY ? 0.0f : bsum * __expf(bmax - nm)) +
-                       (om == -INFINITY ? 0.0f : os * __expf(om - nm));
-            int ni = (om > bmax) ? oi : (bmax > om) ? bidx : min(bidx, oi);
-            bmax = nm; bsum = ns; bidx = ni;
-        }
-        if (mok && g4 == 0) {
-            float* dst = g.stats + ((long long)m * g.stats_ld + n_tile) * 3;
-            dst[0] = bmax; dst[1] = bsum; dst[2] = __int_as_float(bidx);
+            for (int l = 0; l < 3; l++) a1[l] = a2[l];
         }
     }
 }
@@ -344,18 +570,76 @@ hipError_t launch_lx_t(const GemmArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
+template <int EPI>
+hipError_t launch_slab_t(const GemmArgs& a, hipStream_t stream) {
+    const int nt = a.Np / LX_BN;
+    const int mtiles = (a.M + 15) / 16;
+    if (mtiles == 0) return hipSuccess;
+    const int kc = a.Kp / 64;
+    const int lds = kc * 8192 + LX_BN * 4;
+    // dynamic LDS above the default limit must be allowed once per kernel
+    static const hipError_t attr0 = hipFuncSetAttribute((const void*)gemm_slab_kernel<EPI, 0>,
+                                                        hipFuncAttributeMaxDynamicSharedMemorySize, slab_lds_limit());
+    static const hipError_t attr1 = hipFuncSetAttribute((const void*)gemm_slab_kernel<EPI, 1>,
+                                                        hipFuncAttributeMaxDynamicSharedMemorySize, slab_lds_limit());
+    static const hipError_t attr2 = hipFuncSetAttribute((const void*)gemm_slab_kernel<EPI, 2>,
+                                                        hipFuncAttributeMaxDynamicSharedMemorySize, slab_lds_limit());
+    if (attr0 != hipSuccess) return attr0;
+    if (attr1 != hipSuccess) return attr1;
+    if (attr2 != hipSuccess) return attr2;
+    // runs of R groups of 8 tiles: long enough to amortise the slab copy, short enough to fill the chip
+    const int groups = (mtiles + 7) / 8;
+    const int R = std::max(1, std::min(16, groups * nt / 512));
+    const int run_tiles = 8 * R;
+    const int n_runs = (mtiles + run_tiles - 1) / run_tiles;
+    const int grid = 8 * nt * ((n_runs + 7) / 8);
+    switch (kc % 3) {
+        case 0: hipLaunchKernelGGL((gemm_slab_kernel<EPI, 0>), dim3(grid), dim3(512), lds, stream, a, run_tiles, n_runs); break;
+        case 1: hipLaunchKernelGGL((gemm_slab_kernel<EPI, 1>), dim3(grid), dim3(512), lds, stream, a, run_tiles, n_runs); break;
+        default: hipLaunchKernelGGL((gemm_slab_kernel<EPI, 2>), dim3(grid), dim3(512), lds, stream, a, run_tiles, n_runs); break;
+    }
+    return hipGetLastError();
+}
+
+// Which limb-expanded kernel runs: GEMM_AUTO picks the weight-stationary kernel whenever its slab fits
+// in LDS and the batch is large; the other values force one kernel (parity tests and measurement).
+std::atomic<int> g_gemm_kernel{GEMM_AUTO};
+
+template <int EPI>
+hipError_t launch_any_t(const GemmArgs& a, hipStream_t stream) {
+    const int mode = g_gemm_kernel.load(std::memory_order_relaxed);
+    const bool fits = a.Kp >= 128 && (long long)(a.Kp / 64) * 8192 + LX_BN * 4 <= slab_lds_limit();
+    if (fits && (mode == GEMM_SLAB || (mode == GEMM_AUTO && a.M >= kSlabMinRows))) return launch_slab_t<EPI>(a, stream);
+    return launch_lx_t<EPI>(a, stream);
+}
+
 }  // namespace
+
+int select_gemm_kernel(int kind) {
+    if (kind < GEMM_AUTO || kind > GEMM_SLAB) return -1;
+    return g_gemm_kernel.exchange(kind);
+}
+
+int slab_lds_limit() {
+    static const int limit = [] {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess) return 0;
+        return v;
+    }();
+    return limit;
+}
 
 hipError_t launch_gemm_lx(int epi, const GemmArgs& a, hipStream_t stream) {
     if (a.Np % LX_BN || a.Kp % 64 || a.Kp <= 0 || a.M < 0) return hipErrorInvalidValue;
     switch (epi) {
-        case EPI_F32: return launch_lx_t<EPI_F32>(a, stream);
-        case EPI_LATCH: return launch_lx_t<EPI_LATCH>(a, stream);
-        case EPI_GLU: return launch_lx_t<EPI_GLU>(a, stream);
-        case EPI_HIGHWAY: return launch_lx_t<EPI_HIGHWAY>(a, stream);
-        case EPI_RESID: return launch_lx_t<EPI_RESID>(a, stream);
-        case EPI_LOGITS: return launch_lx_t<EPI_LOGITS>(a, stream);
-        case EPI_PROBS: return launch_lx_t<EPI_PROBS>(a, stream);
+        case EPI_F32: return launch_any_t<EPI_F32>(a, stream);
+        case EPI_LATCH: return launch_any_t<EPI_LATCH>(a, stream);
+        case EPI_GLU: return launch_any_t<EPI_GLU>(a, stream);
+        case EPI_HIGHWAY: return launch_any_t<EPI_HIGHWAY>(a, stream);
+        case EPI_RESID: return launch_any_t<EPI_RESID>(a, stream);
+        case EPI_LOGITS: return launch_any_t<EPI_LOGITS>(a, stream);
+        case EPI_PROBS: return launch_any_t<EPI_PROBS>(a, stream);
         default: return hipErrorInvalidValue;
     }
 }

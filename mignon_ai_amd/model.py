@@ -230,3 +230,13 @@ def quantize_f32(w):
     s = np.zeros(1, np.float32)
     check(lib().mg_quantize_f32(ptr(w), len(w), ptr(q), ptr(s), 0, None))
     return q, np.float32(s[0])
+
+
+def gemm_select(kind: str) -> str:
+    """mg_gemm_select: "auto", "stream" or "slab" limb-expanded GEMM kernel for the whole process.
+    Returns the previous selection."""
+    names = ["auto", "stream", "slab"]
+    prev = lib().mg_gemm_select(names.index(kind))
+    check(prev if prev < 0 else 0)
+    return names[prev]
+

@@ -57,3 +57,12 @@ def test_load_without_device_fails_loudly():
     rc = _lib.lib().mg_model_load(buf, len(data), 0, ctypes.byref(h))
     assert rc == _lib.MG_ERR_DEVICE and not h.value
     assert _lib.lib().mg_last_error()
+
+
+def test_gemm_select_validates():
+    L = _lib.lib()
+    assert L.mg_gemm_select(7) == _lib.MG_ERR_INVALID
+    assert b"mg_gemm_select" in L.mg_last_error()
+    prev = L.mg_gemm_select(_lib.MG_GEMM_SLAB)
+    assert prev in (0, 1, 2)
+    assert L.mg_gemm_select(prev) == _lib.MG_GEMM_SLAB
