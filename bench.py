@@ -158,11 +158,12 @@ def synth_ids(seed, tag, shape, V):
 def run(args):
     import torch
 
-    from mignon_ai_amd import Model, gemm_i8_device, gemm_select, mgnn, quantize_f32, synth
+    from mignon_ai_amd import Model, engine_option, gemm_i8_device, mgnn, quantize_f32, synth
 
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU")
-    gemm_select(args.gemm)
+    engine_option("gemm", args.gemm)
+    engine_option("attention", args.attention)
     torch.cuda.set_device(0)
     # Everything runs on one non-default stream: the engine's launches, its HIP-event kernel timing and
     # the torch events bracketing the timed region.
@@ -280,7 +281,7 @@ def run(args):
                                                                                       key=lambda kv: -kv[1][1])}
         out["wall_s"] = round(wall, 3)
     out["cpu_baseline"] = cpu
-    out["gemm_kernel"] = args.gemm
+    out["kernels"] = {"gemm": args.gemm, "attention": args.attention}
     return out
 
 
@@ -294,7 +295,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--gemm", default="auto", choices=["auto", "stream", "slab"],
-                    help="limb-expanded GEMM kernel (mg_gemm_select); both give identical results")
+                    help="limb-expanded GEMM kernel (mg_engine_option); both give identical results")
+    ap.add_argument("--attention", default="auto", choices=["auto", "exact", "mfma"],
+                    help="attention kernel (mg_engine_option): reference order or matrix cores")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

@@ -136,15 +136,23 @@ int mg_gemm_i8(const int8_t* A, int M, int K, const int8_t* W, int N, const floa
  * half away from zero (w/scale), +-127); an all-zero tensor gets scale 1. */
 int mg_quantize_f32(const float* w, long long n, int8_t* q, float* scale, int flags, void* stream);
 
-/* Engine tuning, no reference counterpart. Selects the limb-expanded GEMM kernel for every model of
- * the process: MG_GEMM_AUTO (default) uses the weight-stationary kernel (weights held in LDS, many
- * token tiles streamed through them) for large batches whose weight slab fits in LDS and the streaming
- * kernel otherwise; MG_GEMM_STREAM and MG_GEMM_SLAB force one of them where it applies. Both give the
- * same results. Returns the previous selection, or MG_ERR_INVALID. */
-#define MG_GEMM_AUTO 0
+/* Engine options, no reference counterpart: where two implementations of a stage exist, which one runs,
+ * for every model of the process. Value 0 (the default) chooses automatically.
+ *   MG_OPT_GEMM_KERNEL: MG_GEMM_STREAM streams weight tiles through LDS per token block;
+ *     MG_GEMM_SLAB holds a weight slab in LDS and streams token tiles through it (used where the slab
+ *     fits). Both give bit-identical results; automatic picks the slab kernel for large batches.
+ *   MG_OPT_ATTENTION_KERNEL: MG_ATTN_EXACT keeps the reference's sequential dot-product and softmax
+ *     order (bit-identical given equal inputs); MG_ATTN_MFMA computes scores and P.V on the matrix
+ *     cores (fp32, other summation order). Automatic picks the matrix cores where they apply (head width
+ *     a multiple of 4 up to 64, attended span up to 64 keys, or longer spans for narrower heads).
+ * value < 0 only reads the option. Returns the previous value, or MG_ERR_INVALID. */
+#define MG_OPT_GEMM_KERNEL 0
+#define MG_OPT_ATTENTION_KERNEL 1
 #define MG_GEMM_STREAM 1
 #define MG_GEMM_SLAB 2
-int mg_gemm_select(int kind);
+#define MG_ATTN_EXACT 1
+#define MG_ATTN_MFMA 2
+int mg_engine_option(int option, int value);
 
 #ifdef __cplusplus
 }

@@ -17,7 +17,9 @@ MG_ERR_DEVICE = -3
 MG_ERR_NOMEM = -4
 MG_ERR_UNSUPPORTED = -5
 MG_PTR_DEVICE = 1
-MG_GEMM_AUTO, MG_GEMM_STREAM, MG_GEMM_SLAB = 0, 1, 2
+MG_OPT_GEMM_KERNEL, MG_OPT_ATTENTION_KERNEL = 0, 1
+MG_GEMM_STREAM, MG_GEMM_SLAB = 1, 2
+MG_ATTN_EXACT, MG_ATTN_MFMA = 1, 2
 
 _vp = ctypes.c_void_p
 _i32p = ctypes.POINTER(ctypes.c_int32)
@@ -63,7 +65,7 @@ SIGNATURES = {
     "mg_sessions_free": (None, [_vp]),
     "mg_gemm_i8": (_int, [_vp, _int, _int, _vp, _int, _vp, _vp, _vp, _int, _vp]),
     "mg_quantize_f32": (_int, [_vp, _ll, _vp, _vp, _int, _vp]),
-    "mg_gemm_select": (_int, [_int]),
+    "mg_engine_option": (_int, [_int, _int]),
 }
 
 _lib = None

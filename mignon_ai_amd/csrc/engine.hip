@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstring>
 #include <memory>
@@ -27,8 +28,21 @@
 #include "gemm.hpp"
 #include "kernels.hpp"
 #include "model_file.hpp"
+#include "options.hpp"
 
 namespace mg {
+
+std::atomic<int> g_options[OPT_COUNT];
+
+int option(int opt) { return (opt >= 0 && opt < OPT_COUNT) ? g_options[opt].load(std::memory_order_relaxed) : 0; }
+
+int set_option(int opt, int value) {
+    if (opt < 0 || opt >= OPT_COUNT) return -1;
+    if (value < 0) return g_options[opt].load();
+    if (value > 2) return -1;
+    return g_options[opt].exchange(value);
+}
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -1068,10 +1082,10 @@ int mg_quantize_f32(const float* w, long long n, int8_t* q, float* scale, int fl
     });
 }
 
-int mg_gemm_select(int kind) {
-    const int prev = select_gemm_kernel(kind);
+int mg_engine_option(int opt, int value) {
+    const int prev = set_option(opt, value);
     if (prev < 0) {
-        g_last_error = "mg_gemm_select: unknown kernel selection " + std::to_string(kind);
+        g_last_error = "mg_engine_option: unknown option " + std::to_string(opt) + " or value " + std::to_string(value);
         return MG_ERR_INVALID;
     }
     return prev;

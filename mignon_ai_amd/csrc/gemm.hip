@@ -21,6 +21,7 @@
 
 #include "common.hpp"
 #include "gemm.hpp"
+#include "options.hpp"
 
 namespace mg {
 
@@ -601,24 +602,16 @@ hipError_t launch_slab_t(const GemmArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// Which limb-expanded kernel runs: GEMM_AUTO picks the weight-stationary kernel whenever its slab fits
-// in LDS and the batch is large; the other values force one kernel (parity tests and measurement).
-std::atomic<int> g_gemm_kernel{GEMM_AUTO};
-
 template <int EPI>
 hipError_t launch_any_t(const GemmArgs& a, hipStream_t stream) {
-    const int mode = g_gemm_kernel.load(std::memory_order_relaxed);
+    // automatic: the weight-stationary kernel whenever its slab fits in LDS and the batch is large
+    const int mode = option(OPT_GEMM_KERNEL);
     const bool fits = a.Kp >= 128 && (long long)(a.Kp / 64) * 8192 + LX_BN * 4 <= slab_lds_limit();
     if (fits && (mode == GEMM_SLAB || (mode == GEMM_AUTO && a.M >= kSlabMinRows))) return launch_slab_t<EPI>(a, stream);
     return launch_lx_t<EPI>(a, stream);
 }
 
 }  // namespace
-
-int select_gemm_kernel(int kind) {
-    if (kind < GEMM_AUTO || kind > GEMM_SLAB) return -1;
-    return g_gemm_kernel.exchange(kind);
-}
 
 int slab_lds_limit() {
     static const int limit = [] {

@@ -67,10 +67,8 @@ struct GemmArgs {
     const float* lse = nullptr;       // EPI_PROBS: log-sum-exp per row
 };
 
-// Limb-expanded kernel selection (process-wide): automatic, the streaming kernel, or the
-// weight-stationary kernel wherever its slab fits. Returns the previous selection, or -1.
+// Values of OPT_GEMM_KERNEL.
 enum GemmKernel : int { GEMM_AUTO = 0, GEMM_STREAM = 1, GEMM_SLAB = 2 };
-int select_gemm_kernel(int kind);
 // Token rows from which the weight-stationary kernel is used when its slab fits in LDS.
 constexpr int kSlabMinRows = 8192;
 // Largest dynamic LDS allocation of one workgroup on the current device (bytes).

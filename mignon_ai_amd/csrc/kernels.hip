@@ -5,154 +5,251 @@
 // internal/nn) with the same rounding points; the reduction orders of the reference's AVX2 kernels are
 // reproduced where a result depends on them (RMSNorm's sum of squares, attention dot products, softmax
 // sums, the P.V accumulation), so these stages are bit-identical to the reference given equal inputs.
+#include <algorithm>
+
 #include "common.hpp"
 #include "gemm.hpp"
 #include "kernels.hpp"
+#include "options.hpp"
 
 namespace mg {
 
 namespace {
 
 // ------------------------------------------------------------------------------------------------
-// Row kernel: one workgroup per 16-token tile (one fragment row block of the GEMM operand layout); each
-// of the 4 waves processes 4 token rows, lane holding elements d = lane + 64*i. Limb bytes are staged
-// in LDS in fragment order and the tile's 3*Dp*16 bytes (contiguous in the layout) are written with
-// 16-byte stores.
+// Row kernel: one workgroup (4 waves) per 16-token tile, i.e. one row block of the GEMM operand layout.
+// Wave w owns rows 4w..4w+3 and processes RB of them at a time with all their loads in flight; lane L
+// holds float4 chunks c = L + 64i (elements 4c..4c+3). RMSNorm's sum of squares follows DotF32's AVX2
+// order: 16 sequential partial sums over 16-element chunks, computed for RB rows at once by 16-lane
+// groups. Limb bytes go to a padded LDS copy of the tile's fragments (one dword per chunk and limb),
+// which is then written out with 16-byte stores.
 // ------------------------------------------------------------------------------------------------
 constexpr int ROW_TILE = 16;
+// LDS staging of one 16-row tile in the fragment layout: each 1 KiB fragment padded to 1088 bytes and
+// each 256-byte column group inside it to 272, so that a wave's dword writes of one row spread over
+// the banks.
+__device__ __forceinline__ int stage_off(int o) { return (o >> 10) * 1088 + ((o >> 8) & 3) * 272 + (o & 255); }
 
-template <int NS>
+template <int NS4>
+constexpr int row_batch() { return NS4 <= 2 ? 4 : (NS4 <= 4 ? 2 : 1); }
+
+template <int NS4>
 __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
-    __shared__ float xsh[4][NS * 64];
-    extern __shared__ __align__(16) int8_t stage[];  // [Dp/64][3][1 KiB] when limbs are written
-    const int w = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int D = a.D, Dp = a.Dp;
+    constexpr int RB = row_batch<NS4>();
+    extern __shared__ __align__(16) int8_t row_smem[];
+    int8_t* smem = row_smem;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int D = a.D, Dp = a.Dp, C4 = Dp >> 2;
     const int m_base = blockIdx.x * ROW_TILE;
-    for (int rr = w; rr < ROW_TILE; rr += 4) {
-        const int m = m_base + rr;
-        const bool valid = m < a.M;
-        float x[NS];
-        if (!valid) {
+    int8_t* stage = smem;
+    const int stage_bytes = a.limbs ? (Dp >> 6) * 3 * 1088 : 0;
+    const int xstride = Dp + 16;
+    float* xs = (float*)(smem + stage_bytes) + w * RB * xstride;
+
+    for (int j0 = 0; j0 < 4; j0 += RB) {
+        float4 x[RB][NS4];
+        int rows[RB];
+        // ---- loads (and the embedding / residual writes) for RB rows. Loads are unconditional, from a
+        // row and column clamped into the arrays, all issued before any is used, and masked afterwards
+        // (a guarded load becomes a branch that waits for it on the spot); stores stay guarded. The mode
+        // is tested once, outside the unrolled loops, so that each mode's loads share one basic block.
+        int mcl[RB];
+        bool okr[RB][NS4];
 #pragma unroll
-            for (int i = 0; i < NS; i++) x[i] = 0.0f;
-        } else if (a.mode == ROW_EMBED) {
-            // quant.Model.appendPosition: clamp the id, dequantise the embedding (stream.go:144-152)
-            int id = a.ids[m];
-            if (id < 0 || id >= a.V) id = 0;
-            const int8_t* e = a.emb + (long long)id * D;
+        for (int j = 0; j < RB; j++) {
+            const int m = m_base + 4 * w + j0 + j;
+            rows[j] = m;
+            mcl[j] = min(m, a.M - 1);
 #pragma unroll
-            for (int i = 0; i < NS; i++) {
-                int d = lane + 64 * i;
-                float v = d < D ? (float)e[d] * a.emb_scale : 0.0f;
-                x[i] = v;
-                if (d < Dp) {
-                    a.cur[(long long)m * Dp + d] = v;
-                    a.block_in[(long long)m * Dp + d] = v;
-                }
-            }
-        } else if (a.mode == ROW_RESID) {
+            for (int i = 0; i < NS4; i++) okr[j][i] = m < a.M && lane + 64 * i < C4;
+        }
+        auto coff = [&](int j, int i) { return (long long)mcl[j] * Dp + 4 * min(lane + 64 * i, C4 - 1); };
+        if (a.mode == ROW_RESID) {
             // inter-block residual: blockIn += cur; cur = blockIn (stream.go:157-163)
+            float4 bi[RB][NS4], cu[RB][NS4];
 #pragma unroll
-            for (int i = 0; i < NS; i++) {
-                int d = lane + 64 * i;
-                float v = 0.0f;
-                if (d < Dp) {
-                    long long o = (long long)m * Dp + d;
-                    v = a.block_in[o] + a.cur[o];
-                    a.block_in[o] = v;
-                    a.cur[o] = v;
+            for (int j = 0; j < RB; j++)
+#pragma unroll
+                for (int i = 0; i < NS4; i++) {
+                    bi[j][i] = *(const float4*)(a.block_in + coff(j, i));
+                    cu[j][i] = *(const float4*)(a.cur + coff(j, i));
                 }
-                x[i] = v;
-            }
-        } else {
-            const float* src = a.src ? a.src : a.cur;
-            int lds = a.src ? a.lds : Dp;
-            long long r = a.row_map ? a.row_map[m] : m;
 #pragma unroll
-            for (int i = 0; i < NS; i++) {
-                int d = lane + 64 * i;
-                x[i] = d < D ? src[r * lds + d] : 0.0f;
+            for (int j = 0; j < RB; j++)
+#pragma unroll
+                for (int i = 0; i < NS4; i++) {
+                    const float4 v = make_float4(bi[j][i].x + cu[j][i].x, bi[j][i].y + cu[j][i].y,
+                                                 bi[j][i].z + cu[j][i].z, bi[j][i].w + cu[j][i].w);
+                    if (okr[j][i]) {
+                        *(float4*)(a.block_in + coff(j, i)) = v;
+                        *(float4*)(a.cur + coff(j, i)) = v;
+                    }
+                    x[j][i] = okr[j][i] ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                }
+        } else if (a.mode == ROW_EMBED) {
+            // quant.Model.appendPosition: clamp the id, dequantise (stream.go:144-152)
+            int id[RB];
+#pragma unroll
+            for (int j = 0; j < RB; j++) {
+                int v = a.ids[mcl[j]];
+                id[j] = (v < 0 || v >= a.V) ? 0 : v;
             }
+            int8_t eb[RB][NS4][4];
+#pragma unroll
+            for (int j = 0; j < RB; j++)
+#pragma unroll
+                for (int i = 0; i < NS4; i++)
+#pragma unroll
+                    for (int k = 0; k < 4; k++)
+                        eb[j][i][k] = a.emb[(long long)id[j] * D + min(4 * min(lane + 64 * i, C4 - 1) + k, D - 1)];
+#pragma unroll
+            for (int j = 0; j < RB; j++)
+#pragma unroll
+                for (int i = 0; i < NS4; i++) {
+                    const int c = lane + 64 * i;
+                    float t[4];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) t[k] = (okr[j][i] && 4 * c + k < D) ? (float)eb[j][i][k] * a.emb_scale : 0.0f;
+                    const float4 v = make_float4(t[0], t[1], t[2], t[3]);
+                    if (okr[j][i]) {
+                        *(float4*)(a.cur + coff(j, i)) = v;
+                        *(float4*)(a.block_in + coff(j, i)) = v;
+                    }
+                    x[j][i] = v;
+                }
+        } else {
+            const float* sp = a.src ? a.src : a.cur;
+            const int lds = a.src ? a.lds : Dp;
+            long long r[RB];
+#pragma unroll
+            for (int j = 0; j < RB; j++) r[j] = a.row_map ? a.row_map[mcl[j]] : mcl[j];
+            float4 raw[RB][NS4];
+#pragma unroll
+            for (int j = 0; j < RB; j++)
+#pragma unroll
+                for (int i = 0; i < NS4; i++) raw[j][i] = *(const float4*)(sp + r[j] * lds + 4 * min(lane + 64 * i, C4 - 1));
+#pragma unroll
+            for (int j = 0; j < RB; j++)
+#pragma unroll
+                for (int i = 0; i < NS4; i++) {
+                    // columns past D (and rows or chunks out of range) read as zero
+                    const int c = lane + 64 * i;
+                    const bool ok = okr[j][i];
+                    float4 v = raw[j][i];
+                    v.x = (ok && 4 * c + 0 < D) ? v.x : 0.0f;
+                    v.y = (ok && 4 * c + 1 < D) ? v.y : 0.0f;
+                    v.z = (ok && 4 * c + 2 < D) ? v.z : 0.0f;
+                    v.w = (ok && 4 * c + 3 < D) ? v.w : 0.0f;
+                    x[j][i] = v;
+                }
         }
 
-        float y[NS];
-        if (a.gamma && valid) {
-            // nn.RMSNormForwardF32 (internal/nn/rmsnorm.go:14-32) with DotF32's AVX2 accumulation:
-            // 16 partial sums (two 8-lane registers) over 16-element chunks, an 8-chunk into the first.
-            float* xs = xsh[w];
+        // ---- RMSNorm (nn.RMSNormForwardF32, internal/nn/rmsnorm.go:14-32)
+        if (a.gamma) {
 #pragma unroll
-            for (int i = 0; i < NS; i++) xs[lane + 64 * i] = x[i];
+            for (int j = 0; j < RB; j++)
+#pragma unroll
+                for (int i = 0; i < NS4; i++) {
+                    const int c = lane + 64 * i;
+                    if (c < C4) *(float4*)(xs + j * xstride + 4 * c) = x[j][i];
+                }
             __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes have landed
             __builtin_amdgcn_wave_barrier();
+            // lane 16j + p: partial sum p of row j, sequential over the 16-element chunks
+            const int jr = lane >> 4, p = lane & 15;
+            const float* xr = xs + (jr < RB ? jr : 0) * xstride;
             float part = 0.0f;
-            const int c16 = D / 16;
-            if (lane < 16) {
+            if (jr < RB) {
+                const int c16 = D >> 4;
+#pragma unroll 8
                 for (int c = 0; c < c16; c++) {
-                    float v = xs[16 * c + lane];
+                    const float v = xr[16 * c + p];
                     part = fmaf(v, v, part);
                 }
-                if (lane < 8 && D - 16 * c16 >= 8) {
-                    float v = xs[16 * c16 + lane];
+                if (p < 8 && D - 16 * c16 >= 8) {
+                    const float v = xr[16 * c16 + p];
                     part = fmaf(v, v, part);
                 }
             }
             float v8[8];
+            const int base = lane & 48;
 #pragma unroll
-            for (int j = 0; j < 8; j++) v8[j] = __shfl(part, j, 64) + __shfl(part, j + 8, 64);
+            for (int q = 0; q < 8; q++) v8[q] = __shfl(part, base + q, 64) + __shfl(part, base + q + 8, 64);
             float ss = hreduce8(v8);
-            for (int e = (D / 8) * 8; e < D; e++) {
-                float t = xs[e];
-                float p = t * t;
-                ss = ss + p;
+            for (int e = (D >> 3) << 3; e < D; e++) {
+                const float t = xr[e];
+                const float pp = t * t;
+                ss = ss + pp;
             }
-            float rms = (float)sqrt((double)(ss / (float)D + 1e-5f));
-            float inv = 1.0f / rms;
+            const float rms = (float)sqrt((double)(ss / (float)D + 1e-5f));
+            const float inv = 1.0f / rms;
 #pragma unroll
-            for (int i = 0; i < NS; i++) {
-                int d = lane + 64 * i;
-                float hat = x[i] * inv;
-                y[i] = d < D ? hat * a.gamma[d] : 0.0f;
-            }
-            __builtin_amdgcn_wave_barrier();  // xs is rewritten by this wave's next row
-        } else {
+            for (int j = 0; j < RB; j++) {
+                const float inv_j = __shfl(inv, 16 * j, 64);
 #pragma unroll
-            for (int i = 0; i < NS; i++) y[i] = x[i];
-        }
-
-        if (a.nout && valid) {
-#pragma unroll
-            for (int i = 0; i < NS; i++) {
-                int d = lane + 64 * i;
-                if (d < Dp) a.nout[(long long)m * Dp + d] = y[i];
-            }
-        }
-        if (a.limbs) {
-            float mx = 0.0f;
-#pragma unroll
-            for (int i = 0; i < NS; i++) mx = fmaxf(mx, fabsf(y[i]));
-            mx = wave_max(mx);
-            float sc, inv;
-            limb_scale(mx, sc, inv);
-            // fragment position of element d = lane + 64 i: K step i, lane (rr + 16 (lane>>4)), byte lane&15
-            const int fo = (rr + 16 * (lane >> 4)) * 16 + (lane & 15);
-#pragma unroll
-            for (int i = 0; i < NS; i++) {
-                if (lane + 64 * i < Dp) {
-                    Limbs L = split_limbs(y[i], inv);
-                    stage[(i * 3 + 0) * 1024 + fo] = L.q0;
-                    stage[(i * 3 + 1) * 1024 + fo] = L.q1;
-                    stage[(i * 3 + 2) * 1024 + fo] = L.q2;
+                for (int i = 0; i < NS4; i++) {
+                    const int c = lane + 64 * i;
+                    const float4 gm = *(const float4*)(a.gamma + 4 * min(c, C4 - 1));
+                    if (c < C4) {
+                        float4 v = x[j][i];
+                        v.x = (v.x * inv_j) * gm.x;
+                        v.y = (v.y * inv_j) * gm.y;
+                        v.z = (v.z * inv_j) * gm.z;
+                        v.w = (v.w * inv_j) * gm.w;
+                        x[j][i] = v;
+                    }
                 }
             }
-            if (lane == 0 && valid) a.lscale[m] = sc;
+            __builtin_amdgcn_wave_barrier();  // xs is rewritten by this wave's next rows
+        }
+
+        // ---- outputs: normalised rows, limb expansion into the staged tile
+#pragma unroll
+        for (int j = 0; j < RB; j++) {
+            const int m = rows[j];
+            const bool valid = m < a.M;
+            if (a.nout && valid) {
+#pragma unroll
+                for (int i = 0; i < NS4; i++) {
+                    const int c = lane + 64 * i;
+                    if (c < C4) *(float4*)(a.nout + (long long)m * Dp + 4 * c) = x[j][i];
+                }
+            }
+            if (a.limbs) {
+                float mx = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NS4; i++)
+                    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(x[j][i].x), fabsf(x[j][i].y)), fmaxf(fabsf(x[j][i].z), fabsf(x[j][i].w))));
+                mx = wave_max(mx);
+                float sc, inv;
+                limb_scale(mx, sc, inv);
+                const int rr = 4 * w + j0 + j;
+#pragma unroll
+                for (int i = 0; i < NS4; i++) {
+                    const int c = lane + 64 * i;
+                    if (c < C4) {
+                        const Limbs l0 = split_limbs(x[j][i].x, inv), l1 = split_limbs(x[j][i].y, inv),
+                                    l2 = split_limbs(x[j][i].z, inv), l3 = split_limbs(x[j][i].w, inv);
+                        // elements 4c..4c+3: K step c>>4, byte 4(c&3) of column group (c>>2)&3, row rr
+                        const int o = (c >> 4) * 3072 + (rr + 16 * ((c >> 2) & 3)) * 16 + 4 * (c & 3);
+                        auto pack = [](int8_t b0, int8_t b1, int8_t b2, int8_t b3) {
+                            return (uint32_t)(uint8_t)b0 | ((uint32_t)(uint8_t)b1 << 8) | ((uint32_t)(uint8_t)b2 << 16) |
+                                   ((uint32_t)(uint8_t)b3 << 24);
+                        };
+                        *(uint32_t*)(stage + stage_off(o)) = pack(l0.q0, l1.q0, l2.q0, l3.q0);
+                        *(uint32_t*)(stage + stage_off(o + 1024)) = pack(l0.q1, l1.q1, l2.q1, l3.q1);
+                        *(uint32_t*)(stage + stage_off(o + 2048)) = pack(l0.q2, l1.q2, l2.q2, l3.q2);
+                    }
+                }
+                if (lane == 0 && valid) a.lscale[m] = sc;
+            }
         }
     }
     if (a.limbs) {
         __syncthreads();
         const int bytes = 3 * Dp * ROW_TILE;  // Dp/64 K steps x 3 limbs x 1 KiB
         int8_t* dst = a.limbs + (long long)blockIdx.x * bytes;
-        for (int o = threadIdx.x * 16; o < bytes; o += 256 * 16) *(v4i*)(dst + o) = *(const v4i*)(stage + o);
+        for (int o = threadIdx.x * 16; o < bytes; o += 256 * 16) *(v4i*)(dst + o) = *(const v4i*)(stage + stage_off(o));
     }
 }
 
@@ -177,7 +274,7 @@ __device__ __forceinline__ void store_x_limbs(int8_t* xl, int m, int d, int Dp, 
 // [n | left | g] (stream.go:180-184, ca.AssembleNeighborhood) is limb-expanded with one scale per row.
 // ------------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void scan_kernel(ScanArgs a) {
-    __shared__ float red[2][16];
+    __shared__ float red[2][16][16];  // [round parity][row][wave] row maxima
     // When sequences start on 16-token tile boundaries, a tile's x limbs (3*Dp/64 K steps x 3 limbs x
     // 1 KiB) are staged here and written with 16-byte stores; otherwise bytes go straight out.
     extern __shared__ __align__(16) int8_t stage[];
@@ -188,50 +285,80 @@ __global__ __launch_bounds__(1024) void scan_kernel(ScanArgs a) {
     const int kc = 3 * Dp / 64;
     const bool staged = (T % 16) == 0;
     const int last = a.lens ? a.lens[b] - 1 : -1;
+    const bool on = d < D;
     float g = 0.0f;
-    for (int t = 0; t < T; t++) {
-        const long long m = (long long)b * T + t;
-        float n = 0.0f, left = 0.0f;
-        if (d < D) {
-            n = a.nf[m * Dp + d];
-            float lam = a.lam[m * Dp + d];
-            if (t >= a.dil) left = a.nf[(m - a.dil) * Dp + d];
-            float p1 = lam * g;
-            float p2 = (1.0f - lam) * n;
-            g = p1 + p2;
-        }
-        float mx = fmaxf(fabsf(n), fmaxf(fabsf(left), fabsf(g)));
-        mx = wave_max(mx);
-        if (lane == 0) red[t & 1][w] = mx;
-        __syncthreads();
-        mx = red[t & 1][0];
-        for (int i = 1; i < nw; i++) mx = fmaxf(mx, red[t & 1][i]);
-        float s, inv;
-        limb_scale(mx, s, inv);
-        if (staged) {
-            const float v[3] = {n, left, g};
-            const int rr = (int)(m & 15);
+    // Rounds of 16 positions: every load of the round is issued first (none depends on the latch),
+    // then the sequential recurrence, then the 16 row maxima together.
+    for (int t0 = 0, par = 0; t0 < T; t0 += 16, par ^= 1) {
+        const int nt = min(16, T - t0);
+        const long long m0 = (long long)b * T + t0;
+        float nv[16], lv[16], lm[16];
+        // unconditional loads from clamped addresses (a guarded load becomes a branch that waits)
+        const int dc = min(d, D - 1);
+        const long long seq0 = (long long)b * T;
 #pragma unroll
-            for (int sg = 0; sg < 3; sg++) {
-                Limbs L = split_limbs(v[sg], inv);
-                const int k = sg * Dp + d;
-                const int o = (k >> 6) * 3 * 1024 + ((rr + 16 * ((k >> 4) & 3)) << 4) + (k & 15);
-                stage[o] = L.q0;
-                stage[o + 1024] = L.q1;
-                stage[o + 2048] = L.q2;
-            }
-            if (rr == 15) {
-                __syncthreads();
-                const int bytes = kc * 3 * 1024;
-                int8_t* dst = a.xl + (m >> 4) * (long long)bytes;
-                for (int o = d * 16; o < bytes; o += blockDim.x * 16) *(v4i*)(dst + o) = *(const v4i*)(stage + o);
-                __syncthreads();
-            }
-        } else {
-            store_x_limbs(a.xl, (int)m, d, Dp, kc, n, left, g, inv);
+        for (int k = 0; k < 16; k++) {
+            const long long m = seq0 + min(t0 + k, T - 1);
+            const long long ml = seq0 + max(min(t0 + k, T - 1) - a.dil, 0);
+            const float n_ = a.nf[m * Dp + dc], l_ = a.lam[m * Dp + dc], left_ = a.nf[ml * Dp + dc];
+            nv[k] = on ? n_ : 0.0f;
+            lm[k] = on ? l_ : 0.0f;
+            lv[k] = (on && t0 + k >= a.dil) ? left_ : 0.0f;
         }
-        if (d == 0) a.xs[m] = s;
-        if (t == last && a.g_out) a.g_out[(long long)b * Dp + d] = g;
+        float gv[16], mx[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            if (on && k < nt) {
+                const float p1 = lm[k] * g;  // updateLatch (stream.go:195-205)
+                const float p2 = (1.0f - lm[k]) * nv[k];
+                g = p1 + p2;
+            }
+            gv[k] = on ? g : 0.0f;
+            mx[k] = fmaxf(fabsf(nv[k]), fmaxf(fabsf(lv[k]), fabsf(gv[k])));
+            if (t0 + k == last && a.g_out && on) a.g_out[(long long)b * Dp + d] = gv[k];
+        }
+#pragma unroll
+        for (int k = 0; k < 16; k++) mx[k] = wave_max(mx[k]);
+        if (lane == 0) {
+#pragma unroll
+            for (int k = 0; k < 16; k++) red[par][k][w] = mx[k];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            float v = red[par][k][0];
+            for (int i = 1; i < nw; i++) v = fmaxf(v, red[par][k][i]);
+            mx[k] = v;
+        }
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            if (k >= nt) break;
+            const long long m = m0 + k;
+            float sc, inv;
+            limb_scale(mx[k], sc, inv);
+            if (staged) {
+                const float v[3] = {nv[k], lv[k], gv[k]};
+#pragma unroll
+                for (int sg = 0; sg < 3; sg++) {
+                    Limbs L = split_limbs(v[sg], inv);
+                    const int kk = sg * Dp + d;
+                    const int o = (kk >> 6) * 3 * 1024 + ((k + 16 * ((kk >> 4) & 3)) << 4) + (kk & 15);
+                    stage[o] = L.q0;
+                    stage[o + 1024] = L.q1;
+                    stage[o + 2048] = L.q2;
+                }
+            } else {
+                store_x_limbs(a.xl, (int)m, d, Dp, kc, nv[k], lv[k], gv[k], inv);
+            }
+            if (d == 0) a.xs[m] = sc;
+        }
+        if (staged) {
+            __syncthreads();
+            const int bytes = kc * 3 * 1024;
+            int8_t* dst = a.xl + (m0 >> 4) * (long long)bytes;
+            for (int o = d * 16; o < bytes; o += blockDim.x * 16) *(v4i*)(dst + o) = *(const v4i*)(stage + o);
+            __syncthreads();
+        }
     }
 }
 
@@ -454,6 +581,147 @@ __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
     }
 }
 
+// ------------------------------------------------------------------------------------------------
+// Windowed attention on the matrix cores (v_mfma_f32_16x16x4f32). One wave per 16-query tile of one
+// (sequence, head); four consecutive tiles per workgroup share keys and values through L1.
+//
+// Scores are computed transposed, S^T = K Q^T, so that afterwards lane L holds the scores of query
+// t0 + (L & 15) against keys jb + 4(L >> 4) + r of each 16-key block: exactly the A operand that P.V
+// needs (the K dimension of each P.V step is the four keys {jb + 4g + r}), so P never leaves registers.
+// The head dimension is consumed in the order 16g + 4(L >> 4) + s, which makes every Q and K operand one
+// float4 load; dimensions past dh are zero. Masking, the scale (float32(1/sqrt(dh))), the max-shifted
+// exponentials (the reference's FastExp), 1/sum and p = e*inv follow nn.SoftmaxInPlaceF32; only the
+// summation order of the dot products and of the softmax sum differ from the sequential reference.
+// ------------------------------------------------------------------------------------------------
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+template <int ND, int NKB>
+__global__ __launch_bounds__(256) void attention_mfma_kernel(AttnArgs a, int dh) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int T = a.T, D = a.D, cap = a.cap, ld = 3 * D;
+    const int qtiles = (T + 15) >> 4;
+    const int groups = (qtiles + 3) >> 2;
+    const int b = blockIdx.x / groups;
+    const int tile = (blockIdx.x % groups) * 4 + w;
+    const int h = blockIdx.y;
+    if (tile >= qtiles) return;  // no workgroup barrier below
+    const int t0 = tile * 16;
+    const int qi = lane & 15, kg = lane >> 4;
+    const float* seq = a.qkv + (long long)b * T * ld;
+    const float* qb = seq + h * dh;
+    const float* kb_ = seq + D + h * dh;
+    const float* vb = seq + 2 * D + h * dh;
+    const float scale = (float)(1.0 / sqrt((double)dh));
+
+    // Every load below is unconditional, from an address clamped into the sequence and the head, and
+    // masked afterwards: a guarded load would become a branch that waits for it on the spot.
+    const v4f zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    // Q^T operand: query t0 + qi, dims 16g + 4kg .. +3
+    v4f qv[ND];
+    {
+        const int t = min(t0 + qi, T - 1);
+#pragma unroll
+        for (int g = 0; g < ND; g++) {
+            const int d = 16 * g + 4 * kg;
+            qv[g] = *(const v4f*)(qb + (long long)t * ld + min(d, dh - 4)) * (d < dh ? 1.0f : 0.0f);
+        }
+    }
+    // key blocks [jstart + 16kb, +16) cover every key any query of the tile attends
+    const int jstart = t0 + 16 - 16 * NKB;
+    v4f kv[NKB][ND];
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++) {
+        const int j = jstart + 16 * kb + qi;
+        const bool kok = j >= 0;
+        const float* kp = kb_ + (long long)min(max(j, 0), T - 1) * ld;
+#pragma unroll
+        for (int g = 0; g < ND; g++) {
+            const int d = 16 * g + 4 * kg;
+            kv[kb][g] = *(const v4f*)(kp + min(d, dh - 4)) * ((kok && d < dh) ? 1.0f : 0.0f);
+        }
+    }
+    // values: B operand of P.V, key jstart + 16kb + 4kg + r, dim 16g + qi
+    float vv[NKB][4][ND];
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int j = jstart + 16 * kb + 4 * kg + r;
+            const float* vp = vb + (long long)min(max(j, 0), T - 1) * ld;
+#pragma unroll
+            for (int g = 0; g < ND; g++) {
+                const int d = 16 * g + qi;
+                // a multiply, not a select: clamped addresses hold finite activations, and the compiler
+                // would turn a select of a load back into a branch around the load
+                vv[kb][r][g] = vp[min(d, dh - 1)] * ((j >= 0 && d < dh) ? 1.0f : 0.0f);
+            }
+        }
+    // every load above is issued before the first MFMA waits (where the registers allow it)
+    if constexpr (NKB * ND <= 20) __builtin_amdgcn_sched_barrier(0);
+    v4f s[NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++) {
+        s[kb] = zero4;
+#pragma unroll
+        for (int g = 0; g < ND; g++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) s[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[kb][g][e], qv[g][e], s[kb], 0, 0, 0);
+    }
+    // s[kb][r] = q.k for query t = t0 + qi, key j = jstart + 16kb + 4kg + r
+    const int t = t0 + qi;
+    const int lo = max(window_start(t, a.window), t - cap + 1);
+    float mx = -3.40282347e38f;
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int j = jstart + 16 * kb + 4 * kg + r;
+            const float v = s[kb][r] * scale;
+            s[kb][r] = v;
+            if (j >= lo && j <= t && v > mx) mx = v;
+        }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float sum = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int j = jstart + 16 * kb + 4 * kg + r;
+            const float e = (j >= lo && j <= t) ? fast_exp_ref(s[kb][r] - mx) : 0.0f;
+            s[kb][r] = e;
+            sum += e;
+        }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    const float inv = 1.0f / sum;
+
+    // out = P V: A = P (query qi, key jb + 4kg + r), B = V (key jb + 4kg + r, dim 16g + qi)
+    v4f o[ND];
+#pragma unroll
+    for (int g = 0; g < ND; g++) o[g] = zero4;
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float p = s[kb][r] * inv;
+#pragma unroll
+            for (int g = 0; g < ND; g++) o[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(p, vv[kb][r][g], o[g], 0, 0, 0);
+        }
+    // o[g][r] = out[query t0 + 4kg + r][dim 16g + qi]
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int tq = t0 + 4 * kg + r;
+        if (tq >= T) continue;
+        float* dst = a.att + ((long long)b * T + tq) * a.Dp + h * dh;
+#pragma unroll
+        for (int g = 0; g < ND; g++) {
+            const int d = 16 * g + qi;
+            if (d < dh) dst[d] = o[g][r];
+        }
+    }
+}
+
 // One wavefront per (session, head): lane j scores key j of the ring, lane i accumulates output i.
 template <int DH>
 __global__ __launch_bounds__(64) void attention_step_kernel(AttnStepArgs a) {
@@ -635,9 +903,59 @@ hipError_t attn_t(const AttnArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+template <int ND, int NKB>
+hipError_t attn_mfma_t(const AttnArgs& a, int dh, hipStream_t s) {
+    const int qtiles = (a.T + 15) / 16;
+    const int groups = (qtiles + 3) / 4;
+    hipLaunchKernelGGL((attention_mfma_kernel<ND, NKB>), dim3(a.B * groups, a.heads), dim3(256), 0, s, a, dh);
+    return hipGetLastError();
+}
+
+// Key blocks per 16-query tile: the widest span any query attends is W = min(window, cap) keys, so the
+// tile's keys fit in 1 + ceil((W - 1)/16) blocks of 16. The kernel keeps every block's keys and values
+// in registers, so it runs where ND*NKB <= 20 (head width up to 64 with spans up to 64 keys, narrower
+// heads with longer spans); other shapes take the reference-order kernel.
+int attn_mfma_blocks(const AttnArgs& a) {
+    const int W = a.window > 0 ? std::min(a.window, a.cap) : a.cap;
+    const int nkb = 1 + (W - 1 + 15) / 16;
+    return nkb <= 3 ? 3 : nkb <= 5 ? 5 : nkb <= 9 ? 9 : 17;
+}
+int attn_mfma_nd(int dh) { return dh <= 16 ? 1 : dh <= 32 ? 2 : 4; }
+bool attn_mfma_fits(const AttnArgs& a, int dh) {
+    return dh % 4 == 0 && dh <= 64 && attn_mfma_nd(dh) * attn_mfma_blocks(a) <= 20;
+}
+
+hipError_t attn_mfma(const AttnArgs& a, int dh, hipStream_t s) {
+    switch (attn_mfma_nd(dh) * 100 + attn_mfma_blocks(a)) {
+        case 103: return attn_mfma_t<1, 3>(a, dh, s);
+        case 105: return attn_mfma_t<1, 5>(a, dh, s);
+        case 109: return attn_mfma_t<1, 9>(a, dh, s);
+        case 117: return attn_mfma_t<1, 17>(a, dh, s);
+        case 203: return attn_mfma_t<2, 3>(a, dh, s);
+        case 205: return attn_mfma_t<2, 5>(a, dh, s);
+        case 209: return attn_mfma_t<2, 9>(a, dh, s);
+        case 403: return attn_mfma_t<4, 3>(a, dh, s);
+        case 405: return attn_mfma_t<4, 5>(a, dh, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 template <int DH>
 hipError_t attn_step_t(const AttnStepArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(attention_step_kernel<DH>, dim3(a.S * a.heads), dim3(64), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int NS4>
+hipError_t row_t(const RowArgs& a, hipStream_t s) {
+    const int tiles = (a.M + ROW_TILE - 1) / ROW_TILE;
+    const size_t lds = (a.limbs ? (size_t)(a.Dp / 64) * 3 * 1088 : 0) +
+                       (a.gamma ? (size_t)4 * row_batch<NS4>() * (a.Dp + 16) * sizeof(float) : 0);
+    static const hipError_t attr =
+        hipFuncSetAttribute((const void*)row_kernel<NS4>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return attr;
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(row_kernel<NS4>, dim3(tiles), dim3(256), lds, s, a);
     return hipGetLastError();
 }
 
@@ -645,20 +963,17 @@ hipError_t attn_step_t(const AttnStepArgs& a, hipStream_t s) {
 
 hipError_t launch_row(const RowArgs& a, hipStream_t s) {
     if (a.M <= 0) return hipSuccess;
-    const int ns = a.Dp / 64;
-    if (a.Dp % 64 || ns < 1 || ns > 32) return hipErrorInvalidValue;
-    const int tiles = (a.M + ROW_TILE - 1) / ROW_TILE;
-    const size_t stage = a.limbs ? (size_t)3 * a.Dp * ROW_TILE : 0;
-#define ROW_CASE(N) \
-    case N: hipLaunchKernelGGL(row_kernel<N>, dim3(tiles), dim3(256), stage, s, a); break;
-    switch (ns) {
-        ROW_CASE(1) ROW_CASE(2) ROW_CASE(3) ROW_CASE(4) ROW_CASE(5) ROW_CASE(6) ROW_CASE(7) ROW_CASE(8)
-        ROW_CASE(9) ROW_CASE(10) ROW_CASE(11) ROW_CASE(12) ROW_CASE(13) ROW_CASE(14) ROW_CASE(15) ROW_CASE(16)
-        ROW_CASE(17) ROW_CASE(18) ROW_CASE(19) ROW_CASE(20) ROW_CASE(21) ROW_CASE(22) ROW_CASE(23) ROW_CASE(24)
-        ROW_CASE(25) ROW_CASE(26) ROW_CASE(27) ROW_CASE(28) ROW_CASE(29) ROW_CASE(30) ROW_CASE(31) ROW_CASE(32)
+    if (a.Dp % 64 || a.Dp < 64 || a.Dp > 2048) return hipErrorInvalidValue;
+    switch ((a.Dp + 255) / 256) {
+        case 1: return row_t<1>(a, s);
+        case 2: return row_t<2>(a, s);
+        case 3: return row_t<3>(a, s);
+        case 4: return row_t<4>(a, s);
+        case 5: return row_t<5>(a, s);
+        case 6: return row_t<6>(a, s);
+        case 7: return row_t<7>(a, s);
+        default: return row_t<8>(a, s);
     }
-#undef ROW_CASE
-    return hipGetLastError();
 }
 
 hipError_t launch_scan(const ScanArgs& a, hipStream_t s) {
@@ -699,7 +1014,10 @@ hipError_t launch_latch_step(const LatchStepArgs& a, hipStream_t s) {
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
     if (a.B <= 0 || a.T <= 0) return hipSuccess;
     if (a.heads <= 0 || a.D % a.heads || a.cap <= 0 || a.cap > 256) return hipErrorInvalidValue;
-    DH_SWITCH(a.D / a.heads, attn_t, a, s)
+    const int dh = a.D / a.heads;
+    const int mode = option(OPT_ATTENTION_KERNEL);
+    if (mode != ATTN_EXACT && attn_mfma_fits(a, dh)) return attn_mfma(a, dh, s);
+    DH_SWITCH(dh, attn_t, a, s)
 }
 
 hipError_t launch_attention_step(const AttnStepArgs& a, hipStream_t s) {

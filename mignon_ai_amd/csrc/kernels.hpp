@@ -8,6 +8,9 @@ namespace mg {
 
 enum RowMode : int { ROW_SRC = 0, ROW_EMBED = 1, ROW_RESID = 2 };
 
+// Values of OPT_ATTENTION_KERNEL.
+enum AttnKernel : int { ATTN_AUTO = 0, ATTN_EXACT = 1, ATTN_MFMA = 2 };
+
 struct RowArgs {
     int M = 0, D = 0, Dp = 0;
     int mode = ROW_SRC;

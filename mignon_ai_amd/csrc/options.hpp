@@ -1,0 +1,18 @@
+// Process-wide engine options: which implementation runs where two exist.
+#pragma once
+
+namespace mg {
+
+enum Option : int {
+    OPT_GEMM_KERNEL = 0,       // 0 automatic, 1 streaming, 2 weight-stationary
+    OPT_ATTENTION_KERNEL = 1,  // 0 automatic, 1 reference order (VALU), 2 matrix cores
+    OPT_COUNT
+};
+
+// Current value of an option.
+int option(int opt);
+// Sets an option (value < 0 only reads it); returns the previous value, or -1 for an unknown option or
+// value.
+int set_option(int opt, int value);
+
+}  // namespace mg

@@ -232,11 +232,14 @@ def quantize_f32(w):
     return q, np.float32(s[0])
 
 
-def gemm_select(kind: str) -> str:
-    """mg_gemm_select: "auto", "stream" or "slab" limb-expanded GEMM kernel for the whole process.
-    Returns the previous selection."""
-    names = ["auto", "stream", "slab"]
-    prev = lib().mg_gemm_select(names.index(kind))
+_OPTIONS = {"gemm": (0, ["auto", "stream", "slab"]), "attention": (1, ["auto", "exact", "mfma"])}
+
+
+def engine_option(name: str, value: str | None = None) -> str:
+    """mg_engine_option: which implementation runs for "gemm" ("auto", "stream", "slab") or "attention"
+    ("auto", "exact", "mfma"), for the whole process. Returns the previous value (value None only
+    reads it)."""
+    opt, names = _OPTIONS[name]
+    prev = lib().mg_engine_option(opt, -1 if value is None else names.index(value))
     check(prev if prev < 0 else 0)
     return names[prev]
-

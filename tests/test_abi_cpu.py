@@ -59,10 +59,13 @@ def test_load_without_device_fails_loudly():
     assert _lib.lib().mg_last_error()
 
 
-def test_gemm_select_validates():
+def test_engine_option_validates():
     L = _lib.lib()
-    assert L.mg_gemm_select(7) == _lib.MG_ERR_INVALID
-    assert b"mg_gemm_select" in L.mg_last_error()
-    prev = L.mg_gemm_select(_lib.MG_GEMM_SLAB)
-    assert prev in (0, 1, 2)
-    assert L.mg_gemm_select(prev) == _lib.MG_GEMM_SLAB
+    assert L.mg_engine_option(7, 0) == _lib.MG_ERR_INVALID
+    assert b"mg_engine_option" in L.mg_last_error()
+    assert L.mg_engine_option(_lib.MG_OPT_GEMM_KERNEL, 3) == _lib.MG_ERR_INVALID
+    for opt, val in ((_lib.MG_OPT_GEMM_KERNEL, _lib.MG_GEMM_SLAB), (_lib.MG_OPT_ATTENTION_KERNEL, _lib.MG_ATTN_EXACT)):
+        prev = L.mg_engine_option(opt, val)
+        assert prev in (0, 1, 2)
+        assert L.mg_engine_option(opt, -1) == val
+        assert L.mg_engine_option(opt, prev) == val

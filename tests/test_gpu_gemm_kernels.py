@@ -7,22 +7,22 @@ import numpy as np
 import pytest
 
 from helpers import GOLDEN, assert_close, model_bytes, oracle_model, tiny_spec, uniform_model_bytes
-from mignon_ai_amd import Model, gemm_select, synth
+from mignon_ai_amd import Model, engine_option, synth
 
 pytestmark = pytest.mark.gpu
 
 
 @pytest.fixture
 def restore_selection():
-    prev = gemm_select("auto")
+    prev = engine_option("gemm", "auto")
     yield
-    gemm_select(prev)
+    engine_option("gemm", prev)
 
 
 def _both(m, ids, **kw):
-    gemm_select("stream")
+    engine_option("gemm", "stream")
     a = m.forward_batch(ids, **kw)
-    gemm_select("slab")
+    engine_option("gemm", "slab")
     b = m.forward_batch(ids, **kw)
     return a, b
 
@@ -76,8 +76,8 @@ def test_kernels_identical_c3_batch(restore_selection):
 def test_sessions_identical(restore_selection):
     data = model_bytes("c4")
     prompts = synth.token_ids(25, "kern-c4", (64, 9), 4096)
-    gemm_select("stream")
+    engine_option("gemm", "stream")
     i1, p1 = Model(data).sessions(64).decode_greedy(prompts, 6)
-    gemm_select("slab")
+    engine_option("gemm", "slab")
     i2, p2 = Model(data).sessions(64).decode_greedy(prompts, 6)
     assert np.array_equal(i1, i2) and np.array_equal(p1, p2)
