@@ -75,10 +75,48 @@ __device__ __forceinline__ EpiRow epi_row(const GemmArgs& g, int m) {
     return e;
 }
 
+// Staged output (STG): a wave's 16 x 128 fp32 output tile is written to its LDS region (row stride
+// STG_LD floats: rows start 4 banks apart, so the 16 rows of one column group hit distinct banks) and
+// then stored as rows, two 512-byte row segments per store instruction, instead of sixteen 64-byte
+// pieces: far fewer cache lines per instruction for the address unit.
+constexpr int STG_LD = 132;
+constexpr int STG_BYTES = 8 * 16 * STG_LD * 4;  // eight waves
+
+__device__ __forceinline__ void stg_put(float* stg, int lane, int ti, const float v[4]) {
+    *(float4*)(stg + (lane & 15) * STG_LD + 16 * ti + 4 * (lane >> 4)) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// Rows mt0..mt0+15, channels n0 + [0, 128) of `out` (row stride ldo) from the staged tile.
+__device__ __forceinline__ void stg_flush(const GemmArgs& g, const float* stg, int lane, int mt0, int n0, float* out,
+                                          long long ldo) {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes have landed
+    __builtin_amdgcn_wave_barrier();
+    const int c = 4 * (lane & 31);
+    const int nv = g.nvalid - n0 - c;  // valid channels from this lane's column on
+    const bool vec = nv >= 4 && (ldo & 3) == 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int row = (lane >> 5) + 2 * k;
+        const int m = mt0 + row;
+        const float4 v = *(const float4*)(stg + row * STG_LD + c);
+        if (m < g.M && nv > 0) {
+            float* dst = out + (long long)m * ldo + n0 + c;
+            if (vec) {
+                *(float4*)dst = v;
+            } else {
+                const float t[4] = {v.x, v.y, v.z, v.w};
+                for (int r = 0; r < 4 && r < nv; r++) dst[r] = t[r];
+            }
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
 // bias_t: the bias of this tile's 128 channels (global memory, or the workgroup's LDS copy).
-template <int EPI>
+// STG: outputs of EPI_F32, EPI_LATCH, EPI_PROBS and EPI_LOGITS go through the wave's LDS region `stg`.
+template <int EPI, bool STG = false>
 __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[3][8], int mt0, int n0, int n_tile,
-                                            int lane, const EpiRow& row, const float* bias_t) {
+                                            int lane, const EpiRow& row, const float* bias_t, float* stg = nullptr) {
     const int g4 = lane >> 4;
     const int m = mt0 + (lane & 15);
     const bool mok = m < g.M;
@@ -87,13 +125,13 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
     const bool vec = (g.ldo & 3) == 0;
 
     if constexpr (EPI == EPI_F32 || EPI == EPI_LATCH) {
-        if (!mok) return;
+        if (!STG && !mok) return;
         float* orow = g.out + (long long)m * g.ldo;
 #pragma unroll
         for (int ti = 0; ti < 8; ti++) {
             const int n = nb + ti * 16;
             const int nv = g.nvalid - n;
-            if (nv <= 0) continue;
+            if (!STG && nv <= 0) continue;
             float v[4];
             if constexpr (EPI == EPI_LATCH) {
                 const float4 b = *(const float4*)(bias_t + 4 * g4 + ti * 16);
@@ -104,8 +142,10 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
 #pragma unroll
                 for (int r = 0; r < 4; r++) v[r] = limb_dot(acc, ti, r) * sw;
             }
-            store4(orow + n, v, nv, vec);
+            if constexpr (STG) stg_put(stg, lane, ti, v);
+            else store4(orow + n, v, nv, vec);
         }
+        if constexpr (STG) stg_flush(g, stg, lane, mt0, n0, g.out, g.ldo);
     } else if constexpr (EPI == EPI_RESID) {
         // cur += x.w: all eight row segments are loaded before any is needed (one memory latency)
         if (!mok) return;
@@ -136,7 +176,7 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
         }
     } else if constexpr (EPI == EPI_PROBS) {
         // p = exp(l - lse) = 2^(x.w*log2e + (b - lse)*log2e)
-        if (!mok) return;
+        if (!STG && !mok) return;
         const float l2e = 1.4426950408889634f;
         const float swl = sw * l2e, lsel = row.lse * l2e;
         float* orow = g.out + (long long)m * g.ldo;
@@ -144,14 +184,16 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
         for (int ti = 0; ti < 8; ti++) {
             const int n = nb + ti * 16;
             const int nv = g.nvalid - n;
-            if (nv <= 0) continue;
+            if (!STG && nv <= 0) continue;
             const float4 b = *(const float4*)(bias_t + 4 * g4 + ti * 16);
             const float bb[4] = {b.x, b.y, b.z, b.w};
             float v[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) v[r] = __builtin_amdgcn_exp2f(fmaf(limb_dot(acc, ti, r), swl, fmaf(bb[r], l2e, -lsel)));
-            store4(orow + n, v, nv, vec);
+            if constexpr (STG) stg_put(stg, lane, ti, v);
+            else store4(orow + n, v, nv, vec);
         }
+        if constexpr (STG) stg_flush(g, stg, lane, mt0, n0, g.out, g.ldo);
     } else if constexpr (EPI == EPI_GLU || EPI == EPI_HIGHWAY) {
         // W rows are reordered in blocks of 32: 16 value rows then the 16 matching gate rows, so tile
         // pair (2p, 2p+1) holds value and gate of output channel n0/2 + 16p + 4*(L >> 4) + r.
@@ -222,7 +264,9 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
             float y[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) y[r] = fmaf(limb_dot(acc, ti, r), sw, bb[r]);
-            if (orow && mok) {
+            if constexpr (STG) {
+                if (orow) stg_put(stg, lane, ti, y);
+            } else if (orow && mok) {
                 const int nv = g.nvalid - n;
                 if (nv > 0) store4(orow + n, y, nv, vec);
             }
@@ -259,6 +303,9 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
         if (mok && g4 == 0) {
             float* dst = g.stats + ((long long)m * g.stats_ld + n_tile) * 3;
             dst[0] = bmax; dst[1] = bsum; dst[2] = __int_as_float(bidx);
+        }
+        if constexpr (STG) {
+            if (orow) stg_flush(g, stg, lane, mt0, n0, g.out, g.ldo);
         }
     }
 }
@@ -355,12 +402,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // the read-only slab and its own activation fragments straight from global memory, two K steps ahead
 // (three register sets, rotated by unrolling the K loop by three). The prefetch runs across tiles: the
 // last two K steps of a tile fetch the first two steps of the wave's next tile, before the epilogue's
-// stores. REM = kc % 3 fixes at compile time where those land. Two waves per SIMD: one wave's epilogue
+// stores. REM = kc % 3 (3 for kc == 2) fixes at compile time where those land. Two waves per SIMD: one wave's epilogue
 // overlaps the other's MFMAs.
 //
 // Block b -> (XCD b % 8, slot b / 8); slot -> (channel slab slot % nt, run (slot / nt)*8 + XCD), so all
 // slabs of a run execute on one XCD and its activations are fetched from HBM into that XCD's L2 once.
-template <int EPI, int REM>
+template <int EPI, int REM, bool STG>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_slab_kernel(GemmArgs g,
                                                                                                    int run_tiles,
                                                                                                    int n_runs) {
@@ -374,6 +421,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int kc = g.Kp >> 6;
     float* bias_s = (float*)(slab + kc * 8192);
+    float* stg = STG ? (float*)(slab + kc * 8192 + LX_BN * 4) + w * 16 * STG_LD : nullptr;
 
     {
         // slab[ks][ti][1 KiB] <- W fragments (ks, n0/16 + ti): 8 KiB contiguous per K step
@@ -409,14 +457,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int next = tile + 8;
         const int8_t* np = next < t_end ? ap + 8 * tstep : ap;
         v4i acc[3][8];
-#pragma unroll
-        for (int l = 0; l < 3; l++)
-#pragma unroll
-            for (int ti = 0; ti < 8; ti++) acc[l][ti] = v4i{0, 0, 0, 0};
-        // One K step: multiply step ks held in `cur`; with PF, first prefetch step ks+2 (of this tile, or
-        // of the next) into `nxt`. Every path issues the same loads in the same order, so the compiler's
-        // in-order load counting lets each step wait only for the loads two steps back.
-        auto step = [&](int ks, v4i (&cur)[3], v4i (&nxt)[3], auto pf) {
+        // One K step: multiply step ks held in `cur` (the first step of a tile starts from zero); with
+        // PF, first prefetch step ks+2 (of this tile, or of the next) into `nxt`. Every path issues the
+        // same loads in the same order, so the compiler's in-order load counting lets each step wait
+        // only for the loads two steps back.
+        auto step = [&](int ks, v4i (&cur)[3], v4i (&nxt)[3], auto pf, auto first) {
             if constexpr (decltype(pf)::value) {
                 const int8_t* src = ks + 2 < kc ? ap + (ks + 2) * astep : np + (ks + 2 - kc) * astep;
 #pragma unroll
@@ -430,39 +475,53 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             for (int ti = 0; ti < 8; ti++)
 #pragma unroll
                 for (int l = 0; l < 3; l++)
-                    acc[l][ti] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[ti], cur[l], acc[l][ti], 0, 0, 0);
+                    acc[l][ti] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                        wf[ti], cur[l], decltype(first)::value ? v4i{0, 0, 0, 0} : acc[l][ti], 0, 0, 0);
             // order: the step's global prefetches, its eight LDS reads, then the MFMAs
             if constexpr (decltype(pf)::value) __builtin_amdgcn_sched_group_barrier(0x020, 3, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, 24, 0);
         };
-        constexpr std::true_type PF{};
-        constexpr std::false_type NOPF{};
-        int ks = 0;
-        for (; ks + 3 <= kc; ks += 3) {
-            step(ks, a0, a2, PF);
-            step(ks + 1, a1, a0, PF);
-            step(ks + 2, a2, a1, PF);
-        }
-        if constexpr (REM == 1) step(ks, a0, a2, PF);
-        if constexpr (REM == 2) {
-            // a0 (after this step) and a2 are free for the next tile's first two steps
-            step(ks, a0, a2, NOPF);
+        constexpr std::true_type YES{};
+        constexpr std::false_type NO{};
+        if constexpr (REM == 3) {
+            // kc == 2: a2 is free, and a0 once step 0 is done
+            step(0, a0, a2, NO, YES);
 #pragma unroll
             for (int l = 0; l < 3; l++) a0[l] = *(const v4i*)(np + l * 1024);
 #pragma unroll
             for (int l = 0; l < 3; l++) a2[l] = *(const v4i*)(np + astep + l * 1024);
-            step(ks + 1, a1, a0, NOPF);
+            step(1, a1, a0, NO, NO);
+        } else {
+            step(0, a0, a2, YES, YES);  // kc >= 3
+            step(1, a1, a0, YES, NO);
+            step(2, a2, a1, YES, NO);
+            int ks = 3;
+            for (; ks + 3 <= kc; ks += 3) {
+                step(ks, a0, a2, YES, NO);
+                step(ks + 1, a1, a0, YES, NO);
+                step(ks + 2, a2, a1, YES, NO);
+            }
+            if constexpr (REM == 1) step(ks, a0, a2, YES, NO);
+            if constexpr (REM == 2) {
+                // a0 (after this step) and a2 are free for the next tile's first two steps
+                step(ks, a0, a2, NO, NO);
+#pragma unroll
+                for (int l = 0; l < 3; l++) a0[l] = *(const v4i*)(np + l * 1024);
+#pragma unroll
+                for (int l = 0; l < 3; l++) a2[l] = *(const v4i*)(np + astep + l * 1024);
+                step(ks + 1, a1, a0, NO, NO);
+            }
         }
-        lx_epilogue<EPI>(g, acc, tile * 16, n0, n_tile, lane, row, bias_s);
+        lx_epilogue<EPI, STG>(g, acc, tile * 16, n0, n_tile, lane, row, bias_s, stg);
         if (next >= t_end) break;
         tile = next;
         ap = np;
-        // where the next tile's steps 0 and 1 arrived: (a0, a1), (a1, a2) or (a0, a2) for REM 0, 1, 2
+        // where the next tile's steps 0 and 1 arrived: (a0, a1), (a1, a2) or (a0, a2) for REM 0, 1, 2 (3)
         if constexpr (REM == 1) {
 #pragma unroll
             for (int l = 0; l < 3; l++) { a0[l] = a1[l]; a1[l] = a2[l]; }
-        } else if constexpr (REM == 2) {
+        } else if constexpr (REM >= 2) {
 #pragma unroll
             for (int l = 0; l < 3; l++) a1[l] = a2[l];
         }
@@ -571,35 +630,52 @@ hipError_t launch_lx_t(const GemmArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
+template <int EPI, int REM, bool STG>
+hipError_t slab_launch(const GemmArgs& a, int grid, int lds, int run_tiles, int n_runs, hipStream_t stream) {
+    // dynamic LDS above the default limit must be allowed once per kernel
+    static const hipError_t attr = hipFuncSetAttribute((const void*)gemm_slab_kernel<EPI, REM, STG>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, slab_lds_limit());
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL((gemm_slab_kernel<EPI, REM, STG>), dim3(grid), dim3(512), lds, stream, a, run_tiles, n_runs);
+    return hipGetLastError();
+}
+
+template <int EPI>
+constexpr bool can_stage() { return EPI == EPI_F32 || EPI == EPI_LATCH || EPI == EPI_PROBS || EPI == EPI_LOGITS; }
+
 template <int EPI>
 hipError_t launch_slab_t(const GemmArgs& a, hipStream_t stream) {
     const int nt = a.Np / LX_BN;
     const int mtiles = (a.M + 15) / 16;
     if (mtiles == 0) return hipSuccess;
     const int kc = a.Kp / 64;
-    const int lds = kc * 8192 + LX_BN * 4;
-    // dynamic LDS above the default limit must be allowed once per kernel
-    static const hipError_t attr0 = hipFuncSetAttribute((const void*)gemm_slab_kernel<EPI, 0>,
-                                                        hipFuncAttributeMaxDynamicSharedMemorySize, slab_lds_limit());
-    static const hipError_t attr1 = hipFuncSetAttribute((const void*)gemm_slab_kernel<EPI, 1>,
-                                                        hipFuncAttributeMaxDynamicSharedMemorySize, slab_lds_limit());
-    static const hipError_t attr2 = hipFuncSetAttribute((const void*)gemm_slab_kernel<EPI, 2>,
-                                                        hipFuncAttributeMaxDynamicSharedMemorySize, slab_lds_limit());
-    if (attr0 != hipSuccess) return attr0;
-    if (attr1 != hipSuccess) return attr1;
-    if (attr2 != hipSuccess) return attr2;
+    int lds = kc * 8192 + LX_BN * 4;
+    const bool stg = can_stage<EPI>() && lds + STG_BYTES <= slab_lds_limit();
+    if (stg) lds += STG_BYTES;
     // runs of R groups of 8 tiles: long enough to amortise the slab copy, short enough to fill the chip
     const int groups = (mtiles + 7) / 8;
     const int R = std::max(1, std::min(16, groups * nt / 512));
     const int run_tiles = 8 * R;
     const int n_runs = (mtiles + run_tiles - 1) / run_tiles;
     const int grid = 8 * nt * ((n_runs + 7) / 8);
-    switch (kc % 3) {
-        case 0: hipLaunchKernelGGL((gemm_slab_kernel<EPI, 0>), dim3(grid), dim3(512), lds, stream, a, run_tiles, n_runs); break;
-        case 1: hipLaunchKernelGGL((gemm_slab_kernel<EPI, 1>), dim3(grid), dim3(512), lds, stream, a, run_tiles, n_runs); break;
-        default: hipLaunchKernelGGL((gemm_slab_kernel<EPI, 2>), dim3(grid), dim3(512), lds, stream, a, run_tiles, n_runs); break;
+    // REM = kc % 3 for kc >= 3; 3 marks kc == 2
+    const int rem = kc == 2 ? 3 : kc % 3;
+    if constexpr (can_stage<EPI>()) {
+        if (stg) {
+            switch (rem) {
+                case 0: return slab_launch<EPI, 0, true>(a, grid, lds, run_tiles, n_runs, stream);
+                case 1: return slab_launch<EPI, 1, true>(a, grid, lds, run_tiles, n_runs, stream);
+                case 2: return slab_launch<EPI, 2, true>(a, grid, lds, run_tiles, n_runs, stream);
+                default: return slab_launch<EPI, 3, true>(a, grid, lds, run_tiles, n_runs, stream);
+            }
+        }
     }
-    return hipGetLastError();
+    switch (rem) {
+        case 0: return slab_launch<EPI, 0, false>(a, grid, lds, run_tiles, n_runs, stream);
+        case 1: return slab_launch<EPI, 1, false>(a, grid, lds, run_tiles, n_runs, stream);
+        case 2: return slab_launch<EPI, 2, false>(a, grid, lds, run_tiles, n_runs, stream);
+        default: return slab_launch<EPI, 3, false>(a, grid, lds, run_tiles, n_runs, stream);
+    }
 }
 
 template <int EPI>
