@@ -55,7 +55,16 @@ def cpu_threads():
     return max(1, min(16, os.cpu_count() or 1))
 
 
-def roofline_for(prof, work_per_step, steps):
+def measured_traffic(config, cls):
+    """HBM bytes per launch of a kernel class, from the committed rocprofv3 counter summary of this
+    configuration (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel's ratio; see that file's commands)."""
+    from mignon_ai_amd.profsum import traffic_for
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"{config}_hbm_traffic.md")
+    v = traffic_for(path, cls)
+    return (None, None) if v is None else (round(v), f"profiles/{config}_hbm_traffic.md")
+
+
+def roofline_for(prof, work_per_step, steps, config=None):
     """Dominant kernel class by time; work_per_step maps class -> (bound, algorithmic units per step)."""
     total = {k: v[1] for k, v in prof.items()}
     cands = [k for k in total if k in work_per_step]
@@ -77,6 +86,10 @@ def roofline_for(prof, work_per_step, steps):
     r["kernel"] = dom
     r["per_launch"] = per_launch
     r["avg_launch_ms"] = round(ms / launches, 4)
+    if config:
+        r["traffic"], src = measured_traffic(config, dom)
+        if src:
+            r["traffic_source"] = src
     return dom, r
 
 
@@ -98,26 +111,38 @@ def timed(step, warmup, steps, torch, before=None):
     return ev0.elapsed_time(ev1) / steps, wall
 
 
-def cpu_baseline_forward(data, spec, T, seconds, seed):
+def _repeat(fn, seconds):
+    """Runs fn() until at least `seconds` have passed (at least once); returns (passes, elapsed)."""
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds:
+            return n, dt
+
+
+def cpu_baseline_forward(data, spec, B, T, seconds, seed):
     from oracle import oracle as O
     om = O.OracleModel(O.read_model(data))
     thr = cpu_threads()
-    # a first batch sizes the sample so that it takes about `seconds`
-    probe = synth_ids(seed, "cpu-probe", (thr, min(T, 32)), spec.V)
+    # a first batch of full-length sequences sizes the sample (at most the whole workload) so that it
+    # takes about `seconds`; a sample that is the whole workload is repeated to fill that time
+    probe = synth_ids(seed, "cpu-probe", (thr, T), spec.V)
     t0 = time.perf_counter()
     om.forward_all(probe, nthreads=thr)
     rate = probe.size / max(time.perf_counter() - t0, 1e-6)
-    nseq = int(max(thr, min(4096, rate * seconds / T)))
+    nseq = int(max(min(thr, B), min(B, rate * seconds / T)))
     ids = synth_ids(seed, "cpu-sample", (nseq, T), spec.V)
-    t0 = time.perf_counter()
-    om.forward_all(ids, nthreads=thr)
-    dt = time.perf_counter() - t0
-    return {"value": round(ids.size / dt, 1), "unit": "tokens/s", "cores": thr, "kind": "port",
-            "sample": f"{nseq} sequences x {T} tokens, teacher-forced (session route: every position's logits), "
-                      f"{dt:.1f} s; C++ restatement of the reference Go engine with AVX2 dot kernels"}
+    passes, dt = _repeat(lambda: om.forward_all(ids, nthreads=thr), seconds / 2)
+    return {"value": round(passes * ids.size / dt, 1), "unit": "tokens/s", "cores": thr, "kind": "port",
+            "sample": f"{nseq} of {B} sequences x {T} tokens, {passes} pass(es), teacher-forced (session route: "
+                      f"every position's logits), {dt:.1f} s; C++ restatement of the reference Go engine with AVX2 "
+                      f"dot kernels"}
 
 
-def cpu_baseline_decode(data, spec, P, G, seconds, seed):
+def cpu_baseline_decode(data, spec, S, P, G, seconds, seed):
     from oracle import oracle as O
     om = O.OracleModel(O.read_model(data))
     thr = cpu_threads()
@@ -125,14 +150,12 @@ def cpu_baseline_decode(data, spec, P, G, seconds, seed):
     t0 = time.perf_counter()
     om.greedy(probe, 4, nthreads=thr)
     rate = thr * (P + 4) / max(time.perf_counter() - t0, 1e-6)  # positions per second
-    nses = int(max(thr, min(4096, rate * seconds / (P + G))))
+    nses = int(max(min(thr, S), min(S, rate * seconds / (P + G))))
     prompts = synth_ids(seed, "cpu-sample", (nses, P), spec.V)
-    t0 = time.perf_counter()
-    om.greedy(prompts, G, nthreads=thr)
-    dt = time.perf_counter() - t0
-    return {"value": round(nses * G / dt, 1), "unit": "generated tokens/s", "cores": thr, "kind": "port",
-            "sample": f"{nses} sessions x ({P}-token prefill + {G} greedy tokens), {dt:.1f} s; C++ restatement "
-                      f"of the reference Go engine with AVX2 dot kernels"}
+    passes, dt = _repeat(lambda: om.greedy(prompts, G, nthreads=thr), seconds / 2)
+    return {"value": round(passes * nses * G / dt, 1), "unit": "generated tokens/s", "cores": thr, "kind": "port",
+            "sample": f"{nses} of {S} sessions x ({P}-token prefill + {G} greedy tokens), {passes} pass(es), "
+                      f"{dt:.1f} s; C++ restatement of the reference Go engine with AVX2 dot kernels"}
 
 
 def cpu_baseline_gemm(A, W, s, seconds):
@@ -143,11 +166,10 @@ def cpu_baseline_gemm(A, W, s, seconds):
     O.gemm_i8_ref(A[:rows], W, s, nthreads=thr)
     rate = rows / max(time.perf_counter() - t0, 1e-6)
     n = int(min(len(A), max(rows, rate * seconds)))
-    t0 = time.perf_counter()
-    O.gemm_i8_ref(A[:n], W, s, nthreads=thr)
-    dt = time.perf_counter() - t0
-    return {"value": round(n / dt, 1), "unit": "rows/s", "cores": thr, "kind": "port",
-            "sample": f"{n} of {len(A)} rows, {dt:.1f} s; MatVecInt8 per row (DotInt8F32, AVX2) as the reference"}
+    passes, dt = _repeat(lambda: O.gemm_i8_ref(A[:n], W, s, nthreads=thr), seconds / 2)
+    return {"value": round(passes * n / dt, 1), "unit": "rows/s", "cores": thr, "kind": "port",
+            "sample": f"{n} of {len(A)} rows, {passes} pass(es), {dt:.1f} s; MatVecInt8 per row (DotInt8F32, AVX2) "
+                      f"as the reference"}
 
 
 def synth_ids(seed, tag, shape, V):
@@ -195,9 +217,12 @@ def run(args):
         out.update(value=round(M / (ms / 1e3), 1), unit="tokens/s", ms_per_step=round(ms, 4),
                    config={"workload": "c2: INT8 GEMM A[262144x384] x W[512x384]^T, int32 accumulate, "
                                        "per-channel fp32 scale, fp32 out", "M": M, "K": K, "N": N})
+        traffic, src = measured_traffic("c2", "gemm_i8")
         out["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                           "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "kernel": "gemm_i8",
+                           "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic, "kernel": "gemm_i8",
                            "per_launch": bytes_, "avg_launch_ms": round(ms, 4)}
+        if src:
+            out["roofline"]["traffic_source"] = src
         if not args.no_cpu_baseline:
             cpu = cpu_baseline_gemm(A, W, s, args.cpu_seconds)
         out["wall_s"] = round(wall, 3)
@@ -240,7 +265,7 @@ def run(args):
                                          f"{len(spec.blocks)} blocks heads {spec.heads} window {spec.window} "
                                          f"V{spec.V}; {outputs}", "B": B, "T": T, "params": spec.n_params}
             if not args.no_cpu_baseline:
-                cpu = cpu_baseline_forward(data, spec, T, args.cpu_seconds, args.seed)
+                cpu = cpu_baseline_forward(data, spec, B, T, args.cpu_seconds, args.seed)
         else:  # c4
             S, P, G = cfg["B"], cfg["P"], cfg["G"]
             prompts = torch.from_numpy(synth.token_ids(args.seed, "c4:prompts", (S, P), spec.V)).cuda()
@@ -267,8 +292,8 @@ def run(args):
                                          f"{spec.window} V{spec.V}", "sessions": S, "prompt": P, "generated": G,
                              "params": spec.n_params}
             if not args.no_cpu_baseline:
-                cpu = cpu_baseline_decode(data, spec, P, G, args.cpu_seconds, args.seed)
-        dom, roof = roofline_for(prof, work, args.steps)
+                cpu = cpu_baseline_decode(data, spec, S, P, G, args.cpu_seconds, args.seed)
+        dom, roof = roofline_for(prof, work, args.steps, name)
         out["roofline"] = roof
         total_macs = sum(v for k, v in macs.items() if k != "gemm_probs")
         tok = (cfg["B"] * cfg["T"]) if name != "c4" else cfg["B"] * (cfg["P"] + cfg["G"] - 1)
@@ -293,7 +318,7 @@ def main():
     ap.add_argument("--config", default="c5", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--gemm", default="auto", choices=["auto", "stream", "slab"],
                     help="limb-expanded GEMM kernel (mg_engine_option); both give identical results")
     ap.add_argument("--attention", default="auto", choices=["auto", "exact", "mfma"],

@@ -2,10 +2,11 @@
 
     python -m mignon_ai_amd.profsum stats OUT.md CMD  STATS.csv
         per-kernel launch count, average and total duration from `rocprofv3 --kernel-trace --stats`
-    python -m mignon_ai_amd.profsum pmc OUT.md CMD  COUNTERS.csv [COUNTERS.csv ...] [--calib REGEX BYTES]
+    python -m mignon_ai_amd.profsum pmc OUT.md CMD  COUNTERS.csv [...] [--calib BYTES CAL.csv [...]]
         per-kernel average of every counter per dispatch from `rocprofv3 --pmc` runs; with --calib, the
-        dispatches of the kernel matching REGEX moved BYTES each way, and FETCH_SIZE / WRITE_SIZE of
-        every kernel are also given in bytes scaled by that kernel's counter-to-bytes ratio
+        copy kernel in the CAL files moved BYTES each way per dispatch, and FETCH_SIZE / WRITE_SIZE of
+        every kernel are also given in bytes, scaled by the copy kernel's counter-to-bytes ratio, under
+        the engine's kernel-class name (what bench.py reports and reads back as roofline traffic)
 
 CMD is the command line that produced the files, recorded in the summary.
 """
@@ -34,7 +35,26 @@ def stats(out: str, cmd: str, path: str) -> None:
     _write(out, lines)
 
 
-def pmc(out: str, cmd: str, paths: list[str], calib: tuple[str, int] | None) -> None:
+# kernel name -> the engine's kernel class (mg_model_profile names; GEMM classes by epilogue number)
+_GEMM_EPI = {1: "gemm_qkv", 2: "gemm_latch", 3: "gemm_glu", 4: "gemm_highway", 5: "gemm_out", 6: "gemm_logits",
+             7: "gemm_probs"}
+_CLASSES = [("gemm_c2_kernel", "gemm_i8"), ("row_kernel", "row_norm_pack"), ("scan_kernel", "latch_scan"),
+            ("latch_step_kernel", "latch_step"), ("attention_step_kernel", "attention_step"),
+            ("attention", "attention"), ("head_combine_kernel", "head_combine"), ("bits_kernel", "bits"),
+            ("export_", "state_export")]
+
+
+def kernel_class(name: str) -> str:
+    m = re.search(r"gemm_(?:slab|lx)_kernel<(\d+)", name)
+    if m:
+        return _GEMM_EPI.get(int(m.group(1)), "")
+    for key, cls in _CLASSES:
+        if key in name:
+            return cls
+    return ""
+
+
+def _counters(paths: list[str]):
     acc = defaultdict(lambda: defaultdict(list))  # kernel -> counter -> values per dispatch
     for p in paths:
         per_dispatch = defaultdict(float)
@@ -45,6 +65,15 @@ def pmc(out: str, cmd: str, paths: list[str], calib: tuple[str, int] | None) -> 
             names[r["Dispatch_Id"]] = r["Kernel_Name"]
         for (d, c), v in per_dispatch.items():
             acc[_short(names[d])][c].append(v)
+    return acc
+
+
+def _avg(v):
+    return sum(v) / len(v)
+
+
+def pmc(out: str, cmd: str, paths: list[str], calib: tuple[int, list[str]] | None) -> None:
+    acc = _counters(paths)
     counters = sorted({c for k in acc.values() for c in k})
     lines = [f"Command(s) (from the repository root, one MI355X):", "", "```", cmd, "```", "",
              "Average per dispatch (FETCH_SIZE / WRITE_SIZE in KiB as the counters report them).", ""]
@@ -52,30 +81,49 @@ def pmc(out: str, cmd: str, paths: list[str], calib: tuple[str, int] | None) -> 
               "|---|---:|" + "---:|" * len(counters)]
     for k in sorted(acc):
         n = max(len(v) for v in acc[k].values())
-        cells = []
-        for c in counters:
-            v = acc[k].get(c)
-            cells.append(f"{sum(v) / len(v):.4g}" if v else "")
+        cells = [f"{_avg(acc[k][c]):.4g}" if acc[k].get(c) else "" for c in counters]
         lines.append(f"| `{k}` | {n} | " + " | ".join(cells) + " |")
     if calib:
-        rx, nbytes = re.compile(calib[0]), calib[1]
-        ck = [k for k in acc if rx.search(k)]
+        nbytes, cal_paths = calib
+        cal = _counters(cal_paths)
+        ck = [k for k in cal if "copyBuffer" in k or "copy" in k.lower()]
         if ck:
-            lines += ["", f"Calibration: `{ck[0]}` copies {nbytes} bytes per dispatch.", ""]
+            lines += ["", f"Calibration: `{ck[0]}` (a device-to-device copy) moves {nbytes} bytes each way per "
+                          "dispatch.", ""]
             factors = {}
             for c in ("FETCH_SIZE", "WRITE_SIZE"):
-                v = acc[ck[0]].get(c)
+                v = cal[ck[0]].get(c)
                 if v:
-                    factors[c] = nbytes / (sum(v) / len(v))
-                    lines.append(f"- {c}: {sum(v) / len(v):.6g} per dispatch -> {factors[c]:.2f} bytes per unit")
-            lines += ["", "| kernel | HBM read bytes/dispatch | HBM write bytes/dispatch |", "|---|---:|---:|"]
+                    factors[c] = nbytes / _avg(v)
+                    lines.append(f"- {c}: {_avg(v):.6g} per dispatch -> {factors[c]:.1f} bytes per counter unit")
+            lines += ["", "HBM traffic per dispatch (counter x factor):", "",
+                      "| class | kernel | read bytes | write bytes | total bytes |", "|---|---|---:|---:|---:|"]
             for k in sorted(acc):
-                cells = []
-                for c in ("FETCH_SIZE", "WRITE_SIZE"):
-                    v = acc[k].get(c)
-                    cells.append(f"{sum(v) / len(v) * factors[c]:.4g}" if v and c in factors else "")
-                lines.append(f"| `{k}` | " + " | ".join(cells) + " |")
+                rd, wr = acc[k].get("FETCH_SIZE"), acc[k].get("WRITE_SIZE")
+                if not (rd and wr and "FETCH_SIZE" in factors and "WRITE_SIZE" in factors):
+                    continue
+                r_b, w_b = _avg(rd) * factors["FETCH_SIZE"], _avg(wr) * factors["WRITE_SIZE"]
+                lines.append(f"| {kernel_class(k) or '-'} | `{k}` | {r_b:.6g} | {w_b:.6g} | {r_b + w_b:.6g} |")
     _write(out, lines)
+
+
+def traffic_for(path: str, cls: str) -> float | None:
+    """Total HBM bytes per dispatch recorded for a kernel class in a summary written by `pmc` (the
+    kernel with the most bytes when several implement the class), or None."""
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    best = None
+    for line in text.splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 5 and cells[0] == cls:
+            try:
+                v = float(cells[4])
+            except ValueError:
+                continue
+            best = v if best is None else max(best, v)
+    return best
 
 
 def _write(out: str, lines: list[str]) -> None:
@@ -93,8 +141,8 @@ def main(argv: list[str]) -> None:
     calib = None
     if "--calib" in rest:
         i = rest.index("--calib")
-        calib = (rest[i + 1], int(rest[i + 2]))
-        rest = rest[:i] + rest[i + 3:]
+        calib = (int(rest[i + 1]), rest[i + 2:])
+        rest = rest[:i]
     pmc(out, cmd, rest, calib)
 
 
