@@ -42,6 +42,33 @@ __device__ __forceinline__ Limbs split_limbs(float x, float inv) {
     return Limbs{(int8_t)q0, (int8_t)q1, (int8_t)q2};
 }
 
+// The three digits of four consecutive elements packed as three dwords (element e in byte e of each),
+// equal to split_limbs' digits. Adding 1.5*2^23 rounds a value in [-2^22, 2^22] to the nearest integer
+// (ties to even, like rintf) and leaves that integer's two's-complement low byte as the sum's low
+// mantissa byte, so no clamp or float-to-int conversion is needed: |x*inv| <= 127 (up to rounding) by
+// the choice of scale, and every residual times 254 lies in [-127, 127].
+__device__ __forceinline__ void split4_pack(float4 x, float inv, uint32_t& w0, uint32_t& w1, uint32_t& w2) {
+    const float C = 12582912.0f;  // 1.5 * 2^23
+    const float xs[4] = {x.x, x.y, x.z, x.w};
+    uint32_t b0[4], b1[4], b2[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float y = xs[e] * inv;
+        const float t0 = y + C;
+        const float y1 = (y - (t0 - C)) * kLimbBase;
+        const float t1 = y1 + C;
+        const float y2 = (y1 - (t1 - C)) * kLimbBase;
+        const float t2 = y2 + C;
+        b0[e] = __float_as_uint(t0);
+        b1[e] = __float_as_uint(t1);
+        b2[e] = __float_as_uint(t2);
+    }
+    // v_perm_b32: selector bytes 0-3 take the second operand's bytes, 4-7 the first's, 0x0c gives zero
+    w0 = __builtin_amdgcn_perm(b0[1], b0[0], 0x0c0c0400u) | __builtin_amdgcn_perm(b0[3], b0[2], 0x04000c0cu);
+    w1 = __builtin_amdgcn_perm(b1[1], b1[0], 0x0c0c0400u) | __builtin_amdgcn_perm(b1[3], b1[2], 0x04000c0cu);
+    w2 = __builtin_amdgcn_perm(b2[1], b2[0], 0x0c0c0400u) | __builtin_amdgcn_perm(b2[3], b2[2], 0x04000c0cu);
+}
+
 __device__ __forceinline__ void limb_scale(float amax, float& scale, float& inv) {
     if (amax < kTinyAmax) {
         scale = 0.0f;

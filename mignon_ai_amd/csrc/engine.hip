@@ -492,9 +492,10 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                 ProfScope ps(m->prof, K_LATCH_STEP, s);
                 HIPCHECK(launch_latch_step(la, s));
             } else {
+                // g for every position, written over lambda (each element is read before it is replaced)
                 ScanArgs sa;
-                sa.B = c.B; sa.T = c.T; sa.D = D; sa.Dp = Dp; sa.dil = dil;
-                sa.lam = w.lam.as<float>(); sa.nf = w.nf.as<float>(); sa.xl = w.xl.as<int8_t>(); sa.xs = w.xs.as<float>();
+                sa.B = c.B; sa.T = c.T; sa.D = D; sa.Dp = Dp;
+                sa.lam = w.lam.as<float>(); sa.nf = w.nf.as<float>(); sa.g = w.lam.as<float>();
                 if (c.sess) {
                     sa.lens = c.lens;
                     sa.g_out = c.sess->g.as<float>() + (size_t)bs * c.B * Dp;
@@ -502,8 +503,17 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                     HIPCHECK(launch_export_ring(c.B, c.T, Dp, m->ring, c.lens, w.nf.as<float>(),
                                                 c.sess->norm_ring.as<float>() + (size_t)bs * c.B * m->ring * Dp, s));
                 }
+                {
+                    ProfScope ps(m->prof, K_SCAN, s);
+                    HIPCHECK(launch_scan(sa, s));
+                }
+                // rule input [n | left | g] (stream.go:180-184), limb-expanded with one scale per row
+                RowArgs r;
+                r.M = M; r.mode = ROW_RULE; r.D = D; r.Dp = 3 * Dp; r.seg = Dp; r.dil = dil; r.T = c.T;
+                r.src = w.nf.as<float>(); r.src2 = w.lam.as<float>();
+                r.limbs = w.xl.as<int8_t>(); r.lscale = w.xs.as<float>();
                 ProfScope ps(m->prof, K_SCAN, s);
-                HIPCHECK(launch_scan(sa, s));
+                HIPCHECK(launch_row(r, s));
             }
             // h = GLU(x) (stream.go:214-220) in fp32, then limb-expanded with one scale per row
             g = lx_args(w.xl.as<int8_t>(), w.xs.as<float>(), blk.w1, 2 * Hp, 3 * Dp, M, m->H, blk.s1);

@@ -117,6 +117,41 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
                     }
                     x[j][i] = v;
                 }
+        } else if (a.mode == ROW_RULE) {
+            // rule input [n | left | g] (stream.go:180-184, ca.AssembleNeighborhood): chunk c lies in
+            // segment c / (seg/4) (segments are multiples of 4 columns wide)
+            const int seg = a.seg, s4 = seg >> 2;
+            float4 raw[RB][NS4];
+            bool segok[RB][NS4];
+#pragma unroll
+            for (int j = 0; j < RB; j++)
+#pragma unroll
+                for (int i = 0; i < NS4; i++) {
+                    const int cc = min(lane + 64 * i, C4 - 1);
+                    const int sg = cc / s4, col = 4 * (cc - sg * s4);
+                    const int mm = mcl[j];
+                    const int t = mm % a.T;
+                    const bool has_left = t >= a.dil;
+                    const long long row = sg == 1 ? (has_left ? mm - a.dil : mm) : mm;
+                    const float* base = sg == 2 ? a.src2 : a.src;
+                    raw[j][i] = *(const float4*)(base + row * seg + col);
+                    segok[j][i] = sg != 1 || has_left;
+                }
+#pragma unroll
+            for (int j = 0; j < RB; j++)
+#pragma unroll
+                for (int i = 0; i < NS4; i++) {
+                    const int c = lane + 64 * i;
+                    const int cc = min(c, C4 - 1);
+                    const int col = 4 * (cc - (cc / s4) * s4);
+                    const bool ok = okr[j][i] && segok[j][i];
+                    float4 v = raw[j][i];
+                    v.x = (ok && col + 0 < D) ? v.x : 0.0f;
+                    v.y = (ok && col + 1 < D) ? v.y : 0.0f;
+                    v.z = (ok && col + 2 < D) ? v.z : 0.0f;
+                    v.w = (ok && col + 3 < D) ? v.w : 0.0f;
+                    x[j][i] = v;
+                }
         } else {
             const float* sp = a.src ? a.src : a.cur;
             const int lds = a.src ? a.lds : Dp;
@@ -228,17 +263,13 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
                 for (int i = 0; i < NS4; i++) {
                     const int c = lane + 64 * i;
                     if (c < C4) {
-                        const Limbs l0 = split_limbs(x[j][i].x, inv), l1 = split_limbs(x[j][i].y, inv),
-                                    l2 = split_limbs(x[j][i].z, inv), l3 = split_limbs(x[j][i].w, inv);
+                        uint32_t w0, w1, w2;
+                        split4_pack(x[j][i], inv, w0, w1, w2);
                         // elements 4c..4c+3: K step c>>4, byte 4(c&3) of column group (c>>2)&3, row rr
                         const int o = (c >> 4) * 3072 + (rr + 16 * ((c >> 2) & 3)) * 16 + 4 * (c & 3);
-                        auto pack = [](int8_t b0, int8_t b1, int8_t b2, int8_t b3) {
-                            return (uint32_t)(uint8_t)b0 | ((uint32_t)(uint8_t)b1 << 8) | ((uint32_t)(uint8_t)b2 << 16) |
-                                   ((uint32_t)(uint8_t)b3 << 24);
-                        };
-                        *(uint32_t*)(stage + stage_off(o)) = pack(l0.q0, l1.q0, l2.q0, l3.q0);
-                        *(uint32_t*)(stage + stage_off(o + 1024)) = pack(l0.q1, l1.q1, l2.q1, l3.q1);
-                        *(uint32_t*)(stage + stage_off(o + 2048)) = pack(l0.q2, l1.q2, l2.q2, l3.q2);
+                        *(uint32_t*)(stage + stage_off(o)) = w0;
+                        *(uint32_t*)(stage + stage_off(o + 1024)) = w1;
+                        *(uint32_t*)(stage + stage_off(o + 2048)) = w2;
                     }
                 }
                 if (lane == 0 && valid) a.lscale[m] = sc;
@@ -270,94 +301,39 @@ __device__ __forceinline__ void store_x_limbs(int8_t* xl, int m, int d, int Dp, 
 
 // ------------------------------------------------------------------------------------------------
 // Latch scan: one workgroup per sequence, one thread per channel, sequential over positions.
-// quant.Model.updateLatch (stream.go:195-205): g = lam*g + (1-lam)*n; the rule input
-// [n | left | g] (stream.go:180-184, ca.AssembleNeighborhood) is limb-expanded with one scale per row.
+// quant.Model.updateLatch (stream.go:195-205): g = lam*g + (1-lam)*n, written for every position (the
+// rule input [n | left | g] is then limb-expanded by the row kernel in ROW_RULE mode). Rounds of 16
+// positions: every load of the round is issued first (none depends on the latch), from clamped rows.
 // ------------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void scan_kernel(ScanArgs a) {
-    __shared__ float red[2][16][16];  // [round parity][row][wave] row maxima
-    // When sequences start on 16-token tile boundaries, a tile's x limbs (3*Dp/64 K steps x 3 limbs x
-    // 1 KiB) are staged here and written with 16-byte stores; otherwise bytes go straight out.
-    extern __shared__ __align__(16) int8_t stage[];
     const int b = blockIdx.x;
     const int d = threadIdx.x;
-    const int lane = d & 63, w = d >> 6, nw = blockDim.x >> 6;
     const int D = a.D, Dp = a.Dp, T = a.T;
-    const int kc = 3 * Dp / 64;
-    const bool staged = (T % 16) == 0;
     const int last = a.lens ? a.lens[b] - 1 : -1;
     const bool on = d < D;
+    const int dc = min(d, D - 1);
+    const long long seq0 = (long long)b * T;
     float g = 0.0f;
-    // Rounds of 16 positions: every load of the round is issued first (none depends on the latch),
-    // then the sequential recurrence, then the 16 row maxima together.
-    for (int t0 = 0, par = 0; t0 < T; t0 += 16, par ^= 1) {
+    for (int t0 = 0; t0 < T; t0 += 16) {
         const int nt = min(16, T - t0);
-        const long long m0 = (long long)b * T + t0;
-        float nv[16], lv[16], lm[16];
-        // unconditional loads from clamped addresses (a guarded load becomes a branch that waits)
-        const int dc = min(d, D - 1);
-        const long long seq0 = (long long)b * T;
+        float nv[16], lm[16];
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             const long long m = seq0 + min(t0 + k, T - 1);
-            const long long ml = seq0 + max(min(t0 + k, T - 1) - a.dil, 0);
-            const float n_ = a.nf[m * Dp + dc], l_ = a.lam[m * Dp + dc], left_ = a.nf[ml * Dp + dc];
-            nv[k] = on ? n_ : 0.0f;
-            lm[k] = on ? l_ : 0.0f;
-            lv[k] = (on && t0 + k >= a.dil) ? left_ : 0.0f;
-        }
-        float gv[16], mx[16];
-#pragma unroll
-        for (int k = 0; k < 16; k++) {
-            if (on && k < nt) {
-                const float p1 = lm[k] * g;  // updateLatch (stream.go:195-205)
-                const float p2 = (1.0f - lm[k]) * nv[k];
-                g = p1 + p2;
-            }
-            gv[k] = on ? g : 0.0f;
-            mx[k] = fmaxf(fabsf(nv[k]), fmaxf(fabsf(lv[k]), fabsf(gv[k])));
-            if (t0 + k == last && a.g_out && on) a.g_out[(long long)b * Dp + d] = gv[k];
-        }
-#pragma unroll
-        for (int k = 0; k < 16; k++) mx[k] = wave_max(mx[k]);
-        if (lane == 0) {
-#pragma unroll
-            for (int k = 0; k < 16; k++) red[par][k][w] = mx[k];
-        }
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < 16; k++) {
-            float v = red[par][k][0];
-            for (int i = 1; i < nw; i++) v = fmaxf(v, red[par][k][i]);
-            mx[k] = v;
+            nv[k] = a.nf[m * Dp + dc];
+            lm[k] = a.lam[m * Dp + dc];
         }
 #pragma unroll
         for (int k = 0; k < 16; k++) {
-            if (k >= nt) break;
-            const long long m = m0 + k;
-            float sc, inv;
-            limb_scale(mx[k], sc, inv);
-            if (staged) {
-                const float v[3] = {nv[k], lv[k], gv[k]};
-#pragma unroll
-                for (int sg = 0; sg < 3; sg++) {
-                    Limbs L = split_limbs(v[sg], inv);
-                    const int kk = sg * Dp + d;
-                    const int o = (kk >> 6) * 3 * 1024 + ((k + 16 * ((kk >> 4) & 3)) << 4) + (kk & 15);
-                    stage[o] = L.q0;
-                    stage[o + 1024] = L.q1;
-                    stage[o + 2048] = L.q2;
+            if (k < nt) {
+                if (on) {
+                    const float p1 = lm[k] * g;
+                    const float p2 = (1.0f - lm[k]) * nv[k];
+                    g = p1 + p2;
                 }
-            } else {
-                store_x_limbs(a.xl, (int)m, d, Dp, kc, nv[k], lv[k], gv[k], inv);
+                a.g[(seq0 + t0 + k) * Dp + d] = on ? g : 0.0f;
+                if (t0 + k == last && a.g_out) a.g_out[(long long)b * Dp + d] = on ? g : 0.0f;
             }
-            if (d == 0) a.xs[m] = sc;
-        }
-        if (staged) {
-            __syncthreads();
-            const int bytes = kc * 3 * 1024;
-            int8_t* dst = a.xl + (m0 >> 4) * (long long)bytes;
-            for (int o = d * 16; o < bytes; o += blockDim.x * 16) *(v4i*)(dst + o) = *(const v4i*)(stage + o);
-            __syncthreads();
         }
     }
 }
@@ -963,7 +939,9 @@ hipError_t row_t(const RowArgs& a, hipStream_t s) {
 
 hipError_t launch_row(const RowArgs& a, hipStream_t s) {
     if (a.M <= 0) return hipSuccess;
-    if (a.Dp % 64 || a.Dp < 64 || a.Dp > 2048) return hipErrorInvalidValue;
+    if (a.Dp % 64 || a.Dp < 64 || a.Dp > 3072) return hipErrorInvalidValue;
+    if (a.mode == ROW_RULE && (a.seg % 64 || 3 * a.seg != a.Dp || a.gamma || a.nout || a.T < 1 || a.dil < 0))
+        return hipErrorInvalidValue;
     switch ((a.Dp + 255) / 256) {
         case 1: return row_t<1>(a, s);
         case 2: return row_t<2>(a, s);
@@ -972,15 +950,18 @@ hipError_t launch_row(const RowArgs& a, hipStream_t s) {
         case 5: return row_t<5>(a, s);
         case 6: return row_t<6>(a, s);
         case 7: return row_t<7>(a, s);
-        default: return row_t<8>(a, s);
+        case 8: return row_t<8>(a, s);
+        case 9: return row_t<9>(a, s);
+        case 10: return row_t<10>(a, s);
+        case 11: return row_t<11>(a, s);
+        default: return row_t<12>(a, s);
     }
 }
 
 hipError_t launch_scan(const ScanArgs& a, hipStream_t s) {
     if (a.B <= 0) return hipSuccess;
-    if (a.Dp % 64 || a.Dp > 1024) return hipErrorInvalidValue;
-    const size_t stage = (a.T % 16) == 0 ? (size_t)9 * a.Dp * 16 : 0;
-    hipLaunchKernelGGL(scan_kernel, dim3(a.B), dim3(a.Dp), stage, s, a);
+    if (a.Dp % 64 || a.Dp > 1024 || a.D < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(scan_kernel, dim3(a.B), dim3(a.Dp), 0, s, a);
     return hipGetLastError();
 }
 

@@ -6,7 +6,7 @@
 
 namespace mg {
 
-enum RowMode : int { ROW_SRC = 0, ROW_EMBED = 1, ROW_RESID = 2 };
+enum RowMode : int { ROW_SRC = 0, ROW_EMBED = 1, ROW_RESID = 2, ROW_RULE = 3 };
 
 // Values of OPT_ATTENTION_KERNEL.
 enum AttnKernel : int { ATTN_AUTO = 0, ATTN_EXACT = 1, ATTN_MFMA = 2 };
@@ -27,16 +27,20 @@ struct RowArgs {
     float* nout = nullptr;             // normalised rows [M][Dp], or null
     int8_t* limbs = nullptr;           // limb-expanded rows in the GEMM fragment layout (K = Dp)
     float* lscale = nullptr;           // [M]
+    // ROW_RULE: the rule input [n | left | g] of each position, three segments of `seg` columns (Dp =
+    // 3*seg, D = valid columns per segment): n = src[m], left = src[m - dil] (zero for t < dil, t = m % T),
+    // g = src2[m], all with row stride seg.
+    const float* src2 = nullptr;
+    int seg = 0, dil = 1, T = 1;
 };
 hipError_t launch_row(const RowArgs& a, hipStream_t s);
 
-// Selective latch over whole sequences plus the rule input [n | left | g] (teacher-forced forward).
+// Selective latch over whole sequences (teacher-forced forward): g[m] for every position.
 struct ScanArgs {
-    int B = 0, T = 0, D = 0, Dp = 0, dil = 1;
+    int B = 0, T = 0, D = 0, Dp = 0;
     const float* lam = nullptr;  // [B*T][Dp]
     const float* nf = nullptr;   // [B*T][Dp]
-    int8_t* xl = nullptr;        // [n | left | g] limb-expanded, fragment layout, K = 3*Dp
-    float* xs = nullptr;         // [B*T]
+    float* g = nullptr;          // [B*T][Dp] latch state after each position (may be lam itself)
     const int32_t* lens = nullptr;  // per-sequence length (export position lens[b]-1) or null
     float* g_out = nullptr;         // exported latch state [B][Dp] or null
 };
