@@ -759,21 +759,33 @@ __global__ __launch_bounds__(64) void attention_step_kernel(AttnStepArgs a) {
 // ------------------------------------------------------------------------------------------------
 // Head statistics, log-probs, bits
 // ------------------------------------------------------------------------------------------------
-__global__ void head_combine_kernel(HeadCombineArgs a) {
-    const int m = blockIdx.x * blockDim.x + threadIdx.x;
-    if (m >= a.M) return;
-    const float* st = a.stats + (long long)m * a.ntiles * 3;
+// Per-row softmax statistics from the logits GEMM's per-tile (max, sum exp(l - max), first argmax).
+// Sixteen lanes per row read the row's tiles coalesced (lane l takes tiles l, l+16, ...), then merge
+// across the group with xor shuffles: the larger max wins and rescales the other sum, equal maxima keep
+// the smaller index (the reference's first maximum, internal/generate/greedy.go:89-102).
+__device__ __forceinline__ void merge_stats(float& bm, float& bs, int& bi, float om, float os, int oi) {
+    if (om == -INFINITY) return;
+    const float nm = fmaxf(bm, om);
+    const float ns = (bm == -INFINITY ? 0.0f : bs * __expf(bm - nm)) + os * __expf(om - nm);
+    const int ni = (om > bm) ? oi : (bm > om) ? bi : min(bi, oi);
+    bm = nm; bs = ns; bi = ni;
+}
+
+__global__ __launch_bounds__(256) void head_combine_kernel(HeadCombineArgs a) {
+    const int l = threadIdx.x & 15;
+    const int m = blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int mc = min(m, a.M - 1);
+    const float* st = a.stats + (long long)mc * a.ntiles * 3;
     float bm = -INFINITY, bs = 0.0f;
     int bi = 0x7fffffff;
-    for (int t = 0; t < a.ntiles; t++) {
-        float om = st[3 * t], os = st[3 * t + 1];
-        int oi = __float_as_int(st[3 * t + 2]);
-        if (om == -INFINITY) continue;
-        float nm = fmaxf(bm, om);
-        float ns = (bm == -INFINITY ? 0.0f : bs * __expf(bm - nm)) + os * __expf(om - nm);
-        int ni = (om > bm) ? oi : (bm > om) ? bi : min(bi, oi);
-        bm = nm; bs = ns; bi = ni;
+    for (int t = l; t < a.ntiles; t += 16) merge_stats(bm, bs, bi, st[3 * t], st[3 * t + 1], __float_as_int(st[3 * t + 2]));
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) {
+        const float om = __shfl_xor(bm, o, 16), os = __shfl_xor(bs, o, 16);
+        const int oi = __shfl_xor(bi, o, 16);
+        merge_stats(bm, bs, bi, om, os, oi);
     }
+    if (l != 0 || m >= a.M) return;
     float lse = bm + logf(bs);
     if (a.lse) a.lse[m] = lse;
     if (a.argmax) a.argmax[m] = bi;
@@ -1009,7 +1021,7 @@ hipError_t launch_attention_step(const AttnStepArgs& a, hipStream_t s) {
 
 hipError_t launch_head_combine(const HeadCombineArgs& a, hipStream_t s) {
     if (a.M <= 0) return hipSuccess;
-    hipLaunchKernelGGL(head_combine_kernel, dim3((a.M + 255) / 256), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(head_combine_kernel, dim3((a.M + 15) / 16), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

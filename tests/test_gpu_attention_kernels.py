@@ -33,7 +33,8 @@ def _both(data, ids):
 
 
 @pytest.mark.parametrize("window,context,T", [(7, 64, 45), (64, 64, 130), (0, 64, 50), (0, 64, 200), (0, 128, 150),
-                                              (0, 256, 300), (100, 256, 180)])
+                                              (0, 256, 300), (100, 256, 180), (7, 64, 64), (64, 64, 128),
+                                              (0, 64, 192), (30, 128, 160)])
 def test_windows_and_lengths(restore_selection, window, context, T):
     """Key spans of 7..256 (1 to 17 blocks of 16 keys) and sequences past the context."""
     spec = tiny_spec([(2, 2, 1), (1, 2, 2)], V=96, D=64, H=48, heads=4, window=window, context=context)
@@ -42,11 +43,13 @@ def test_windows_and_lengths(restore_selection, window, context, T):
     _both(data, ids)
 
 
-@pytest.mark.parametrize("D,heads", [(8, 2), (48, 3), (96, 4), (128, 4)])
-def test_head_widths(restore_selection, D, heads):
+@pytest.mark.parametrize("D,heads,T", [(8, 2, 70), (48, 3, 70), (96, 4, 70), (128, 4, 70), (8, 2, 48), (48, 3, 80),
+                                        (96, 4, 96), (128, 8, 64), (128, 4, 32)])
+def test_head_widths(restore_selection, D, heads, T):
+    """Head widths 4..32, whole and partial 16-query tiles."""
     spec = tiny_spec([(1, 2, 1), (1, 2, 1)], V=64, D=D, H=32, heads=heads, window=20)
     data = uniform_model_bytes(spec, scale=0.3)
-    ids = synth.token_ids(32, f"attn-d{D}", (2, 70), 64)
+    ids = synth.token_ids(32, f"attn-d{D}-{T}", (2, T), 64)
     _both(data, ids)
 
 
