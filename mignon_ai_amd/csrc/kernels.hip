@@ -756,6 +756,93 @@ __global__ __launch_bounds__(64) void attention_step_kernel(AttnStepArgs a) {
     }
 }
 
+// Decode attention, staged: the span's key and value head slices go to LDS with 16-byte loads (eight
+// lanes per 128 bytes, a batch of loads in flight before any is stored), then the same reference-order
+// scores, softmax and P.V as attention_step_kernel, read from LDS: bit-identical results, one memory
+// round trip per batch instead of one per key.
+template <int DH>
+__global__ __launch_bounds__(64) void attention_step_lds_kernel(AttnStepArgs a) {
+    constexpr int DS = DH + 4;  // LDS row stride (16-byte rows, consecutive rows 4 banks apart)
+    constexpr int C4 = DH / 4;
+    extern __shared__ __align__(16) float step_smem[];
+    const int cap = a.cap;
+    float* ks = step_smem;          // [cap][DS]
+    float* vs = ks + cap * DS;      // [cap][DS]
+    float* es = vs + cap * DS;      // [cap]
+    __shared__ float inv_sh;
+    const int s_ = blockIdx.x / a.heads, h = blockIdx.x % a.heads;
+    const int lane = threadIdx.x;
+    const int D = a.D;
+    const int pos = a.pos[s_];
+    const int lo = max(window_start(pos, a.window), pos - cap + 1);
+    const int span = pos - lo + 1;
+    const float* qkv = a.qkv + (long long)s_ * 3 * D;
+    const float* kr = a.kring + (long long)s_ * cap * D + h * DH;
+    const float* vr = a.vring + (long long)s_ * cap * D + h * DH;
+    // rows jj = 0..span-1 hold key/value j = lo + jj (the current position's from qkv, not yet in the ring)
+    const int n4 = span * C4;
+    for (int e0 = 0; e0 < n4; e0 += 8 * 64) {
+        float4 kb[8], vb[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int e = min(e0 + u * 64 + lane, n4 - 1);
+            const int jj = e / C4, c = e - jj * C4;
+            const int j = lo + jj;
+            const float* kp = j == pos ? qkv + D + h * DH : kr + (long long)(j % cap) * D;
+            const float* vp = j == pos ? qkv + 2 * D + h * DH : vr + (long long)(j % cap) * D;
+            kb[u] = *(const float4*)(kp + 4 * c);
+            vb[u] = *(const float4*)(vp + 4 * c);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int e = e0 + u * 64 + lane;
+            if (e < n4) {
+                const int jj = e / C4, c = e - jj * C4;
+                *(float4*)(ks + jj * DS + 4 * c) = kb[u];
+                *(float4*)(vs + jj * DS + 4 * c) = vb[u];
+            }
+        }
+    }
+    float q[DH];
+#pragma unroll
+    for (int i = 0; i < DH; i += 4) {
+        const float4 t = *(const float4*)(qkv + h * DH + i);
+        q[i] = t.x; q[i + 1] = t.y; q[i + 2] = t.z; q[i + 3] = t.w;
+    }
+    __syncthreads();
+    const float scale = (float)(1.0 / sqrt((double)DH));
+    float mx = -3.40282347e38f;
+    for (int jj = lane; jj < span; jj += 64) {
+        const float sc = dot_ref_lds4<DH>(q, ks + jj * DS) * scale;
+        es[jj] = sc;
+        mx = fmaxf(mx, sc);
+    }
+    mx = wave_max(mx);
+    for (int jj = lane; jj < span; jj += 64) es[jj] = fast_exp_ref(es[jj] - mx);
+    __syncthreads();
+    if (lane == 0) {
+        float sum = 0.0f;  // nn.SoftmaxInPlaceF32's sequential sum
+#pragma unroll 8
+        for (int jj = 0; jj < span; jj++) sum += es[jj];
+        inv_sh = 1.0f / sum;
+    }
+    __syncthreads();
+    const float inv = inv_sh;
+    for (int i = lane; i < DH; i += 64) {
+        float o = 0.0f;
+#pragma unroll 8
+        for (int jj = 0; jj < span; jj++) o = axpy_ref<DH>(i, es[jj] * inv, vs[jj * DS + i], o);
+        a.att[(long long)s_ * a.Dp + h * DH + i] = o;
+    }
+    // record this position's key and value (slot pos % cap; the evicted key is outside the window)
+    float* kw = a.kring + (long long)s_ * cap * D + (long long)(pos % cap) * D + h * DH;
+    float* vw = a.vring + (long long)s_ * cap * D + (long long)(pos % cap) * D + h * DH;
+    for (int i = lane; i < DH; i += 64) {
+        kw[i] = qkv[D + h * DH + i];
+        vw[i] = qkv[2 * D + h * DH + i];
+    }
+}
+
 // ------------------------------------------------------------------------------------------------
 // Head statistics, log-probs, bits
 // ------------------------------------------------------------------------------------------------
@@ -930,6 +1017,13 @@ hipError_t attn_mfma(const AttnArgs& a, int dh, hipStream_t s) {
 
 template <int DH>
 hipError_t attn_step_t(const AttnStepArgs& a, hipStream_t s) {
+    if constexpr (DH % 4 == 0) {
+        const size_t lds = ((size_t)2 * a.cap * (DH + 4) + a.cap) * sizeof(float);
+        if (lds <= 64 * 1024) {
+            hipLaunchKernelGGL(attention_step_lds_kernel<DH>, dim3(a.S * a.heads), dim3(64), lds, s, a);
+            return hipGetLastError();
+        }
+    }
     hipLaunchKernelGGL(attention_step_kernel<DH>, dim3(a.S * a.heads), dim3(64), 0, s, a);
     return hipGetLastError();
 }
