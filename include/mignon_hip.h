@@ -125,6 +125,73 @@ long long mg_sessions_device_bytes(const mg_sessions* s);
 int mg_sessions_count(const mg_sessions* s);
 void mg_sessions_free(mg_sessions* s);
 
+/* eval nll.score's per-target log-probabilities over many token sequences in one batched pass
+ * (internal/eval/eval.go:25-50, window internal/eval/suite.go:196-198, logProb :200-208). Sequence q is
+ * tokens[offsets[q] .. offsets[q+1]); each of its targets t = 1..len-1 is scored from
+ * window(seq[:t], context) (then Call's truncation to max_context), as log-softmax of seq[t].
+ * logprob receives, sequence after sequence, max(len-1, 0) fp32 values; NaN marks a target that is not
+ * scored (id outside [0, V), or context <= 0). offsets has n_seq+1 entries. Host pointers. */
+int mg_score_sequences(mg_model* m, const int32_t* tokens, const long long* offsets, int n_seq, int context,
+                       float* logprob);
+
+/* ---- Text: the tokenizer stored in a model file and the generation / evaluation drivers over it ---- */
+typedef struct mg_tokenizer mg_tokenizer;
+
+/* tokenizer.FromVocabAndMerges on a model file's header after tokenizer.CheckFormat
+ * (internal/quant/checkpoint.go:201-207, internal/tokenizer/tokenizer.go:60-72, format.go:12-17).
+ * *out = NULL (and MG_OK) when the file has no vocabulary; MG_ERR_FORMAT for any other format version. */
+int mg_tokenizer_load(const uint8_t* data, size_t n, mg_tokenizer** out);
+void mg_tokenizer_free(mg_tokenizer* t);
+/* Tokenizer.VocabSize (internal/tokenizer/tokenizer.go:86-90). */
+int mg_tokenizer_vocab_size(const mg_tokenizer* t);
+/* PadTokenID (0 when absent), UnkTokenID, UserTokenID, BotTokenID, EOSTokenID (-1 when absent)
+ * (internal/tokenizer/tokenizer.go:320-347). */
+#define MG_TOKEN_PAD 0
+#define MG_TOKEN_UNK 1
+#define MG_TOKEN_USER 2
+#define MG_TOKEN_BOT 3
+#define MG_TOKEN_EOS 4
+int mg_tokenizer_special(const mg_tokenizer* t, int which);
+/* Encode (internal/tokenizer/tokenizer.go:268-318), EncodePrompt / EncodeReply (template.go:11-21) of
+ * UTF-8 text of n bytes. Writes at most cap ids and returns how many the text encodes to. */
+#define MG_ENCODE_TEXT 0
+#define MG_ENCODE_PROMPT 1
+#define MG_ENCODE_REPLY 2
+long long mg_tokenizer_encode(mg_tokenizer* t, const char* text, size_t n, int mode, int32_t* ids, long long cap);
+/* Decode (internal/tokenizer/tokenizer.go:348-367): writes at most cap bytes (no terminator) and returns
+ * the decoded length in bytes. */
+long long mg_tokenizer_decode(const mg_tokenizer* t, const int32_t* ids, long long n, char* out, long long cap);
+/* The vocabulary entry of id (Tokenizer.Vocab[id]): writes at most cap bytes (no terminator) and returns
+ * its length, or MG_ERR_INVALID for an id outside the vocabulary. */
+long long mg_tokenizer_token(const mg_tokenizer* t, int id, char* out, long long cap);
+/* TokenBytes (internal/tokenizer/bytes.go:13-22): out[V]. */
+int mg_tokenizer_token_bytes(const mg_tokenizer* t, int32_t* out);
+/* splitWords (internal/tokenizer/pretokenize.go:39-67): the end offset (bytes) of every pre-token of the
+ * text; writes at most cap and returns the count. */
+long long mg_pretokenize(const char* text, size_t n, long long* ends, long long cap);
+
+/* infer.Generate's greedy branch (pkg/infer/infer.go:64-84, generate.DecodeGreedy and greedyLoop,
+ * internal/generate/greedy.go:43-102) for n prompts at once, on device sessions of window `context`:
+ * each prompt (UTF-8, prompt_lens[i] bytes) goes through the chat template when chat != 0; the reply
+ * stops before <EOS>, <USER> or <BOT> or after max_tokens (> 0) tokens. out_ids / out_probs are
+ * [n][max_tokens]; out_counts[i] is the reply length. Decode the ids with mg_tokenizer_decode and trim
+ * surrounding whitespace for infer.Result.Text. */
+int mg_generate_greedy(mg_model* m, mg_tokenizer* t, const char* const* prompts, const size_t* prompt_lens, int n,
+                       int context, int max_tokens, int chat, int32_t* out_ids, double* out_probs,
+                       int32_t* out_counts);
+
+/* eval.HeldOut (internal/eval/eval.go:12-17). */
+typedef struct {
+    double loss, ppl, bpb;
+    long long tokens;
+} mg_heldout_t;
+/* eval.Perplexity (internal/eval/eval.go:50-75; per_doc == 0: text is one stream, max_count caps the
+ * targets) and eval.PerplexityPerDoc (internal/eval/perdoc.go:12-48; per_doc != 0: documents split on
+ * "<EOS>", each scored from a fresh <EOS>, max_count caps the documents), all targets in one batched pass
+ * (mg_score_sequences). max_count <= 0: no cap. */
+int mg_perplexity(mg_model* m, mg_tokenizer* t, const char* text, size_t n, int context, int max_count, int per_doc,
+                  mg_heldout_t* out);
+
 /* Standalone INT8 GEMM (kernels.MatVecInt8 per row, internal/kernels/int8.go:31-41, on integer
  * activations): acc[m][n] = sum_k A[m][k]*W[n][k] exactly in int32, C[m][n] = float(acc)*scale[n].
  * A [M][K], W [N][K] (one row per output channel), scale [N], C [M][N], acc [M][N] (optional).

@@ -37,6 +37,11 @@ class ModelInfo(ctypes.Structure):
                 ("norm_ring", _int), ("attn_cache", _int), ("num_params", _ll)]
 
 
+class HeldOut(ctypes.Structure):
+    """eval.HeldOut (internal/eval/eval.go:12-17)."""
+    _fields_ = [("loss", ctypes.c_double), ("ppl", ctypes.c_double), ("bpb", ctypes.c_double), ("tokens", _ll)]
+
+
 class KernelTime(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char * 32), ("launches", _ll), ("total_ms", ctypes.c_double)]
 
@@ -66,6 +71,18 @@ SIGNATURES = {
     "mg_gemm_i8": (_int, [_vp, _int, _int, _vp, _int, _vp, _vp, _vp, _int, _vp]),
     "mg_quantize_f32": (_int, [_vp, _ll, _vp, _vp, _int, _vp]),
     "mg_engine_option": (_int, [_int, _int]),
+    "mg_score_sequences": (_int, [_vp, _vp, _vp, _int, _int, _vp]),
+    "mg_tokenizer_load": (_int, [_u8p, ctypes.c_size_t, ctypes.POINTER(_vp)]),
+    "mg_tokenizer_free": (None, [_vp]),
+    "mg_tokenizer_vocab_size": (_int, [_vp]),
+    "mg_tokenizer_special": (_int, [_vp, _int]),
+    "mg_tokenizer_encode": (_ll, [_vp, ctypes.c_char_p, ctypes.c_size_t, _int, _vp, _ll]),
+    "mg_tokenizer_decode": (_ll, [_vp, _vp, _ll, _vp, _ll]),
+    "mg_tokenizer_token": (_ll, [_vp, _int, _vp, _ll]),
+    "mg_tokenizer_token_bytes": (_int, [_vp, _vp]),
+    "mg_pretokenize": (_ll, [ctypes.c_char_p, ctypes.c_size_t, _vp, _ll]),
+    "mg_generate_greedy": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp, _vp, _vp]),
+    "mg_perplexity": (_int, [_vp, _vp, ctypes.c_char_p, ctypes.c_size_t, _int, _int, _int, _vp]),
 }
 
 _lib = None

@@ -18,7 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(OUT_DIR, "libmignon_hip.so")
-SOURCES = ["gemm.hip", "kernels.hip", "engine.hip"]
+SOURCES = ["gemm.hip", "kernels.hip", "engine.hip", "text.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
@@ -31,7 +31,7 @@ def build(verbose: bool = False) -> str:
     os.makedirs(OUT_DIR, exist_ok=True)
     objs = []
     for src in SOURCES:
-        obj = os.path.join(OUT_DIR, src.replace(".hip", ".o"))
+        obj = os.path.join(OUT_DIR, os.path.splitext(src)[0] + ".o")
         cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)

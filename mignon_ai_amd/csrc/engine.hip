@@ -17,6 +17,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstring>
+#include <limits>
 #include <memory>
 #include <mutex>
 #include <stdexcept>
@@ -29,6 +30,7 @@
 #include "kernels.hpp"
 #include "model_file.hpp"
 #include "options.hpp"
+#include "text_abi.hpp"
 
 namespace mg {
 
@@ -451,6 +453,16 @@ __global__ void window_ids_kernel(int S, int max_len, int window, int Tw, const 
     if (threadIdx.x == 0) lens_out[s] = L;
 }
 
+// Scoring windows: row r of a [B][T] token matrix is tokens[start[r] .. start[r] + len[r]), padded with id 0
+// (positions past len[r] are never scored, and no position depends on a later one).
+__global__ void gather_rows_kernel(int B, int T, const int32_t* tokens, const long long* start, const int32_t* len,
+                                   int32_t* out) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)B * T) return;
+    const int r = (int)(i / T), t = (int)(i - (long long)r * T);
+    out[i] = t < len[r] ? tokens[start[r] + t] : 0;
+}
+
 // ------------------------------------------------------------------------------------------------
 // The model body over M rows. Batched mode (sess == null): rows are B sequences of T positions.
 // Prefill export (sess != null, step == false): also writes the session state at each sequence's last
@@ -641,6 +653,12 @@ extern "C" {
 
 const char* mg_last_error(void) { return g_last_error.c_str(); }
 
+}  // extern "C"
+
+void mg::set_last_error(const std::string& msg) { g_last_error = msg; }
+
+extern "C" {
+
 int mg_model_load(const uint8_t* data, size_t n, int max_context, mg_model** out) {
     return guarded([&] {
         require(data != nullptr && out != nullptr, "mg_model_load: null argument");
@@ -815,6 +833,104 @@ int mg_forward_batch(mg_model* m, const int32_t* ids, int B, int T, float* logit
                 HIPCHECK(hipStreamSynchronize(s));
                 st.bufs.clear();
             }
+        }
+        return MG_OK;
+    });
+}
+
+int mg_score_sequences(mg_model* m, const int32_t* tokens, const long long* offsets, int n_seq, int context,
+                       float* logprob) {
+    return guarded([&] {
+        require(m && offsets && logprob, "mg_score_sequences: null argument");
+        require(n_seq >= 0, "mg_score_sequences: negative sequence count");
+        require(offsets[0] >= 0, "mg_score_sequences: negative offset");
+        long long n_targets = 0;
+        for (int q = 0; q < n_seq; q++) {
+            require(offsets[q + 1] >= offsets[q], "mg_score_sequences: offsets must not decrease");
+            n_targets += std::max<long long>(offsets[q + 1] - offsets[q] - 1, 0);
+        }
+        const long long n_tok = offsets[n_seq];
+        require(n_tok == 0 || tokens, "mg_score_sequences: null tokens");
+        const float qnan = std::numeric_limits<float>::quiet_NaN();
+        std::fill(logprob, logprob + n_targets, qnan);
+        // window(tokens[:t], contextSize) (internal/eval/suite.go:196-198), then Call's truncation to
+        // maxContext; an empty window gives no logits and nothing is scored (internal/eval/eval.go:27-33)
+        const int W = std::min(context, m->max_context);
+        if (n_targets == 0 || W <= 0) return MG_OK;
+
+        // One row per window: the first W targets of a sequence share the row of its first W tokens (the
+        // prefix of target t is tokens[0..t), fresh from position 0); every later target t has its own row
+        // tokens[t-W .. t), scored at its last position.
+        struct Row {
+            long long start, out;
+            int len, first, count;
+        };
+        std::vector<Row> rows;
+        long long out0 = 0;
+        for (int q = 0; q < n_seq; q++) {
+            const long long off = offsets[q], L = offsets[q + 1] - offsets[q];
+            if (L < 2) continue;
+            const int n0 = (int)std::min<long long>(L - 1, W);
+            rows.push_back({off, out0, n0, 0, n0});
+            for (long long t = W + 1; t < L; t++) rows.push_back({off + t - W, out0 + t - 1, W, W - 1, 1});
+            out0 += L - 1;
+        }
+        std::stable_sort(rows.begin(), rows.end(), [](const Row& a, const Row& b) { return a.len > b.len; });
+
+        long long row_tokens = 0;
+        for (const Row& r : rows) row_tokens += r.len;
+        // every chunk holds at most `cap` row tokens (cap >= the longest row, so a chunk is never empty)
+        const long long cap = std::min<long long>(kMaxChunkTokens, row_tokens);
+        const size_t max_rows = std::min<size_t>(rows.size(), (size_t)cap);
+
+        Guard gd(m);
+        hipStream_t s = m->stream;
+        ensure_ws(m, (int)cap);
+        Workspace& w = m->ws;
+        Staging st;
+        int32_t* tok_d = st.in(tokens, (size_t)n_tok, s);
+        long long* start_d = st.out<long long>(max_rows);
+        int32_t* len_d = st.out<int32_t>(max_rows);
+        std::vector<long long> h_start;
+        std::vector<int32_t> h_len, h_map, h_tgt;
+        std::vector<float> h_lp;
+        for (size_t r0 = 0; r0 < rows.size();) {
+            const int T = rows[r0].len;
+            const size_t r1 = std::min(rows.size(), r0 + (size_t)(cap / T));
+            const int B = (int)(r1 - r0);
+            h_start.clear(); h_len.clear(); h_map.clear(); h_tgt.clear();
+            for (size_t r = r0; r < r1; r++) {
+                const Row& row = rows[r];
+                h_start.push_back(row.start);
+                h_len.push_back(row.len);
+                for (int k = 0; k < row.count; k++) {
+                    const int pos = row.first + k;
+                    h_map.push_back((int32_t)((r - r0) * T + pos));
+                    h_tgt.push_back(tokens[row.start + pos + 1]);
+                }
+            }
+            const int Ms = (int)h_map.size();
+            HIPCHECK(hipMemcpyAsync(start_d, h_start.data(), (size_t)B * 8, hipMemcpyHostToDevice, s));
+            HIPCHECK(hipMemcpyAsync(len_d, h_len.data(), (size_t)B * 4, hipMemcpyHostToDevice, s));
+            HIPCHECK(hipMemcpyAsync(w.rowmap.p, h_map.data(), (size_t)Ms * 4, hipMemcpyHostToDevice, s));
+            HIPCHECK(hipMemcpyAsync(w.tgt.p, h_tgt.data(), (size_t)Ms * 4, hipMemcpyHostToDevice, s));
+            int32_t* ids_d = w.ids.as<int32_t>();
+            hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)(((long long)B * T + 255) / 256)), dim3(256), 0, s, B, T,
+                               tok_d, start_d, len_d, ids_d);
+            HIPCHECK(hipGetLastError());
+            BodyCtx c;
+            c.B = B; c.T = T; c.ids = ids_d;
+            run_body(m, c, s);
+            HeadCombineArgs hc;
+            hc.logprob = w.logprob.as<float>();
+            run_head(m, Ms, w.rowmap.as<int32_t>(), w.tgt.as<int32_t>(), nullptr, hc, s);
+            h_lp.resize(Ms);
+            HIPCHECK(hipMemcpyAsync(h_lp.data(), w.logprob.p, (size_t)Ms * 4, hipMemcpyDeviceToHost, s));
+            HIPCHECK(hipStreamSynchronize(s));
+            size_t k = 0;
+            for (size_t r = r0; r < r1; r++)
+                for (int j = 0; j < rows[r].count; j++) logprob[rows[r].out + j] = h_lp[k++];
+            r0 = r1;
         }
         return MG_OK;
     });

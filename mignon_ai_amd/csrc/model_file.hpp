@@ -88,10 +88,11 @@ inline const mgjson::Value* tensor_data(const mgjson::Value* t) { return t ? t->
 
 }  // namespace detail
 
-// quant.Decode (internal/quant/checkpoint.go:162-212).
-inline HostModel decode_model_file(const uint8_t* data, size_t n) {
+// The container of a model file (internal/binfmt/binfmt.go; legacy JSON files are the header alone):
+// returns the parsed JSON header and, for binary files, where the arrays begin.
+inline mgjson::Value parse_model_header(const uint8_t* data, size_t n, const uint8_t** arrays_out,
+                                        size_t* arrays_n_out) {
     using namespace detail;
-    HostModel m;
     mgjson::Value cp;
     bool binary = n >= 4 && std::memcmp(data, "MGNN", 4) == 0;
     const uint8_t* arrays = nullptr;
@@ -114,6 +115,19 @@ inline HostModel decode_model_file(const uint8_t* data, size_t n) {
         cp = mgjson::parse((const char*)data, n);
     }
     if (cp.kind != mgjson::Value::Object) throw FormatError("model file header is not an object");
+    if (arrays_out) *arrays_out = arrays;
+    if (arrays_n_out) *arrays_n_out = arrays_n;
+    return cp;
+}
+
+// quant.Decode (internal/quant/checkpoint.go:162-212).
+inline HostModel decode_model_file(const uint8_t* data, size_t n) {
+    using namespace detail;
+    HostModel m;
+    const uint8_t* arrays = nullptr;
+    size_t arrays_n = 0;
+    const mgjson::Value cp = parse_model_header(data, n, &arrays, &arrays_n);
+    const bool binary = arrays != nullptr;
     m.V = (int)cp.number_or("vocab_size", 0);
     m.D = (int)cp.number_or("state_size", 0);
     m.H = (int)cp.number_or("hidden_size", 0);

@@ -13,6 +13,8 @@ the model's stream.
 from __future__ import annotations
 
 import ctypes
+import json
+import struct
 
 import numpy as np
 
@@ -21,6 +23,16 @@ from ._lib import MG_PTR_DEVICE, ModelInfo, check, lib, ptr
 
 def _i32(a):
     return np.ascontiguousarray(a, dtype=np.int32)
+
+
+def read_metadata(data: bytes) -> dict:
+    """The metadata object of a model file's JSON header (binary container or legacy JSON file)."""
+    if len(data) >= 12 and data[:4] == b"MGNN":
+        n = struct.unpack_from("<I", data, 8)[0]
+        hdr = json.loads(data[12:12 + n])
+    else:
+        hdr = json.loads(data)
+    return hdr.get("metadata") or {}
 
 
 class Model:

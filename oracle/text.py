@@ -1,0 +1,327 @@
+"""CPU restatement of the reference's text path: tokenizer, chat template, greedy decoding and held-out
+scoring, in plain Python over the oracle's model sessions.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/ as the checker of the product's text layer
+(mignon_ai_amd/csrc/tokenizer.hpp, text.cpp), never by the product.
+
+Text is bytes and is read as Go reads strings: an invalid UTF-8 byte is one U+FFFD rune of width 1.
+  - split_words: splitWords (internal/tokenizer/pretokenize.go:19-67)
+  - Tokenizer.encode_word / encode / decode: internal/tokenizer/tokenizer.go:179-227, 268-318, 348-367
+  - encode_prompt / encode_reply / drop_oldest_turns: internal/tokenizer/template.go:11-35
+  - token_bytes: internal/tokenizer/bytes.go:13-22
+  - argmax_prob / greedy_loop / decode_greedy: internal/generate/greedy.go:43-102
+  - generate: pkg/infer/infer.go:64-84 (greedy branch)
+  - perplexity / perplexity_per_doc: internal/eval/eval.go:25-75, internal/eval/perdoc.go:12-48,
+    window and logProb internal/eval/suite.go:196-208, BitsPerByte internal/tokenizer/bytes.go:5-11
+Character classes use Python's unicodedata (Go's unicode.IsSpace / IsPunct / IsSymbol / IsDigit).
+"""
+from __future__ import annotations
+
+import json
+import math
+import struct
+import unicodedata
+
+PAD, UNK, USER, BOT, EOS = "<PAD>", "<UNK>", "<USER>", "<BOT>", "<EOS>"
+FORMAT_VERSION = 2
+MAX_WORD_BYTES = 128
+CHAT_MAX_RESPONSE_TOKENS = 60
+DOC_SEPARATOR = b"<EOS>"
+DOC_PADDING = b"\n\n"
+
+_WORD, _SPACE, _PUNCT, _DIGIT = 0, 1, 2, 3
+_LATIN1_SPACE = {0x09, 0x0A, 0x0B, 0x0C, 0x0D, 0x20, 0x85, 0xA0}
+_OTHER_SPACE = {0x1680, 0x2028, 0x2029, 0x202F, 0x205F, 0x3000} | set(range(0x2000, 0x200B))
+RUNE_ERROR = 0xFFFD
+
+
+def char_class(r: int) -> int:
+    if (r <= 0xFF and r in _LATIN1_SPACE) or (r > 0xFF and r in _OTHER_SPACE):
+        return _SPACE
+    cat = unicodedata.category(chr(r))
+    if cat[0] in "PS":
+        return _PUNCT
+    if cat == "Nd":
+        return _DIGIT
+    return _WORD
+
+
+def decode_rune(b: bytes, i: int) -> tuple[int, int]:
+    """utf8.DecodeRuneInString at byte i: (rune, width); a byte that does not start a valid, complete
+    encoding is (U+FFFD, 1). Validity is what Python's strict decoder accepts for that one sequence."""
+    b0 = b[i]
+    if b0 < 0x80:
+        return b0, 1
+    n = 2 if 0xC0 <= b0 < 0xE0 else 3 if 0xE0 <= b0 < 0xF0 else 4 if 0xF0 <= b0 < 0xF8 else 0
+    if n and i + n <= len(b):
+        try:
+            s = b[i:i + n].decode("utf-8")
+            return ord(s), n
+        except UnicodeDecodeError:
+            pass
+    return RUNE_ERROR, 1
+
+
+def runes(b: bytes):
+    i = 0
+    while i < len(b):
+        r, w = decode_rune(b, i)
+        yield i, r, w
+        i += w
+
+
+def split_words(text: bytes) -> list[bytes]:
+    out = []
+    start, cur = 0, _SPACE
+    for i, r, _ in runes(text):
+        c = char_class(r)
+        if i == start:
+            cur = c
+            continue
+        if c == cur and c != _DIGIT and i - start < MAX_WORD_BYTES:
+            continue
+        if cur == _SPACE and c != _SPACE and text[i - 1] == 0x20:
+            if i - 1 > start:
+                out.append(text[start:i - 1])
+            start = i - 1
+        else:
+            out.append(text[start:i])
+            start = i
+        cur = c
+    if start < len(text):
+        out.append(text[start:])
+    return out
+
+
+class TokenizerError(ValueError):
+    pass
+
+
+def read_header(data: bytes) -> dict:
+    if len(data) >= 4 and data[:4] == b"MGNN":
+        if len(data) < 12:
+            raise TokenizerError("binary model file is truncated")
+        n = struct.unpack_from("<I", data, 8)[0]
+        return json.loads(data[12:12 + n])
+    return json.loads(data)
+
+
+class Tokenizer:
+    def __init__(self, vocab: list[str], merges: list[tuple[str, str]]):
+        self.vocab = list(vocab)
+        self.token_to_id = {}
+        for i, s in enumerate(self.vocab):
+            self.token_to_id[s] = i
+        self.ranks = {}
+        for r, (a, b) in enumerate(merges):
+            self.ranks[a + "\x00" + b] = r
+
+    @classmethod
+    def from_model_file(cls, data: bytes) -> "Tokenizer | None":
+        hdr = read_header(data)
+        vocab = hdr.get("vocab") or []
+        if not vocab:
+            return None
+        version = (hdr.get("metadata") or {}).get("tokenizer_version", 0)
+        if version != FORMAT_VERSION:
+            raise TokenizerError(f"tokenizer format version {version} is not supported (want {FORMAT_VERSION}): "
+                                 "retrain the model")
+        return cls(vocab, [(m["pair1"], m["pair2"]) for m in (hdr.get("merges") or [])])
+
+    def _special(self, tok):
+        return self.token_to_id.get(tok, -1)
+
+    def eos_id(self):
+        return self._special(EOS)
+
+    def user_id(self):
+        return self._special(USER)
+
+    def bot_id(self):
+        return self._special(BOT)
+
+    def pad_id(self):
+        return self.token_to_id.get(PAD, 0)
+
+    def encode_word(self, word: bytes) -> list[int]:
+        toks = [chr(r) for _, r, _ in runes(word)]
+        while len(toks) > 1:
+            best_rank, best = None, -1
+            for i in range(len(toks) - 1):
+                r = self.ranks.get(toks[i] + "\x00" + toks[i + 1])
+                if r is not None and (best_rank is None or r < best_rank):
+                    best_rank, best = r, i
+            if best < 0:
+                break
+            toks[best:best + 2] = [toks[best] + toks[best + 1]]
+        unk = self.token_to_id.get(UNK, 0)
+        return [self.token_to_id.get(t, unk) for t in toks]
+
+    def encode_plain(self, text: bytes) -> list[int]:
+        ids = []
+        for w in split_words(text):
+            ids.extend(self.encode_word(w))
+        return ids
+
+    def encode(self, text) -> list[int]:
+        if isinstance(text, str):
+            text = text.encode("utf-8")
+        ids = []
+        rem = text
+        while rem:
+            s = rem.find(b"<")
+            if s < 0:
+                ids.extend(self.encode_plain(rem))
+                break
+            e = rem.find(b">", s)
+            if e < 0:
+                ids.extend(self.encode_plain(rem))
+                break
+            cand = rem[s:e + 1]
+            try:
+                key = cand.decode("utf-8")
+            except UnicodeDecodeError:
+                key = None
+            if key is not None and key in self.token_to_id:
+                if s > 0:
+                    ids.extend(self.encode_plain(rem[:s]))
+                ids.append(self.token_to_id[key])
+                rem = rem[e + 1:]
+            else:
+                ids.extend(self.encode_plain(rem[:s + 1]))
+                rem = rem[s + 1:]
+        return ids
+
+    def decode(self, ids) -> bytes:
+        out = []
+        for i in ids:
+            i = int(i)
+            if 0 <= i < len(self.vocab):
+                t = self.vocab[i]
+                if t in (PAD, EOS, USER, BOT):
+                    continue
+                out.append("�" if t == UNK else t)
+        return "".join(out).encode("utf-8", errors="surrogatepass")
+
+    def encode_prompt(self, prompt) -> list[int]:
+        return [self.user_id()] + self.encode(prompt) + [self.bot_id()]
+
+    def encode_reply(self, reply) -> list[int]:
+        return self.encode(reply) + [self.eos_id()]
+
+    def drop_oldest_turns(self, history: list[int], max_len: int) -> list[int]:
+        eos = self.eos_id()
+        history = list(history)
+        while len(history) > max(max_len, 0):
+            if eos not in history:
+                return []
+            history = history[history.index(eos) + 1:]
+        return history
+
+    def token_bytes(self) -> list[int]:
+        return [len(self.decode([i])) for i in range(len(self.vocab))]
+
+
+def argmax_prob(logits) -> tuple[int, float]:
+    vals = [float(v) for v in logits]
+    best = 0
+    for i, v in enumerate(vals):
+        if v > vals[best]:
+            best = i
+    s = 0.0
+    for v in vals:
+        s += math.exp(v - vals[best])
+    return best, 1.0 / s
+
+
+def greedy_loop(session, context, max_tokens: int, stops=()) -> tuple[list[int], list[float]]:
+    ids, probs = [], []
+    logits = session.prefill(list(context)) if context else None
+    while len(ids) < max_tokens and logits is not None and len(logits) > 0:
+        best, prob = argmax_prob(logits)
+        if best in stops:
+            break
+        ids.append(best)
+        probs.append(prob)
+        if len(ids) < max_tokens:
+            logits = session.append(best)
+    return ids, probs
+
+
+def generate(model, tok: Tokenizer, prompt, context_size: int, max_tokens: int = 0, chat: bool = True):
+    """infer.Generate, greedy: (trimmed reply bytes, token ids, probabilities). `model` has new_session."""
+    if max_tokens <= 0:
+        max_tokens = CHAT_MAX_RESPONSE_TOKENS
+    ctx = tok.encode_prompt(prompt) if chat else tok.encode(prompt)
+    ids, probs = greedy_loop(model.new_session(context_size), ctx, max_tokens,
+                             stops=(tok.eos_id(), tok.user_id(), tok.bot_id()))
+    return tok.decode(ids).strip(), ids, probs
+
+
+def log_prob(logits, target: int) -> float:
+    m = max(float(v) for v in logits)
+    s = sum(math.exp(float(v) - m) for v in logits)
+    return float(logits[target]) - m - math.log(s)
+
+
+def score(call, tokens: list[int], context: int) -> list[float | None]:
+    """nll.score's per-target terms: log-prob of tokens[t] from window(tokens[:t], context), t = 1..len-1;
+    None where nothing is scored. `call(ids)` is quant.Model.Call (logits, or None/empty for no input)."""
+    out = []
+    for t in range(1, len(tokens)):
+        win = tokens[max(0, t - context):t] if context > 0 else []
+        logits = call(win) if win else None
+        tg = tokens[t]
+        out.append(log_prob(logits, tg) if logits is not None and len(logits) > 0 and 0 <= tg < len(logits) else None)
+    return out
+
+
+def held_out(terms, targets, token_bytes):
+    nats, nbytes, count = 0.0, 0, 0
+    for lp, tg in zip(terms, targets):
+        if lp is None:
+            continue
+        nats -= lp
+        nbytes += token_bytes[tg]
+        count += 1
+    if count == 0:
+        return dict(loss=0.0, ppl=0.0, bpb=0.0, tokens=0)
+    avg = nats / count
+    return dict(loss=avg, ppl=math.exp(avg), bpb=nats / (math.log(2) * nbytes) if nbytes > 0 else 0.0, tokens=count)
+
+
+def perplexity(call, tok: Tokenizer, text: bytes, context: int, max_tokens: int = 0):
+    if not text:
+        return held_out([], [], [])
+    tokens = tok.encode(text)
+    if len(tokens) < 2:
+        return held_out([], [], [])
+    num = len(tokens) - 1
+    if max_tokens > 0 and num > max_tokens:
+        num = max_tokens
+    tokens = tokens[:num + 1]
+    return held_out(score(call, tokens, context), tokens[1:], tok.token_bytes())
+
+
+def split_docs(text: bytes) -> list[bytes]:
+    docs = []
+    for d in text.split(DOC_SEPARATOR):
+        if d.startswith(DOC_PADDING):
+            d = d[len(DOC_PADDING):]
+        if d.endswith(DOC_PADDING):
+            d = d[:-len(DOC_PADDING)]
+        if d:
+            docs.append(d)
+    return docs
+
+
+def perplexity_per_doc(call, tok: Tokenizer, text: bytes, context: int, max_docs: int = 0):
+    docs = split_docs(text)
+    if max_docs > 0:
+        docs = docs[:max_docs]
+    terms, targets = [], []
+    for d in docs:
+        tokens = [tok.eos_id()] + tok.encode(d)
+        terms += score(call, tokens, context)
+        targets += tokens[1:]
+    return held_out(terms, targets, tok.token_bytes())

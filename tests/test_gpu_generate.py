@@ -1,6 +1,8 @@
-"""Greedy chat generation on the GPU engine against the CPU oracle, on the reference's trained
-order-search model (tests/golden/orders.mgn): the README's known answer, and every reply to the 168
-hand-written requests identical (tokens and text), one session at a time and as one batch of sessions."""
+"""The library's text layer on the GPU against the oracle's text path (oracle/text.py over the CPU oracle), on
+the reference's trained order-search model (tests/golden/orders.mgn): the README's known answer, and every
+reply to the 168 hand-written requests identical (tokens, text; probabilities within 1e-4), for one prompt
+at a time and all prompts in one batch."""
+import ctypes
 import json
 import os
 
@@ -8,7 +10,9 @@ import numpy as np
 import pytest
 
 from helpers import GOLDEN, oracle_model
+from mignon_ai_amd._lib import check, lib, ptr
 from mignon_ai_amd.generate import Generator
+from oracle import text as T
 
 pytestmark = pytest.mark.gpu
 
@@ -16,6 +20,7 @@ ORDERS = os.path.join(GOLDEN, "orders.mgn")
 REQUEST = "unpaid electronics orders over $500 from last month"
 ANSWER = "orders find --status unpaid --category electronics --min-amount 500 --when last-month"
 MAX_REPLY_TOKENS = 80  # examples/order-search/orders.js:20
+CONTEXT = 128
 PROB_RTOL = 1e-4
 
 
@@ -32,7 +37,7 @@ def gpu(data):
 
 @pytest.fixture(scope="module")
 def ref(data):
-    return Generator.from_bytes(data, provider=oracle_model(data))
+    return oracle_model(data), T.Tokenizer.from_model_file(data)
 
 
 @pytest.fixture(scope="module")
@@ -41,33 +46,56 @@ def requests_():
         return [p["instruction"].strip() for p in json.load(f)]
 
 
-def _same(a, b, what):
-    assert a.text == b.text, f"{what}: {a.text!r} != {b.text!r}"
-    assert [p.text for p in a.tokens] == [p.text for p in b.tokens], what
-    pa = np.array([p.prob for p in a.tokens])
-    pb = np.array([p.prob for p in b.tokens])
-    assert np.all(np.abs(pa - pb) <= PROB_RTOL * pb), what
+def _check(got, ref, prompt, max_tokens=MAX_REPLY_TOKENS, chat=True):
+    m, tok = ref
+    text, ids, probs = T.generate(m, tok, prompt, CONTEXT, max_tokens, chat=chat)
+    assert got.ids == ids, prompt
+    assert got.text == text.decode(), prompt
+    assert np.all(np.abs(np.array([p.prob for p in got.tokens]) - np.array(probs)) <= PROB_RTOL * np.array(probs))
 
 
 def test_readme_answer_on_gpu(gpu):
     r = gpu.generate(REQUEST)
     assert r.text == ANSWER
     assert len(r.tokens) > 3 and 0 < r.min_prob <= 1
+    assert "".join(p.text for p in r.tokens).strip() == r.text
 
 
 def test_replies_match_oracle(gpu, ref, requests_):
-    for q in requests_[::4]:
-        _same(gpu.generate(q, MAX_REPLY_TOKENS), ref.generate(q, MAX_REPLY_TOKENS), q)
+    for q in requests_[::6]:
+        _check(gpu.generate(q, MAX_REPLY_TOKENS), ref, q)
 
 
 def test_batched_replies_match_oracle(gpu, ref, requests_):
     got = gpu.generate_batch(requests_, MAX_REPLY_TOKENS)
     assert len(got) == len(requests_)
     for q, g in zip(requests_, got):
-        _same(g, ref.generate(q, MAX_REPLY_TOKENS), q)
+        _check(g, ref, q)
 
 
-def test_batched_max_tokens_and_empty(gpu):
+def test_max_tokens_and_empty_batch(gpu, ref):
     got = gpu.generate_batch(["unpaid orders", REQUEST], 2)
     assert all(len(r.tokens) <= 2 for r in got)
+    for q, g in zip(["unpaid orders", REQUEST], got):
+        _check(g, ref, q, max_tokens=2)
     assert gpu.generate_batch([]) == []
+    assert len(gpu.generate("unpaid orders").tokens) <= 60  # infer.DefaultMaxTokens
+
+
+def test_plain_continuation_and_empty_prompt(gpu, ref):
+    """DecodeGreedy with Chat false continues the raw text; an empty plain prompt prefills nothing and gets
+    no reply (greedy.go:43-49,66-67)."""
+    prompts = [b"orders find --status", b"", b"unpaid"]
+    n, K = len(prompts), 12
+    arr = (ctypes.c_char_p * n)(*prompts)
+    lens = (ctypes.c_size_t * n)(*[len(p) for p in prompts])
+    ids = np.full((n, K), -7, np.int32)
+    probs = np.zeros((n, K))
+    counts = np.full(n, -1, np.int32)
+    check(lib().mg_generate_greedy(gpu.model.handle, gpu.tok.handle, arr, lens, n, CONTEXT, K, 0, ptr(ids),
+                                   ptr(probs), ptr(counts)))
+    m, tok = ref
+    for i, p in enumerate(prompts):
+        _, want, _ = T.generate(m, tok, p, CONTEXT, K, chat=False)
+        assert counts[i] == len(want) and ids[i, :counts[i]].tolist() == want
+    assert counts[1] == 0
