@@ -11,6 +11,11 @@ is already resident in HBM:
   c4            4096 sessions: 32-token prefill + 64 greedy tokens (value counts generated tokens)
   c2            the standalone INT8 GEMM 262144 x 384 x 512 (value counts rows = tokens)
   c1            64 x 128 tokens of the tiny model: logits
+  score         eval.Perplexity over a 65536-token stream of the c3 model, context 128: one batched pass
+                over every target's window (mg_score_sequences; value counts scored targets)
+  chat          infer.Generate (greedy, chat template, at most 80 tokens) for the 168 order-search requests
+                x 24 on the reference's trained orders.mgn, all in one batch (mg_generate_greedy; value
+                counts requests)
 
 roofline: the kernel class with the largest share of the timed region, its algorithmic work per launch
 (int8 MACs x 2 for GEMMs, compulsory bytes for memory-bound kernels) over its average launch time, both
@@ -33,6 +38,8 @@ sys.path.insert(0, ROOT)
 METRIC = "INT8 tokens/sec (batched forward + decode); % of int8-MFMA / HBM roofline"
 PEAK_MFMA_TOPS = 5000.0   # MI355X dense int8 MFMA, TOP/s
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, GB/s
+SCORE_TOKENS, SCORE_CONTEXT = 65536, 128
+CHAT_REPEAT, CHAT_MAX_TOKENS = 24, 80   # max reply tokens: examples/order-search/orders.js:20
 
 
 def per_token_macs(spec):
@@ -172,6 +179,48 @@ def cpu_baseline_gemm(A, W, s, seconds):
                       f"as the reference"}
 
 
+def cpu_baseline_score(data, tokens, context, seconds):
+    """eval.Perplexity's loop as the reference runs it: one Call of the target's window per target, on one
+    core, over the first targets of the stream."""
+    from oracle import oracle as O
+    om = O.OracleModel(O.read_model(data))
+    tok = [int(t) for t in tokens]
+    done = [0]
+
+    def one():
+        t = 1 + done[0] % (len(tok) - 1)
+        om.call(tok[max(0, t - context):t])
+        done[0] += 1
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds / 2:
+        for _ in range(8):
+            one()
+    dt = time.perf_counter() - t0
+    return {"value": round(done[0] / dt, 1), "unit": "targets/s", "cores": 1, "kind": "port",
+            "sample": f"the first {done[0]} targets of the stream, one {context}-token window Call each (the "
+                      f"reference's sequential nll.score loop), {dt:.1f} s; C++ restatement of the reference Go "
+                      f"engine with AVX2 dot kernels"}
+
+
+def cpu_baseline_chat(data, requests, max_tokens, seconds):
+    """infer.Generate per request, sequentially, as the reference's web page and check.js run it."""
+    from oracle import oracle as O
+    from oracle import text as T
+    om = O.OracleModel(O.read_model(data))
+    tok = T.Tokenizer.from_model_file(data)
+    ctx = T.read_header(data)["metadata"]["context_size"]
+    n, gen = 0, 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds / 2:
+        _, ids, _ = T.generate(om, tok, requests[n % len(requests)], ctx, max_tokens)
+        n += 1
+        gen += len(ids)
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 1), "unit": "requests/s", "cores": 1, "kind": "port",
+            "sample": f"{n} requests ({gen} generated tokens) one after another, {dt:.1f} s; the restated "
+                      f"tokenizer and greedy loop over the C++ restatement of the reference Go engine"}
+
+
 def synth_ids(seed, tag, shape, V):
     from mignon_ai_amd import synth
     return synth.token_ids(seed, tag, shape, V)
@@ -226,6 +275,72 @@ def run(args):
         if not args.no_cpu_baseline:
             cpu = cpu_baseline_gemm(A, W, s, args.cpu_seconds)
         out["wall_s"] = round(wall, 3)
+    elif name == "score":
+        from mignon_ai_amd.evaluate import score_sequences
+        cfg = synth.CONFIGS["c3"]
+        spec = cfg["spec"]
+        data = mgnn.build_model_file(spec, args.seed, quantize_f32)
+        m = Model(data)
+        m.set_stream(torch.cuda.current_stream().cuda_stream)
+        N, W = SCORE_TOKENS, SCORE_CONTEXT
+        stream_ids = synth.token_ids(args.seed, "score:stream", (N,), spec.V)
+
+        def step():
+            score_sequences(m, [stream_ids], W)
+
+        ms, wall = timed(step, args.warmup, args.steps, torch, before=lambda: m.profile(True))
+        prof = m.profile_read()
+        m.profile(False)
+        targets = N - 1
+        rows = 1 + (N - 1 - W)
+        positions = W + (rows - 1) * W
+        macs = per_token_macs(spec)
+        work = {k: ("mfma", 2 * v * positions) for k, v in macs.items() if v and k not in ("gemm_logits", "gemm_probs")}
+        work["gemm_logits"] = ("mfma", 2 * macs["gemm_logits"] * targets)
+        out.update(value=round(targets / (ms / 1e3), 1), unit="targets/s", ms_per_step=round(ms, 4))
+        out["config"] = {"workload": f"score: eval.Perplexity over a {N}-token stream, context {W}, of the c3 model "
+                                     f"(D{spec.D} H{spec.H} {len(spec.blocks)} blocks heads {spec.heads} window "
+                                     f"{spec.window} V{spec.V}); host token stream in, per-target log-probs out",
+                         "tokens": N, "context": W, "window_rows": rows, "body_positions": positions,
+                         "params": spec.n_params}
+        dom, roof = roofline_for(prof, work, args.steps, None)
+        out["roofline"] = roof
+        out["kernels_ms_per_step"] = {k: round(v[1] / args.steps, 3) for k, v in sorted(prof.items(),
+                                                                                      key=lambda kv: -kv[1][1])}
+        out["wall_s"] = round(wall, 3)
+        if not args.no_cpu_baseline:
+            cpu = cpu_baseline_score(data, stream_ids, W, args.cpu_seconds)
+    elif name == "chat":
+        from mignon_ai_amd.generate import Generator
+        with open(os.path.join(ROOT, "tests", "golden", "orders.mgn"), "rb") as f:
+            data = f.read()
+        with open(os.path.join(ROOT, "tests", "golden", "orders_handwritten.json")) as f:
+            requests = [p["instruction"].strip() for p in json.load(f)]
+        g = Generator.from_bytes(data)
+        g.model.set_stream(torch.cuda.current_stream().cuda_stream)
+        batch = requests * CHAT_REPEAT
+        res = [None]
+
+        def step():
+            res[0] = g.generate_batch(batch, CHAT_MAX_TOKENS)
+
+        ms, wall = timed(step, args.warmup, args.steps, torch, before=lambda: g.model.profile(True))
+        prof = g.model.profile_read()
+        g.model.profile(False)
+        gen = sum(len(r.tokens) for r in res[0])
+        out.update(value=round(len(batch) / (ms / 1e3), 1), unit="requests/s", ms_per_step=round(ms, 4))
+        out["config"] = {"workload": f"chat: infer.Generate (greedy, chat template, max {CHAT_MAX_TOKENS} tokens) "
+                                     f"for the {len(requests)} order-search requests x {CHAT_REPEAT} in one batch, "
+                                     f"orders.mgn (the reference's trained 538k-parameter model); text in, text out",
+                         "requests": len(batch), "generated_tokens": gen,
+                         "generated_tokens_per_s": round(gen / (ms / 1e3), 1)}
+        out["data"] = "the reference's order-search requests (tests/golden/orders_handwritten.json)"
+        out["kernels_ms_per_step"] = {k: round(v[1] / args.steps, 3) for k, v in sorted(prof.items(),
+                                                                                      key=lambda kv: -kv[1][1])}
+        out["roofline"] = None
+        out["wall_s"] = round(wall, 3)
+        if not args.no_cpu_baseline:
+            cpu = cpu_baseline_chat(data, requests, CHAT_MAX_TOKENS, args.cpu_seconds)
     else:
         cfg = synth.CONFIGS[name]
         spec = cfg["spec"]
@@ -315,7 +430,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--config", default="c5", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--config", default="c5", choices=["c1", "c2", "c3", "c4", "c5", "score", "chat"])
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)

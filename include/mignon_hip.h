@@ -118,6 +118,14 @@ int mg_sessions_step(mg_sessions* s, const int32_t* ids, float* logits, int32_t*
 int mg_sessions_decode_greedy(mg_sessions* s, const int32_t* prompts, const int32_t* lens, int max_len,
                               int max_tokens, int32_t* out_ids, double* out_probs, int flags);
 
+/* generate.greedyLoop with stop tokens (internal/generate/greedy.go:63-87) for every session: as
+ * mg_sessions_decode_greedy, and each session's reply ends before the first of its n_stops (<= 8) stop
+ * ids; out_counts[n] receives the reply lengths. Entries of out_ids / out_probs past a session's count
+ * are unspecified: decoding ends once every session has stopped. */
+int mg_sessions_decode_greedy_until(mg_sessions* s, const int32_t* prompts, const int32_t* lens, int max_len,
+                                    int max_tokens, const int32_t* stops, int n_stops, int32_t* out_ids,
+                                    double* out_probs, int32_t* out_counts, int flags);
+
 /* quantSession.StateBytes (internal/quant/session.go:65-68, formula internal/quant/stream.go:87-101). */
 long long mg_sessions_state_bytes(const mg_sessions* s);
 /* Device bytes actually held per session. */

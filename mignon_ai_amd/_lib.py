@@ -64,6 +64,7 @@ SIGNATURES = {
     "mg_sessions_prefill": (_int, [_vp, _vp, _vp, _int, _vp, _vp, _vp, _int]),
     "mg_sessions_step": (_int, [_vp, _vp, _vp, _vp, _vp, _int]),
     "mg_sessions_decode_greedy": (_int, [_vp, _vp, _vp, _int, _int, _vp, _vp, _int]),
+    "mg_sessions_decode_greedy_until": (_int, [_vp, _vp, _vp, _int, _int, _vp, _int, _vp, _vp, _vp, _int]),
     "mg_sessions_state_bytes": (_ll, [_vp]),
     "mg_sessions_device_bytes": (_ll, [_vp]),
     "mg_sessions_count": (_int, [_vp]),

@@ -196,6 +196,17 @@ struct mg_sessions {
     mg_model* m = nullptr;
     int n = 0, window = 0;
     mg::DevBuf norm_ring, g, kring, vring, pos, next_ids, out_ids, out_probs, logits, argmax, prob;
+    // stop-token bookkeeping of mg_sessions_decode_greedy_until: per-session reply length, the stopped
+    // count, and a ring of pinned host slots the count is copied to after each step (one event each)
+    static constexpr int kStopRing = 8;
+    mg::DevBuf stop_count, stopped;
+    int32_t* stop_host = nullptr;
+    hipEvent_t stop_ev[kStopRing] = {};
+    ~mg_sessions() {
+        for (hipEvent_t& e : stop_ev)
+            if (e) (void)hipEventDestroy(e);
+        if (stop_host) (void)hipHostFree(stop_host);
+    }
 };
 
 namespace mg {
@@ -451,6 +462,38 @@ __global__ void window_ids_kernel(int S, int max_len, int window, int Tw, const 
     int L = min(len, window), off = len - L;
     for (int t = threadIdx.x; t < Tw; t += blockDim.x) out[(long long)s * Tw + t] = t < L ? in[(long long)s * max_len + off + t] : 0;
     if (threadIdx.x == 0) lens_out[s] = L;
+}
+
+// Stop tokens of a batched greedy decode: count[i] is -1 while session i runs, then the column of its first
+// stop token (its reply length); *stopped counts sessions that have stopped.
+constexpr int kMaxStops = 8;
+struct StopSet {
+    int32_t id[kMaxStops];
+    int n;
+};
+
+__global__ void stop_init_kernel(int S, int32_t* count, int32_t* stopped) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < S) count[i] = -1;
+    if (i == 0) *stopped = 0;
+}
+
+__global__ void stop_scan_kernel(int S, int col, const int32_t* ids, int ld, StopSet stops, int32_t* count,
+                                 int32_t* stopped) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= S || count[i] >= 0) return;
+    const int32_t t = ids[(long long)i * ld + col];
+    bool hit = false;
+    for (int k = 0; k < stops.n; k++) hit |= t == stops.id[k];
+    if (hit) {
+        count[i] = col;
+        atomicAdd(stopped, 1);
+    }
+}
+
+__global__ void stop_finish_kernel(int S, int max_tokens, int32_t* count) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < S && count[i] < 0) count[i] = max_tokens;
 }
 
 // Scoring windows: row r of a [B][T] token matrix is tokens[start[r] .. start[r] + len[r]), padded with id 0
@@ -1103,6 +1146,88 @@ int mg_sessions_decode_greedy(mg_sessions* s, const int32_t* prompts, const int3
         if (!dev) {
             HIPCHECK(hipMemcpyAsync(out_ids, oi, (size_t)S * max_tokens * 4, hipMemcpyDeviceToHost, st));
             if (out_probs) HIPCHECK(hipMemcpyAsync(out_probs, op, (size_t)S * max_tokens * 8, hipMemcpyDeviceToHost, st));
+            HIPCHECK(hipStreamSynchronize(st));
+        }
+        return MG_OK;
+    });
+}
+
+int mg_sessions_decode_greedy_until(mg_sessions* s, const int32_t* prompts, const int32_t* lens, int max_len,
+                                    int max_tokens, const int32_t* stops, int n_stops, int32_t* out_ids,
+                                    double* out_probs, int32_t* out_counts, int flags) {
+    return guarded([&] {
+        require(s && prompts && lens && out_ids && out_counts, "mg_sessions_decode_greedy_until: null argument");
+        require(max_len > 0 && max_tokens >= 0, "mg_sessions_decode_greedy_until: bad lengths");
+        require(n_stops >= 0 && n_stops <= kMaxStops && (n_stops == 0 || stops),
+                "mg_sessions_decode_greedy_until: at most 8 stop tokens");
+        mg_model* m = s->m;
+        Guard gd(m);
+        hipStream_t st = m->stream;
+        const bool dev = flags & MG_PTR_DEVICE;
+        const int S = s->n;
+        if (max_tokens == 0) {
+            if (dev) HIPCHECK(hipMemsetAsync(out_counts, 0, (size_t)S * 4, st));
+            else std::fill(out_counts, out_counts + S, 0);
+            return MG_OK;
+        }
+        if (!dev)
+            for (int i = 0; i < S; i++)
+                require(lens[i] >= 1 && lens[i] <= max_len,
+                        "mg_sessions_decode_greedy_until: lengths must be in 1..max_len");
+        StopSet set{};
+        set.n = n_stops;
+        for (int k = 0; k < n_stops; k++) set.id[k] = stops[k];
+        if (!s->stop_host) {
+            HIPCHECK(hipHostMalloc((void**)&s->stop_host, mg_sessions::kStopRing * sizeof(int32_t)));
+            for (hipEvent_t& e : s->stop_ev) HIPCHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        }
+        s->stop_count.ensure((size_t)S * 4);
+        s->stopped.ensure(16);
+        int32_t* cnt = s->stop_count.as<int32_t>();
+        int32_t* stopped = s->stopped.as<int32_t>();
+        Staging sg;
+        const int32_t* p_d = dev ? prompts : sg.in(prompts, (size_t)S * max_len, st);
+        const int32_t* l_d = dev ? lens : sg.in(lens, (size_t)S, st);
+        int32_t* oi = dev ? out_ids : sg.out<int32_t>((size_t)S * max_tokens);
+        double* op = out_probs ? (dev ? out_probs : sg.out<double>((size_t)S * max_tokens)) : nullptr;
+        const dim3 g1((S + 255) / 256), b1(256);
+        hipLaunchKernelGGL(stop_init_kernel, g1, b1, 0, st, S, cnt, stopped);
+        HIPCHECK(hipGetLastError());
+        auto scan = [&](int col) {
+            hipLaunchKernelGGL(stop_scan_kernel, g1, b1, 0, st, S, col, (const int32_t*)oi, max_tokens, set, cnt,
+                               stopped);
+            HIPCHECK(hipGetLastError());
+            const int slot = col % mg_sessions::kStopRing;
+            HIPCHECK(hipMemcpyAsync(s->stop_host + slot, stopped, 4, hipMemcpyDeviceToHost, st));
+            HIPCHECK(hipEventRecord(s->stop_ev[slot], st));
+        };
+        HeadCombineArgs hc;
+        hc.next_ids = s->next_ids.as<int32_t>();
+        hc.out_ids = oi; hc.out_probs = op; hc.out_ld = max_tokens; hc.out_col = 0;
+        prefill_device(s, p_d, l_d, max_len, nullptr, hc, st);
+        scan(0);
+        // The host stays at most kLag steps ahead of the device: before enqueuing step k it waits for the
+        // stopped count of column k-1-kLag, and ends the loop once every session has stopped.
+        constexpr int kLag = 2;
+        for (int k = 1; k < max_tokens; k++) {
+            const int c = k - 1 - kLag;
+            if (c >= 0) {
+                const int slot = c % mg_sessions::kStopRing;
+                HIPCHECK(hipEventSynchronize(s->stop_ev[slot]));
+                if (s->stop_host[slot] >= S) break;
+            }
+            hc.out_col = k;
+            step_device(s, s->next_ids.as<int32_t>(), nullptr, hc, st);
+            scan(k);
+        }
+        hipLaunchKernelGGL(stop_finish_kernel, g1, b1, 0, st, S, max_tokens, cnt);
+        HIPCHECK(hipGetLastError());
+        if (dev) {
+            HIPCHECK(hipMemcpyAsync(out_counts, cnt, (size_t)S * 4, hipMemcpyDeviceToDevice, st));
+        } else {
+            HIPCHECK(hipMemcpyAsync(out_ids, oi, (size_t)S * max_tokens * 4, hipMemcpyDeviceToHost, st));
+            if (out_probs) HIPCHECK(hipMemcpyAsync(out_probs, op, (size_t)S * max_tokens * 8, hipMemcpyDeviceToHost, st));
+            HIPCHECK(hipMemcpyAsync(out_counts, cnt, (size_t)S * 4, hipMemcpyDeviceToHost, st));
             HIPCHECK(hipStreamSynchronize(st));
         }
         return MG_OK;

@@ -209,26 +209,22 @@ int mg_generate_greedy(mg_model* m, mg_tokenizer* t, const char* const* prompts,
             std::copy(c.begin(), c.end(), arr.begin() + (size_t)r * L);
             lens[r] = (int32_t)c.size();
         }
-        std::vector<int32_t> ids((size_t)S * max_tokens);
+        std::vector<int32_t> ids((size_t)S * max_tokens), counts(S);
         std::vector<double> probs((size_t)S * max_tokens);
+        // greedyLoop stops before <EOS>, <USER> or <BOT> (those the vocabulary has)
+        std::vector<int32_t> stops;
+        for (int id : {t->tok->eos_id(), t->tok->user_id(), t->tok->bot_id()})
+            if (id >= 0) stops.push_back(id);
         mg_sessions* ss = nullptr;
         engine(mg_sessions_create(m, S, context, &ss));
-        const int rc = mg_sessions_decode_greedy(ss, arr.data(), lens.data(), L, max_tokens, ids.data(), probs.data(), 0);
+        const int rc = mg_sessions_decode_greedy_until(ss, arr.data(), lens.data(), L, max_tokens, stops.data(),
+                                                       (int)stops.size(), ids.data(), probs.data(), counts.data(), 0);
         mg_sessions_free(ss);
         engine(rc);
-        // greedyLoop stops before a stop token; a greedy token depends only on the tokens before it, so the
-        // batched decode's first stop token ends the reply
-        const int stops[3] = {t->tok->eos_id(), t->tok->user_id(), t->tok->bot_id()};
         for (int r = 0; r < S; r++) {
-            const int i = live[r];
-            int k = 0;
-            while (k < max_tokens) {
-                const int32_t id = ids[(size_t)r * max_tokens + k];
-                if (id == stops[0] || id == stops[1] || id == stops[2]) break;
-                out_ids[(size_t)i * max_tokens + k] = id;
-                out_probs[(size_t)i * max_tokens + k] = probs[(size_t)r * max_tokens + k];
-                k++;
-            }
+            const int i = live[r], k = counts[r];
+            std::copy_n(ids.begin() + (size_t)r * max_tokens, k, out_ids + (size_t)i * max_tokens);
+            std::copy_n(probs.begin() + (size_t)r * max_tokens, k, out_probs + (size_t)i * max_tokens);
             out_counts[i] = k;
         }
         return MG_OK;

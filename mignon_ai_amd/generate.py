@@ -30,15 +30,21 @@ class Piece:
 
 @dataclass
 class Result:
-    """infer.Result: the reply, trimmed of surrounding whitespace, and its tokens."""
+    """infer.Result: the reply, trimmed of surrounding whitespace, and its tokens (built on first use from
+    the token ids, their probabilities and the tokenizer's per-token texts)."""
     text: str
-    tokens: list[Piece] = field(default_factory=list)
     ids: list[int] = field(default_factory=list)
+    probs: list[float] = field(default_factory=list)
+    _texts: list[str] | None = field(default=None, repr=False, compare=False)
+
+    @property
+    def tokens(self) -> list[Piece]:
+        return [Piece(self._texts[t], p) for t, p in zip(self.ids, self.probs)]
 
     @property
     def min_prob(self) -> float:
         """infer.Result.MinProb (pkg/infer/infer.go:54-62)."""
-        return min((p.prob for p in self.tokens), default=1.0)
+        return min(self.probs, default=1.0)
 
 
 class Generator:
@@ -84,10 +90,10 @@ class Generator:
         counts = np.empty(n, np.int32)
         check(lib().mg_generate_greedy(self.model.handle, self.tok.handle, arr, lens, n, self.context_size(),
                                        max_tokens, int(self.task() == TASK_CHAT), ptr(ids), ptr(probs), ptr(counts)))
+        texts = self.tok.piece_texts()
         out = []
         for i in range(n):
             k = int(counts[i])
             row = ids[i, :k].tolist()
-            pieces = [Piece(self.tok.decode([t]), float(p)) for t, p in zip(row, probs[i, :k])]
-            out.append(Result(text=self.tok.decode(row).strip(), tokens=pieces, ids=row))
+            out.append(Result("".join([texts[t] for t in row]).strip(), row, probs[i, :k].tolist(), texts))
         return out

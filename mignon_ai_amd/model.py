@@ -185,6 +185,21 @@ class Sessions:
         check(lib().mg_sessions_decode_greedy(self._h, ptr(p), ptr(lens), L, int(max_tokens), ptr(ids), ptr(probs), 0))
         return ids, probs
 
+    def decode_greedy_until(self, prompts2d, max_tokens, stops, lens=None):
+        """greedyLoop with stop tokens: (ids [n][max_tokens], probs, counts [n]); row i's reply is
+        ids[i, :counts[i]] (it ends before the first stop token); later entries are unspecified."""
+        p = _i32(prompts2d)
+        n, L = p.shape
+        lens = _i32(lens if lens is not None else np.full(n, L))
+        st = _i32(list(stops))
+        ids = np.empty((n, max_tokens), np.int32)
+        probs = np.empty((n, max_tokens), np.float64)
+        counts = np.empty(n, np.int32)
+        check(lib().mg_sessions_decode_greedy_until(self._h, ptr(p), ptr(lens), L, int(max_tokens),
+                                                    ptr(st) if st.size else None, int(st.size), ptr(ids), ptr(probs),
+                                                    ptr(counts), 0))
+        return ids, probs, counts
+
     def decode_greedy_device(self, prompts, lens, max_tokens, out_ids, out_probs):
         n, L = prompts.shape
         check(lib().mg_sessions_decode_greedy(self._h, ptr(prompts), ptr(lens), L, int(max_tokens), ptr(out_ids),

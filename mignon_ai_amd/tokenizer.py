@@ -129,6 +129,13 @@ class Tokenizer:
     def decode(self, ids) -> str:
         return self.decode_bytes(ids).decode("utf-8", errors="replace")
 
+    def piece_texts(self) -> list[str]:
+        """Decode([id]) for every id (cached): the text each token contributes; Decode of a sequence is the
+        concatenation of its tokens' texts."""
+        if getattr(self, "_pieces", None) is None:
+            self._pieces = [self.decode([i]) for i in range(self.vocab_size())]
+        return self._pieces
+
     def token_bytes(self) -> list[int]:
         out = np.empty(self.vocab_size(), np.int32)
         check(lib().mg_tokenizer_token_bytes(self._h, ptr(out)))

@@ -3,7 +3,7 @@ import numpy as np
 import pytest
 
 from helpers import EQUIV_CASES, assert_close, equiv_model_bytes, model_bytes, oracle_model
-from mignon_ai_amd import Model, synth
+from mignon_ai_amd import MignonError, Model, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -76,3 +76,42 @@ def test_greedy_decode_matches_oracle():
     rid, rprob = om.greedy(prompts, G)
     assert np.array_equal(ids, rid)
     assert np.allclose(probs, rprob, rtol=1e-4)
+
+
+def _first_stop(row, stops, G):
+    for k, t in enumerate(row):
+        if int(t) in stops:
+            return k
+    return G
+
+
+def test_greedy_until_stops():
+    """greedyLoop with stop tokens (internal/generate/greedy.go:63-87) on device sessions: each reply is the
+    stop-free greedy decode cut before its first stop token, with the same probabilities, whether sessions
+    stop early, at the first token, or never (the loop ends once every session has stopped)."""
+    data = model_bytes("c3")
+    spec = synth.CONFIGS["c3"]["spec"]
+    gm = Model(data)
+    S, P, G = 64, 12, 40
+    prompts = synth.token_ids(8, "until:prompts", (S, P), spec.V)
+    lens = np.random.default_rng(2).integers(1, P + 1, S).astype(np.int32)
+    full_ids, full_probs = gm.sessions(S).decode_greedy(prompts, G, lens)
+    vals, freq = np.unique(full_ids, return_counts=True)
+    frequent = [int(v) for v in vals[np.argsort(-freq)][:3]]
+    v0, f0 = np.unique(full_ids[:, 0], return_counts=True)
+    first = [int(v) for v in v0[np.argsort(-f0)][:8]]
+    cases = [frequent, first, [], [spec.V + 5]]
+    for stops in cases:
+        ids, probs, counts = gm.sessions(S).decode_greedy_until(prompts, G, stops, lens)
+        for i in range(S):
+            k = _first_stop(full_ids[i], set(stops), G)
+            assert counts[i] == k, (stops, i)
+            assert np.array_equal(ids[i, :k], full_ids[i, :k])
+            assert np.array_equal(probs[i, :k], full_probs[i, :k])
+    # every session stops at its first token: all counts 0
+    same = np.repeat(prompts[:1], S, axis=0)
+    one = np.full(S, lens[0], np.int32)
+    _, _, counts = gm.sessions(S).decode_greedy_until(same, G, [int(full_ids[0, 0])], one)
+    assert not counts.any()
+    with pytest.raises(MignonError):
+        gm.sessions(S).decode_greedy_until(prompts, G, list(range(9)), lens)
