@@ -13,6 +13,8 @@ is already resident in HBM:
   c1            64 x 128 tokens of the tiny model: logits
   score         eval.Perplexity over a 65536-token stream of the c3 model, context 128: one batched pass
                 over every target's window (mg_score_sequences; value counts scored targets)
+  sample        c4's sessions and lengths with sampled tokens (temperature 0.7, top-k 40, top-p 0.9,
+                repetition penalty 1.2, trigram blocking; mg_sessions_decode_sample; value counts tokens)
   chat          infer.Generate (greedy, chat template, at most 80 tokens) for the 168 order-search requests
                 x 24 on the reference's trained orders.mgn, all in one batch (mg_generate_greedy; value
                 counts requests)
@@ -40,6 +42,7 @@ PEAK_MFMA_TOPS = 5000.0   # MI355X dense int8 MFMA, TOP/s
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, GB/s
 SCORE_TOKENS, SCORE_CONTEXT = 65536, 128
 CHAT_REPEAT, CHAT_MAX_TOKENS = 24, 80   # max reply tokens: examples/order-search/orders.js:20
+SAMPLE_PARAMS = dict(temperature=0.7, top_k=40, top_p=0.9, rep_penalty=1.2)
 
 
 def per_token_macs(spec):
@@ -342,7 +345,7 @@ def run(args):
         if not args.no_cpu_baseline:
             cpu = cpu_baseline_chat(data, requests, CHAT_MAX_TOKENS, args.cpu_seconds)
     else:
-        cfg = synth.CONFIGS[name]
+        cfg = synth.CONFIGS["c4" if name == "sample" else name]
         spec = cfg["spec"]
         data = mgnn.build_model_file(spec, args.seed, quantize_f32)
         m = Model(data)
@@ -381,16 +384,22 @@ def run(args):
                                          f"V{spec.V}; {outputs}", "B": B, "T": T, "params": spec.n_params}
             if not args.no_cpu_baseline:
                 cpu = cpu_baseline_forward(data, spec, B, T, args.cpu_seconds, args.seed)
-        else:  # c4
+        else:  # c4, sample
             S, P, G = cfg["B"], cfg["P"], cfg["G"]
-            prompts = torch.from_numpy(synth.token_ids(args.seed, "c4:prompts", (S, P), spec.V)).cuda()
+            prompts_h = synth.token_ids(args.seed, "c4:prompts", (S, P), spec.V)
+            prompts = torch.from_numpy(prompts_h).cuda()
             lens = torch.full((S,), P, dtype=torch.int32, device="cuda")
             oid = torch.empty((S, G), dtype=torch.int32, device="cuda")
             opb = torch.empty((S, G), dtype=torch.float64, device="cuda")
             sess = m.sessions(S)
+            if name == "sample":
+                seeds = list(range(S))
 
-            def step():
-                sess.decode_greedy_device(prompts, lens, G, oid, opb)
+                def step():
+                    sess.decode_sample(prompts_h, G, seeds, **SAMPLE_PARAMS)
+            else:
+                def step():
+                    sess.decode_greedy_device(prompts, lens, G, oid, opb)
 
             positions = S * (P + G - 1)
             work = {k: ("mfma", 2 * v * positions) for k, v in macs.items() if v and k != "gemm_probs"}
@@ -402,16 +411,19 @@ def run(args):
             m.profile(False)
             value = S * G / (ms / 1e3)
             out.update(value=round(value, 1), unit="generated tokens/s", ms_per_step=round(ms, 4))
-            out["config"] = {"workload": f"c4: {S} sessions, {P}-token prefill + {G} greedy tokens, D{spec.D} "
+            how = "greedy" if name == "c4" else "sampled (" + ", ".join(f"{k} {v}" for k, v in SAMPLE_PARAMS.items()) + ")"
+            out["config"] = {"workload": f"{name}: {S} sessions, {P}-token prefill + {G} {how} tokens, D{spec.D} "
                                          f"H{spec.H} {len(spec.blocks)} blocks heads {spec.heads} window "
                                          f"{spec.window} V{spec.V}", "sessions": S, "prompt": P, "generated": G,
                              "params": spec.n_params}
             if not args.no_cpu_baseline:
                 cpu = cpu_baseline_decode(data, spec, S, P, G, args.cpu_seconds, args.seed)
+                if name == "sample":
+                    cpu["sample"] += "; greedy choice in place of sampling (a lower bound of the reference's time)"
         dom, roof = roofline_for(prof, work, args.steps, name)
         out["roofline"] = roof
         total_macs = sum(v for k, v in macs.items() if k != "gemm_probs")
-        tok = (cfg["B"] * cfg["T"]) if name != "c4" else cfg["B"] * (cfg["P"] + cfg["G"] - 1)
+        tok = (cfg["B"] * cfg["T"]) if name not in ("c4", "sample") else cfg["B"] * (cfg["P"] + cfg["G"] - 1)
         path_tops = 2 * total_macs * tok / (ms / 1e3) / 1e12
         out["path_roofline"] = {"bound": "mfma", "achieved": round(path_tops, 2), "peak": PEAK_MFMA_TOPS,
                                 "unit": "TFLOP/s", "frac": round(path_tops / PEAK_MFMA_TOPS, 4),
@@ -430,7 +442,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--config", default="c5", choices=["c1", "c2", "c3", "c4", "c5", "score", "chat"])
+    ap.add_argument("--config", default="c5", choices=["c1", "c2", "c3", "c4", "c5", "score", "chat", "sample"])
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)

@@ -126,6 +126,33 @@ int mg_sessions_decode_greedy_until(mg_sessions* s, const int32_t* prompts, cons
                                     int max_tokens, const int32_t* stops, int n_stops, int32_t* out_ids,
                                     double* out_probs, int32_t* out_counts, int flags);
 
+/* generate.Sampling's numeric fields (internal/generate/chat.go:43-55): temperature <= 0.001 is argmax;
+ * rep_penalty > 1 scales down the last 6 tokens' logits; top_k <= 0 and top_p >= 0.9999 disable
+ * truncation. penalize_prompt: the repetition window starts in the prompt (generate.Text) rather than
+ * in the reply (generate.Chat). */
+typedef struct {
+    double temperature, rep_penalty, top_p;
+    int top_k, penalize_prompt;
+} mg_sampling_t;
+
+/* generate.SampleRawLogitsAdvanced (internal/generate/sample.go:31-171) for n rows of float64 logits [n][V]
+ * (V <= 8192): repetition penalty over recent[i][0..recent_len[i]) (recent_ld per row; recent may be NULL),
+ * then argmax, temperature sampling or top-k / top-p truncated sampling with the uniform u[i] in [0, 1)
+ * standing for the reference's rand.Float64(). Candidates of equal probability sort by token id (the
+ * reference's sort leaves their order open). out[n]. Runs on the current device. */
+int mg_sample_logits(const double* logits, int n, int V, const int32_t* recent, const int32_t* recent_len,
+                     int recent_ld, const mg_sampling_t* sp, const double* u, int32_t* out);
+
+/* generate.sampleContinuation (internal/generate/sample.go:196-247) for every session: Prefill, then per
+ * step the trigram ban over the reply, SampleRawLogitsAdvanced over the last 6 tokens of (prompt if
+ * penalize_prompt) + reply, a stop before any of the n_stops (<= 8) stop ids, Append. The reference
+ * draws from Go's global math/rand, randomly seeded; here session i's draw at step k is the (k+1)-th
+ * output of SplitMix64 seeded with seeds[i], top 53 bits over 2^53. out_ids [n][max_tokens],
+ * out_counts[n] as mg_sessions_decode_greedy_until. Vocabularies up to 8192 tokens. */
+int mg_sessions_decode_sample(mg_sessions* s, const int32_t* prompts, const int32_t* lens, int max_len, int max_tokens,
+                              const mg_sampling_t* sp, const uint64_t* seeds, const int32_t* stops, int n_stops,
+                              int32_t* out_ids, int32_t* out_counts, int flags);
+
 /* quantSession.StateBytes (internal/quant/session.go:65-68, formula internal/quant/stream.go:87-101). */
 long long mg_sessions_state_bytes(const mg_sessions* s);
 /* Device bytes actually held per session. */
@@ -187,6 +214,16 @@ long long mg_pretokenize(const char* text, size_t n, long long* ends, long long 
 int mg_generate_greedy(mg_model* m, mg_tokenizer* t, const char* const* prompts, const size_t* prompt_lens, int n,
                        int context, int max_tokens, int chat, int32_t* out_ids, double* out_probs,
                        int32_t* out_counts);
+
+/* infer.Generate's sampling branch (pkg/infer/infer.go:85-95) for n prompts at once: generate.Chat when
+ * chat != 0 (the prompt trimmed of surrounding whitespace, an empty one getting no reply, the chat template,
+ * the repetition window over the reply; internal/generate/chat.go:104-140), generate.Text otherwise (the
+ * prompt as is, the window starting in the prompt; chat.go:62-70). sp->penalize_prompt is ignored. Replies
+ * stop before <EOS>, <USER> or <BOT> or after max_tokens (> 0) tokens; seeds[i] seeds prompt i's draws
+ * (mg_sessions_decode_sample). out_ids [n][max_tokens], out_counts[n]. */
+int mg_generate_sample(mg_model* m, mg_tokenizer* t, const char* const* prompts, const size_t* prompt_lens, int n,
+                       int context, int max_tokens, int chat, const mg_sampling_t* sp, const uint64_t* seeds,
+                       int32_t* out_ids, int32_t* out_counts);
 
 /* eval.HeldOut (internal/eval/eval.go:12-17). */
 typedef struct {

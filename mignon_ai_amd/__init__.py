@@ -6,4 +6,5 @@ Python binding (model.py), the model-file writer (mgnn.py), the benchmark config
 synthetic weights (synth.py) and the build script (build.py).
 """
 from ._lib import LIB_PATH, MignonError, lib  # noqa: F401
-from .model import Model, Session, Sessions, engine_option, gemm_i8, gemm_i8_device, quantize_f32  # noqa: F401
+from .model import (Model, Session, Sessions, engine_option, gemm_i8, gemm_i8_device, quantize_f32,  # noqa: F401
+                    sample_logits)

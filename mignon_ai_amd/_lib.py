@@ -37,6 +37,12 @@ class ModelInfo(ctypes.Structure):
                 ("norm_ring", _int), ("attn_cache", _int), ("num_params", _ll)]
 
 
+class Sampling(ctypes.Structure):
+    """mg_sampling_t: generate.Sampling's numeric fields."""
+    _fields_ = [("temperature", ctypes.c_double), ("rep_penalty", ctypes.c_double), ("top_p", ctypes.c_double),
+                ("top_k", _int), ("penalize_prompt", _int)]
+
+
 class HeldOut(ctypes.Structure):
     """eval.HeldOut (internal/eval/eval.go:12-17)."""
     _fields_ = [("loss", ctypes.c_double), ("ppl", ctypes.c_double), ("bpb", ctypes.c_double), ("tokens", _ll)]
@@ -84,6 +90,9 @@ SIGNATURES = {
     "mg_pretokenize": (_ll, [ctypes.c_char_p, ctypes.c_size_t, _vp, _ll]),
     "mg_generate_greedy": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp, _vp, _vp]),
     "mg_perplexity": (_int, [_vp, _vp, ctypes.c_char_p, ctypes.c_size_t, _int, _int, _int, _vp]),
+    "mg_sample_logits": (_int, [_vp, _int, _int, _vp, _vp, _int, _vp, _vp, _vp]),
+    "mg_sessions_decode_sample": (_int, [_vp, _vp, _vp, _int, _int, _vp, _vp, _vp, _int, _vp, _vp, _int]),
+    "mg_generate_sample": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp, _vp, _vp, _vp]),
 }
 
 _lib = None

@@ -30,6 +30,7 @@
 #include "kernels.hpp"
 #include "model_file.hpp"
 #include "options.hpp"
+#include "sample.hpp"
 #include "text_abi.hpp"
 
 namespace mg {
@@ -115,12 +116,12 @@ struct DevBlock {
 // Kernel classes timed by the optional profiler (HIP events around every launch on the launch stream).
 enum KClass : int {
     K_ROW = 0, K_GEMM_LATCH, K_SCAN, K_LATCH_STEP, K_GEMM_GLU, K_GEMM_HIGHWAY, K_GEMM_QKV, K_ATTN, K_ATTN_STEP,
-    K_GEMM_OUT, K_GEMM_LOGITS, K_HEAD_COMBINE, K_GEMM_PROBS, K_BITS, K_EXPORT, K_GEMM_I8, K_NCLASS
+    K_GEMM_OUT, K_GEMM_LOGITS, K_HEAD_COMBINE, K_GEMM_PROBS, K_BITS, K_EXPORT, K_GEMM_I8, K_SAMPLE, K_NCLASS
 };
 const char* const kClassNames[K_NCLASS] = {
     "row_norm_pack", "gemm_latch", "latch_scan", "latch_step", "gemm_glu", "gemm_highway", "gemm_qkv",
     "attention", "attention_step", "gemm_out", "gemm_logits", "head_combine", "gemm_probs", "bits",
-    "state_export", "gemm_i8"};
+    "state_export", "gemm_i8", "sample"};
 
 struct Profile {
     bool on = false;
@@ -687,6 +688,69 @@ int guarded(F&& f) {
 
 constexpr long long kMaxChunkTokens = 1 << 19;  // tokens per workspace pass of a teacher-forced batch
 
+// Stop tokens of a batched decode: after each column is written, scan() marks the sessions whose token is
+// a stop token and copies the stopped count into a pinned host slot behind an event; keep_going(k) holds
+// the host at most kLag steps ahead of the device and says whether step k is still needed.
+struct StopTracker {
+    static constexpr int kLag = 2;
+    mg_sessions* s;
+    int S, max_tokens;
+    StopSet set;
+    const int32_t* ids;
+    int32_t *cnt, *stopped;
+    hipStream_t st;
+
+    StopTracker(mg_sessions* ss, int max_tok, const int32_t* stops, int n_stops, const int32_t* out_ids_d,
+                hipStream_t stream)
+        : s(ss), S(ss->n), max_tokens(max_tok), set{}, ids(out_ids_d), st(stream) {
+        set.n = n_stops;
+        for (int k = 0; k < n_stops; k++) set.id[k] = stops[k];
+        if (!s->stop_host) {
+            HIPCHECK(hipHostMalloc((void**)&s->stop_host, mg_sessions::kStopRing * sizeof(int32_t)));
+            for (hipEvent_t& e : s->stop_ev) HIPCHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        }
+        s->stop_count.ensure((size_t)S * 4);
+        s->stopped.ensure(16);
+        cnt = s->stop_count.as<int32_t>();
+        stopped = s->stopped.as<int32_t>();
+        hipLaunchKernelGGL(stop_init_kernel, dim3((S + 255) / 256), dim3(256), 0, st, S, cnt, stopped);
+        HIPCHECK(hipGetLastError());
+    }
+    void scan(int col) {
+        hipLaunchKernelGGL(stop_scan_kernel, dim3((S + 255) / 256), dim3(256), 0, st, S, col, ids, max_tokens, set, cnt,
+                           stopped);
+        HIPCHECK(hipGetLastError());
+        const int slot = col % mg_sessions::kStopRing;
+        HIPCHECK(hipMemcpyAsync(s->stop_host + slot, stopped, 4, hipMemcpyDeviceToHost, st));
+        HIPCHECK(hipEventRecord(s->stop_ev[slot], st));
+    }
+    bool keep_going(int k) {
+        const int c = k - 1 - kLag;
+        if (c < 0) return true;
+        const int slot = c % mg_sessions::kStopRing;
+        HIPCHECK(hipEventSynchronize(s->stop_ev[slot]));
+        return s->stop_host[slot] < S;
+    }
+    void finish() {
+        hipLaunchKernelGGL(stop_finish_kernel, dim3((S + 255) / 256), dim3(256), 0, st, S, max_tokens, cnt);
+        HIPCHECK(hipGetLastError());
+    }
+};
+
+// Outputs of a batched decode: device calls leave ids (and probabilities) where they were written and
+// only move the reply lengths; host calls copy everything back and wait.
+void copy_decode_outputs(bool dev, int S, int max_tokens, const int32_t* oi, const double* op, const int32_t* cnt,
+                         int32_t* out_ids, double* out_probs, int32_t* out_counts, hipStream_t st) {
+    if (dev) {
+        HIPCHECK(hipMemcpyAsync(out_counts, cnt, (size_t)S * 4, hipMemcpyDeviceToDevice, st));
+        return;
+    }
+    HIPCHECK(hipMemcpyAsync(out_ids, oi, (size_t)S * max_tokens * 4, hipMemcpyDeviceToHost, st));
+    if (out_probs && op) HIPCHECK(hipMemcpyAsync(out_probs, op, (size_t)S * max_tokens * 8, hipMemcpyDeviceToHost, st));
+    HIPCHECK(hipMemcpyAsync(out_counts, cnt, (size_t)S * 4, hipMemcpyDeviceToHost, st));
+    HIPCHECK(hipStreamSynchronize(st));
+}
+
 }  // namespace
 }  // namespace mg
 
@@ -1165,71 +1229,131 @@ int mg_sessions_decode_greedy_until(mg_sessions* s, const int32_t* prompts, cons
         hipStream_t st = m->stream;
         const bool dev = flags & MG_PTR_DEVICE;
         const int S = s->n;
-        if (max_tokens == 0) {
-            if (dev) HIPCHECK(hipMemsetAsync(out_counts, 0, (size_t)S * 4, st));
-            else std::fill(out_counts, out_counts + S, 0);
-            return MG_OK;
-        }
         if (!dev)
             for (int i = 0; i < S; i++)
                 require(lens[i] >= 1 && lens[i] <= max_len,
                         "mg_sessions_decode_greedy_until: lengths must be in 1..max_len");
-        StopSet set{};
-        set.n = n_stops;
-        for (int k = 0; k < n_stops; k++) set.id[k] = stops[k];
-        if (!s->stop_host) {
-            HIPCHECK(hipHostMalloc((void**)&s->stop_host, mg_sessions::kStopRing * sizeof(int32_t)));
-            for (hipEvent_t& e : s->stop_ev) HIPCHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        if (max_tokens == 0) {
+            if (!dev) std::fill(out_counts, out_counts + S, 0);
+            else HIPCHECK(launch_fill_i32(out_counts, S, 0, st));
+            return MG_OK;
         }
-        s->stop_count.ensure((size_t)S * 4);
-        s->stopped.ensure(16);
-        int32_t* cnt = s->stop_count.as<int32_t>();
-        int32_t* stopped = s->stopped.as<int32_t>();
         Staging sg;
         const int32_t* p_d = dev ? prompts : sg.in(prompts, (size_t)S * max_len, st);
         const int32_t* l_d = dev ? lens : sg.in(lens, (size_t)S, st);
         int32_t* oi = dev ? out_ids : sg.out<int32_t>((size_t)S * max_tokens);
         double* op = out_probs ? (dev ? out_probs : sg.out<double>((size_t)S * max_tokens)) : nullptr;
-        const dim3 g1((S + 255) / 256), b1(256);
-        hipLaunchKernelGGL(stop_init_kernel, g1, b1, 0, st, S, cnt, stopped);
-        HIPCHECK(hipGetLastError());
-        auto scan = [&](int col) {
-            hipLaunchKernelGGL(stop_scan_kernel, g1, b1, 0, st, S, col, (const int32_t*)oi, max_tokens, set, cnt,
-                               stopped);
-            HIPCHECK(hipGetLastError());
-            const int slot = col % mg_sessions::kStopRing;
-            HIPCHECK(hipMemcpyAsync(s->stop_host + slot, stopped, 4, hipMemcpyDeviceToHost, st));
-            HIPCHECK(hipEventRecord(s->stop_ev[slot], st));
-        };
+        StopTracker tr(s, max_tokens, stops, n_stops, oi, st);
         HeadCombineArgs hc;
         hc.next_ids = s->next_ids.as<int32_t>();
         hc.out_ids = oi; hc.out_probs = op; hc.out_ld = max_tokens; hc.out_col = 0;
         prefill_device(s, p_d, l_d, max_len, nullptr, hc, st);
-        scan(0);
-        // The host stays at most kLag steps ahead of the device: before enqueuing step k it waits for the
-        // stopped count of column k-1-kLag, and ends the loop once every session has stopped.
-        constexpr int kLag = 2;
-        for (int k = 1; k < max_tokens; k++) {
-            const int c = k - 1 - kLag;
-            if (c >= 0) {
-                const int slot = c % mg_sessions::kStopRing;
-                HIPCHECK(hipEventSynchronize(s->stop_ev[slot]));
-                if (s->stop_host[slot] >= S) break;
-            }
+        tr.scan(0);
+        for (int k = 1; k < max_tokens && tr.keep_going(k); k++) {
             hc.out_col = k;
             step_device(s, s->next_ids.as<int32_t>(), nullptr, hc, st);
-            scan(k);
+            tr.scan(k);
         }
-        hipLaunchKernelGGL(stop_finish_kernel, g1, b1, 0, st, S, max_tokens, cnt);
-        HIPCHECK(hipGetLastError());
-        if (dev) {
-            HIPCHECK(hipMemcpyAsync(out_counts, cnt, (size_t)S * 4, hipMemcpyDeviceToDevice, st));
-        } else {
-            HIPCHECK(hipMemcpyAsync(out_ids, oi, (size_t)S * max_tokens * 4, hipMemcpyDeviceToHost, st));
-            if (out_probs) HIPCHECK(hipMemcpyAsync(out_probs, op, (size_t)S * max_tokens * 8, hipMemcpyDeviceToHost, st));
-            HIPCHECK(hipMemcpyAsync(out_counts, cnt, (size_t)S * 4, hipMemcpyDeviceToHost, st));
-            HIPCHECK(hipStreamSynchronize(st));
+        tr.finish();
+        copy_decode_outputs(dev, S, max_tokens, oi, op, tr.cnt, out_ids, out_probs, out_counts, st);
+        return MG_OK;
+    });
+}
+
+int mg_sessions_decode_sample(mg_sessions* s, const int32_t* prompts, const int32_t* lens, int max_len, int max_tokens,
+                              const mg_sampling_t* sp, const uint64_t* seeds, const int32_t* stops, int n_stops,
+                              int32_t* out_ids, int32_t* out_counts, int flags) {
+    return guarded([&] {
+        require(s && prompts && lens && sp && seeds && out_ids && out_counts, "mg_sessions_decode_sample: null argument");
+        require(max_len > 0 && max_tokens >= 0, "mg_sessions_decode_sample: bad lengths");
+        require(n_stops >= 0 && n_stops <= kMaxStops && (n_stops == 0 || stops),
+                "mg_sessions_decode_sample: at most 8 stop tokens");
+        mg_model* m = s->m;
+        if (m->V > kMaxSampleVocab)
+            throw Error(MG_ERR_UNSUPPORTED, "mg_sessions_decode_sample: vocabularies above " +
+                                                std::to_string(kMaxSampleVocab) + " tokens are not supported");
+        Guard gd(m);
+        hipStream_t st = m->stream;
+        const bool dev = flags & MG_PTR_DEVICE;
+        const int S = s->n, V = m->V;
+        if (!dev)
+            for (int i = 0; i < S; i++)
+                require(lens[i] >= 1 && lens[i] <= max_len, "mg_sessions_decode_sample: lengths must be in 1..max_len");
+        if (max_tokens == 0) {
+            if (!dev) std::fill(out_counts, out_counts + S, 0);
+            else HIPCHECK(launch_fill_i32(out_counts, S, 0, st));
+            return MG_OK;
         }
+        Staging sg;
+        const int32_t* p_d = dev ? prompts : sg.in(prompts, (size_t)S * max_len, st);
+        const int32_t* l_d = dev ? lens : sg.in(lens, (size_t)S, st);
+        const uint64_t* seed_d = dev ? seeds : sg.in(seeds, (size_t)S, st);
+        int32_t* oi = dev ? out_ids : sg.out<int32_t>((size_t)S * max_tokens);
+        s->logits.ensure((size_t)S * V * 4);
+        float* lg = s->logits.as<float>();
+        StopTracker tr(s, max_tokens, stops, n_stops, oi, st);
+        SampleArgs sa;
+        sa.n = S; sa.V = V; sa.n2 = sample_n2(V);
+        sa.logits32 = lg; sa.ld = V;
+        if (sp->penalize_prompt) {
+            sa.prefix = p_d; sa.prefix_ld = max_len; sa.prefix_len = l_d;
+        }
+        sa.hist = oi; sa.hist_ld = max_tokens; sa.trigram = true;
+        sa.p.temperature = sp->temperature; sa.p.rep_penalty = sp->rep_penalty;
+        sa.p.top_p = sp->top_p; sa.p.top_k = sp->top_k;
+        sa.seeds = seed_d;
+        sa.out = oi; sa.out_ld = max_tokens;
+        sa.next_ids = s->next_ids.as<int32_t>();
+        auto pick = [&](int col) {
+            sa.col = col; sa.step = col; sa.out_col = col;
+            ProfScope ps(m->prof, K_SAMPLE, st);
+            HIPCHECK(launch_sample(sa, st));
+            tr.scan(col);
+        };
+        HeadCombineArgs hc;  // the sampler, not the argmax, picks each token
+        prefill_device(s, p_d, l_d, max_len, lg, hc, st);
+        pick(0);
+        for (int k = 1; k < max_tokens && tr.keep_going(k); k++) {
+            step_device(s, s->next_ids.as<int32_t>(), lg, hc, st);
+            pick(k);
+        }
+        tr.finish();
+        copy_decode_outputs(dev, S, max_tokens, oi, nullptr, tr.cnt, out_ids, nullptr, out_counts, st);
+        return MG_OK;
+    });
+}
+
+int mg_sample_logits(const double* logits, int n, int V, const int32_t* recent, const int32_t* recent_len,
+                     int recent_ld, const mg_sampling_t* sp, const double* u, int32_t* out) {
+    return guarded([&] {
+        require(logits && sp && u && out && (recent == nullptr || recent_len), "mg_sample_logits: null argument");
+        require(n >= 0 && V > 0 && recent_ld >= 0, "mg_sample_logits: bad shape");
+        if (V > kMaxSampleVocab)
+            throw Error(MG_ERR_UNSUPPORTED, "mg_sample_logits: vocabularies above " + std::to_string(kMaxSampleVocab) +
+                                                " tokens are not supported");
+        if (n == 0) return MG_OK;
+        int dev = 0;
+        HIPCHECK(hipGetDevice(&dev));
+        hipStream_t st = nullptr;
+        Staging sg;
+        SampleArgs sa;
+        sa.n = n; sa.V = V; sa.n2 = sample_n2(V);
+        sa.logits64 = sg.in(logits, (size_t)n * V, st); sa.ld = V;
+        if (recent) {
+            for (int i = 0; i < n; i++)
+                require(recent_len[i] >= 0 && recent_len[i] <= recent_ld, "mg_sample_logits: bad recent length");
+            sa.prefix = sg.in(recent, (size_t)n * recent_ld, st);
+            sa.prefix_ld = recent_ld;
+            sa.prefix_len = sg.in(recent_len, (size_t)n, st);
+        }
+        sa.p.temperature = sp->temperature; sa.p.rep_penalty = sp->rep_penalty;
+        sa.p.top_p = sp->top_p; sa.p.top_k = sp->top_k;
+        sa.u = sg.in(u, (size_t)n, st);
+        int32_t* o = sg.out<int32_t>((size_t)n);
+        sa.out = o; sa.out_ld = 1;
+        HIPCHECK(launch_sample(sa, st));
+        HIPCHECK(hipMemcpyAsync(out, o, (size_t)n * 4, hipMemcpyDeviceToHost, st));
+        HIPCHECK(hipStreamSynchronize(st));
         return MG_OK;
     });
 }

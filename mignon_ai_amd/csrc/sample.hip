@@ -1,0 +1,342 @@
+// Token sampling on the device: generate.SampleRawLogitsAdvanced (internal/generate/sample.go:31-171) and
+// the per-step rules of sampleContinuation (sample.go:196-247: trigram blocking, repetition window), one
+// workgroup per row.
+//
+// Every quantity the reference computes in float64 is computed in float64 here, in the reference's order:
+// the softmax denominators and every cumulative sum are sequential sums in the order the reference adds
+// (index order, or descending probability after the sort), so the chosen token is the one the reference
+// picks for the same logits and the same uniform draw. The candidate sort orders equal probabilities by
+// token index (Go's pdqsort leaves their order unspecified).
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cstdint>
+
+#include "sample.hpp"
+
+namespace mg {
+
+namespace {
+
+constexpr int kThreads = 256;
+
+// SplitMix64's output function (Vigna): the uniform of draw k from seed s is the top 53 bits of
+// mix64(s + k * golden), k = step + 1, i.e. the k-th output of a SplitMix64 generator seeded with s.
+__device__ __forceinline__ double uniform_draw(uint64_t seed, int step) {
+    uint64_t z = seed + 0x9E3779B97F4A7C15ull * (uint64_t)(step + 1);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return (double)(z >> 11) * 0x1.0p-53;
+}
+
+// (value, index) ordering of the candidate sort: larger value first, then smaller index
+__device__ __forceinline__ bool before(double va, int ia, double vb, int ib) {
+    return va > vb || (va == vb && ia < ib);
+}
+
+__device__ void bitonic_desc(double* key, int* idx, int n2) {
+    for (int k = 2; k <= n2; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = threadIdx.x; i < n2; i += blockDim.x) {
+                const int l = i ^ j;
+                if (l > i) {
+                    const bool up = (i & k) == 0;  // this block of k ends up in descending order
+                    const double a = key[i], b = key[l];
+                    const int ia = idx[i], ib = idx[l];
+                    const bool swap = up ? before(b, ib, a, ia) : before(a, ia, b, ib);
+                    if (swap) {
+                        key[i] = b; key[l] = a;
+                        idx[i] = ib; idx[l] = ia;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+__device__ __forceinline__ void block_argmax(double v, int i, double* red_v, int* red_i, double& best_v, int& best_i) {
+    // first maximum: larger value, then smaller index
+    for (int o = 32; o > 0; o >>= 1) {
+        const double ov = __shfl_xor(v, o);
+        const int oi = __shfl_xor(i, o);
+        if (before(ov, oi, v, i)) { v = ov; i = oi; }
+    }
+    const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if ((threadIdx.x & 63) == 0) { red_v[w] = v; red_i[w] = i; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double bv = red_v[0];
+        int bi = red_i[0];
+        for (int k = 1; k < nw; k++)
+            if (before(red_v[k], red_i[k], bv, bi)) { bv = red_v[k]; bi = red_i[k]; }
+        red_v[0] = bv; red_i[0] = bi;
+    }
+    __syncthreads();
+    best_v = red_v[0];
+    best_i = red_i[0];
+    __syncthreads();
+}
+
+// Sequential float64 sum x[0] + x[1] + ... in that order (the reference's loop); with prefix, x[i] is
+// replaced by the running sum through i. One lane; the next eight values are read before the current eight
+// are added.
+__device__ double seq_sum(double* x, int n, bool prefix) {
+    double s = 0.0;
+    const int n8 = ((uintptr_t)x & 15) == 0 ? n & ~7 : 0;
+    if (n8) {
+        double2 b0 = *(const double2*)(x), b1 = *(const double2*)(x + 2);
+        double2 b2 = *(const double2*)(x + 4), b3 = *(const double2*)(x + 6);
+        for (int i = 0; i < n8; i += 8) {
+            const int j = min(i + 8, n8 - 8);  // the next batch (the last batch reads itself again)
+            const double2 c0 = *(const double2*)(x + j), c1 = *(const double2*)(x + j + 2);
+            const double2 c2 = *(const double2*)(x + j + 4), c3 = *(const double2*)(x + j + 6);
+            double2 o0, o1, o2, o3;
+            s += b0.x; o0.x = s; s += b0.y; o0.y = s;
+            s += b1.x; o1.x = s; s += b1.y; o1.y = s;
+            s += b2.x; o2.x = s; s += b2.y; o2.y = s;
+            s += b3.x; o3.x = s; s += b3.y; o3.y = s;
+            if (prefix) {
+                *(double2*)(x + i) = o0; *(double2*)(x + i + 2) = o1;
+                *(double2*)(x + i + 4) = o2; *(double2*)(x + i + 6) = o3;
+            }
+            b0 = c0; b1 = c1; b2 = c2; b3 = c3;
+        }
+    }
+    for (int i = n8; i < n; i++) {
+        s += x[i];
+        if (prefix) x[i] = s;
+    }
+    return s;
+}
+
+// The first k with r <= x[0] + ... + x[k] (summed in order), or dflt: the sequential scan of the
+// reference, for short candidate lists.
+__device__ int seq_find(const double* x, int n, double r, int dflt) {
+    double cum = 0.0;
+    for (int i = 0; i < n; i++) {
+        cum += x[i];
+        if (r <= cum) return i;
+    }
+    return dflt;
+}
+
+constexpr int kExtract = 64;  // candidates taken one by one before falling back to a full sort
+
+__global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
+    __shared__ double cand_v[kExtract];
+    __shared__ int cand_i[kExtract];
+    extern __shared__ __align__(16) double smp_smem[];
+    __shared__ double red_v[kThreads / 64];
+    __shared__ int red_i[kThreads / 64];
+    __shared__ int chosen_sh;
+    const int row = blockIdx.x;
+    const int V = a.V, n2 = a.n2;
+    double* key = smp_smem;           // [n2] logits, then probabilities
+    int* idx = (int*)(smp_smem + n2);  // [n2] token ids once sorted
+    const long long base = (long long)row * a.ld;
+    for (int i = threadIdx.x; i < V; i += blockDim.x)
+        key[i] = a.logits32 ? (double)a.logits32[base + i] : a.logits64[base + i];
+    __syncthreads();
+
+    if (threadIdx.x == 0) {
+        const int col = a.hist ? a.col : 0;
+        const int32_t* g = a.hist ? a.hist + (long long)row * a.hist_ld : nullptr;
+        // trigram blocking over the generated tokens (sample.go:211-224)
+        if (a.trigram && col >= 2) {
+            const int32_t w1 = g[col - 2], w2 = g[col - 1];
+            for (int i = 0; i + 2 < col; i++)
+                if (g[i] == w1 && g[i + 1] == w2) {
+                    const int32_t b = g[i + 2];
+                    if (b >= 0 && b < V) key[b] = -DBL_MAX;
+                }
+        }
+        // repetition penalty over the last kRepWindow tokens of prefix + generated, each distinct
+        // token once (sample.go:47-66, window sample.go:206-209)
+        if (a.p.rep_penalty > 1.0) {
+            int32_t w[kRepWindow];
+            int nwin = 0;
+            const int from_hist = min(col, kRepWindow);
+            const int plen = a.prefix_len ? a.prefix_len[row] : 0;
+            const int from_pre = min(plen, kRepWindow - from_hist);
+            const int32_t* pre = a.prefix ? a.prefix + (long long)row * a.prefix_ld : nullptr;
+            for (int k = plen - from_pre; k < plen; k++) w[nwin++] = pre[k];
+            for (int k = col - from_hist; k < col; k++) w[nwin++] = g[k];
+            for (int i = 0; i < nwin; i++) {
+                const int32_t t = w[i];
+                if (t < 0 || t >= V) continue;
+                bool seen = false;
+                for (int j = 0; j < i; j++) seen |= w[j] == t;
+                if (!seen) key[t] = key[t] > 0 ? key[t] / a.p.rep_penalty : key[t] * a.p.rep_penalty;
+            }
+        }
+    }
+    __syncthreads();
+
+    int chosen = 0;
+    if (a.p.temperature <= 0.001) {
+        double v = -INFINITY;  // the first maximum, as the reference's scan from index 0
+        int bi = 0x7fffffff;
+        for (int i = threadIdx.x; i < V; i += blockDim.x)
+            if (before(key[i], i, v, bi)) { v = key[i]; bi = i; }
+        double bv;
+        block_argmax(v, bi, red_v, red_i, bv, chosen);
+    } else {
+        const double invT = 1.0 / a.p.temperature;
+        double v = -DBL_MAX;
+        for (int i = threadIdx.x; i < V; i += blockDim.x) {
+            const double sc = key[i] * invT;
+            key[i] = sc;
+            v = fmax(v, sc);
+        }
+        double mx;
+        int dummy;
+        block_argmax(v, 0, red_v, red_i, mx, dummy);
+        for (int i = threadIdx.x; i < V; i += blockDim.x) key[i] = exp(key[i] - mx);
+        __syncthreads();
+        const double u = a.u ? a.u[row] : uniform_draw(a.seeds[row], a.step);
+        if (a.p.top_k <= 0 && a.p.top_p >= 0.9999) {
+            // pure temperature sampling (sample.go:91-109): the running sums never decrease (every term
+            // is >= 0), so the first index whose running sum reaches r is the count of those below it
+            if (threadIdx.x == 0) red_v[0] = u * seq_sum(key, V, true);
+            __syncthreads();
+            const double r = red_v[0];
+            int below = 0;
+            for (int i = threadIdx.x; i < V; i += blockDim.x) below += key[i] < r;
+            for (int o = 32; o > 0; o >>= 1) below += __shfl_xor(below, o);
+            __syncthreads();
+            if ((threadIdx.x & 63) == 0) red_i[threadIdx.x >> 6] = below;
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                int t = 0;
+                for (int w = 0; w < (int)(blockDim.x >> 6); w++) t += red_i[w];
+                chosen_sh = t < V ? t : 0;
+            }
+            __syncthreads();
+            chosen = chosen_sh;
+        } else {
+            // truncated sampling (sample.go:111-171): probabilities p / sum(p), then the candidates in
+            // descending order (equal probabilities by token id), cut by top-k and top-p
+            if (threadIdx.x == 0) red_v[0] = 1.0 / seq_sum(key, V, false);
+            __syncthreads();
+            const double inv = red_v[0];
+            for (int i = threadIdx.x; i < V; i += blockDim.x) key[i] *= inv;
+            __syncthreads();
+            const int kcap = (a.p.top_k > 0 && a.p.top_k < V) ? a.p.top_k : V;
+            const bool use_p = a.p.top_p > 0.0 && a.p.top_p < 1.0;
+            int active = 0;
+            const double* cv = cand_v;
+            const int* ci = cand_i;
+            if (kcap <= kExtract || use_p) {
+                // the candidates one at a time, most probable first, until top-k or top-p is met
+                const int rounds = min(kcap, kExtract);
+                double cp = 0.0;
+                for (int r = 0; r < rounds && active == 0; r++) {
+                    double bv = -INFINITY;
+                    int bi = 0x7fffffff;
+                    for (int i = threadIdx.x; i < V; i += blockDim.x)
+                        if (before(key[i], i, bv, bi)) { bv = key[i]; bi = i; }
+                    double best_v;
+                    int best_i;
+                    block_argmax(bv, bi, red_v, red_i, best_v, best_i);
+                    if (threadIdx.x == 0) {
+                        cand_v[r] = best_v;
+                        cand_i[r] = best_i;
+                        key[best_i] = -2.0;  // taken: below every probability
+                        cp += best_v;
+                        chosen_sh = (use_p && cp >= a.p.top_p) ? r + 1 : (r + 1 == kcap ? kcap : 0);
+                    }
+                    __syncthreads();
+                    active = chosen_sh;
+                    __syncthreads();
+                }
+                if (active == 0) {  // top-p not reached within kExtract candidates: sort them all
+                    if (threadIdx.x == 0)
+                        for (int r = 0; r < rounds; r++) key[cand_i[r]] = cand_v[r];
+                    __syncthreads();
+                }
+            }
+            if (active == 0) {
+                for (int i = threadIdx.x; i < n2; i += blockDim.x) {
+                    if (i < V) {
+                        idx[i] = i;
+                    } else {
+                        key[i] = -1.0;  // padding sorts last
+                        idx[i] = 0x7fffffff;
+                    }
+                }
+                __syncthreads();
+                bitonic_desc(key, idx, n2);
+                if (threadIdx.x == 0) {
+                    int act = kcap;
+                    if (use_p) {
+                        double cp = 0.0;
+                        int cut = 0;
+                        for (int i = 0; i < act; i++) {
+                            cp += key[i];
+                            cut = i + 1;
+                            if (cp >= a.p.top_p) break;
+                        }
+                        act = cut;
+                    }
+                    chosen_sh = act;
+                }
+                __syncthreads();
+                active = chosen_sh;
+                cv = key;
+                ci = idx;
+                __syncthreads();
+            }
+            if (threadIdx.x == 0) {
+                int c;
+                if (active == 1) {
+                    c = ci[0];
+                } else {  // sampleFromCDF (sample.go:173-190)
+                    double sp = 0.0;
+                    for (int i = 0; i < active; i++) sp += cv[i];
+                    const double r = u * sp;
+                    c = ci[active - 1];
+                    const int k = seq_find(cv, active, r, -1);
+                    if (k >= 0) c = ci[k];
+                }
+                chosen_sh = c;
+            }
+            __syncthreads();
+            chosen = chosen_sh;
+        }
+    }
+    if (threadIdx.x == 0) {
+        a.out[(long long)row * a.out_ld + a.out_col] = chosen;
+        if (a.next_ids) a.next_ids[row] = chosen;
+    }
+}
+
+}  // namespace
+
+int sample_n2(int V) {
+    int n2 = 1;
+    while (n2 < V) n2 <<= 1;
+    return n2;
+}
+
+size_t sample_lds_bytes(int V) { return (size_t)sample_n2(V) * (sizeof(double) + sizeof(int)); }
+
+hipError_t launch_sample(const SampleArgs& a, hipStream_t s) {
+    if (a.n <= 0) return hipSuccess;
+    // the candidate sort (and its index array) is only reachable when top-k leaves more than kExtract
+    // candidates or top-p is on; otherwise the row of float64 values is all the kernel keeps in LDS
+    const bool truncated = a.p.temperature > 0.001 && !(a.p.top_k <= 0 && a.p.top_p >= 0.9999);
+    const int kcap = (a.p.top_k > 0 && a.p.top_k < a.V) ? a.p.top_k : a.V;
+    const bool use_p = a.p.top_p > 0.0 && a.p.top_p < 1.0;
+    const bool may_sort = truncated && (kcap > kExtract || use_p);
+    const size_t lds = may_sort ? sample_lds_bytes(a.V) : (size_t)a.V * sizeof(double);
+    static const hipError_t attr = hipFuncSetAttribute((const void*)sample_rows_kernel,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       (int)sample_lds_bytes(kMaxSampleVocab));
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL(sample_rows_kernel, dim3(a.n), dim3(kThreads), lds, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace mg

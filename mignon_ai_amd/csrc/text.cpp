@@ -80,6 +80,24 @@ std::vector<std::string> split_docs(const std::string& text) {
     return docs;
 }
 
+// strings.TrimSpace: the byte range of text without leading and trailing unicode.IsSpace runes
+std::pair<size_t, size_t> trim_space(const char* text, size_t n) {
+    const unsigned char* t = (const unsigned char*)text;
+    size_t b = 0, e = 0;
+    bool any = false;
+    for (size_t i = 0; i < n;) {
+        int w;
+        const bool space = mg::char_class(mg::decode_rune(t + i, n - i, w)) == mg::CLS_SPACE;
+        if (!space) {
+            if (!any) b = i;
+            any = true;
+            e = i + w;
+        }
+        i += w;
+    }
+    return any ? std::make_pair(b, e) : std::make_pair(size_t(0), size_t(0));
+}
+
 }  // namespace
 
 extern "C" {
@@ -225,6 +243,63 @@ int mg_generate_greedy(mg_model* m, mg_tokenizer* t, const char* const* prompts,
             const int i = live[r], k = counts[r];
             std::copy_n(ids.begin() + (size_t)r * max_tokens, k, out_ids + (size_t)i * max_tokens);
             std::copy_n(probs.begin() + (size_t)r * max_tokens, k, out_probs + (size_t)i * max_tokens);
+            out_counts[i] = k;
+        }
+        return MG_OK;
+    });
+}
+
+int mg_generate_sample(mg_model* m, mg_tokenizer* t, const char* const* prompts, const size_t* prompt_lens, int n,
+                       int context, int max_tokens, int chat, const mg_sampling_t* sp, const uint64_t* seeds,
+                       int32_t* out_ids, int32_t* out_counts) {
+    return guarded([&] {
+        need(m && t && sp && out_counts && (n == 0 || (prompts && prompt_lens && seeds && out_ids)),
+             "mg_generate_sample: null argument");
+        need(n >= 0 && max_tokens > 0, "mg_generate_sample: n must be >= 0 and max_tokens > 0");
+        if (n == 0) return MG_OK;
+        std::vector<std::vector<int32_t>> ctx(n);
+        std::vector<int> live;
+        int L = 0;
+        for (int i = 0; i < n; i++) {
+            out_counts[i] = 0;
+            need(prompts[i] != nullptr || prompt_lens[i] == 0, "mg_generate_sample: null prompt");
+            if (chat) {  // ChatWithHistory (internal/generate/chat.go:104-130): a trimmed prompt, no history
+                const auto r = trim_space(prompts[i], prompt_lens[i]);
+                if (r.second == r.first) continue;
+                t->tok->encode_prompt(prompts[i] + r.first, r.second - r.first, ctx[i]);
+            } else {  // Text (chat.go:62-70)
+                t->tok->encode(prompts[i], prompt_lens[i], ctx[i]);
+            }
+            if (!ctx[i].empty()) {
+                live.push_back(i);
+                L = std::max<int>(L, (int)ctx[i].size());
+            }
+        }
+        if (live.empty()) return MG_OK;
+        const int S = (int)live.size();
+        std::vector<int32_t> arr((size_t)S * L, t->tok->pad_id()), lens(S), ids((size_t)S * max_tokens), counts(S);
+        std::vector<uint64_t> sd(S);
+        for (int r = 0; r < S; r++) {
+            const auto& c = ctx[live[r]];
+            std::copy(c.begin(), c.end(), arr.begin() + (size_t)r * L);
+            lens[r] = (int32_t)c.size();
+            sd[r] = seeds[live[r]];
+        }
+        // Text penalises repeats of the prompt's last tokens; Chat's repetition window starts in the reply
+        mg_sampling_t p = *sp;
+        p.penalize_prompt = chat ? 0 : 1;
+        std::vector<int32_t> stops;
+        for (int id : {t->tok->eos_id(), t->tok->user_id(), t->tok->bot_id()})
+            if (id >= 0) stops.push_back(id);
+        mg_sessions* ss = nullptr;
+        engine(mg_sessions_create(m, S, context, &ss));
+        const int rc = mg_sessions_decode_sample(ss, arr.data(), lens.data(), L, max_tokens, &p, sd.data(), stops.data(),
+                                                 (int)stops.size(), ids.data(), counts.data(), 0);
+        mg_sessions_free(ss);
+        engine(rc);
+        for (int r = 0; r < S; r++) {
+            const int i = live[r], k = counts[r];
+            std::copy_n(ids.begin() + (size_t)r * max_tokens, k, out_ids + (size_t)i * max_tokens);
             out_counts[i] = k;
         }
         return MG_OK;

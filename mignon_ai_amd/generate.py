@@ -1,24 +1,36 @@
-"""Text generation through the library: infer.Generate's greedy branch (pkg/infer/infer.go:64-84;
-generate.DecodeGreedy / greedyLoop, internal/generate/greedy.go:43-102) over batched device sessions,
-with the tokenizer stored in the model file (mg_generate_greedy).
+"""Text generation through the library: infer.Generate (pkg/infer/infer.go:64-96) over batched device
+sessions, with the tokenizer stored in the model file. Temperature 0 decodes greedily
+(generate.DecodeGreedy / greedyLoop, internal/generate/greedy.go:43-102; mg_generate_greedy); above 0 the
+reply is sampled (generate.Chat / Text over sampleContinuation, internal/generate/chat.go,
+sample.go; mg_generate_sample), each prompt's draws seeded by its own seed.
 
     g = Generator.load("orders.mgn")
     g.generate("unpaid orders").text
     g.generate_batch(requests, max_tokens=80)
+    g.generate_batch(requests, temperature=0.7, top_k=40, top_p=0.9, rep_penalty=1.2, seeds=range(len(requests)))
 """
 from __future__ import annotations
 
 import ctypes
+import os
 from dataclasses import dataclass, field
 
 import numpy as np
 
-from ._lib import check, lib, ptr
+from ._lib import Sampling, check, lib, ptr
 from .model import Model, read_metadata
 from .tokenizer import Tokenizer
 
 CHAT_MAX_RESPONSE_TOKENS = 60  # internal/generate/constants.go:6 (infer.DefaultMaxTokens)
 TASK_CHAT = "chat"             # model.TaskChat
+# unicode.IsSpace, what strings.TrimSpace removes (Python's str.strip() without arguments removes more)
+GO_SPACE = "\t\n\v\f\r \x85\xa0\u1680\u2000\u2001\u2002\u2003\u2004\u2005\u2006\u2007\u2008\u2009\u200a" \
+           "\u2028\u2029\u202f\u205f\u3000"
+
+
+def trim_space(text: str) -> str:
+    """strings.TrimSpace."""
+    return text.strip(GO_SPACE)
 
 
 @dataclass
@@ -71,29 +83,51 @@ class Generator:
         """model.Model.ContextSize: the metadata's context_size."""
         return int(self.metadata.get("context_size", 0))
 
-    def generate(self, prompt, max_tokens: int = 0) -> Result:
-        """infer.Generate with Temperature 0."""
-        return self.generate_batch([prompt], max_tokens)[0]
+    def generate(self, prompt, max_tokens: int = 0, temperature: float = 0.0, top_k: int = 0, top_p: float = 0.0,
+                 rep_penalty: float = 0.0, seed: int | None = None) -> Result:
+        """infer.Generate with infer.Options' fields."""
+        return self.generate_batch([prompt], max_tokens, temperature, top_k, top_p, rep_penalty,
+                                   None if seed is None else [seed])[0]
 
-    def generate_batch(self, prompts, max_tokens: int = 0) -> list[Result]:
-        """infer.Generate for every prompt, all decoded together on device sessions."""
+    def generate_batch(self, prompts, max_tokens: int = 0, temperature: float = 0.0, top_k: int = 0,
+                       top_p: float = 0.0, rep_penalty: float = 0.0, seeds=None) -> list[Result]:
+        """infer.Generate for every prompt, all decoded together on device sessions. When sampling, seeds[i]
+        (a 64-bit integer) fixes prompt i's draws; without seeds they are drawn from os.urandom, as the
+        reference's global generator is seeded at random."""
         if max_tokens <= 0:
             max_tokens = CHAT_MAX_RESPONSE_TOKENS
         n = len(prompts)
         if n == 0:
             return []
+        chat = self.task() == TASK_CHAT
         enc = [p.encode("utf-8") if isinstance(p, str) else bytes(p) for p in prompts]
         arr = (ctypes.c_char_p * n)(*enc)
         lens = (ctypes.c_size_t * n)(*[len(b) for b in enc])
         ids = np.empty((n, max_tokens), np.int32)
-        probs = np.empty((n, max_tokens), np.float64)
         counts = np.empty(n, np.int32)
-        check(lib().mg_generate_greedy(self.model.handle, self.tok.handle, arr, lens, n, self.context_size(),
-                                       max_tokens, int(self.task() == TASK_CHAT), ptr(ids), ptr(probs), ptr(counts)))
         texts = self.tok.piece_texts()
+        if temperature <= 0:
+            probs = np.empty((n, max_tokens), np.float64)
+            check(lib().mg_generate_greedy(self.model.handle, self.tok.handle, arr, lens, n, self.context_size(),
+                                           max_tokens, int(chat), ptr(ids), ptr(probs), ptr(counts)))
+            out = []
+            for i in range(n):
+                k = int(counts[i])
+                row = ids[i, :k].tolist()
+                out.append(Result(trim_space("".join([texts[t] for t in row])), row, probs[i, :k].tolist(), texts))
+            return out
+        sp = Sampling(temperature=temperature, rep_penalty=rep_penalty, top_p=top_p if top_p > 0 else 1.0,
+                      top_k=top_k, penalize_prompt=0)
+        if seeds is None:
+            seeds = np.frombuffer(os.urandom(8 * n), np.uint64)
+        sd = np.ascontiguousarray(np.asarray([int(x) & (2 ** 64 - 1) for x in seeds], np.uint64))
+        if sd.size != n:
+            raise ValueError("one seed per prompt")
+        check(lib().mg_generate_sample(self.model.handle, self.tok.handle, arr, lens, n, self.context_size(),
+                                       max_tokens, int(chat), ctypes.byref(sp), ptr(sd), ptr(ids), ptr(counts)))
         out = []
         for i in range(n):
-            k = int(counts[i])
-            row = ids[i, :k].tolist()
-            out.append(Result("".join([texts[t] for t in row]).strip(), row, probs[i, :k].tolist(), texts))
+            row = ids[i, :int(counts[i])].tolist()
+            text = "".join([texts[t] for t in row])
+            out.append(Result(trim_space(text) if chat else text, row, [], texts))  # Tokens stay empty
         return out

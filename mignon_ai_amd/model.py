@@ -200,6 +200,24 @@ class Sessions:
                                                     ptr(counts), 0))
         return ids, probs, counts
 
+    def decode_sample(self, prompts2d, max_tokens, seeds, temperature=1.0, top_k=0, top_p=1.0, rep_penalty=1.0,
+                      penalize_prompt=False, stops=(), lens=None):
+        """sampleContinuation for every session (mg_sessions_decode_sample): (ids [n][max_tokens], counts [n]);
+        row i's reply is ids[i, :counts[i]]. seeds[i] fixes session i's draws."""
+        from ._lib import Sampling
+        p = _i32(prompts2d)
+        n, L = p.shape
+        lens = _i32(lens if lens is not None else np.full(n, L))
+        st = _i32(list(stops))
+        sd = np.ascontiguousarray(np.asarray([int(x) & (2 ** 64 - 1) for x in seeds], np.uint64))
+        sp = Sampling(temperature=temperature, rep_penalty=rep_penalty, top_p=top_p, top_k=top_k,
+                      penalize_prompt=int(penalize_prompt))
+        ids = np.empty((n, max_tokens), np.int32)
+        counts = np.empty(n, np.int32)
+        check(lib().mg_sessions_decode_sample(self._h, ptr(p), ptr(lens), L, int(max_tokens), ctypes.byref(sp), ptr(sd),
+                                              ptr(st) if st.size else None, int(st.size), ptr(ids), ptr(counts), 0))
+        return ids, counts
+
     def decode_greedy_device(self, prompts, lens, max_tokens, out_ids, out_probs):
         n, L = prompts.shape
         check(lib().mg_sessions_decode_greedy(self._h, ptr(prompts), ptr(lens), L, int(max_tokens), ptr(out_ids),
@@ -260,6 +278,28 @@ def quantize_f32(w):
 
 
 _OPTIONS = {"gemm": (0, ["auto", "stream", "slab"]), "attention": (1, ["auto", "exact", "mfma"])}
+
+
+def sample_logits(logits, recent=None, temperature=1.0, top_k=0, top_p=1.0, rep_penalty=1.0, u=None):
+    """generate.SampleRawLogitsAdvanced on the current GPU for every row of float64 logits [n][V]
+    (mg_sample_logits): recent is a list of per-row token lists (the repetition window), u the per-row
+    uniforms standing for rand.Float64()."""
+    from ._lib import Sampling
+    lg = np.ascontiguousarray(logits, np.float64)
+    n, V = lg.shape
+    uu = np.ascontiguousarray(u if u is not None else np.zeros(n), np.float64)
+    rp = rl = None
+    ld = 0
+    if recent is not None:
+        ld = max([len(r) for r in recent] + [1])
+        rp = np.zeros((n, ld), np.int32)
+        rl = np.array([len(r) for r in recent], np.int32)
+        for i, r in enumerate(recent):
+            rp[i, :len(r)] = r
+    sp = Sampling(temperature=temperature, rep_penalty=rep_penalty, top_p=top_p, top_k=top_k, penalize_prompt=0)
+    out = np.empty(n, np.int32)
+    check(lib().mg_sample_logits(ptr(lg), n, V, ptr(rp), ptr(rl), ld, ctypes.byref(sp), ptr(uu), ptr(out)))
+    return out
 
 
 def engine_option(name: str, value: str | None = None) -> str:

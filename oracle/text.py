@@ -13,6 +13,9 @@ Text is bytes and is read as Go reads strings: an invalid UTF-8 byte is one U+FF
   - generate: pkg/infer/infer.go:64-84 (greedy branch)
   - perplexity / perplexity_per_doc: internal/eval/eval.go:25-75, internal/eval/perdoc.go:12-48,
     window and logProb internal/eval/suite.go:196-208, BitsPerByte internal/tokenizer/bytes.go:5-11
+  - sample_raw_logits / sample_continuation: internal/generate/sample.go:31-247 (rand.Float64() replaced
+    by uniform_draw, the draw the library defines); generate_sample: pkg/infer/infer.go:85-95,
+    generate.Chat / Text (internal/generate/chat.go:62-140)
 Character classes use Python's unicodedata (Go's unicode.IsSpace / IsPunct / IsSymbol / IsDigit).
 """
 from __future__ import annotations
@@ -325,3 +328,132 @@ def perplexity_per_doc(call, tok: Tokenizer, text: bytes, context: int, max_docs
         terms += score(call, tokens, context)
         targets += tokens[1:]
     return held_out(terms, targets, tok.token_bytes())
+
+
+# ---- sampling (internal/generate/sample.go, chat.go) ----
+
+CHAT_REPETITION_WINDOW = 6
+_M64 = (1 << 64) - 1
+
+
+def uniform_draw(seed: int, step: int) -> float:
+    """Draw `step` (from 0) of a prompt's generator: the (step+1)-th SplitMix64 output for `seed`, top 53 bits
+    over 2^53."""
+    z = (seed + 0x9E3779B97F4A7C15 * (step + 1)) & _M64
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & _M64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & _M64
+    z ^= z >> 31
+    return (z >> 11) * 2.0 ** -53
+
+
+def sample_raw_logits(logits, recent, temperature, rep_penalty, top_k, top_p, u) -> int:
+    """SampleRawLogitsAdvanced (sample.go:31-171) with rand.Float64() replaced by the uniform u; candidates
+    of equal probability in token order."""
+    V = len(logits)
+    if V == 0:
+        return 0
+    lg = [float(x) for x in logits]
+    if rep_penalty > 1.0 and recent:
+        for i, t in enumerate(recent):
+            if t < 0 or t >= V or t in recent[:i]:
+                continue
+            lg[t] = lg[t] / rep_penalty if lg[t] > 0 else lg[t] * rep_penalty
+    if temperature <= 0.001:
+        best = 0
+        for i in range(1, V):
+            if lg[i] > lg[best]:
+                best = i
+        return best
+    inv_t = 1.0 / temperature
+    mx = -1.7976931348623157e308
+    for i in range(V):
+        lg[i] *= inv_t
+        if lg[i] > mx:
+            mx = lg[i]
+    p = [math.exp(x - mx) for x in lg]
+    s = 0.0
+    for x in p:
+        s += x
+    if top_k <= 0 and top_p >= 0.9999:
+        r = u * s
+        cum = 0.0
+        for i in range(V):
+            cum += p[i]
+            if r <= cum:
+                return i
+        return 0
+    inv = 1.0 / s
+    cand = sorted(((x * inv, i) for i, x in enumerate(p)), key=lambda c: (-c[0], c[1]))
+    active = V
+    if 0 < top_k < active:
+        active = top_k
+    if 0.0 < top_p < 1.0:
+        cp, cut = 0.0, 0
+        for i in range(active):
+            cp += cand[i][0]
+            cut = i + 1
+            if cp >= top_p:
+                break
+        active = cut
+    cand = cand[:active]
+    if len(cand) == 1:
+        return cand[0][1]
+    sp = 0.0
+    for c in cand:
+        sp += c[0]
+    r = u * sp
+    cum = 0.0
+    for c in cand:
+        cum += c[0]
+        if r <= cum:
+            return c[1]
+    return cand[-1][1]
+
+
+def sample_continuation(session, context, penalty_prefix, max_tokens, temperature, rep_penalty, top_k, top_p, seed,
+                        stops=()):
+    """sampleContinuation (sample.go:196-247) with draw k of `seed` at step k."""
+    recent = list(penalty_prefix)
+    gen = []
+    logits = session.prefill(list(context)) if context else None
+    while len(gen) < max_tokens and logits is not None and len(logits) > 0:
+        window = recent[-CHAT_REPETITION_WINDOW:]
+        lg = [float(x) for x in logits]
+        if len(gen) >= 2:
+            w1, w2 = gen[-2], gen[-1]
+            for i in range(len(gen) - 2):
+                if gen[i] == w1 and gen[i + 1] == w2 and 0 <= gen[i + 2] < len(lg):
+                    lg[gen[i + 2]] = -1.7976931348623157e308
+        nxt = sample_raw_logits(lg, window, temperature, rep_penalty, top_k, top_p, uniform_draw(seed, len(gen)))
+        if nxt in stops:
+            break
+        gen.append(nxt)
+        recent.append(nxt)
+        if len(gen) < max_tokens:
+            logits = session.append(nxt)
+    return gen
+
+
+GO_SPACE = ("\t\n\v\f\r \x85\xa0\u1680\u2000\u2001\u2002\u2003\u2004\u2005\u2006\u2007\u2008\u2009\u200a"
+            "\u2028\u2029\u202f\u205f\u3000")  # unicode.IsSpace, what strings.TrimSpace removes
+
+
+def generate_sample(model, tok: Tokenizer, prompt: str, context_size: int, max_tokens: int, temperature: float,
+                    top_k: int, top_p: float, rep_penalty: float, seed: int, chat: bool = True):
+    """infer.Generate's sampling branch: generate.Chat (trimmed prompt, reply window) or generate.Text
+    (prompt as is, window from the prompt). Returns (text, ids)."""
+    stops = (tok.eos_id(), tok.user_id(), tok.bot_id())
+    if top_p <= 0:
+        top_p = 1.0
+    if chat:
+        p = prompt.strip(GO_SPACE)
+        if not p:
+            return "", []
+        ctx, prefix = tok.encode_prompt(p), []
+    else:
+        ctx = tok.encode(prompt)
+        prefix = ctx
+    ids = sample_continuation(model.new_session(context_size), ctx, prefix, max_tokens, temperature, rep_penalty,
+                              top_k, top_p, seed, stops)
+    text = tok.decode(ids).decode("utf-8", errors="replace")
+    return (text.strip(GO_SPACE) if chat else text), ids
