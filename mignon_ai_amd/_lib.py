@@ -109,6 +109,13 @@ def lib():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"HIP engine library not built: {LIB_PATH} (run python -m mignon_ai_amd.build)")
+        # PyTorch ships its own HIP runtime. Two runtimes in one process do not share the device (the
+        # one initialised second finds none), so when torch is installed it is loaded first and the
+        # library binds to the same libamdhip64.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(L, name)

@@ -407,7 +407,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 //
 // Block b -> (XCD b % 8, slot b / 8); slot -> (channel slab slot % nt, run (slot / nt)*8 + XCD), so all
 // slabs of a run execute on one XCD and its activations are fetched from HBM into that XCD's L2 once.
-template <int EPI, int REM, bool STG>
+template <int EPI, int REM, bool STG, int KCF = 0>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_slab_kernel(GemmArgs g,
                                                                                                    int run_tiles,
                                                                                                    int n_runs) {
@@ -445,6 +445,46 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const long long tstep = (long long)kc * astep;
 
     const int8_t* ap = g.A + (long long)tile * tstep + lane * 16;
+    if constexpr (KCF > 0) {
+        // Short K (kc == KCF): the whole next tile's A fragments are loaded right after this tile's
+        // MFMAs, before its outputs are stored. Loads and stores share one in-order completion counter,
+        // so no load the MFMAs wait for is ever queued behind a tile's stores.
+        v4i a[KCF][3];
+#pragma unroll
+        for (int ks = 0; ks < KCF; ks++)
+#pragma unroll
+            for (int l = 0; l < 3; l++) a[ks][l] = *(const v4i*)(ap + ks * astep + l * 1024);
+        for (;;) {
+            const EpiRow row = epi_row<EPI>(g, tile * 16 + (lane & 15));
+            const int next = tile + 8;
+            const int8_t* np = next < t_end ? ap + 8 * tstep : ap;
+            v4i acc[3][8];
+#pragma unroll
+            for (int ks = 0; ks < KCF; ks++) {
+                v4i wf[8];
+                const int8_t* wp = wlane + ks * 8192;
+#pragma unroll
+                for (int ti = 0; ti < 8; ti++) wf[ti] = *(const v4i*)(wp + ti * 1024);
+#pragma unroll
+                for (int ti = 0; ti < 8; ti++)
+#pragma unroll
+                    for (int l = 0; l < 3; l++)
+                        acc[l][ti] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[ti], a[ks][l],
+                                                                           ks == 0 ? v4i{0, 0, 0, 0} : acc[l][ti], 0, 0, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 24, 0);
+            }
+#pragma unroll
+            for (int ks = 0; ks < KCF; ks++)
+#pragma unroll
+                for (int l = 0; l < 3; l++) a[ks][l] = *(const v4i*)(np + ks * astep + l * 1024);
+            lx_epilogue<EPI, STG>(g, acc, tile * 16, n0, n_tile, lane, row, bias_s, stg);
+            if (next >= t_end) break;
+            tile = next;
+            ap = np;
+        }
+        return;
+    }
     v4i a0[3], a1[3], a2[3];
 #pragma unroll
     for (int l = 0; l < 3; l++) a0[l] = *(const v4i*)(ap + l * 1024);
@@ -630,14 +670,21 @@ hipError_t launch_lx_t(const GemmArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-template <int EPI, int REM, bool STG>
+template <int EPI, int REM, bool STG, int KCF = 0>
 hipError_t slab_launch(const GemmArgs& a, int grid, int lds, int run_tiles, int n_runs, hipStream_t stream) {
     // dynamic LDS above the default limit must be allowed once per kernel
-    static const hipError_t attr = hipFuncSetAttribute((const void*)gemm_slab_kernel<EPI, REM, STG>,
+    static const hipError_t attr = hipFuncSetAttribute((const void*)gemm_slab_kernel<EPI, REM, STG, KCF>,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, slab_lds_limit());
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((gemm_slab_kernel<EPI, REM, STG>), dim3(grid), dim3(512), lds, stream, a, run_tiles, n_runs);
+    hipLaunchKernelGGL((gemm_slab_kernel<EPI, REM, STG, KCF>), dim3(grid), dim3(512), lds, stream, a, run_tiles, n_runs);
     return hipGetLastError();
+}
+
+// whole-tile prefetch for kc in {4, 6}; 0 when the pipelined loop is used
+template <int EPI, bool STG>
+hipError_t slab_launch_full(int kc, const GemmArgs& a, int grid, int lds, int run_tiles, int n_runs, hipStream_t stream) {
+    if (kc == 4) return slab_launch<EPI, 0, STG, 4>(a, grid, lds, run_tiles, n_runs, stream);
+    return slab_launch<EPI, 0, STG, 6>(a, grid, lds, run_tiles, n_runs, stream);
 }
 
 template <int EPI>
@@ -660,7 +707,9 @@ hipError_t launch_slab_t(const GemmArgs& a, hipStream_t stream) {
     const int grid = 8 * nt * ((n_runs + 7) / 8);
     // REM = kc % 3 for kc >= 3; 3 marks kc == 2
     const int rem = kc == 2 ? 3 : kc % 3;
+    const bool full = kc == 4 || kc == 6;
     if constexpr (can_stage<EPI>()) {
+        if (stg && full) return slab_launch_full<EPI, true>(kc, a, grid, lds, run_tiles, n_runs, stream);
         if (stg) {
             switch (rem) {
                 case 0: return slab_launch<EPI, 0, true>(a, grid, lds, run_tiles, n_runs, stream);
@@ -670,6 +719,7 @@ hipError_t launch_slab_t(const GemmArgs& a, hipStream_t stream) {
             }
         }
     }
+    if (full) return slab_launch_full<EPI, false>(kc, a, grid, lds, run_tiles, n_runs, stream);
     switch (rem) {
         case 0: return slab_launch<EPI, 0, false>(a, grid, lds, run_tiles, n_runs, stream);
         case 1: return slab_launch<EPI, 1, false>(a, grid, lds, run_tiles, n_runs, stream);
