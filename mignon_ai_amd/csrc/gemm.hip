@@ -27,6 +27,8 @@ namespace mg {
 
 namespace {
 
+typedef float f4v __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ void store4(float* dst, const float v[4], int nvalid_here, bool aligned) {
     if (nvalid_here >= 4 && aligned) {
         *(float4*)dst = make_float4(v[0], v[1], v[2], v[3]);
@@ -86,7 +88,10 @@ __device__ __forceinline__ void stg_put(float* stg, int lane, int ti, const floa
     *(float4*)(stg + (lane & 15) * STG_LD + 16 * ti + 4 * (lane >> 4)) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
-// Rows mt0..mt0+15, channels n0 + [0, 128) of `out` (row stride ldo) from the staged tile.
+// Rows mt0..mt0+15, channels n0 + [0, 128) of `out` (row stride ldo) from the staged tile. NT: streaming
+// (non-temporal) stores of whole 512-byte row segments, for outputs far larger than the L2 (the next
+// kernel reads them back from memory in any case).
+template <bool NT = false>
 __device__ __forceinline__ void stg_flush(const GemmArgs& g, const float* stg, int lane, int mt0, int n0, float* out,
                                           long long ldo) {
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes have landed
@@ -102,7 +107,12 @@ __device__ __forceinline__ void stg_flush(const GemmArgs& g, const float* stg, i
         if (m < g.M && nv > 0) {
             float* dst = out + (long long)m * ldo + n0 + c;
             if (vec) {
-                *(float4*)dst = v;
+                if constexpr (NT) {
+                    const f4v t = {v.x, v.y, v.z, v.w};
+                    __builtin_nontemporal_store(t, (f4v*)dst);
+                } else {
+                    *(float4*)dst = v;
+                }
             } else {
                 const float t[4] = {v.x, v.y, v.z, v.w};
                 for (int r = 0; r < 4 && r < nv; r++) dst[r] = t[r];
@@ -145,7 +155,7 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
             if constexpr (STG) stg_put(stg, lane, ti, v);
             else store4(orow + n, v, nv, vec);
         }
-        if constexpr (STG) stg_flush(g, stg, lane, mt0, n0, g.out, g.ldo);
+        if constexpr (STG) stg_flush<true>(g, stg, lane, mt0, n0, g.out, g.ldo);
     } else if constexpr (EPI == EPI_RESID) {
         // cur += x.w: all eight row segments are loaded before any is needed (one memory latency)
         if (!mok) return;
@@ -193,7 +203,7 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
             if constexpr (STG) stg_put(stg, lane, ti, v);
             else store4(orow + n, v, nv, vec);
         }
-        if constexpr (STG) stg_flush(g, stg, lane, mt0, n0, g.out, g.ldo);
+        if constexpr (STG) stg_flush<true>(g, stg, lane, mt0, n0, g.out, g.ldo);
     } else if constexpr (EPI == EPI_GLU || EPI == EPI_HIGHWAY) {
         // W rows are reordered in blocks of 32: 16 value rows then the 16 matching gate rows, so tile
         // pair (2p, 2p+1) holds value and gate of output channel n0/2 + 16p + 4*(L >> 4) + r.
