@@ -571,16 +571,29 @@ __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
 // ------------------------------------------------------------------------------------------------
 typedef float v4f __attribute__((ext_vector_type(4)));
 
+// Windowed causal attention on the fp32 matrix cores. A workgroup is four waves; wave w takes the 16
+// queries of tile 4*grp + w for head blockIdx.y. The 16*(NKB+3) keys the four tiles attend are staged in
+// LDS once: keys first (row-major), then, over the same buffer, values transposed, so that every matrix
+// operand is one 16-byte LDS read. Per wave: S^T = K Q^T over NKB blocks of 16 keys (dims 16g + 4kg + e),
+// the reference's softmax in registers, then out = P V.
 template <int ND, int NKB>
 __global__ __launch_bounds__(256) void attention_mfma_kernel(AttnArgs a, int dh) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    constexpr int KEYS = 16 * (NKB + 3);  // keys of the workgroup's four query tiles
+    constexpr int DP = 16 * ND;           // head width padded to the MFMA's 16
+    constexpr int KS = DP + 4;            // LDS row stride of K (floats)
+    constexpr int VS = KEYS + 4;          // LDS row stride of V^T (floats)
+    constexpr int CH = DP / 4;            // 16-byte chunks per key row
+    constexpr int NCH = KEYS * CH;
+    constexpr int PER = (NCH + 255) / 256;
+    extern __shared__ __align__(16) float att_lds[];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, tid = threadIdx.x;
     const int T = a.T, D = a.D, cap = a.cap, ld = 3 * D;
     const int qtiles = (T + 15) >> 4;
     const int groups = (qtiles + 3) >> 2;
     const int b = blockIdx.x / groups;
-    const int tile = (blockIdx.x % groups) * 4 + w;
+    const int grp = blockIdx.x % groups;
+    const int tile = grp * 4 + w;
     const int h = blockIdx.y;
-    if (tile >= qtiles) return;  // no workgroup barrier below
     const int t0 = tile * 16;
     const int qi = lane & 15, kg = lane >> 4;
     const float* seq = a.qkv + (long long)b * T * ld;
@@ -588,10 +601,23 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(AttnArgs a, int dh)
     const float* kb_ = seq + D + h * dh;
     const float* vb = seq + 2 * D + h * dh;
     const float scale = (float)(1.0 / sqrt((double)dh));
+    const int kbase = grp * 64 + 16 - 16 * NKB;  // key of LDS row 0
 
-    // Every load below is unconditional, from an address clamped into the sequence and the head, and
-    // masked afterwards: a guarded load would become a branch that waits for it on the spot.
+    // Every global load is unconditional, from an address clamped into the sequence and the head, and
+    // masked afterwards (a guarded load becomes a branch that waits for it on the spot). Keys outside
+    // [0, T) and dims past dh are zero.
     const v4f zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    v4f kreg[PER], vreg[PER];
+#pragma unroll
+    for (int p = 0; p < PER; p++) {
+        const int e = min(tid + 256 * p, NCH - 1);
+        const int key = e / CH, d = 4 * (e - key * CH);
+        const int j = kbase + key;
+        const long long off = (long long)min(max(j, 0), T - 1) * ld + min(d, dh - 4);
+        const float mask = (j >= 0 && j < T && d < dh) ? 1.0f : 0.0f;
+        kreg[p] = *(const v4f*)(kb_ + off) * mask;
+        vreg[p] = *(const v4f*)(vb + off) * mask;
+    }
     // Q^T operand: query t0 + qi, dims 16g + 4kg .. +3
     v4f qv[ND];
     {
@@ -602,49 +628,39 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(AttnArgs a, int dh)
             qv[g] = *(const v4f*)(qb + (long long)t * ld + min(d, dh - 4)) * (d < dh ? 1.0f : 0.0f);
         }
     }
-    // key blocks [jstart + 16kb, +16) cover every key any query of the tile attends
-    const int jstart = t0 + 16 - 16 * NKB;
-    v4f kv[NKB][ND];
 #pragma unroll
-    for (int kb = 0; kb < NKB; kb++) {
-        const int j = jstart + 16 * kb + qi;
-        const bool kok = j >= 0;
-        const float* kp = kb_ + (long long)min(max(j, 0), T - 1) * ld;
-#pragma unroll
-        for (int g = 0; g < ND; g++) {
-            const int d = 16 * g + 4 * kg;
-            kv[kb][g] = *(const v4f*)(kp + min(d, dh - 4)) * ((kok && d < dh) ? 1.0f : 0.0f);
+    for (int p = 0; p < PER; p++) {
+        const int e = tid + 256 * p;
+        if (e < NCH) {
+            const int key = e / CH, c = e - key * CH;
+            *(v4f*)(att_lds + key * KS + 4 * c) = kreg[p];
         }
     }
-    // values: B operand of P.V, key jstart + 16kb + 4kg + r, dim 16g + qi
-    float vv[NKB][4][ND];
-#pragma unroll
-    for (int kb = 0; kb < NKB; kb++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int j = jstart + 16 * kb + 4 * kg + r;
-            const float* vp = vb + (long long)min(max(j, 0), T - 1) * ld;
-#pragma unroll
-            for (int g = 0; g < ND; g++) {
-                const int d = 16 * g + qi;
-                // a multiply, not a select: clamped addresses hold finite activations, and the compiler
-                // would turn a select of a load back into a branch around the load
-                vv[kb][r][g] = vp[min(d, dh - 1)] * ((j >= 0 && d < dh) ? 1.0f : 0.0f);
-            }
-        }
-    // every load above is issued before the first MFMA waits (where the registers allow it)
-    if constexpr (NKB * ND <= 20) __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    // s[kb][r] = q.k for query t0 + qi and key kbase + 16(w + kb) + 4kg + r
     v4f s[NKB];
 #pragma unroll
     for (int kb = 0; kb < NKB; kb++) {
         s[kb] = zero4;
 #pragma unroll
-        for (int g = 0; g < ND; g++)
+        for (int g = 0; g < ND; g++) {
+            const v4f kv = *(const v4f*)(att_lds + (16 * (w + kb) + qi) * KS + 16 * g + 4 * kg);
 #pragma unroll
-            for (int e = 0; e < 4; e++) s[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[kb][g][e], qv[g][e], s[kb], 0, 0, 0);
+            for (int e = 0; e < 4; e++) s[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[e], qv[g][e], s[kb], 0, 0, 0);
+        }
     }
-    // s[kb][r] = q.k for query t = t0 + qi, key j = jstart + 16kb + 4kg + r
+    __syncthreads();  // every wave's keys are read: the buffer takes the values
+#pragma unroll
+    for (int p = 0; p < PER; p++) {
+        const int e = tid + 256 * p;
+        if (e < NCH) {
+            const int key = e / CH, c = e - key * CH;
+#pragma unroll
+            for (int i = 0; i < 4; i++) att_lds[(4 * c + i) * VS + key] = vreg[p][i];
+        }
+    }
     const int t = t0 + qi;
+    const int jstart = kbase + 16 * w;
     const int lo = max(window_start(t, a.window), t - cap + 1);
     float mx = -3.40282347e38f;
 #pragma unroll
@@ -671,7 +687,7 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(AttnArgs a, int dh)
     sum += __shfl_xor(sum, 16, 64);
     sum += __shfl_xor(sum, 32, 64);
     const float inv = 1.0f / sum;
-
+    __syncthreads();
     // out = P V: A = P (query qi, key jb + 4kg + r), B = V (key jb + 4kg + r, dim 16g + qi)
     v4f o[ND];
 #pragma unroll
@@ -679,11 +695,12 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(AttnArgs a, int dh)
 #pragma unroll
     for (int kb = 0; kb < NKB; kb++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float p = s[kb][r] * inv;
+        for (int g = 0; g < ND; g++) {
+            const v4f vv = *(const v4f*)(att_lds + (16 * g + qi) * VS + 16 * (w + kb) + 4 * kg);
 #pragma unroll
-            for (int g = 0; g < ND; g++) o[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(p, vv[kb][r][g], o[g], 0, 0, 0);
+            for (int r = 0; r < 4; r++) o[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(s[kb][r] * inv, vv[r], o[g], 0, 0, 0);
         }
+    if (tile >= qtiles) return;
     // o[g][r] = out[query t0 + 4kg + r][dim 16g + qi]
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -982,7 +999,12 @@ template <int ND, int NKB>
 hipError_t attn_mfma_t(const AttnArgs& a, int dh, hipStream_t s) {
     const int qtiles = (a.T + 15) / 16;
     const int groups = (qtiles + 3) / 4;
-    hipLaunchKernelGGL((attention_mfma_kernel<ND, NKB>), dim3(a.B * groups, a.heads), dim3(256), 0, s, a, dh);
+    constexpr int KEYS = 16 * (NKB + 3), DP = 16 * ND;
+    constexpr size_t lds = sizeof(float) * std::max(KEYS * (DP + 4), DP * (KEYS + 4));
+    static const hipError_t attr = hipFuncSetAttribute((const void*)attention_mfma_kernel<ND, NKB>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL((attention_mfma_kernel<ND, NKB>), dim3(a.B * groups, a.heads), dim3(256), lds, s, a, dh);
     return hipGetLastError();
 }
 
