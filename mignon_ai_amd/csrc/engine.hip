@@ -686,7 +686,7 @@ int guarded(F&& f) {
     }
 }
 
-constexpr long long kMaxChunkTokens = 1 << 19;  // tokens per workspace pass of a teacher-forced batch
+constexpr long long kMaxChunkTokens = 1 << 20;  // tokens per workspace pass of a teacher-forced batch
 
 // Stop tokens of a batched decode: after each column is written, scan() marks the sessions whose token is
 // a stop token and copies the stopped count into a pinned host slot behind an event; keep_going(k) holds
