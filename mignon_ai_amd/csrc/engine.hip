@@ -635,6 +635,7 @@ void run_head(mg_model* m, int M, const int32_t* row_map, const int32_t* tgt, fl
     GemmArgs g = lx_args(w.nl.as<int8_t>(), w.ns.as<float>(), m->headw, m->Vp, m->Dp, M, m->V, m->head_scale);
     g.bias = m->headb; g.out = logits_out; g.ldo = m->V;
     g.stats = w.stats.as<float>(); g.stats_ld = m->Vp / LX_BN;
+    g.want_argmax = hc.argmax || hc.next_ids || hc.out_ids;
     g.tgt = tgt; g.tlog = w.tlog.as<float>();
     gemm(m, EPI_LOGITS, g, s);
     hc.M = M; hc.ntiles = m->Vp / LX_BN; hc.stats = w.stats.as<float>(); hc.V = m->V;

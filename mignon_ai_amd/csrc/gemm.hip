@@ -99,13 +99,17 @@ __device__ __forceinline__ void stg_flush(const GemmArgs& g, const float* stg, i
     const int c = 4 * (lane & 31);
     const int nv = g.nvalid - n0 - c;  // valid channels from this lane's column on
     const bool vec = nv >= 4 && (ldo & 3) == 0;
+    // row mt0 + (L >> 5) + 2k: a wave-uniform base plus a per-lane offset that is the same for every
+    // tile (no per-row 64-bit multiplies)
+    float* const base = out + (long long)mt0 * ldo + n0;
+    const long long loff = (long long)(lane >> 5) * ldo + c;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
         const int row = (lane >> 5) + 2 * k;
         const int m = mt0 + row;
         const float4 v = *(const float4*)(stg + row * STG_LD + c);
         if (m < g.M && nv > 0) {
-            float* dst = out + (long long)m * ldo + n0 + c;
+            float* dst = base + 2 * k * ldo + loff;
             if (vec) {
                 if constexpr (NT) {
                     const f4v t = {v.x, v.y, v.z, v.w};
@@ -259,45 +263,49 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
         }
     } else if constexpr (EPI == EPI_LOGITS) {
         // Logits of this lane's 32 channels (vocabulary padding has bias -inf and zero weights, so its
-        // logits are -inf), four at a time: running max with its first index, and the sum of
-        // exp(l - max) rescaled whenever the max rises.
+        // logits are -inf): their max, then the sum of exp(l - max) and the first channel holding the max.
+        // Two passes over registers: no running rescale, and the argmax only when it is wanted.
         const float l2e = 1.4426950408889634f;
-        float bmax = -INFINITY, bsum = 0.0f;
-        int bidx = 0x7fffffff;
         const int t = row.tgt - nb;  // the target's position among this lane's channels
         float* orow = g.out ? g.out + (long long)m * g.ldo : nullptr;
+        float y[8][4];
 #pragma unroll
         for (int ti = 0; ti < 8; ti++) {
             const int n = nb + ti * 16;
             const float4 b = *(const float4*)(bias_t + 4 * g4 + ti * 16);
             const float bb[4] = {b.x, b.y, b.z, b.w};
-            float y[4];
 #pragma unroll
-            for (int r = 0; r < 4; r++) y[r] = fmaf(limb_dot(acc, ti, r), sw, bb[r]);
+            for (int r = 0; r < 4; r++) y[ti][r] = fmaf(limb_dot(acc, ti, r), sw, bb[r]);
             if constexpr (STG) {
-                if (orow) stg_put(stg, lane, ti, y);
+                if (orow) stg_put(stg, lane, ti, y[ti]);
             } else if (orow && mok) {
                 const int nv = g.nvalid - n;
-                if (nv > 0) store4(orow + n, y, nv, vec);
+                if (nv > 0) store4(orow + n, y[ti], nv, vec);
             }
-            float mx = bmax;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {  // channels rise with (ti, r): ties keep the first index
-                const bool up = y[r] > mx;
-                mx = up ? y[r] : mx;
-                bidx = up ? n + r : bidx;
-            }
-            const float ml = mx == -INFINITY ? 0.0f : mx * l2e;
-            const float rescale = bmax == mx ? 1.0f : __builtin_amdgcn_exp2f(fmaf(bmax, l2e, -ml));
-            float s = bsum * rescale;
-#pragma unroll
-            for (int r = 0; r < 4; r++) s += __builtin_amdgcn_exp2f(fmaf(y[r], l2e, -ml));
-            bsum = s;
-            bmax = mx;
             if (mok && t >= ti * 16 && t < ti * 16 + 4) {
                 const int r = t & 3;
-                g.tlog[m] = r == 0 ? y[0] : r == 1 ? y[1] : r == 2 ? y[2] : y[3];
+                g.tlog[m] = r == 0 ? y[ti][0] : r == 1 ? y[ti][1] : r == 2 ? y[ti][2] : y[ti][3];
             }
+        }
+        float mx = y[0][0];
+#pragma unroll
+        for (int ti = 0; ti < 8; ti++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) mx = fmaxf(mx, y[ti][r]);
+        const float ml = mx == -INFINITY ? 0.0f : mx * l2e;
+        float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ti = 0; ti < 8; ti++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) s4[r] += __builtin_amdgcn_exp2f(fmaf(y[ti][r], l2e, -ml));
+        float bmax = mx, bsum = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+        int bidx = 0x7fffffff;
+        if (g.want_argmax && mx > -INFINITY) {
+            // channels rise with (ti, r): scanning downwards, the last hit is the first index
+#pragma unroll
+            for (int ti = 7; ti >= 0; ti--)
+#pragma unroll
+                for (int r = 3; r >= 0; r--) bidx = y[ti][r] == mx ? nb + ti * 16 + r : bidx;
         }
         // the four lane groups interleave channels: combine, the smaller index wins ties
 #pragma unroll
@@ -428,7 +436,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int run = (slot / nt) * 8 + (blockIdx.x & 7);
     if (run >= n_runs) return;
     const int n0 = n_tile * LX_BN;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // the wave index, in a scalar register: tile indices and every address derived from them stay scalar
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kc = g.Kp >> 6;
     float* bias_s = (float*)(slab + kc * 8192);
     float* stg = STG ? (float*)(slab + kc * 8192 + LX_BN * 4) + w * 16 * STG_LD : nullptr;

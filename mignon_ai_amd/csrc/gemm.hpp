@@ -62,6 +62,7 @@ struct GemmArgs {
     int ldcur = 0;
     float* stats = nullptr;           // EPI_LOGITS: [m][stats_ld][3] = max, sum exp(l - max), argmax
     int stats_ld = 0;
+    int want_argmax = 1;              // EPI_LOGITS: 0 leaves the argmax entry of the statistics unset
     const int32_t* tgt = nullptr;     // EPI_LOGITS: target id per row (or null)
     float* tlog = nullptr;            // EPI_LOGITS: target logit per row
     const float* lse = nullptr;       // EPI_PROBS: log-sum-exp per row
