@@ -257,9 +257,18 @@ int mg_quantize_f32(const float* w, long long n, int8_t* q, float* scale, int fl
  *     order (bit-identical given equal inputs); MG_ATTN_MFMA computes scores and P.V on the matrix
  *     cores (fp32, other summation order). Automatic picks the matrix cores where they apply (head width
  *     a multiple of 4 up to 64, attended span up to 64 keys, or longer spans for narrower heads).
+ *   MG_OPT_SCAN_KERNEL: MG_SCAN_SEPARATE writes the latch state of every position, then limb-expands
+ *     the rule input [n | left | g] in a second kernel; MG_SCAN_FUSED does both in one pass without
+ *     writing the latch state. Both give byte-identical operands. The fused kernel applies where the
+ *     sequence length is a multiple of 16 and the padded width at most 1024; elsewhere the separate
+ *     kernels run whatever the option says. Automatic fuses where it applies to batches of many
+ *     sequences (one workgroup per sequence).
  * value < 0 only reads the option. Returns the previous value, or MG_ERR_INVALID. */
 #define MG_OPT_GEMM_KERNEL 0
 #define MG_OPT_ATTENTION_KERNEL 1
+#define MG_OPT_SCAN_KERNEL 2
+#define MG_SCAN_SEPARATE 1
+#define MG_SCAN_FUSED 2
 #define MG_GEMM_STREAM 1
 #define MG_GEMM_SLAB 2
 #define MG_ATTN_EXACT 1

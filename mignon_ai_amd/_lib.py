@@ -17,9 +17,10 @@ MG_ERR_DEVICE = -3
 MG_ERR_NOMEM = -4
 MG_ERR_UNSUPPORTED = -5
 MG_PTR_DEVICE = 1
-MG_OPT_GEMM_KERNEL, MG_OPT_ATTENTION_KERNEL = 0, 1
+MG_OPT_GEMM_KERNEL, MG_OPT_ATTENTION_KERNEL, MG_OPT_SCAN_KERNEL = 0, 1, 2
 MG_GEMM_STREAM, MG_GEMM_SLAB = 1, 2
 MG_ATTN_EXACT, MG_ATTN_MFMA = 1, 2
+MG_SCAN_SEPARATE, MG_SCAN_FUSED = 1, 2
 
 _vp = ctypes.c_void_p
 _i32p = ctypes.POINTER(ctypes.c_int32)

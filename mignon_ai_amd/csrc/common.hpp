@@ -69,6 +69,28 @@ __device__ __forceinline__ void split4_pack(float4 x, float inv, uint32_t& w0, u
     w2 = __builtin_amdgcn_perm(b2[1], b2[0], 0x0c0c0400u) | __builtin_amdgcn_perm(b2[3], b2[2], 0x04000c0cu);
 }
 
+// split4_pack for two consecutive elements: their digits in bytes 0 and 1 of each word.
+__device__ __forceinline__ void split2_pack(float2 x, float inv, uint32_t& w0, uint32_t& w1, uint32_t& w2) {
+    const float C = 12582912.0f;  // 1.5 * 2^23
+    const float xs[2] = {x.x, x.y};
+    uint32_t b0[2], b1[2], b2[2];
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        const float y = xs[e] * inv;
+        const float t0 = y + C;
+        const float y1 = (y - (t0 - C)) * kLimbBase;
+        const float t1 = y1 + C;
+        const float y2 = (y1 - (t1 - C)) * kLimbBase;
+        const float t2 = y2 + C;
+        b0[e] = __float_as_uint(t0);
+        b1[e] = __float_as_uint(t1);
+        b2[e] = __float_as_uint(t2);
+    }
+    w0 = __builtin_amdgcn_perm(b0[1], b0[0], 0x0c0c0400u);
+    w1 = __builtin_amdgcn_perm(b1[1], b1[0], 0x0c0c0400u);
+    w2 = __builtin_amdgcn_perm(b2[1], b2[0], 0x0c0c0400u);
+}
+
 __device__ __forceinline__ void limb_scale(float amax, float& scale, float& inv) {
     if (amax < kTinyAmax) {
         scale = 0.0f;

@@ -559,17 +559,27 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                     HIPCHECK(launch_export_ring(c.B, c.T, Dp, m->ring, c.lens, w.nf.as<float>(),
                                                 c.sess->norm_ring.as<float>() + (size_t)bs * c.B * m->ring * Dp, s));
                 }
-                {
-                    ProfScope ps(m->prof, K_SCAN, s);
-                    HIPCHECK(launch_scan(sa, s));
-                }
                 // rule input [n | left | g] (stream.go:180-184), limb-expanded with one scale per row
-                RowArgs r;
-                r.M = M; r.mode = ROW_RULE; r.D = D; r.Dp = 3 * Dp; r.seg = Dp; r.dil = dil; r.T = c.T;
-                r.src = w.nf.as<float>(); r.src2 = w.lam.as<float>();
-                r.limbs = w.xl.as<int8_t>(); r.lscale = w.xs.as<float>();
-                ProfScope ps(m->prof, K_SCAN, s);
-                HIPCHECK(launch_row(r, s));
+                // The fused kernel runs one workgroup per sequence: automatic selection wants enough of
+                // them (at least 2048 waves) to cover the latency of its sequential rounds.
+                const int sk = option(OPT_SCAN_KERNEL);
+                const bool many = (long long)c.B * ((Dp / 2 + 63) / 64) >= 2048;
+                if (scan_rule_fits(c.T, Dp, dil) && (sk == 2 || (sk == 0 && many))) {
+                    sa.dil = dil; sa.xl = w.xl.as<int8_t>(); sa.xs = w.xs.as<float>();
+                    ProfScope ps(m->prof, K_SCAN, s);
+                    HIPCHECK(launch_scan_rule(sa, s));
+                } else {
+                    {
+                        ProfScope ps(m->prof, K_SCAN, s);
+                        HIPCHECK(launch_scan(sa, s));
+                    }
+                    RowArgs r;
+                    r.M = M; r.mode = ROW_RULE; r.D = D; r.Dp = 3 * Dp; r.seg = Dp; r.dil = dil; r.T = c.T;
+                    r.src = w.nf.as<float>(); r.src2 = w.lam.as<float>();
+                    r.limbs = w.xl.as<int8_t>(); r.lscale = w.xs.as<float>();
+                    ProfScope ps(m->prof, K_SCAN, s);
+                    HIPCHECK(launch_row(r, s));
+                }
             }
             // h = GLU(x) (stream.go:214-220) in fp32, then limb-expanded with one scale per row
             g = lx_args(w.xl.as<int8_t>(), w.xs.as<float>(), blk.w1, 2 * Hp, 3 * Dp, M, m->H, blk.s1);

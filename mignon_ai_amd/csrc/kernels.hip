@@ -338,6 +338,177 @@ __global__ __launch_bounds__(1024) void scan_kernel(ScanArgs a) {
     }
 }
 
+// Row maxima of 16 positions across a wave: v[k] is this lane's value for position k. Each exchange
+// halves the set a lane keeps (the half its lane bit selects) and folds in the partner's maxima of that
+// half; afterwards lane L holds the wave's maximum for position 8*b5 + 4*b4 + 2*b3 + b2 (bK = bit K
+// of L), in all four lanes that share bits 2..5.
+// (The empty asm makes each pair's values opaque, so that the compiler selects between the two values
+// and does not turn the choice into a lane-dependent index into the array.)
+__device__ __forceinline__ float opaque(float x) {
+    asm("" : "+v"(x));
+    return x;
+}
+
+__device__ __forceinline__ float wave_max16(float (&v)[16], int lane) {
+#pragma unroll
+    for (int h = 8, o = 32; h >= 1; h >>= 1, o >>= 1) {
+        const bool hi = (lane & o) != 0;
+#pragma unroll
+        for (int i = 0; i < h; i++) {
+            const float lo = opaque(v[i]), up = opaque(v[i + h]);
+            const float keep = hi ? up : lo;
+            const float send = hi ? lo : up;
+            v[i] = fmaxf(keep, __shfl_xor(send, o, 64));
+        }
+    }
+    float r = v[0];
+    r = fmaxf(r, __shfl_xor(r, 2, 64));
+    r = fmaxf(r, __shfl_xor(r, 1, 64));
+    return r;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Latch scan fused with the rule input. One workgroup per sequence; thread j owns channels 2j, 2j+1
+// and runs the recurrence over the positions in rounds of one 16-token tile (T is a multiple of 16, so
+// a tile never spans two sequences). Per round:
+//   - loads of n and lambda for the 16 positions, all issued first;
+//   - g = lam*g + (1-lam)*n with scan_kernel's rounding (stream.go:195-205);
+//   - the absmax of each row [n | left | g] (stream.go:180-184): the wave maxima of |n| and |g|
+//     (wave_max16) are combined through LDS, and the left segment's maximum is the max|n| of row
+//     t - dil, kept in a 64-row ring (dilations are at most 48, so the ring never overwrites a row
+//     still needed);
+//   - the three segments, limb-expanded into LDS in the fragment layout, one at a time, each stored as
+//     whole 1 KiB fragments; the left neighbours n[t - dil] are loaded again (from cache) only then.
+// The output is byte-identical to scan_kernel followed by row_kernel in ROW_RULE mode, without writing
+// g and reading it back. g is stored only as a session's exported state.
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(512) void scan_rule_kernel(ScanArgs a) {
+    extern __shared__ __align__(16) int8_t sr_smem[];
+    const int b = blockIdx.x, j = threadIdx.x, lane = j & 63, w = j >> 6, nw = blockDim.x >> 6;
+    const int D = a.D, Dp = a.Dp, T = a.T, C2 = Dp >> 1, dil = a.dil;
+    const int jc = min(j, C2 - 1);
+    const int seg_bytes = (Dp >> 6) * 3072;  // one segment of a tile: Dp/64 K steps x 3 limbs x 1 KiB
+    int8_t* stage = sr_smem;
+    float* red = (float*)(sr_smem + (seg_bytes >> 10) * 1088);  // [2][nw][16] wave maxima of |n|, |g|
+    float* nring = red + 32 * nw;                                // [64] max|n| of row t at t & 63
+    float* part = nring + 64;                                    // [16] max(|n|, |g|) of the round's rows
+    float* invs = part + 16;                                     // [16] 127 / row absmax
+    const long long seq0 = (long long)b * T;
+    const int last = a.lens ? a.lens[b] - 1 : -1;
+    const bool on = j < C2;
+    const bool c0 = on && 2 * j < D, c1 = on && 2 * j + 1 < D;  // columns past D are zero
+    // elements 2j, 2j+1 of a row: chunk cc of four, K step cc>>4, byte 4(cc&3) + 2(j&1) of column group
+    // (cc>>2)&3
+    const int cc = j >> 1;
+    const int o0 = (cc >> 4) * 3072 + 256 * ((cc >> 2) & 3) + 4 * (cc & 3) + 2 * (j & 1);
+    const int p = 8 * ((lane >> 5) & 1) + 4 * ((lane >> 4) & 1) + 2 * ((lane >> 3) & 1) + ((lane >> 2) & 1);
+    float g0 = 0.0f, g1 = 0.0f;
+    // n and lambda of the round, loaded while the previous round is packed and stored
+    float2 nv[16], gv[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        nv[k] = *(const float2*)(a.nf + (seq0 + k) * Dp + 2 * jc);
+        gv[k] = *(const float2*)(a.lam + (seq0 + k) * Dp + 2 * jc);
+    }
+    for (int t0 = 0; t0 < T; t0 += 16) {
+        float mn[16], mg[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const float n0 = c0 ? nv[k].x : 0.0f, n1 = c1 ? nv[k].y : 0.0f;
+            if (c0) {
+                const float p1 = gv[k].x * g0;
+                const float p2 = (1.0f - gv[k].x) * n0;
+                g0 = p1 + p2;
+            }
+            if (c1) {
+                const float p1 = gv[k].y * g1;
+                const float p2 = (1.0f - gv[k].y) * n1;
+                g1 = p1 + p2;
+            }
+            nv[k] = make_float2(n0, n1);
+            gv[k] = make_float2(g0, g1);
+            mn[k] = fmaxf(fabsf(n0), fabsf(n1));
+            mg[k] = fmaxf(fabsf(g0), fabsf(g1));
+            if (t0 + k == last && a.g_out && on) *(float2*)(a.g_out + (long long)b * Dp + 2 * j) = gv[k];
+        }
+        const float wn = wave_max16(mn, lane);
+        const float wg = wave_max16(mg, lane);
+        if ((lane & 3) == 0) {
+            red[w * 16 + p] = wn;
+            red[(nw + w) * 16 + p] = wg;
+        }
+        __syncthreads();
+        if (j < 16) {
+            float nr = red[j], gr = red[nw * 16 + j];
+            for (int v = 1; v < nw; v++) {
+                nr = fmaxf(nr, red[v * 16 + j]);
+                gr = fmaxf(gr, red[(nw + v) * 16 + j]);
+            }
+            nring[(t0 + j) & 63] = nr;
+            part[j] = fmaxf(nr, gr);
+        }
+        __syncthreads();
+        if (j < 16) {
+            const int t = t0 + j;
+            const float mx = fmaxf(part[j], t >= dil ? nring[(t - dil) & 63] : 0.0f);
+            float sc, inv;
+            limb_scale(mx, sc, inv);
+            a.xs[seq0 + t] = sc;
+            invs[j] = inv;
+        }
+        __syncthreads();
+        // the left neighbours (recently loaded rows: from cache), staged second
+        float2 lv[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const int t = t0 + k;
+            const float2 v = *(const float2*)(a.nf + (seq0 + max(t - dil, 0)) * Dp + 2 * jc);
+            const bool hl = t >= dil;
+            lv[k] = make_float2((hl && c0) ? v.x : 0.0f, (hl && c1) ? v.y : 0.0f);
+        }
+        // the next round's n and lambda (this round's again after the last: in bounds, unused)
+        const int tn = t0 + 16 < T ? t0 + 16 : t0;
+        float2 nvn[16], gvn[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            nvn[k] = *(const float2*)(a.nf + (seq0 + tn + k) * Dp + 2 * jc);
+            gvn[k] = *(const float2*)(a.lam + (seq0 + tn + k) * Dp + 2 * jc);
+        }
+        float inv[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) inv[k] = invs[k];
+        int8_t* dst = a.xl + (seq0 + t0) / 16 * (3LL * seg_bytes);  // this tile's rule-input fragments
+        auto segment = [&](const float2 (&x)[16], int sg) {
+            if (on) {
+                // o0 + 16k stays inside o0's 256-byte column group (o0 & 255 <= 14), so every digit's LDS
+                // address is sb plus a constant
+                int8_t* sb = stage + stage_off(o0);
+#pragma unroll
+                for (int k = 0; k < 16; k++) {
+                    uint32_t w0, w1, w2;
+                    split2_pack(x[k], inv[k], w0, w1, w2);
+                    *(uint16_t*)(sb + 16 * k) = (uint16_t)w0;
+                    *(uint16_t*)(sb + 16 * k + 1088) = (uint16_t)w1;
+                    *(uint16_t*)(sb + 16 * k + 2176) = (uint16_t)w2;
+                }
+            }
+            __syncthreads();
+            for (int o = j * 16; o < seg_bytes; o += blockDim.x * 16)
+                *(v4i*)(dst + sg * seg_bytes + o) = *(const v4i*)(stage + stage_off(o));
+            __syncthreads();
+        };
+        segment(nv, 0);
+        segment(lv, 1);
+        segment(gv, 2);
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            nv[k] = nvn[k];
+            gv[k] = gvn[k];
+        }
+    }
+}
+
+
 __global__ __launch_bounds__(1024) void latch_step_kernel(LatchStepArgs a) {
     __shared__ float red[16];
     const int s_ = blockIdx.x;
@@ -1090,6 +1261,17 @@ hipError_t launch_scan(const ScanArgs& a, hipStream_t s) {
     if (a.B <= 0) return hipSuccess;
     if (a.Dp % 64 || a.Dp > 1024 || a.D < 1) return hipErrorInvalidValue;
     hipLaunchKernelGGL(scan_kernel, dim3(a.B), dim3(a.Dp), 0, s, a);
+    return hipGetLastError();
+}
+
+bool scan_rule_fits(int T, int Dp, int dil) { return T % 16 == 0 && Dp % 64 == 0 && Dp <= 1024 && dil >= 1 && dil <= 48; }
+
+hipError_t launch_scan_rule(const ScanArgs& a, hipStream_t s) {
+    if (!scan_rule_fits(a.T, a.Dp, a.dil) || a.D > a.Dp) return hipErrorInvalidValue;
+    if (a.B == 0 || a.T == 0) return hipSuccess;
+    const int threads = ((a.Dp / 2 + 63) / 64) * 64;
+    const size_t lds = (size_t)(a.Dp / 64) * 3 * 1088 + (2 * (threads / 64) * 16 + 64 + 16 + 16) * sizeof(float);
+    hipLaunchKernelGGL(scan_rule_kernel, dim3(a.B), dim3(threads), lds, s, a);
     return hipGetLastError();
 }
 

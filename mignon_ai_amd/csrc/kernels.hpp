@@ -43,8 +43,15 @@ struct ScanArgs {
     float* g = nullptr;          // [B*T][Dp] latch state after each position (may be lam itself)
     const int32_t* lens = nullptr;  // per-sequence length (export position lens[b]-1) or null
     float* g_out = nullptr;         // exported latch state [B][Dp] or null
+    // scan_rule only: the rule input [n | left | g] limb-expanded (K = 3*Dp) with one scale per row
+    int dil = 1;
+    int8_t* xl = nullptr;
+    float* xs = nullptr;
 };
 hipError_t launch_scan(const ScanArgs& a, hipStream_t s);
+// Whether launch_scan_rule takes these sizes (T a multiple of 16, Dp <= 1024, dilation at most 48).
+bool scan_rule_fits(int T, int Dp, int dil);
+hipError_t launch_scan_rule(const ScanArgs& a, hipStream_t s);
 
 // One streaming position per session: latch update, norm ring write and the rule input.
 struct LatchStepArgs {

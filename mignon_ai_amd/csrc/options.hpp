@@ -6,6 +6,7 @@ namespace mg {
 enum Option : int {
     OPT_GEMM_KERNEL = 0,       // 0 automatic, 1 streaming, 2 weight-stationary
     OPT_ATTENTION_KERNEL = 1,  // 0 automatic, 1 reference order (VALU), 2 matrix cores
+    OPT_SCAN_KERNEL = 2,       // 0 automatic, 1 latch scan then rule-input packing, 2 fused
     OPT_COUNT
 };
 

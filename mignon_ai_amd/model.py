@@ -277,7 +277,8 @@ def quantize_f32(w):
     return q, np.float32(s[0])
 
 
-_OPTIONS = {"gemm": (0, ["auto", "stream", "slab"]), "attention": (1, ["auto", "exact", "mfma"])}
+_OPTIONS = {"gemm": (0, ["auto", "stream", "slab"]), "attention": (1, ["auto", "exact", "mfma"]),
+            "scan": (2, ["auto", "separate", "fused"])}
 
 
 def sample_logits(logits, recent=None, temperature=1.0, top_k=0, top_p=1.0, rep_penalty=1.0, u=None):
@@ -303,8 +304,8 @@ def sample_logits(logits, recent=None, temperature=1.0, top_k=0, top_p=1.0, rep_
 
 
 def engine_option(name: str, value: str | None = None) -> str:
-    """mg_engine_option: which implementation runs for "gemm" ("auto", "stream", "slab") or "attention"
-    ("auto", "exact", "mfma"), for the whole process. Returns the previous value (value None only
+    """mg_engine_option: which implementation runs for "gemm" ("auto", "stream", "slab"), "attention"
+    ("auto", "exact", "mfma") or "scan" ("auto", "separate", "fused"), for the whole process. Returns the previous value (value None only
     reads it)."""
     opt, names = _OPTIONS[name]
     prev = lib().mg_engine_option(opt, -1 if value is None else names.index(value))
