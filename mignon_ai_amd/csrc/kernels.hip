@@ -730,7 +730,7 @@ __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
 
 // ------------------------------------------------------------------------------------------------
 // Windowed attention on the matrix cores (v_mfma_f32_16x16x4f32). One wave per 16-query tile of one
-// (sequence, head); four consecutive tiles per workgroup share keys and values through L1.
+// (sequence, head); G consecutive tiles per workgroup share keys and values staged in LDS.
 //
 // Scores are computed transposed, S^T = K Q^T, so that afterwards lane L holds the scores of query
 // t0 + (L & 15) against keys jb + 4(L >> 4) + r of each 16-key block: exactly the A operand that P.V
@@ -742,28 +742,30 @@ __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
 // ------------------------------------------------------------------------------------------------
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-// Windowed causal attention on the fp32 matrix cores. A workgroup is four waves; wave w takes the 16
-// queries of tile 4*grp + w for head blockIdx.y. The 16*(NKB+3) keys the four tiles attend are staged in
+// Windowed causal attention on the fp32 matrix cores. A workgroup is G waves; wave w takes the 16
+// queries of tile G*grp + w for head blockIdx.y. The 16*(NKB+G-1) keys the G tiles attend are staged in
 // LDS once: keys first (row-major), then, over the same buffer, values transposed, so that every matrix
 // operand is one 16-byte LDS read. Per wave: S^T = K Q^T over NKB blocks of 16 keys (dims 16g + 4kg + e),
-// the reference's softmax in registers, then out = P V.
-template <int ND, int NKB>
-__global__ __launch_bounds__(256) void attention_mfma_kernel(AttnArgs a, int dh) {
-    constexpr int KEYS = 16 * (NKB + 3);  // keys of the workgroup's four query tiles
+// the reference's softmax in registers, then out = P V. More tiles per workgroup read each key and value
+// from memory fewer times (G = 8 covers a 128-token sequence with every key loaded once).
+template <int ND, int NKB, int G>
+__global__ __launch_bounds__(64 * G) void attention_mfma_kernel(AttnArgs a, int dh) {
+    constexpr int NT = 64 * G;            // threads
+    constexpr int KEYS = 16 * (NKB + G - 1);  // keys of the workgroup's G query tiles
     constexpr int DP = 16 * ND;           // head width padded to the MFMA's 16
     constexpr int KS = DP + 4;            // LDS row stride of K (floats)
     constexpr int VS = KEYS + 4;          // LDS row stride of V^T (floats)
     constexpr int CH = DP / 4;            // 16-byte chunks per key row
     constexpr int NCH = KEYS * CH;
-    constexpr int PER = (NCH + 255) / 256;
+    constexpr int PER = (NCH + NT - 1) / NT;
     extern __shared__ __align__(16) float att_lds[];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, tid = threadIdx.x;
     const int T = a.T, D = a.D, cap = a.cap, ld = 3 * D;
     const int qtiles = (T + 15) >> 4;
-    const int groups = (qtiles + 3) >> 2;
+    const int groups = (qtiles + G - 1) / G;
     const int b = blockIdx.x / groups;
     const int grp = blockIdx.x % groups;
-    const int tile = grp * 4 + w;
+    const int tile = grp * G + w;
     const int h = blockIdx.y;
     const int t0 = tile * 16;
     const int qi = lane & 15, kg = lane >> 4;
@@ -772,7 +774,7 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(AttnArgs a, int dh)
     const float* kb_ = seq + D + h * dh;
     const float* vb = seq + 2 * D + h * dh;
     const float scale = (float)(1.0 / sqrt((double)dh));
-    const int kbase = grp * 64 + 16 - 16 * NKB;  // key of LDS row 0
+    const int kbase = grp * 16 * G + 16 - 16 * NKB;  // key of LDS row 0
 
     // Every global load is unconditional, from an address clamped into the sequence and the head, and
     // masked afterwards (a guarded load becomes a branch that waits for it on the spot). Keys outside
@@ -781,7 +783,7 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(AttnArgs a, int dh)
     v4f kreg[PER], vreg[PER];
 #pragma unroll
     for (int p = 0; p < PER; p++) {
-        const int e = min(tid + 256 * p, NCH - 1);
+        const int e = min(tid + NT * p, NCH - 1);
         const int key = e / CH, d = 4 * (e - key * CH);
         const int j = kbase + key;
         const long long off = (long long)min(max(j, 0), T - 1) * ld + min(d, dh - 4);
@@ -801,7 +803,7 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(AttnArgs a, int dh)
     }
 #pragma unroll
     for (int p = 0; p < PER; p++) {
-        const int e = tid + 256 * p;
+        const int e = tid + NT * p;
         if (e < NCH) {
             const int key = e / CH, c = e - key * CH;
             *(v4f*)(att_lds + key * KS + 4 * c) = kreg[p];
@@ -823,7 +825,7 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(AttnArgs a, int dh)
     __syncthreads();  // every wave's keys are read: the buffer takes the values
 #pragma unroll
     for (int p = 0; p < PER; p++) {
-        const int e = tid + 256 * p;
+        const int e = tid + NT * p;
         if (e < NCH) {
             const int key = e / CH, c = e - key * CH;
 #pragma unroll
@@ -1166,17 +1168,24 @@ hipError_t attn_t(const AttnArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int ND, int NKB>
-hipError_t attn_mfma_t(const AttnArgs& a, int dh, hipStream_t s) {
+template <int ND, int NKB, int G>
+hipError_t attn_mfma_g(const AttnArgs& a, int dh, hipStream_t s) {
     const int qtiles = (a.T + 15) / 16;
-    const int groups = (qtiles + 3) / 4;
-    constexpr int KEYS = 16 * (NKB + 3), DP = 16 * ND;
+    const int groups = (qtiles + G - 1) / G;
+    constexpr int KEYS = 16 * (NKB + G - 1), DP = 16 * ND;
     constexpr size_t lds = sizeof(float) * std::max(KEYS * (DP + 4), DP * (KEYS + 4));
-    static const hipError_t attr = hipFuncSetAttribute((const void*)attention_mfma_kernel<ND, NKB>,
+    static const hipError_t attr = hipFuncSetAttribute((const void*)attention_mfma_kernel<ND, NKB, G>,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((attention_mfma_kernel<ND, NKB>), dim3(a.B * groups, a.heads), dim3(256), lds, s, a, dh);
+    hipLaunchKernelGGL((attention_mfma_kernel<ND, NKB, G>), dim3(a.B * groups, a.heads), dim3(64 * G), lds, s, a,
+                       dh);
     return hipGetLastError();
+}
+
+// Eight query tiles per workgroup where sequences have at least six (fewer would leave waves idle).
+template <int ND, int NKB>
+hipError_t attn_mfma_t(const AttnArgs& a, int dh, hipStream_t s) {
+    return (a.T + 15) / 16 >= 6 ? attn_mfma_g<ND, NKB, 8>(a, dh, s) : attn_mfma_g<ND, NKB, 4>(a, dh, s);
 }
 
 // Key blocks per 16-query tile: the widest span any query attends is W = min(window, cap) keys, so the
