@@ -526,14 +526,24 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
     const int M = c.B * c.T;
     const int Dp = m->Dp, Hp = m->Hp, D = m->D;
     int bs = 0, ab = 0;
+    // The inter-block residual (blockIn += cur; cur = blockIn, stream.go:157-163) is done by the last GEMM
+    // of a block when the next block has steps: it adds its new state into blockIn instead of storing
+    // cur. The next block then reads its input from blockIn (norm and first highway), and cur is only
+    // written again by that highway.
+    bool in_bin = false;  // this block's input is in blockIn, and cur is stale
     for (size_t b = 0; b < m->blocks.size(); b++) {
         const DevBlock& blk = m->blocks[b];
         const int mode = b == 0 ? ROW_EMBED : ROW_RESID;
+        const bool fuse_next = b + 1 < m->blocks.size() && m->blocks[b + 1].steps > 0 && (blk.attn || blk.steps > 0);
         if (blk.steps == 0) row_call(m, M, mode, c.ids, nullptr, 0, nullptr, nullptr, nullptr, false, s);
         for (int st = 0; st < blk.steps; st++, bs++) {
             const int dil = blk.dilation(st);
             // n = RMSNorm(cur; gamma) (stream.go:166-171), fused with the embedding / residual at step 0
-            row_call(m, M, st == 0 ? mode : ROW_SRC, c.ids, nullptr, 0, nullptr, blk.gamma, w.nf.as<float>(), true, s);
+            if (st == 0 && in_bin)
+                row_call(m, M, ROW_SRC, nullptr, w.bin.as<float>(), Dp, nullptr, blk.gamma, w.nf.as<float>(), true, s);
+            else
+                row_call(m, M, st == 0 ? mode : ROW_SRC, c.ids, nullptr, 0, nullptr, blk.gamma, w.nf.as<float>(), true,
+                         s);
             // lambda = sigmoid_clamped(n.W_sel*s + base) (stream.go:195-205)
             GemmArgs g = lx_args(w.nl.as<int8_t>(), w.ns.as<float>(), blk.wsel, m->NpD, Dp, M, D, blk.ssel);
             g.bias = m->latch_base; g.out = w.lam.as<float>(); g.ldo = Dp;
@@ -595,6 +605,8 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
             // cur = highway(cur, W2 h) (stream.go:222-229)
             g = lx_args(w.hl.as<int8_t>(), w.hs.as<float>(), blk.w2, 2 * Dp, Hp, M, D, blk.s2);
             g.bias = blk.b2; g.cur = w.cur.as<float>(); g.ldcur = Dp;
+            if (st == 0 && in_bin) g.cur_in = w.bin.as<float>();
+            if (st + 1 == blk.steps && !blk.attn && fuse_next) g.resid = w.bin.as<float>();
             gemm(m, EPI_HIGHWAY, g, s);
         }
         if (blk.attn) {
@@ -628,9 +640,11 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
             row_call(m, M, ROW_SRC, nullptr, w.att.as<float>(), Dp, nullptr, nullptr, nullptr, true, s);
             g = lx_args(w.nl.as<int8_t>(), w.ns.as<float>(), blk.wo, m->NpD, Dp, M, D, blk.so);
             g.cur = w.cur.as<float>(); g.ldcur = Dp;
+            if (fuse_next) g.resid = w.bin.as<float>();
             gemm(m, EPI_RESID, g, s);
             ab++;
         }
+        in_bin = fuse_next;
     }
     if (m->blocks.empty()) row_call(m, M, ROW_EMBED, c.ids, nullptr, 0, nullptr, nullptr, nullptr, false, s);
 }

@@ -161,11 +161,14 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
         }
         if constexpr (STG) stg_flush<true>(g, stg, lane, mt0, n0, g.out, g.ldo);
     } else if constexpr (EPI == EPI_RESID) {
-        // cur += x.w: all eight row segments are loaded before any is needed (one memory latency)
+        // cur += x.w: all eight row segments are loaded before any is needed (one memory latency). With
+        // resid, the new state is added into resid instead (blockIn += cur) and cur is left as it was.
         if (!mok) return;
-        float* crow = g.cur + (long long)m * g.ldcur;
+        const long long ro = (long long)m * g.ldcur;
+        const float* crow = (g.cur_in ? g.cur_in : g.cur) + ro;
+        float* orow = g.resid ? g.resid + ro : g.cur + ro;
         const bool cvec = (g.ldcur & 3) == 0;
-        float c[8][4];
+        float c[8][4], rs[8][4];
 #pragma unroll
         for (int ti = 0; ti < 8; ti++) {
             const int n = nb + ti * 16;
@@ -173,9 +176,16 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
             if (nv >= 4 && cvec) {
                 const float4 t = *(const float4*)(crow + n);
                 c[ti][0] = t.x; c[ti][1] = t.y; c[ti][2] = t.z; c[ti][3] = t.w;
+                if (g.resid) {
+                    const float4 u = *(const float4*)(orow + n);
+                    rs[ti][0] = u.x; rs[ti][1] = u.y; rs[ti][2] = u.z; rs[ti][3] = u.w;
+                }
             } else {
 #pragma unroll
-                for (int r = 0; r < 4; r++) c[ti][r] = r < nv ? crow[n + r] : 0.0f;
+                for (int r = 0; r < 4; r++) {
+                    c[ti][r] = r < nv ? crow[n + r] : 0.0f;
+                    if (g.resid) rs[ti][r] = r < nv ? orow[n + r] : 0.0f;
+                }
             }
         }
 #pragma unroll
@@ -186,7 +196,11 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
             float v[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) v[r] = c[ti][r] + limb_dot(acc, ti, r) * sw;
-            store4(crow + n, v, nv, cvec);
+            if (g.resid) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) v[r] = rs[ti][r] + v[r];  // blockIn += cur (stream.go:157-163)
+            }
+            store4(orow + n, v, nv, cvec);
         }
     } else if constexpr (EPI == EPI_PROBS) {
         // p = exp(l - lse) = 2^(x.w*log2e + (b - lse)*log2e)
@@ -212,12 +226,16 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
         // W rows are reordered in blocks of 32: 16 value rows then the 16 matching gate rows, so tile
         // pair (2p, 2p+1) holds value and gate of output channel n0/2 + 16p + 4*(L >> 4) + r.
         if (!mok) return;
-        float c[4][4];
-        float* crow = nullptr;
+        float c[4][4], rs[4][4];
+        const float* crow = nullptr;
+        float* wrow = nullptr;
         const bool cvec = (g.ldcur & 3) == 0;
         if constexpr (EPI == EPI_HIGHWAY) {
-            // the four cur segments this lane updates, loaded together
-            crow = g.cur + (long long)m * g.ldcur;
+            // the four cur segments this lane updates (and, with resid, the four it adds into), loaded
+            // together
+            const long long ro = (long long)m * g.ldcur;
+            crow = (g.cur_in ? g.cur_in : g.cur) + ro;
+            wrow = g.resid ? g.resid + ro : g.cur + ro;
 #pragma unroll
             for (int p = 0; p < 4; p++) {
                 const int ch = n0 / 2 + p * 16 + 4 * g4;
@@ -225,9 +243,16 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
                 if (nv >= 4 && cvec) {
                     const float4 t = *(const float4*)(crow + ch);
                     c[p][0] = t.x; c[p][1] = t.y; c[p][2] = t.z; c[p][3] = t.w;
+                    if (g.resid) {
+                        const float4 u = *(const float4*)(wrow + ch);
+                        rs[p][0] = u.x; rs[p][1] = u.y; rs[p][2] = u.z; rs[p][3] = u.w;
+                    }
                 } else {
 #pragma unroll
-                    for (int r = 0; r < 4; r++) c[p][r] = r < nv ? crow[ch + r] : 0.0f;
+                    for (int r = 0; r < 4; r++) {
+                        c[p][r] = r < nv ? crow[ch + r] : 0.0f;
+                        if (g.resid) rs[p][r] = r < nv ? wrow[ch + r] : 0.0f;
+                    }
                 }
             }
         }
@@ -258,7 +283,11 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
                     const float b = gt[r] * ov[r];
                     v[r] = a + b;
                 }
-                store4(crow + ch, v, nv, cvec);
+                if (g.resid) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) v[r] = rs[p][r] + v[r];  // blockIn += cur (stream.go:157-163)
+                }
+                store4(wrow + ch, v, nv, cvec);
             }
         }
     } else if constexpr (EPI == EPI_LOGITS) {

@@ -60,6 +60,9 @@ struct GemmArgs {
     int32_t* out_i32 = nullptr;       // EPI_C2 raw accumulators (row stride ldo)
     float* cur = nullptr;             // EPI_HIGHWAY / EPI_RESID state, row stride ldcur
     int ldcur = 0;
+    const float* cur_in = nullptr;    // EPI_HIGHWAY / EPI_RESID: read the state from here (null: from cur)
+    float* resid = nullptr;           // EPI_HIGHWAY / EPI_RESID: when set, the new state v is added into
+                                      // it (resid += v, the inter-block residual) instead of stored to cur
     float* stats = nullptr;           // EPI_LOGITS: [m][stats_ld][3] = max, sum exp(l - max), argmax
     int stats_ld = 0;
     int want_argmax = 1;              // EPI_LOGITS: 0 leaves the argmax entry of the statistics unset

@@ -81,3 +81,25 @@ def test_forward_out_of_range_ids_clamp():
     out = gm.forward_batch(ids)
     ref = om.forward_all(ids)
     assert_close(out["logits"], ref)
+
+
+@pytest.mark.parametrize("heads", [0, 2])
+def test_block_residual_paths(heads):
+    """The inter-block residual is added by a block's last GEMM (out projection, or the last highway)
+    when the next block has steps, and by the row kernel otherwise: blocks without steps (attention only,
+    or nothing but the residual) between blocks with steps, decoded through both routes, against the
+    oracle; then the same model through sessions (prefill and streamed steps)."""
+    from helpers import tiny_spec, uniform_model_bytes
+    spec = tiny_spec([(2, 2, 1), (0, 2, 1), (1, 2, 1), (2, 3, 1)], V=61, D=24, H=20, heads=heads,
+                     window=9 if heads else 0)
+    data = uniform_model_bytes(spec, scale=0.4)
+    gm = Model(data)
+    om = oracle_model(data)
+    ids = synth.token_ids(41, f"resid{heads}", (3, 40), spec.V)
+    assert_close(gm.forward_batch(ids)["logits"], om.forward_all(ids), what=f"blocks with and without steps, heads {heads}")
+    ss = gm.sessions(3)
+    lg, am, pb = ss.prefill(ids[:, :20])
+    assert_close(lg, om.forward_all(ids[:, :20])[:, -1], what="session prefill")
+    for t in range(20, 24):
+        lg, am, pb = ss.step(ids[:, t])
+        assert_close(lg, om.forward_all(ids[:, :t + 1])[:, -1], what=f"session step {t}")
