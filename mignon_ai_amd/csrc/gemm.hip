@@ -330,11 +330,14 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
         float bmax = mx, bsum = (s4[0] + s4[1]) + (s4[2] + s4[3]);
         int bidx = 0x7fffffff;
         if (g.want_argmax && mx > -INFINITY) {
-            // channels rise with (ti, r): scanning downwards, the last hit is the first index
+            // channels rise with (ti, r): scanning downwards, the last hit is the first index (kept as the
+            // offset 16ti + r, a literal, and turned into a channel once)
+            int off = 0;
 #pragma unroll
             for (int ti = 7; ti >= 0; ti--)
 #pragma unroll
-                for (int r = 3; r >= 0; r--) bidx = y[ti][r] == mx ? nb + ti * 16 + r : bidx;
+                for (int r = 3; r >= 0; r--) off = y[ti][r] == mx ? ti * 16 + r : off;
+            bidx = nb + off;
         }
         // the four lane groups interleave channels: combine, the smaller index wins ties
 #pragma unroll
@@ -755,7 +758,9 @@ hipError_t launch_slab_t(const GemmArgs& a, hipStream_t stream) {
     const int grid = 8 * nt * ((n_runs + 7) / 8);
     // REM = kc % 3 for kc >= 3; 3 marks kc == 2
     const int rem = kc == 2 ? 3 : kc % 3;
-    const bool full = kc == 4 || kc == 6;
+    // The whole-tile prefetch holds 18-24 more registers per K step; the residual epilogue's loads (state
+    // and blockIn rows) do not fit beside it without spilling.
+    const bool full = (kc == 4 || kc == 6) && EPI != EPI_RESID;
     if constexpr (can_stage<EPI>()) {
         if (stg && full) return slab_launch_full<EPI, true>(kc, a, grid, lds, run_tiles, n_runs, stream);
         if (stg) {
