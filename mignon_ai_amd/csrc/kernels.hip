@@ -742,6 +742,13 @@ __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
 // ------------------------------------------------------------------------------------------------
 typedef float v4f __attribute__((ext_vector_type(4)));
 
+// Column swizzle of the transposed values in LDS: row r (a head dimension) stores key k at column
+// k ^ vswz(r). The swizzle flips bits 2-3 of the key, so groups of four keys stay contiguous and
+// 16-byte aligned (every P.V operand is still one 16-byte read, conflict-free) and a key never leaves its
+// block of 16. The transposing writes, where 16 lanes write one key's 16 dimension-quads, then spread
+// over all banks instead of two.
+__device__ __forceinline__ int vswz(int r) { return 4 * ((r >> 3) & 3); }
+
 // Windowed causal attention on the fp32 matrix cores. A workgroup is G waves; wave w takes the 16
 // queries of tile G*grp + w for head blockIdx.y. The 16*(NKB+G-1) keys the G tiles attend are staged in
 // LDS once: keys first (row-major), then, over the same buffer, values transposed, so that every matrix
@@ -829,7 +836,7 @@ __global__ __launch_bounds__(64 * G) void attention_mfma_kernel(AttnArgs a, int 
         if (e < NCH) {
             const int key = e / CH, c = e - key * CH;
 #pragma unroll
-            for (int i = 0; i < 4; i++) att_lds[(4 * c + i) * VS + key] = vreg[p][i];
+            for (int i = 0; i < 4; i++) att_lds[(4 * c + i) * VS + (key ^ vswz(4 * c + i))] = vreg[p][i];
         }
     }
     const int t = t0 + qi;
@@ -869,7 +876,7 @@ __global__ __launch_bounds__(64 * G) void attention_mfma_kernel(AttnArgs a, int 
     for (int kb = 0; kb < NKB; kb++)
 #pragma unroll
         for (int g = 0; g < ND; g++) {
-            const v4f vv = *(const v4f*)(att_lds + (16 * g + qi) * VS + 16 * (w + kb) + 4 * kg);
+            const v4f vv = *(const v4f*)(att_lds + (16 * g + qi) * VS + ((16 * (w + kb) + 4 * kg) ^ vswz(16 * g + qi)));
 #pragma unroll
             for (int r = 0; r < 4; r++) o[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(s[kb][r] * inv, vv[r], o[g], 0, 0, 0);
         }
