@@ -755,8 +755,9 @@ hipError_t launch_slab_t(const GemmArgs& a, hipStream_t stream) {
     const bool stg = can_stage<EPI>() && lds + STG_BYTES <= slab_lds_limit();
     if (stg) lds += STG_BYTES;
     // runs of R groups of 8 tiles: long enough to amortise the slab copy, short enough to fill the chip
+    // (wide GEMMs have workgroups to spare and take longer runs)
     const int groups = (mtiles + 7) / 8;
-    const int R = std::max(1, std::min(16, groups * nt / 512));
+    const int R = std::max(1, std::min(nt >= 8 ? 32 : 16, groups * nt / 512));
     const int run_tiles = 8 * R;
     const int n_runs = (mtiles + run_tiles - 1) / run_tiles;
     const int grid = 8 * nt * ((n_runs + 7) / 8);
