@@ -130,6 +130,8 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
     extern __shared__ __align__(16) double smp_smem[];
     __shared__ double red_v[kThreads / 64];
     __shared__ int red_i[kThreads / 64];
+    __shared__ double red2_v[2][kThreads / 64];
+    __shared__ int red2_i[2][kThreads / 64];
     __shared__ int chosen_sh;
     const int row = blockIdx.x;
     const int V = a.V, n2 = a.n2;
@@ -229,29 +231,45 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
             const double* cv = cand_v;
             const int* ci = cand_i;
             if (kcap <= kExtract || use_p) {
-                // the candidates one at a time, most probable first, until top-k or top-p is met
+                // the candidates one at a time, most probable first, until top-k or top-p is met. One
+                // barrier per candidate: every thread combines the wave maxima itself (the same values in
+                // the same order, so every thread reaches the same candidate, running sum and decision),
+                // the maxima alternate between two buffers, and a taken candidate is marked by the one
+                // thread whose scan reads it.
                 const int rounds = min(kcap, kExtract);
+                const int nw = blockDim.x >> 6;
                 double cp = 0.0;
-                for (int r = 0; r < rounds && active == 0; r++) {
+                for (int r = 0; r < rounds; r++) {
                     double bv = -INFINITY;
                     int bi = 0x7fffffff;
                     for (int i = threadIdx.x; i < V; i += blockDim.x)
                         if (before(key[i], i, bv, bi)) { bv = key[i]; bi = i; }
-                    double best_v;
-                    int best_i;
-                    block_argmax(bv, bi, red_v, red_i, best_v, best_i);
+                    for (int o = 32; o > 0; o >>= 1) {
+                        const double ov = __shfl_xor(bv, o);
+                        const int oi = __shfl_xor(bi, o);
+                        if (before(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+                    }
+                    double* rv = red2_v[r & 1];
+                    int* ri = red2_i[r & 1];
+                    if ((threadIdx.x & 63) == 0) { rv[threadIdx.x >> 6] = bv; ri[threadIdx.x >> 6] = bi; }
+                    __syncthreads();
+                    double best_v = rv[0];
+                    int best_i = ri[0];
+                    for (int k = 1; k < nw; k++)
+                        if (before(rv[k], ri[k], best_v, best_i)) { best_v = rv[k]; best_i = ri[k]; }
                     if (threadIdx.x == 0) {
                         cand_v[r] = best_v;
                         cand_i[r] = best_i;
-                        key[best_i] = -2.0;  // taken: below every probability
-                        cp += best_v;
-                        chosen_sh = (use_p && cp >= a.p.top_p) ? r + 1 : (r + 1 == kcap ? kcap : 0);
                     }
-                    __syncthreads();
-                    active = chosen_sh;
-                    __syncthreads();
+                    if (best_i % (int)blockDim.x == (int)threadIdx.x) key[best_i] = -2.0;  // taken: below every probability
+                    cp += best_v;
+                    if ((use_p && cp >= a.p.top_p) || r + 1 == kcap) {
+                        active = r + 1;
+                        break;
+                    }
                 }
                 if (active == 0) {  // top-p not reached within kExtract candidates: sort them all
+                    __syncthreads();
                     if (threadIdx.x == 0)
                         for (int r = 0; r < rounds; r++) key[cand_i[r]] = cand_v[r];
                     __syncthreads();
