@@ -80,31 +80,48 @@ __device__ __forceinline__ void block_argmax(double v, int i, double* red_v, int
 }
 
 // Sequential float64 sum x[0] + x[1] + ... in that order (the reference's loop); with prefix, x[i] is
-// replaced by the running sum through i. One lane; the next eight values are read before the current eight
-// are added.
+// replaced by the running sum through i. One lane, in batches of 16 values held in two register sets that
+// alternate: each batch's LDS reads are issued before the previous batch's additions (scheduling barriers
+// keep them there), so the chain of dependent additions does not wait for LDS.
+template <int B>
+__device__ __forceinline__ void seq_batch(double* x, int i, const double2 (&v)[B / 2], double& s, bool prefix) {
+    double2 o[B / 2];
+#pragma unroll
+    for (int k = 0; k < B / 2; k++) {
+        s += v[k].x;
+        o[k].x = s;
+        s += v[k].y;
+        o[k].y = s;
+    }
+    if (prefix) {
+#pragma unroll
+        for (int k = 0; k < B / 2; k++) *(double2*)(x + i + 2 * k) = o[k];
+    }
+}
+
 __device__ double seq_sum(double* x, int n, bool prefix) {
+    constexpr int B = 16;
     double s = 0.0;
-    const int n8 = ((uintptr_t)x & 15) == 0 ? n & ~7 : 0;
-    if (n8) {
-        double2 b0 = *(const double2*)(x), b1 = *(const double2*)(x + 2);
-        double2 b2 = *(const double2*)(x + 4), b3 = *(const double2*)(x + 6);
-        for (int i = 0; i < n8; i += 8) {
-            const int j = min(i + 8, n8 - 8);  // the next batch (the last batch reads itself again)
-            const double2 c0 = *(const double2*)(x + j), c1 = *(const double2*)(x + j + 2);
-            const double2 c2 = *(const double2*)(x + j + 4), c3 = *(const double2*)(x + j + 6);
-            double2 o0, o1, o2, o3;
-            s += b0.x; o0.x = s; s += b0.y; o0.y = s;
-            s += b1.x; o1.x = s; s += b1.y; o1.y = s;
-            s += b2.x; o2.x = s; s += b2.y; o2.y = s;
-            s += b3.x; o3.x = s; s += b3.y; o3.y = s;
-            if (prefix) {
-                *(double2*)(x + i) = o0; *(double2*)(x + i + 2) = o1;
-                *(double2*)(x + i + 4) = o2; *(double2*)(x + i + 6) = o3;
-            }
-            b0 = c0; b1 = c1; b2 = c2; b3 = c3;
+    const int nb = ((uintptr_t)x & 15) == 0 ? n / (2 * B) * (2 * B) : 0;
+    if (nb) {
+        double2 v0[B / 2], v1[B / 2];
+#pragma unroll
+        for (int k = 0; k < B / 2; k++) v0[k] = *(const double2*)(x + 2 * k);
+        for (int i = 0; i < nb; i += 2 * B) {
+#pragma unroll
+            for (int k = 0; k < B / 2; k++) v1[k] = *(const double2*)(x + i + B + 2 * k);
+            __builtin_amdgcn_sched_barrier(0);
+            seq_batch<B>(x, i, v0, s, prefix);
+            __builtin_amdgcn_sched_barrier(0);
+            const int j = min(i + 2 * B, nb - B);  // the next pair's first batch (past the end: a batch again)
+#pragma unroll
+            for (int k = 0; k < B / 2; k++) v0[k] = *(const double2*)(x + j + 2 * k);
+            __builtin_amdgcn_sched_barrier(0);
+            seq_batch<B>(x, i + B, v1, s, prefix);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
-    for (int i = n8; i < n; i++) {
+    for (int i = nb; i < n; i++) {
         s += x[i];
         if (prefix) x[i] = s;
     }
