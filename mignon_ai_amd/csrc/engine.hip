@@ -197,6 +197,7 @@ struct mg_sessions {
     mg_model* m = nullptr;
     int n = 0, window = 0;
     mg::DevBuf norm_ring, g, kring, vring, pos, next_ids, out_ids, out_probs, logits, argmax, prob;
+    mg::DevBuf sample_ws;  // the sampler's exponentials and row sums
     // stop-token bookkeeping of mg_sessions_decode_greedy_until: per-session reply length, the stopped
     // count, and a ring of pinned host slots the count is copied to after each step (one event each)
     static constexpr int kStopRing = 8;
@@ -1329,6 +1330,9 @@ int mg_sessions_decode_sample(mg_sessions* s, const int32_t* prompts, const int3
         sa.seeds = seed_d;
         sa.out = oi; sa.out_ld = max_tokens;
         sa.next_ids = s->next_ids.as<int32_t>();
+        s->sample_ws.ensure(sample_scratch_bytes(S, V));
+        sa.scratch = s->sample_ws.as<double>();
+        sa.sums = sa.scratch + (size_t)S * V;
         auto pick = [&](int col) {
             sa.col = col; sa.step = col; sa.out_col = col;
             ProfScope ps(m->prof, K_SAMPLE, st);
@@ -1376,6 +1380,8 @@ int mg_sample_logits(const double* logits, int n, int V, const int32_t* recent, 
         sa.u = sg.in(u, (size_t)n, st);
         int32_t* o = sg.out<int32_t>((size_t)n);
         sa.out = o; sa.out_ld = 1;
+        sa.scratch = sg.out<double>(sample_scratch_bytes(n, V) / sizeof(double));
+        sa.sums = sa.scratch + (size_t)n * V;
         HIPCHECK(launch_sample(sa, st));
         HIPCHECK(hipMemcpyAsync(out, o, (size_t)n * 4, hipMemcpyDeviceToHost, st));
         HIPCHECK(hipStreamSynchronize(st));

@@ -56,6 +56,33 @@ __device__ void bitonic_desc(double* key, int* idx, int n2) {
     }
 }
 
+// One step of a wave-wide (value, index) argmax through DPP lane moves (VALU latency, no LDS round
+// trip): lanes outside row_mask keep their own pair.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void argmax_dpp(double& v, int& i) {
+    const int lo = __double2loint(v), hi = __double2hiint(v);
+    const int olo = __builtin_amdgcn_update_dpp(lo, lo, CTRL, ROW_MASK, 0xF, false);
+    const int ohi = __builtin_amdgcn_update_dpp(hi, hi, CTRL, ROW_MASK, 0xF, false);
+    const int oi = __builtin_amdgcn_update_dpp(i, i, CTRL, ROW_MASK, 0xF, false);
+    const double ov = __hiloint2double(ohi, olo);
+    if (before(ov, oi, v, i)) { v = ov; i = oi; }
+}
+
+// The wave's first maximum (larger value, then smaller index), in every lane: quad swaps, half-row and
+// row mirrors, then the row broadcasts carry each row's result upwards so that lane 63 holds the wave's.
+__device__ __forceinline__ void wave_argmax(double& v, int& i) {
+    argmax_dpp<0xB1, 0xF>(v, i);   // quad_perm [1,0,3,2]
+    argmax_dpp<0x4E, 0xF>(v, i);   // quad_perm [2,3,0,1]
+    argmax_dpp<0x141, 0xF>(v, i);  // row_half_mirror
+    argmax_dpp<0x140, 0xF>(v, i);  // row_mirror
+    argmax_dpp<0x142, 0xA>(v, i);  // row_bcast:15 into rows 1 and 3
+    argmax_dpp<0x143, 0xC>(v, i);  // row_bcast:31 into rows 2 and 3
+    const int lo = __builtin_amdgcn_readlane(__double2loint(v), 63);
+    const int hi = __builtin_amdgcn_readlane(__double2hiint(v), 63);
+    i = __builtin_amdgcn_readlane(i, 63);
+    v = __hiloint2double(hi, lo);
+}
+
 __device__ __forceinline__ void block_argmax(double v, int i, double* red_v, int* red_i, double& best_v, int& best_i) {
     // first maximum: larger value, then smaller index
     for (int o = 32; o > 0; o >>= 1) {
@@ -141,6 +168,9 @@ __device__ int seq_find(const double* x, int n, double r, int dflt) {
 
 constexpr int kExtract = 64;  // candidates taken one by one before falling back to a full sort
 
+// PHASE: 0 the whole draw; 1 up to the exponentials, stored to a.scratch; 2 from the exponentials in
+// a.scratch and their sums in a.sums (sample_sum_kernel) on, truncated sampling only.
+template <int PHASE>
 __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
     __shared__ double cand_v[kExtract];
     __shared__ int cand_i[kExtract];
@@ -155,11 +185,15 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
     double* key = smp_smem;           // [n2] logits, then probabilities
     int* idx = (int*)(smp_smem + n2);  // [n2] token ids once sorted
     const long long base = (long long)row * a.ld;
-    for (int i = threadIdx.x; i < V; i += blockDim.x)
-        key[i] = a.logits32 ? (double)a.logits32[base + i] : a.logits64[base + i];
+    if constexpr (PHASE == 2) {
+        for (int i = threadIdx.x; i < V; i += blockDim.x) key[i] = a.scratch[(long long)row * V + i];
+    } else {
+        for (int i = threadIdx.x; i < V; i += blockDim.x)
+            key[i] = a.logits32 ? (double)a.logits32[base + i] : a.logits64[base + i];
+    }
     __syncthreads();
 
-    if (threadIdx.x == 0) {
+    if (PHASE != 2 && threadIdx.x == 0) {
         const int col = a.hist ? a.col : 0;
         const int32_t* g = a.hist ? a.hist + (long long)row * a.hist_ld : nullptr;
         // trigram blocking over the generated tokens (sample.go:211-224)
@@ -202,18 +236,25 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
         double bv;
         block_argmax(v, bi, red_v, red_i, bv, chosen);
     } else {
-        const double invT = 1.0 / a.p.temperature;
-        double v = -DBL_MAX;
-        for (int i = threadIdx.x; i < V; i += blockDim.x) {
-            const double sc = key[i] * invT;
-            key[i] = sc;
-            v = fmax(v, sc);
+        if constexpr (PHASE != 2) {
+            const double invT = 1.0 / a.p.temperature;
+            double v = -DBL_MAX;
+            for (int i = threadIdx.x; i < V; i += blockDim.x) {
+                const double sc = key[i] * invT;
+                key[i] = sc;
+                v = fmax(v, sc);
+            }
+            double mx;
+            int dummy;
+            block_argmax(v, 0, red_v, red_i, mx, dummy);
+            for (int i = threadIdx.x; i < V; i += blockDim.x) {
+                const double e = exp(key[i] - mx);
+                if constexpr (PHASE == 1) a.scratch[(long long)row * V + i] = e;
+                else key[i] = e;
+            }
+            if constexpr (PHASE == 1) return;
+            __syncthreads();
         }
-        double mx;
-        int dummy;
-        block_argmax(v, 0, red_v, red_i, mx, dummy);
-        for (int i = threadIdx.x; i < V; i += blockDim.x) key[i] = exp(key[i] - mx);
-        __syncthreads();
         const double u = a.u ? a.u[row] : uniform_draw(a.seeds[row], a.step);
         if (a.p.top_k <= 0 && a.p.top_p >= 0.9999) {
             // pure temperature sampling (sample.go:91-109): the running sums never decrease (every term
@@ -237,7 +278,7 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
         } else {
             // truncated sampling (sample.go:111-171): probabilities p / sum(p), then the candidates in
             // descending order (equal probabilities by token id), cut by top-k and top-p
-            if (threadIdx.x == 0) red_v[0] = 1.0 / seq_sum(key, V, false);
+            if (threadIdx.x == 0) red_v[0] = 1.0 / (PHASE == 2 ? a.sums[row] : seq_sum(key, V, false));
             __syncthreads();
             const double inv = red_v[0];
             for (int i = threadIdx.x; i < V; i += blockDim.x) key[i] *= inv;
@@ -248,27 +289,42 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
             const double* cv = cand_v;
             const int* ci = cand_i;
             if (kcap <= kExtract || use_p) {
-                // the candidates one at a time, most probable first, until top-k or top-p is met. One
-                // barrier per candidate: every thread combines the wave maxima itself (the same values in
-                // the same order, so every thread reaches the same candidate, running sum and decision),
-                // the maxima alternate between two buffers, and a taken candidate is marked by the one
-                // thread whose scan reads it.
+                // the candidates one at a time, most probable first, until top-k or top-p is met. Each
+                // thread keeps the best of its own tokens and each wave the best of its threads'; after a
+                // candidate is taken only its thread rescans (its other tokens) and only its wave reduces
+                // again. One barrier per candidate: every thread combines the waves' bests itself (the
+                // same values in the same order, so every thread reaches the same candidate, running sum
+                // and decision), and the waves' bests alternate between two buffers.
                 const int rounds = min(kcap, kExtract);
-                const int nw = blockDim.x >> 6;
+                const int nw = blockDim.x >> 6, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+                auto local_best = [&](double& bv, int& bi) {  // this thread's tokens, 8 reads at a time
+                    bv = -INFINITY;
+                    bi = 0x7fffffff;
+                    for (int i0 = threadIdx.x; i0 < V; i0 += 8 * kThreads) {
+                        double kv[8];
+#pragma unroll
+                        for (int k = 0; k < 8; k++) kv[k] = key[min(i0 + k * kThreads, V - 1)];
+#pragma unroll
+                        for (int k = 0; k < 8; k++) {
+                            const int i = i0 + k * kThreads;
+                            if (i < V && before(kv[k], i, bv, bi)) { bv = kv[k]; bi = i; }
+                        }
+                    }
+                };
+                auto wave_best = [&](double v, int i, double& wv_out, int& wi_out) {
+                    wave_argmax(v, i);
+                    wv_out = v;
+                    wi_out = i;
+                };
+                double lb_v, wb_v;
+                int lb_i, wb_i;
+                local_best(lb_v, lb_i);
+                wave_best(lb_v, lb_i, wb_v, wb_i);
                 double cp = 0.0;
                 for (int r = 0; r < rounds; r++) {
-                    double bv = -INFINITY;
-                    int bi = 0x7fffffff;
-                    for (int i = threadIdx.x; i < V; i += blockDim.x)
-                        if (before(key[i], i, bv, bi)) { bv = key[i]; bi = i; }
-                    for (int o = 32; o > 0; o >>= 1) {
-                        const double ov = __shfl_xor(bv, o);
-                        const int oi = __shfl_xor(bi, o);
-                        if (before(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-                    }
                     double* rv = red2_v[r & 1];
                     int* ri = red2_i[r & 1];
-                    if ((threadIdx.x & 63) == 0) { rv[threadIdx.x >> 6] = bv; ri[threadIdx.x >> 6] = bi; }
+                    if (lane == 0) { rv[wv] = wb_v; ri[wv] = wb_i; }
                     __syncthreads();
                     double best_v = rv[0];
                     int best_i = ri[0];
@@ -278,11 +334,18 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
                         cand_v[r] = best_v;
                         cand_i[r] = best_i;
                     }
-                    if (best_i % (int)blockDim.x == (int)threadIdx.x) key[best_i] = -2.0;  // taken: below every probability
                     cp += best_v;
                     if ((use_p && cp >= a.p.top_p) || r + 1 == kcap) {
                         active = r + 1;
                         break;
+                    }
+                    const int owner = best_i % (int)blockDim.x;
+                    if (owner >> 6 == wv) {  // the taken token's wave (uniform branch)
+                        if (owner == (int)threadIdx.x) {
+                            key[best_i] = -2.0;  // taken: below every probability
+                            local_best(lb_v, lb_i);
+                        }
+                        wave_best(lb_v, lb_i, wb_v, wb_i);
                     }
                 }
                 if (active == 0) {  // top-p not reached within kExtract candidates: sort them all
@@ -347,7 +410,58 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
     }
 }
 
+// The rows' sequential float64 sums, one lane per row (each lane's chain of dependent additions runs
+// beside 63 others instead of alone in a workgroup): sums[row] = e[0] + e[1] + ... in index order. For
+// pure temperature sampling (pure != 0) the lane also draws: the first index whose running sum reaches
+// u * sum (the same sums again), or 0 when none does.
+__global__ __launch_bounds__(64) void sample_sum_kernel(SampleArgs a, int pure) {
+    const int row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= a.n) return;
+    const int V = a.V;
+    const double* e = a.scratch + (long long)row * V;
+    // batches of 8, the next batch's loads issued before the current batch's additions
+    constexpr int B = 8;
+    double s = 0.0;
+    const int nb = V / B * B;
+    if (nb) {
+        double cur[B];
+#pragma unroll
+        for (int k = 0; k < B; k++) cur[k] = e[k];
+        for (int i = 0; i < nb; i += B) {
+            const int j = min(i + B, nb - B);  // the next batch (the last batch reads itself again)
+            double nxt[B];
+#pragma unroll
+            for (int k = 0; k < B; k++) nxt[k] = e[j + k];
+#pragma unroll
+            for (int k = 0; k < B; k++) s += cur[k];
+#pragma unroll
+            for (int k = 0; k < B; k++) cur[k] = nxt[k];
+        }
+    }
+    for (int i = nb; i < V; i++) s += e[i];
+    if (!pure) {
+        a.sums[row] = s;
+        return;
+    }
+    const double u = a.u ? a.u[row] : uniform_draw(a.seeds[row], a.step);
+    const double r = u * s;
+    double c = 0.0;
+    int t = V;
+    for (int i = 0; i < V; i++) {
+        c += e[i];
+        if (c >= r) {
+            t = i;
+            break;
+        }
+    }
+    const int chosen = t < V ? t : 0;
+    a.out[(long long)row * a.out_ld + a.out_col] = chosen;
+    if (a.next_ids) a.next_ids[row] = chosen;
+}
+
 }  // namespace
+
+size_t sample_scratch_bytes(int n, int V) { return ((size_t)n * V + (size_t)n) * sizeof(double); }
 
 int sample_n2(int V) {
     int n2 = 1;
@@ -366,11 +480,27 @@ hipError_t launch_sample(const SampleArgs& a, hipStream_t s) {
     const bool use_p = a.p.top_p > 0.0 && a.p.top_p < 1.0;
     const bool may_sort = truncated && (kcap > kExtract || use_p);
     const size_t lds = may_sort ? sample_lds_bytes(a.V) : (size_t)a.V * sizeof(double);
-    static const hipError_t attr = hipFuncSetAttribute((const void*)sample_rows_kernel,
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                       (int)sample_lds_bytes(kMaxSampleVocab));
-    if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL(sample_rows_kernel, dim3(a.n), dim3(kThreads), lds, s, a);
+    static const hipError_t attr0 = hipFuncSetAttribute((const void*)sample_rows_kernel<0>,
+                                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                        (int)sample_lds_bytes(kMaxSampleVocab));
+    static const hipError_t attr2 = hipFuncSetAttribute((const void*)sample_rows_kernel<2>,
+                                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                        (int)sample_lds_bytes(kMaxSampleVocab));
+    static const hipError_t attr1 = hipFuncSetAttribute((const void*)sample_rows_kernel<1>,
+                                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                        (int)(kMaxSampleVocab * sizeof(double)));
+    if (attr0 != hipSuccess) return attr0;
+    if (attr1 != hipSuccess) return attr1;
+    if (attr2 != hipSuccess) return attr2;
+    const bool sampled = a.p.temperature > 0.001;
+    if (!sampled || !a.scratch || !a.sums) {
+        hipLaunchKernelGGL(sample_rows_kernel<0>, dim3(a.n), dim3(kThreads), lds, s, a);
+        return hipGetLastError();
+    }
+    // three passes: exponentials per row, the rows' sums one lane per row, then the truncated draw
+    hipLaunchKernelGGL(sample_rows_kernel<1>, dim3(a.n), dim3(kThreads), (size_t)a.V * sizeof(double), s, a);
+    hipLaunchKernelGGL(sample_sum_kernel, dim3((a.n + 63) / 64), dim3(64), 0, s, a, truncated ? 0 : 1);
+    if (truncated) hipLaunchKernelGGL(sample_rows_kernel<2>, dim3(a.n), dim3(kThreads), lds, s, a);
     return hipGetLastError();
 }
 

@@ -36,7 +36,14 @@ struct SampleArgs {
     int32_t* out = nullptr;               // chosen token -> out[row * out_ld + out_col]
     int out_ld = 1, out_col = 0;
     int32_t* next_ids = nullptr;          // [n] or null
+    // Workspace of the three-pass form of sampled draws (temperature above 0.001): the exponentials
+    // [n][V] and the rows' sums [n]. Without it one kernel does everything, the sequential float64 sum of
+    // each row in one lane of its workgroup.
+    double* scratch = nullptr;
+    double* sums = nullptr;
 };
+// Bytes of SampleArgs::scratch plus SampleArgs::sums for n rows of V tokens.
+size_t sample_scratch_bytes(int n, int V);
 
 int sample_n2(int V);
 size_t sample_lds_bytes(int V);
