@@ -289,65 +289,72 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
             const double* cv = cand_v;
             const int* ci = cand_i;
             if (kcap <= kExtract || use_p) {
-                // the candidates one at a time, most probable first, until top-k or top-p is met. Each
-                // thread keeps the best of its own tokens and each wave the best of its threads'; after a
-                // candidate is taken only its thread rescans (its other tokens) and only its wave reduces
-                // again. One barrier per candidate: every thread combines the waves' bests itself (the
-                // same values in the same order, so every thread reaches the same candidate, running sum
-                // and decision), and the waves' bests alternate between two buffers.
+                // The candidates one at a time, most probable first, until top-k or top-p is met, by the
+                // first wave alone (no barriers). Lane L owns tokens L, L + 64, ... and keeps the four best
+                // of them sorted in registers; a round is one wave argmax over the lanes' heads (DPP), then
+                // the winning lane pops its head. A lane rescans its tokens (the taken ones marked below
+                // every probability) only when all four of its cached ones are taken.
                 const int rounds = min(kcap, kExtract);
-                const int nw = blockDim.x >> 6, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-                auto local_best = [&](double& bv, int& bi) {  // this thread's tokens, 8 reads at a time
-                    bv = -INFINITY;
-                    bi = 0x7fffffff;
-                    for (int i0 = threadIdx.x; i0 < V; i0 += 8 * kThreads) {
-                        double kv[8];
+                if (threadIdx.x < 64) {
+                    const int lane = threadIdx.x;
+                    double cv4[4];
+                    int ci4[4];
+                    auto refill = [&]() {
 #pragma unroll
-                        for (int k = 0; k < 8; k++) kv[k] = key[min(i0 + k * kThreads, V - 1)];
+                        for (int q = 0; q < 4; q++) { cv4[q] = -INFINITY; ci4[q] = 0x7fffffff; }
+                        for (int i0 = lane; i0 < V; i0 += 8 * 64) {
+                            double kv[8];
 #pragma unroll
-                        for (int k = 0; k < 8; k++) {
-                            const int i = i0 + k * kThreads;
-                            if (i < V && before(kv[k], i, bv, bi)) { bv = kv[k]; bi = i; }
+                            for (int k = 0; k < 8; k++) kv[k] = key[min(i0 + 64 * k, V - 1)];
+#pragma unroll
+                            for (int k = 0; k < 8; k++) {
+                                const int i = i0 + 64 * k;
+                                double v = kv[k];
+                                int vi = i;
+                                if (i >= V || !before(v, vi, cv4[3], ci4[3])) continue;
+                                // insertion into the sorted four
+#pragma unroll
+                                for (int q = 0; q < 4; q++) {
+                                    if (before(v, vi, cv4[q], ci4[q])) {
+                                        const double tv = cv4[q];
+                                        const int ti = ci4[q];
+                                        cv4[q] = v; ci4[q] = vi;
+                                        v = tv; vi = ti;
+                                    }
+                                }
+                            }
+                        }
+                    };
+                    refill();
+                    int taken = 0;  // this lane's tokens taken since its last refill
+                    double cp = 0.0;
+                    int act = 0;
+                    for (int r = 0; r < rounds; r++) {
+                        double bv = cv4[0];
+                        int bi = ci4[0];
+                        wave_argmax(bv, bi);
+                        if (lane == 0) { cand_v[r] = bv; cand_i[r] = bi; }
+                        cp += bv;
+                        if ((use_p && cp >= a.p.top_p) || r + 1 == kcap) {
+                            act = r + 1;
+                            break;
+                        }
+                        if ((bi & 63) == lane) {
+                            key[bi] = -2.0;  // taken: below every probability
+                            cv4[0] = cv4[1]; ci4[0] = ci4[1];
+                            cv4[1] = cv4[2]; ci4[1] = ci4[2];
+                            cv4[2] = cv4[3]; ci4[2] = ci4[3];
+                            cv4[3] = -INFINITY; ci4[3] = 0x7fffffff;
+                            if (++taken == 4) {
+                                refill();
+                                taken = 0;
+                            }
                         }
                     }
-                };
-                auto wave_best = [&](double v, int i, double& wv_out, int& wi_out) {
-                    wave_argmax(v, i);
-                    wv_out = v;
-                    wi_out = i;
-                };
-                double lb_v, wb_v;
-                int lb_i, wb_i;
-                local_best(lb_v, lb_i);
-                wave_best(lb_v, lb_i, wb_v, wb_i);
-                double cp = 0.0;
-                for (int r = 0; r < rounds; r++) {
-                    double* rv = red2_v[r & 1];
-                    int* ri = red2_i[r & 1];
-                    if (lane == 0) { rv[wv] = wb_v; ri[wv] = wb_i; }
-                    __syncthreads();
-                    double best_v = rv[0];
-                    int best_i = ri[0];
-                    for (int k = 1; k < nw; k++)
-                        if (before(rv[k], ri[k], best_v, best_i)) { best_v = rv[k]; best_i = ri[k]; }
-                    if (threadIdx.x == 0) {
-                        cand_v[r] = best_v;
-                        cand_i[r] = best_i;
-                    }
-                    cp += best_v;
-                    if ((use_p && cp >= a.p.top_p) || r + 1 == kcap) {
-                        active = r + 1;
-                        break;
-                    }
-                    const int owner = best_i % (int)blockDim.x;
-                    if (owner >> 6 == wv) {  // the taken token's wave (uniform branch)
-                        if (owner == (int)threadIdx.x) {
-                            key[best_i] = -2.0;  // taken: below every probability
-                            local_best(lb_v, lb_i);
-                        }
-                        wave_best(lb_v, lb_i, wb_v, wb_i);
-                    }
+                    if (lane == 0) chosen_sh = act;
                 }
+                __syncthreads();
+                active = chosen_sh;
                 if (active == 0) {  // top-p not reached within kExtract candidates: sort them all
                     __syncthreads();
                     if (threadIdx.x == 0)
