@@ -426,23 +426,29 @@ __global__ __launch_bounds__(64) void sample_sum_kernel(SampleArgs a, int pure) 
     if (row >= a.n) return;
     const int V = a.V;
     const double* e = a.scratch + (long long)row * V;
-    // batches of 8, the next batch's loads issued before the current batch's additions
-    constexpr int B = 8;
+    // batches of 16 in two register sets that alternate: a batch's loads are issued a whole batch of
+    // additions before they are needed (scheduling barriers keep them there)
+    constexpr int B = 16;
     double s = 0.0;
-    const int nb = V / B * B;
+    const int nb = V / (2 * B) * (2 * B);
     if (nb) {
-        double cur[B];
+        double v0[B], v1[B];
 #pragma unroll
-        for (int k = 0; k < B; k++) cur[k] = e[k];
-        for (int i = 0; i < nb; i += B) {
-            const int j = min(i + B, nb - B);  // the next batch (the last batch reads itself again)
-            double nxt[B];
+        for (int k = 0; k < B; k++) v0[k] = e[k];
+        for (int i = 0; i < nb; i += 2 * B) {
 #pragma unroll
-            for (int k = 0; k < B; k++) nxt[k] = e[j + k];
+            for (int k = 0; k < B; k++) v1[k] = e[i + B + k];
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int k = 0; k < B; k++) s += cur[k];
+            for (int k = 0; k < B; k++) s += v0[k];
+            __builtin_amdgcn_sched_barrier(0);
+            const int j = min(i + 2 * B, nb - B);  // the next pair's first batch (past the end: a batch again)
 #pragma unroll
-            for (int k = 0; k < B; k++) cur[k] = nxt[k];
+            for (int k = 0; k < B; k++) v0[k] = e[j + k];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int k = 0; k < B; k++) s += v1[k];
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     for (int i = nb; i < V; i++) s += e[i];
