@@ -92,10 +92,14 @@ __device__ __forceinline__ void stg_put(float* stg, int lane, int ti, const floa
     *(float4*)(stg + (lane & 15) * STG_LD + 16 * ti + 4 * (lane >> 4)) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
-// Rows mt0..mt0+15, channels n0 + [0, 128) of `out` (row stride ldo) from the staged tile. NT: streaming
-// (non-temporal) stores of whole 512-byte row segments, for outputs far larger than the L2 (the next
-// kernel reads them back from memory in any case).
-template <bool NT = false>
+// Rows mt0..mt0+15, channels n0 + [0, 128) of `out` (row stride ldo) from the staged tile, as whole
+// 512-byte row segments. Store kinds: ST_PLAIN; ST_NT non-temporal, for outputs far larger than the L2
+// that the next kernel reads back from memory in any case; ST_STREAM non-temporal with both coherence
+// scope bits set (sc0 sc1 nt), for a final output no kernel reads again (measured on the probabilities
+// GEMM: 21.0 ms per c5 step against 22.0 with ST_NT and 23.7 with ST_PLAIN).
+enum StoreKind : int { ST_PLAIN = 0, ST_NT = 1, ST_STREAM = 2 };
+
+template <int SK = ST_PLAIN>
 __device__ __forceinline__ void stg_flush(const GemmArgs& g, const float* stg, int lane, int mt0, int n0, float* out,
                                           long long ldo) {
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes have landed
@@ -115,7 +119,10 @@ __device__ __forceinline__ void stg_flush(const GemmArgs& g, const float* stg, i
         if (m < g.M && nv > 0) {
             float* dst = base + 2 * k * ldo + loff;
             if (vec) {
-                if constexpr (NT) {
+                if constexpr (SK == ST_STREAM) {
+                    const f4v t = {v.x, v.y, v.z, v.w};
+                    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1 nt" ::"v"(dst), "v"(t) : "memory");
+                } else if constexpr (SK == ST_NT) {
                     const f4v t = {v.x, v.y, v.z, v.w};
                     __builtin_nontemporal_store(t, (f4v*)dst);
                 } else {
@@ -163,7 +170,7 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
             if constexpr (STG) stg_put(stg, lane, ti, v);
             else store4(orow + n, v, nv, vec);
         }
-        if constexpr (STG) stg_flush<true>(g, stg, lane, mt0, n0, g.out, g.ldo);
+        if constexpr (STG) stg_flush<ST_NT>(g, stg, lane, mt0, n0, g.out, g.ldo);
     } else if constexpr (EPI == EPI_RESID) {
         // cur += x.w: all eight row segments are loaded before any is needed (one memory latency). With
         // resid, the new state is added into resid instead (blockIn += cur) and cur is left as it was.
@@ -225,7 +232,7 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
             if constexpr (STG) stg_put(stg, lane, ti, v);
             else store4(orow + n, v, nv, vec);
         }
-        if constexpr (STG) stg_flush<true>(g, stg, lane, mt0, n0, g.out, g.ldo);
+        if constexpr (STG) stg_flush<ST_STREAM>(g, stg, lane, mt0, n0, g.out, g.ldo);
     } else if constexpr (EPI == EPI_GLU || EPI == EPI_HIGHWAY) {
         // W rows are reordered in blocks of 32: 16 value rows then the 16 matching gate rows, so tile
         // pair (2p, 2p+1) holds value and gate of output channel n0/2 + 16p + 4*(L >> 4) + r.
