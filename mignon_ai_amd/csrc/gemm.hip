@@ -366,7 +366,7 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
             dst[0] = bmax; dst[1] = bsum; dst[2] = __int_as_float(bidx);
         }
         if constexpr (STG) {
-            if (orow) stg_flush(g, stg, lane, mt0, n0, g.out, g.ldo);
+            if (orow) stg_flush<ST_STREAM>(g, stg, lane, mt0, n0, g.out, g.ldo);
         }
     }
 }
