@@ -634,6 +634,50 @@ __device__ __forceinline__ float dot_ref_lds4(const float (&q)[DH], const float*
 // One workgroup per (sequence, 64-query tile, head). Keys of the tile's whole window are staged in LDS,
 // each lane scores its query against them (DotF32 order), runs the reference softmax, then the values
 // replace the keys in LDS for the P.V accumulation.
+// dot_ref_lds4 with the row in registers (DH a multiple of 4): the same products and additions in the
+// same order.
+template <int DH>
+__device__ __forceinline__ float dot_ref_reg4(const float (&q)[DH], const float4 (&r4)[DH / 4]) {
+    float a0[8], a1[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) { a0[j] = 0.0f; a1[j] = 0.0f; }
+    int i = 0;
+#pragma unroll
+    for (; i + 16 <= DH; i += 16) {
+        const float4 k0 = r4[i / 4], k1 = r4[i / 4 + 1], k2 = r4[i / 4 + 2], k3 = r4[i / 4 + 3];
+        a0[0] = fmaf(q[i + 0], k0.x, a0[0]); a0[1] = fmaf(q[i + 1], k0.y, a0[1]);
+        a0[2] = fmaf(q[i + 2], k0.z, a0[2]); a0[3] = fmaf(q[i + 3], k0.w, a0[3]);
+        a0[4] = fmaf(q[i + 4], k1.x, a0[4]); a0[5] = fmaf(q[i + 5], k1.y, a0[5]);
+        a0[6] = fmaf(q[i + 6], k1.z, a0[6]); a0[7] = fmaf(q[i + 7], k1.w, a0[7]);
+        a1[0] = fmaf(q[i + 8], k2.x, a1[0]); a1[1] = fmaf(q[i + 9], k2.y, a1[1]);
+        a1[2] = fmaf(q[i + 10], k2.z, a1[2]); a1[3] = fmaf(q[i + 11], k2.w, a1[3]);
+        a1[4] = fmaf(q[i + 12], k3.x, a1[4]); a1[5] = fmaf(q[i + 13], k3.y, a1[5]);
+        a1[6] = fmaf(q[i + 14], k3.z, a1[6]); a1[7] = fmaf(q[i + 15], k3.w, a1[7]);
+    }
+    if (i + 8 <= DH) {
+        const float4 k0 = r4[i / 4], k1 = r4[i / 4 + 1];
+        a0[0] = fmaf(q[i + 0], k0.x, a0[0]); a0[1] = fmaf(q[i + 1], k0.y, a0[1]);
+        a0[2] = fmaf(q[i + 2], k0.z, a0[2]); a0[3] = fmaf(q[i + 3], k0.w, a0[3]);
+        a0[4] = fmaf(q[i + 4], k1.x, a0[4]); a0[5] = fmaf(q[i + 5], k1.y, a0[5]);
+        a0[6] = fmaf(q[i + 6], k1.z, a0[6]); a0[7] = fmaf(q[i + 7], k1.w, a0[7]);
+        i += 8;
+    }
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = a0[j] + a1[j];
+    float s = hreduce8(v);
+    if (i < DH) {  // DH % 8 == 4: the last four, unfused
+        const float4 k = r4[i / 4];
+        const float t[4] = {k.x, k.y, k.z, k.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float p = q[i + e] * t[e];
+            s = s + p;
+        }
+    }
+    return s;
+}
+
 template <int DH>
 __global__ __launch_bounds__(64) void attention_kernel(AttnArgs a) {
     constexpr int DS = att_stride<DH>();
@@ -953,6 +997,91 @@ __global__ __launch_bounds__(64) void attention_step_kernel(AttnStepArgs a) {
     }
 }
 
+// attention_step_lds_kernel for caches of at most 64 positions with each lane's key row in registers:
+// lane jj loads key lo + jj itself and scores it, so only the values (and the scores) go through LDS,
+// about half the LDS of the staged kernel and twice the waves per CU. Bit-identical to it: the same
+// reference-order dot product, softmax and P.V.
+template <int DH>
+__global__ __launch_bounds__(64) void attention_step_rk_kernel(AttnStepArgs a) {
+    constexpr int DS = DH + 4;
+    constexpr int C4 = DH / 4;
+    extern __shared__ __align__(16) float rk_smem[];
+    const int cap = a.cap;
+    float* vs = rk_smem;          // [cap][DS]
+    float* es = vs + cap * DS;    // [cap]
+    __shared__ float rk_inv;
+    const int s_ = blockIdx.x / a.heads, h = blockIdx.x % a.heads;
+    const int lane = threadIdx.x;
+    const int D = a.D;
+    const int pos = a.pos[s_];
+    const int lo = max(window_start(pos, a.window), pos - cap + 1);
+    const int span = pos - lo + 1;  // at most cap <= 64
+    const float* qkv = a.qkv + (long long)s_ * 3 * D;
+    const float* kr = a.kring + (long long)s_ * cap * D + h * DH;
+    const float* vr = a.vring + (long long)s_ * cap * D + h * DH;
+    // this lane's key row (key lo + lane; the current position's from qkv, not yet in the ring)
+    float4 krow[C4];
+    {
+        const int j = lo + min(lane, span - 1);
+        const float* kp = j == pos ? qkv + D + h * DH : kr + (long long)(j % cap) * D;
+#pragma unroll
+        for (int c = 0; c < C4; c++) krow[c] = *(const float4*)(kp + 4 * c);
+    }
+    // values: rows jj = 0..span-1 into LDS, every load issued first
+    const int n4 = span * C4;
+    for (int e0 = 0; e0 < n4; e0 += 8 * 64) {
+        float4 vb[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int e = min(e0 + u * 64 + lane, n4 - 1);
+            const int jj = e / C4, c = e - jj * C4;
+            const int j = lo + jj;
+            const float* vp = j == pos ? qkv + 2 * D + h * DH : vr + (long long)(j % cap) * D;
+            vb[u] = *(const float4*)(vp + 4 * c);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int e = e0 + u * 64 + lane;
+            if (e < n4) {
+                const int jj = e / C4, c = e - jj * C4;
+                *(float4*)(vs + jj * DS + 4 * c) = vb[u];
+            }
+        }
+    }
+    float q[DH];
+#pragma unroll
+    for (int i = 0; i < DH; i += 4) {
+        const float4 t = *(const float4*)(qkv + h * DH + i);
+        q[i] = t.x; q[i + 1] = t.y; q[i + 2] = t.z; q[i + 3] = t.w;
+    }
+    const float scale = (float)(1.0 / sqrt((double)DH));
+    const float sc = dot_ref_reg4<DH>(q, krow) * scale;
+    const float mx = wave_max(lane < span ? sc : -3.40282347e38f);
+    if (lane < span) es[lane] = fast_exp_ref(sc - mx);
+    __syncthreads();
+    if (lane == 0) {
+        float sum = 0.0f;  // nn.SoftmaxInPlaceF32's sequential sum
+#pragma unroll 8
+        for (int jj = 0; jj < span; jj++) sum += es[jj];
+        rk_inv = 1.0f / sum;
+    }
+    __syncthreads();
+    const float inv = rk_inv;
+    for (int i = lane; i < DH; i += 64) {
+        float o = 0.0f;
+#pragma unroll 8
+        for (int jj = 0; jj < span; jj++) o = axpy_ref<DH>(i, es[jj] * inv, vs[jj * DS + i], o);
+        a.att[(long long)s_ * a.Dp + h * DH + i] = o;
+    }
+    // record this position's key and value (slot pos % cap; the evicted key is outside the window)
+    float* kw = a.kring + (long long)s_ * cap * D + (long long)(pos % cap) * D + h * DH;
+    float* vw = a.vring + (long long)s_ * cap * D + (long long)(pos % cap) * D + h * DH;
+    for (int i = lane; i < DH; i += 64) {
+        kw[i] = qkv[D + h * DH + i];
+        vw[i] = qkv[2 * D + h * DH + i];
+    }
+}
+
 // Decode attention, staged: the span's key and value head slices go to LDS with 16-byte loads (eight
 // lanes per 128 bytes, a batch of loads in flight before any is stored), then the same reference-order
 // scores, softmax and P.V as attention_step_kernel, read from LDS: bit-identical results, one memory
@@ -1226,6 +1355,13 @@ hipError_t attn_mfma(const AttnArgs& a, int dh, hipStream_t s) {
 
 template <int DH>
 hipError_t attn_step_t(const AttnStepArgs& a, hipStream_t s) {
+    if constexpr (DH % 4 == 0 && DH <= 64) {
+        if (a.cap <= 64) {
+            const size_t lds = ((size_t)a.cap * (DH + 4) + a.cap) * sizeof(float);
+            hipLaunchKernelGGL(attention_step_rk_kernel<DH>, dim3(a.S * a.heads), dim3(64), lds, s, a);
+            return hipGetLastError();
+        }
+    }
     if constexpr (DH % 4 == 0) {
         const size_t lds = ((size_t)2 * a.cap * (DH + 4) + a.cap) * sizeof(float);
         if (lds <= 64 * 1024) {
