@@ -484,8 +484,9 @@ def main():
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(json.dumps({"error": "this build measures one GPU only: the path shards by sequence with no "
-                                   "exchange step, so N>1 is not run (see the sharding note in DESIGN.md)",
+        print(json.dumps({"error": "this build measures one GPU only: the path shards by sequence (one process "
+                                   "per GPU on its share of the batch, weights replicated, no exchange step), "
+                                   "so N>1 is not run",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     out = run(args)
