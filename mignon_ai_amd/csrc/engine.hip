@@ -628,7 +628,7 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
             } else {
                 if (c.sess) {
                     ProfScope ps(m->prof, K_EXPORT, s);
-                    HIPCHECK(launch_export_kv(c.B, c.T, D, m->cap, c.lens, w.qkv.as<float>(),
+                    HIPCHECK(launch_export_kv(c.B, c.T, D, m->heads, m->cap, c.lens, w.qkv.as<float>(),
                                               c.sess->kring.as<float>() + (size_t)ab * c.B * m->cap * D,
                                               c.sess->vring.as<float>() + (size_t)ab * c.B * m->cap * D, s));
                 }

@@ -952,8 +952,8 @@ __global__ __launch_bounds__(64) void attention_step_kernel(AttnStepArgs a) {
     const int lo = max(window_start(pos, a.window), pos - cap + 1);
     const int span = pos - lo + 1;
     const float* qkv = a.qkv + (long long)s_ * 3 * D;
-    const float* kr = a.kring + (long long)s_ * cap * D;
-    const float* vr = a.vring + (long long)s_ * cap * D;
+    const float* kr = a.kring + ((long long)s_ * a.heads + h) * cap * DH;
+    const float* vr = a.vring + ((long long)s_ * a.heads + h) * cap * DH;
     for (int i = lane; i < DH; i += 64) qs[i] = qkv[h * DH + i];
     __syncthreads();
     float q[DH];
@@ -963,7 +963,7 @@ __global__ __launch_bounds__(64) void attention_step_kernel(AttnStepArgs a) {
     float mx = -3.40282347e38f;
     for (int jj = lane; jj < span; jj += 64) {
         int j = lo + jj;
-        const float* k = (j == pos) ? qkv + D + h * DH : kr + (long long)(j % cap) * D + h * DH;
+        const float* k = (j == pos) ? qkv + D + h * DH : kr + (long long)(j % cap) * DH;
         float s = dot_f32_ref<DH>(q, k) * scale;
         es[jj] = s;
         mx = fmaxf(mx, s);
@@ -983,14 +983,14 @@ __global__ __launch_bounds__(64) void attention_step_kernel(AttnStepArgs a) {
         for (int jj = 0; jj < span; jj++) {
             int j = lo + jj;
             float p = es[jj] * inv;
-            float v = (j == pos) ? qkv[2 * D + h * DH + i] : vr[(long long)(j % cap) * D + h * DH + i];
+            float v = (j == pos) ? qkv[2 * D + h * DH + i] : vr[(long long)(j % cap) * DH + i];
             o = axpy_ref<DH>(i, p, v, o);
         }
         a.att[(long long)s_ * a.Dp + h * DH + i] = o;
     }
     // record this position's key and value (slot pos % cap; the evicted key is outside the window)
-    float* kw = a.kring + (long long)s_ * cap * D + (long long)(pos % cap) * D + h * DH;
-    float* vw = a.vring + (long long)s_ * cap * D + (long long)(pos % cap) * D + h * DH;
+    float* kw = a.kring + (((long long)s_ * a.heads + h) * cap + pos % cap) * DH;
+    float* vw = a.vring + (((long long)s_ * a.heads + h) * cap + pos % cap) * DH;
     for (int i = lane; i < DH; i += 64) {
         kw[i] = qkv[D + h * DH + i];
         vw[i] = qkv[2 * D + h * DH + i];
@@ -1000,15 +1000,19 @@ __global__ __launch_bounds__(64) void attention_step_kernel(AttnStepArgs a) {
 // attention_step_lds_kernel for caches of at most 64 positions with each lane's key row in registers:
 // lane jj loads key lo + jj itself and scores it, so only the values (and the scores) go through LDS,
 // about half the LDS of the staged kernel and twice the waves per CU. Bit-identical to it: the same
-// reference-order dot product, softmax and P.V.
+// reference-order dot product, softmax and P.V. Every global load (the query, this position's key and
+// value, the key rows, the value rows) is issued before the first wait, so a wave makes one memory
+// round trip.
 template <int DH>
 __global__ __launch_bounds__(64) void attention_step_rk_kernel(AttnStepArgs a) {
     constexpr int DS = DH + 4;
     constexpr int C4 = DH / 4;
+    static_assert(3 * C4 <= 64, "one float4 of q, k or v per lane");
     extern __shared__ __align__(16) float rk_smem[];
     const int cap = a.cap;
     float* vs = rk_smem;          // [cap][DS]
-    float* es = vs + cap * DS;    // [cap]
+    float* qs = vs + cap * DS;    // [DH]
+    float* es = qs + DH;          // [cap]
     __shared__ float rk_inv;
     const int s_ = blockIdx.x / a.heads, h = blockIdx.x % a.heads;
     const int lane = threadIdx.x;
@@ -1017,41 +1021,46 @@ __global__ __launch_bounds__(64) void attention_step_rk_kernel(AttnStepArgs a) {
     const int lo = max(window_start(pos, a.window), pos - cap + 1);
     const int span = pos - lo + 1;  // at most cap <= 64
     const float* qkv = a.qkv + (long long)s_ * 3 * D;
-    const float* kr = a.kring + (long long)s_ * cap * D + h * DH;
-    const float* vr = a.vring + (long long)s_ * cap * D + h * DH;
+    const float* kr = a.kring + ((long long)s_ * a.heads + h) * cap * DH;
+    const float* vr = a.vring + ((long long)s_ * a.heads + h) * cap * DH;
+    // lanes 0..3*C4-1: one float4 each of this position's q, k and v (part lane / C4, chunk lane % C4)
+    const int qpart = min(lane / C4, 2), qc = lane % C4;
+    const float4 mine = *(const float4*)(qkv + qpart * D + h * DH + 4 * qc);
+    // ring slot of key lo + jj (jj < span <= cap): one wrap, no division per key
+    const int lo_slot = lo % cap;
+    auto slot = [&](int jj) { const int r = lo_slot + jj; return r >= cap ? r - cap : r; };
     // this lane's key row (key lo + lane; the current position's from qkv, not yet in the ring)
     float4 krow[C4];
     {
-        const int j = lo + min(lane, span - 1);
-        const float* kp = j == pos ? qkv + D + h * DH : kr + (long long)(j % cap) * D;
+        const int jj = min(lane, span - 1);
+        const float* kp = jj == span - 1 ? qkv + D + h * DH : kr + (long long)slot(jj) * DH;
 #pragma unroll
         for (int c = 0; c < C4; c++) krow[c] = *(const float4*)(kp + 4 * c);
     }
-    // values: rows jj = 0..span-1 into LDS, every load issued first
+    // values: rows jj = 0..span-1 into LDS, every load issued before the first store. Lanes past the
+    // end repeat the last element (the same bytes to the same address), so no store is conditional and
+    // no load can be moved next to its store.
     const int n4 = span * C4;
     for (int e0 = 0; e0 < n4; e0 += 8 * 64) {
         float4 vb[8];
+        int off[8];
 #pragma unroll
         for (int u = 0; u < 8; u++) {
             const int e = min(e0 + u * 64 + lane, n4 - 1);
             const int jj = e / C4, c = e - jj * C4;
-            const int j = lo + jj;
-            const float* vp = j == pos ? qkv + 2 * D + h * DH : vr + (long long)(j % cap) * D;
+            const float* vp = jj == span - 1 ? qkv + 2 * D + h * DH : vr + (long long)slot(jj) * DH;
             vb[u] = *(const float4*)(vp + 4 * c);
+            off[u] = jj * DS + 4 * c;
         }
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int e = e0 + u * 64 + lane;
-            if (e < n4) {
-                const int jj = e / C4, c = e - jj * C4;
-                *(float4*)(vs + jj * DS + 4 * c) = vb[u];
-            }
-        }
+        for (int u = 0; u < 8; u++) *(float4*)(vs + off[u]) = vb[u];
     }
+    if (lane < C4) *(float4*)(qs + 4 * lane) = mine;
+    __syncthreads();
     float q[DH];
 #pragma unroll
     for (int i = 0; i < DH; i += 4) {
-        const float4 t = *(const float4*)(qkv + h * DH + i);
+        const float4 t = *(const float4*)(qs + i);
         q[i] = t.x; q[i + 1] = t.y; q[i + 2] = t.z; q[i + 3] = t.w;
     }
     const float scale = (float)(1.0 / sqrt((double)DH));
@@ -1074,11 +1083,9 @@ __global__ __launch_bounds__(64) void attention_step_rk_kernel(AttnStepArgs a) {
         a.att[(long long)s_ * a.Dp + h * DH + i] = o;
     }
     // record this position's key and value (slot pos % cap; the evicted key is outside the window)
-    float* kw = a.kring + (long long)s_ * cap * D + (long long)(pos % cap) * D + h * DH;
-    float* vw = a.vring + (long long)s_ * cap * D + (long long)(pos % cap) * D + h * DH;
-    for (int i = lane; i < DH; i += 64) {
-        kw[i] = qkv[D + h * DH + i];
-        vw[i] = qkv[2 * D + h * DH + i];
+    if (lane >= C4 && lane < 3 * C4) {
+        float* ring = lane < 2 * C4 ? a.kring : a.vring;
+        *(float4*)(ring + (((long long)s_ * a.heads + h) * cap + pos % cap) * DH + 4 * qc) = mine;
     }
 }
 
@@ -1103,8 +1110,8 @@ __global__ __launch_bounds__(64) void attention_step_lds_kernel(AttnStepArgs a) 
     const int lo = max(window_start(pos, a.window), pos - cap + 1);
     const int span = pos - lo + 1;
     const float* qkv = a.qkv + (long long)s_ * 3 * D;
-    const float* kr = a.kring + (long long)s_ * cap * D + h * DH;
-    const float* vr = a.vring + (long long)s_ * cap * D + h * DH;
+    const float* kr = a.kring + ((long long)s_ * a.heads + h) * cap * DH;
+    const float* vr = a.vring + ((long long)s_ * a.heads + h) * cap * DH;
     // rows jj = 0..span-1 hold key/value j = lo + jj (the current position's from qkv, not yet in the ring)
     const int n4 = span * C4;
     for (int e0 = 0; e0 < n4; e0 += 8 * 64) {
@@ -1114,8 +1121,8 @@ __global__ __launch_bounds__(64) void attention_step_lds_kernel(AttnStepArgs a) 
             const int e = min(e0 + u * 64 + lane, n4 - 1);
             const int jj = e / C4, c = e - jj * C4;
             const int j = lo + jj;
-            const float* kp = j == pos ? qkv + D + h * DH : kr + (long long)(j % cap) * D;
-            const float* vp = j == pos ? qkv + 2 * D + h * DH : vr + (long long)(j % cap) * D;
+            const float* kp = j == pos ? qkv + D + h * DH : kr + (long long)(j % cap) * DH;
+            const float* vp = j == pos ? qkv + 2 * D + h * DH : vr + (long long)(j % cap) * DH;
             kb[u] = *(const float4*)(kp + 4 * c);
             vb[u] = *(const float4*)(vp + 4 * c);
         }
@@ -1161,8 +1168,8 @@ __global__ __launch_bounds__(64) void attention_step_lds_kernel(AttnStepArgs a) 
         a.att[(long long)s_ * a.Dp + h * DH + i] = o;
     }
     // record this position's key and value (slot pos % cap; the evicted key is outside the window)
-    float* kw = a.kring + (long long)s_ * cap * D + (long long)(pos % cap) * D + h * DH;
-    float* vw = a.vring + (long long)s_ * cap * D + (long long)(pos % cap) * D + h * DH;
+    float* kw = a.kring + (((long long)s_ * a.heads + h) * cap + pos % cap) * DH;
+    float* vw = a.vring + (((long long)s_ * a.heads + h) * cap + pos % cap) * DH;
     for (int i = lane; i < DH; i += 64) {
         kw[i] = qkv[D + h * DH + i];
         vw[i] = qkv[2 * D + h * DH + i];
@@ -1267,16 +1274,21 @@ __global__ void export_ring_kernel(int B, int T, int Dp, int ring, const int32_t
             nr[((long long)b * ring + p % ring) * Dp + d] = nf[((long long)b * T + p) * Dp + d];
 }
 
-__global__ void export_kv_kernel(int B, int T, int D, int cap, const int32_t* lens, const float* qkv, float* kr,
-                                 float* vr) {
+// The rings are head-major, [session][head][slot][dh], so that a decode step's key and value rows of one
+// head are one contiguous block.
+__global__ void export_kv_kernel(int B, int T, int D, int heads, int cap, const int32_t* lens, const float* qkv,
+                                 float* kr, float* vr) {
     const int b = blockIdx.x;
     const int len = lens[b];
     const int p0 = max(0, len - cap);
+    const int dh = D / heads;
     for (int p = p0; p < len; p++)
         for (int d = threadIdx.x; d < D; d += blockDim.x) {
             const float* row = qkv + ((long long)b * T + p) * 3 * D;
-            kr[((long long)b * cap + p % cap) * D + d] = row[D + d];
-            vr[((long long)b * cap + p % cap) * D + d] = row[2 * D + d];
+            const int h = d / dh;
+            const long long o = (((long long)b * heads + h) * cap + p % cap) * dh + (d - h * dh);
+            kr[o] = row[D + d];
+            vr[o] = row[2 * D + d];
         }
 }
 
@@ -1357,7 +1369,7 @@ template <int DH>
 hipError_t attn_step_t(const AttnStepArgs& a, hipStream_t s) {
     if constexpr (DH % 4 == 0 && DH <= 64) {
         if (a.cap <= 64) {
-            const size_t lds = ((size_t)a.cap * (DH + 4) + a.cap) * sizeof(float);
+            const size_t lds = ((size_t)a.cap * (DH + 4) + DH + a.cap) * sizeof(float);
             hipLaunchKernelGGL(attention_step_rk_kernel<DH>, dim3(a.S * a.heads), dim3(64), lds, s, a);
             return hipGetLastError();
         }
@@ -1499,10 +1511,11 @@ hipError_t launch_export_ring(int B, int T, int Dp, int ring, const int32_t* len
     return hipGetLastError();
 }
 
-hipError_t launch_export_kv(int B, int T, int D, int cap, const int32_t* lens, const float* qkv, float* kring,
-                            float* vring, hipStream_t s) {
+hipError_t launch_export_kv(int B, int T, int D, int heads, int cap, const int32_t* lens, const float* qkv,
+                            float* kring, float* vring, hipStream_t s) {
     if (B <= 0) return hipSuccess;
-    hipLaunchKernelGGL(export_kv_kernel, dim3(B), dim3(256), 0, s, B, T, D, cap, lens, qkv, kring, vring);
+    if (heads <= 0 || D % heads != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(export_kv_kernel, dim3(B), dim3(256), 0, s, B, T, D, heads, cap, lens, qkv, kring, vring);
     return hipGetLastError();
 }
 

@@ -79,8 +79,8 @@ struct AttnStepArgs {
     int S = 0, D = 0, Dp = 0, heads = 0, window = 0, cap = 0;
     const int32_t* pos = nullptr;  // [S]
     const float* qkv = nullptr;    // [S][3D]
-    float* kring = nullptr;        // [S][cap][D]
-    float* vring = nullptr;        // [S][cap][D]
+    float* kring = nullptr;        // [S][heads][cap][D / heads]
+    float* vring = nullptr;        // [S][heads][cap][D / heads]
     float* att = nullptr;          // [S][Dp]
 };
 hipError_t launch_attention_step(const AttnStepArgs& a, hipStream_t s);
@@ -113,8 +113,8 @@ hipError_t launch_quantize(const float* w, long long n, int8_t* q, float* scale,
 // Session state export after a batched prefill.
 hipError_t launch_export_ring(int B, int T, int Dp, int ring, const int32_t* lens, const float* nf, float* norm_ring,
                               hipStream_t s);
-hipError_t launch_export_kv(int B, int T, int D, int cap, const int32_t* lens, const float* qkv, float* kring,
-                            float* vring, hipStream_t s);
+hipError_t launch_export_kv(int B, int T, int D, int heads, int cap, const int32_t* lens, const float* qkv,
+                            float* kring, float* vring, hipStream_t s);
 hipError_t launch_set_pos(int S, const int32_t* lens, int32_t* pos, int add, hipStream_t s);
 hipError_t launch_fill_i32(int32_t* p, int n, int v, hipStream_t s);
 hipError_t launch_fill_f32(float* p, long long n, float v, hipStream_t s);
