@@ -1333,6 +1333,7 @@ int mg_sessions_decode_sample(mg_sessions* s, const int32_t* prompts, const int3
         s->sample_ws.ensure(sample_scratch_bytes(S, V));
         sa.scratch = s->sample_ws.as<double>();
         sa.sums = sa.scratch + (size_t)S * V;
+        sa.flags = (int32_t*)(sa.sums + S);
         auto pick = [&](int col) {
             sa.col = col; sa.step = col; sa.out_col = col;
             ProfScope ps(m->prof, K_SAMPLE, st);
@@ -1382,6 +1383,7 @@ int mg_sample_logits(const double* logits, int n, int V, const int32_t* recent, 
         sa.out = o; sa.out_ld = 1;
         sa.scratch = sg.out<double>(sample_scratch_bytes(n, V) / sizeof(double));
         sa.sums = sa.scratch + (size_t)n * V;
+        sa.flags = (int32_t*)(sa.sums + n);
         HIPCHECK(launch_sample(sa, st));
         HIPCHECK(hipMemcpyAsync(out, o, (size_t)n * 4, hipMemcpyDeviceToHost, st));
         HIPCHECK(hipStreamSynchronize(st));

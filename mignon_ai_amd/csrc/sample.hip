@@ -186,6 +186,7 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
     int* idx = (int*)(smp_smem + n2);  // [n2] token ids once sorted
     const long long base = (long long)row * a.ld;
     if constexpr (PHASE == 2) {
+        if (a.flags && a.flags[row] == 0) return;  // drawn by sample_pick_kernel
         for (int i = threadIdx.x; i < V; i += blockDim.x) key[i] = a.scratch[(long long)row * V + i];
     } else {
         for (int i = threadIdx.x; i < V; i += blockDim.x)
@@ -417,6 +418,96 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
     }
 }
 
+// Truncated draw of one row by one wave, from the exponentials in a.scratch and the row sums in
+// a.sums (top-k of at most kExtract, or top-p): p = e * (1 / sum), then the candidates one at a time,
+// most probable first (equal probabilities by token id), until top-k or top-p is met, and the draw over
+// them (sample.go:111-190). Lane L owns tokens L, L + 64, ... and keeps the four best of them sorted in
+// registers; a round is one wave argmax over the lanes' heads, then the winning lane pops its head. The
+// candidates come out in descending order, so the ones taken so far are exactly those at or before the
+// last one taken: a lane whose four are all taken rescans its tokens past that point. The row stays in
+// global memory (no LDS staging), so many rows run per CU. A row whose top-p mass is not reached within
+// kExtract candidates is flagged for sample_rows_kernel<2>, which sorts it.
+__global__ __launch_bounds__(64) void sample_pick_kernel(SampleArgs a) {
+    __shared__ double cand_v[kExtract];
+    __shared__ int cand_i[kExtract];
+    const int row = blockIdx.x, lane = threadIdx.x, V = a.V;
+    const double* e = a.scratch + (long long)row * V;
+    const double inv = 1.0 / a.sums[row];
+    const int kcap = (a.p.top_k > 0 && a.p.top_k < V) ? a.p.top_k : V;
+    const bool use_p = a.p.top_p > 0.0 && a.p.top_p < 1.0;
+    const int rounds = min(kcap, kExtract);
+    double cv4[4];
+    int ci4[4];
+    double lv = INFINITY;  // the last candidate taken: every token at or before it is taken
+    int li = -1;
+    auto refill = [&]() {
+#pragma unroll
+        for (int q = 0; q < 4; q++) { cv4[q] = -INFINITY; ci4[q] = 0x7fffffff; }
+        for (int i0 = lane; i0 < V; i0 += 8 * 64) {
+            double kv[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) kv[k] = e[min(i0 + 64 * k, V - 1)] * inv;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int i = i0 + 64 * k;
+                double v = kv[k];
+                int vi = i;
+                if (i >= V || !before(lv, li, v, vi) || !before(v, vi, cv4[3], ci4[3])) continue;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    if (before(v, vi, cv4[q], ci4[q])) {
+                        const double tv = cv4[q];
+                        const int ti = ci4[q];
+                        cv4[q] = v; ci4[q] = vi;
+                        v = tv; vi = ti;
+                    }
+                }
+            }
+        }
+    };
+    refill();
+    int taken = 0;  // this lane's tokens taken since its last refill
+    double cp = 0.0;
+    int act = 0;
+    for (int r = 0; r < rounds; r++) {
+        double bv = cv4[0];
+        int bi = ci4[0];
+        wave_argmax(bv, bi);
+        if (lane == 0) { cand_v[r] = bv; cand_i[r] = bi; }
+        cp += bv;
+        if ((use_p && cp >= a.p.top_p) || r + 1 == kcap) {
+            act = r + 1;
+            break;
+        }
+        if ((bi & 63) == lane) {
+            cv4[0] = cv4[1]; ci4[0] = ci4[1];
+            cv4[1] = cv4[2]; ci4[1] = ci4[2];
+            cv4[2] = cv4[3]; ci4[2] = ci4[3];
+            cv4[3] = -INFINITY; ci4[3] = 0x7fffffff;
+            if (++taken == 4) {
+                lv = bv; li = bi;
+                refill();
+                taken = 0;
+            }
+        }
+    }
+    if (lane != 0) return;
+    a.flags[row] = act == 0;
+    if (act == 0) return;
+    int c = cand_i[0];
+    if (act > 1) {  // sampleFromCDF (sample.go:173-190)
+        const double u = a.u ? a.u[row] : uniform_draw(a.seeds[row], a.step);
+        double sp = 0.0;
+        for (int i = 0; i < act; i++) sp += cand_v[i];
+        const double r = u * sp;
+        c = cand_i[act - 1];
+        const int k = seq_find(cand_v, act, r, -1);
+        if (k >= 0) c = cand_i[k];
+    }
+    a.out[(long long)row * a.out_ld + a.out_col] = c;
+    if (a.next_ids) a.next_ids[row] = c;
+}
+
 // The rows' sequential float64 sums, one lane per row (each lane's chain of dependent additions runs
 // beside 63 others instead of alone in a workgroup): sums[row] = e[0] + e[1] + ... in index order. For
 // pure temperature sampling (pure != 0) the lane also draws: the first index whose running sum reaches
@@ -474,7 +565,9 @@ __global__ __launch_bounds__(64) void sample_sum_kernel(SampleArgs a, int pure) 
 
 }  // namespace
 
-size_t sample_scratch_bytes(int n, int V) { return ((size_t)n * V + (size_t)n) * sizeof(double); }
+size_t sample_scratch_bytes(int n, int V) {
+    return ((size_t)n * V + (size_t)n) * sizeof(double) + ((size_t)n * sizeof(int32_t) + 7) / 8 * 8;
+}
 
 int sample_n2(int V) {
     int n2 = 1;
@@ -510,10 +603,19 @@ hipError_t launch_sample(const SampleArgs& a, hipStream_t s) {
         hipLaunchKernelGGL(sample_rows_kernel<0>, dim3(a.n), dim3(kThreads), lds, s, a);
         return hipGetLastError();
     }
-    // three passes: exponentials per row, the rows' sums one lane per row, then the truncated draw
+    // three passes: exponentials per row, the rows' sums one lane per row, then the truncated draw (one
+    // wave per row; the rows it flags, and every row when top-k exceeds kExtract without top-p, sorted)
     hipLaunchKernelGGL(sample_rows_kernel<1>, dim3(a.n), dim3(kThreads), (size_t)a.V * sizeof(double), s, a);
     hipLaunchKernelGGL(sample_sum_kernel, dim3((a.n + 63) / 64), dim3(64), 0, s, a, truncated ? 0 : 1);
-    if (truncated) hipLaunchKernelGGL(sample_rows_kernel<2>, dim3(a.n), dim3(kThreads), lds, s, a);
+    if (truncated) {
+        SampleArgs b = a;
+        b.flags = nullptr;
+        if ((kcap <= kExtract || use_p) && a.flags) {
+            hipLaunchKernelGGL(sample_pick_kernel, dim3(a.n), dim3(64), 0, s, a);
+            b.flags = a.flags;
+        }
+        hipLaunchKernelGGL(sample_rows_kernel<2>, dim3(a.n), dim3(kThreads), lds, s, b);
+    }
     return hipGetLastError();
 }
 

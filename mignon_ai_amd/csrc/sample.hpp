@@ -41,8 +41,12 @@ struct SampleArgs {
     // each row in one lane of its workgroup.
     double* scratch = nullptr;
     double* sums = nullptr;
+    // [n] per-row flags of the same workspace: set for the rows whose top-p mass is not reached within
+    // the candidates taken one by one, which then take the full sort
+    int32_t* flags = nullptr;
 };
-// Bytes of SampleArgs::scratch plus SampleArgs::sums for n rows of V tokens.
+// Bytes of SampleArgs::scratch, SampleArgs::sums and SampleArgs::flags for n rows of V tokens, laid out
+// in that order (sums at scratch + n * V, flags right after the sums).
 size_t sample_scratch_bytes(int n, int V);
 
 int sample_n2(int V);
