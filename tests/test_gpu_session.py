@@ -115,3 +115,29 @@ def test_greedy_until_stops():
     assert not counts.any()
     with pytest.raises(MignonError):
         gm.sessions(S).decode_greedy_until(prompts, G, list(range(9)), lens)
+
+
+@pytest.mark.parametrize("D,heads,context,window", [(32, 2, 256, 0), (128, 2, 256, 0), (64, 1, 64, 0),
+                                                    (40, 2, 128, 30)])
+def test_decode_attention_kernels(D, heads, context, window):
+    """Streamed steps through each decode-attention kernel equal the teacher-forced batch: caches of more
+    than 64 positions with keys and values staged in LDS (head width 16), one lane per key where that
+    staging would not fit (head width 64, cache 256), and caches of at most 64 positions with key rows in
+    registers (head widths 64 and 20, the last with a window of 30 inside a 128-token context); the last
+    step also against the oracle."""
+    from helpers import tiny_spec, uniform_model_bytes
+    spec = tiny_spec([(1, 2, 1), (1, 2, 1)], V=64, D=D, H=32, heads=heads, window=window, context=context)
+    data = uniform_model_bytes(spec, scale=0.3)
+    gm = Model(data)
+    S = 6
+    T = min(100, context)
+    P = T // 3
+    ids = synth.token_ids(12, f"dec-attn{D}-{heads}-{context}-{window}", (S, T), spec.V)
+    full = gm.forward_batch(ids)["logits"]
+    ss = gm.sessions(S)
+    lg, _, _ = ss.prefill(ids[:, :P])
+    assert_close(lg, full[:, P - 1], what="prefill")
+    for t in range(P, T):
+        lg, _, _ = ss.step(ids[:, t])
+        assert_close(lg, full[:, t], what=f"step {t}")
+    assert_close(lg[:2], oracle_model(data).forward_all(ids[:2])[:, -1], what="oracle, last step")
