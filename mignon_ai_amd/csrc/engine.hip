@@ -612,6 +612,7 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
         }
         if (blk.attn) {
             // attendPosition (internal/quant/attention.go:69-104)
+            bool att_limbs = false;  // the attention kernel wrote the out projection's operand itself
             row_call(m, M, ROW_SRC, nullptr, nullptr, 0, nullptr, blk.anorm, nullptr, true, s);
             GemmArgs g = lx_args(w.nl.as<int8_t>(), w.ns.as<float>(), blk.qkv, m->Np3, Dp, M, 3 * D, blk.sqkv);
             g.out = w.qkv.as<float>(); g.ldo = 3 * D;
@@ -624,7 +625,14 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                 aa.vring = c.sess->vring.as<float>() + (size_t)ab * c.B * m->cap * D;
                 aa.att = w.att.as<float>();
                 ProfScope ps(m->prof, K_ATTN_STEP, s);
-                HIPCHECK(launch_attention_step(aa, s));
+                if (attention_step_rows_fits(aa)) {
+                    // the output goes straight to the out projection's limbs
+                    aa.xl = w.nl.as<int8_t>(); aa.xs = w.ns.as<float>();
+                    HIPCHECK(launch_attention_step_rows(aa, s));
+                    att_limbs = true;
+                } else {
+                    HIPCHECK(launch_attention_step(aa, s));
+                }
             } else {
                 if (c.sess) {
                     ProfScope ps(m->prof, K_EXPORT, s);
@@ -638,7 +646,7 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                 ProfScope ps(m->prof, K_ATTN, s);
                 HIPCHECK(launch_attention(aa, s));
             }
-            row_call(m, M, ROW_SRC, nullptr, w.att.as<float>(), Dp, nullptr, nullptr, nullptr, true, s);
+            if (!att_limbs) row_call(m, M, ROW_SRC, nullptr, w.att.as<float>(), Dp, nullptr, nullptr, nullptr, true, s);
             g = lx_args(w.nl.as<int8_t>(), w.ns.as<float>(), blk.wo, m->NpD, Dp, M, D, blk.so);
             g.cur = w.cur.as<float>(); g.ldcur = Dp;
             if (fuse_next) g.resid = w.bin.as<float>();

@@ -997,25 +997,33 @@ __global__ __launch_bounds__(64) void attention_step_kernel(AttnStepArgs a) {
     }
 }
 
-// attention_step_lds_kernel for caches of at most 64 positions with each lane's key row in registers:
-// lane jj loads key lo + jj itself and scores it, so only the values (and the scores) go through LDS,
-// about half the LDS of the staged kernel and twice the waves per CU. Bit-identical to it: the same
-// reference-order dot product, softmax and P.V. Every global load (the query, this position's key and
-// value, the key rows, the value rows) is issued before the first wait, so a wave makes one memory
-// round trip.
+// Makes this wave's LDS writes visible to its own later reads (LDS operations of one wave complete in
+// order): a workgroup-wide barrier is not needed where every LDS region is private to one wave.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+}
+
+// LDS floats of one head in rk_head: the values [cap][DH + 4], the query [DH], the scores [cap].
+__host__ __device__ constexpr int rk_lds_floats(int cap, int dh) { return cap * (dh + 4) + dh + cap; }
+
+// One (session, head) of decode attention for caches of at most 64 positions, by one wave, with each
+// lane's key row in registers: lane jj loads key lo + jj itself and scores it, so only the values (and
+// the scores) go through LDS, about half the LDS of the staged kernel and twice the waves per CU.
+// Bit-identical to it: the same reference-order dot product, softmax and P.V. Every global load (the
+// query, this position's key and value, the key rows, the value rows) is issued before the first wait,
+// so a wave makes one memory round trip. `sm` (rk_lds_floats) and `inv_sh` are private to the wave.
+// Returns output element `lane` of the head (lanes < DH) and records this position's key and value in
+// the ring.
 template <int DH>
-__global__ __launch_bounds__(64) void attention_step_rk_kernel(AttnStepArgs a) {
+__device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, int lane, float* sm, float& inv_sh) {
     constexpr int DS = DH + 4;
     constexpr int C4 = DH / 4;
     static_assert(3 * C4 <= 64, "one float4 of q, k or v per lane");
-    extern __shared__ __align__(16) float rk_smem[];
     const int cap = a.cap;
-    float* vs = rk_smem;          // [cap][DS]
+    float* vs = sm;               // [cap][DS]
     float* qs = vs + cap * DS;    // [DH]
     float* es = qs + DH;          // [cap]
-    __shared__ float rk_inv;
-    const int s_ = blockIdx.x / a.heads, h = blockIdx.x % a.heads;
-    const int lane = threadIdx.x;
     const int D = a.D;
     const int pos = a.pos[s_];
     const int lo = max(window_start(pos, a.window), pos - cap + 1);
@@ -1056,7 +1064,7 @@ __global__ __launch_bounds__(64) void attention_step_rk_kernel(AttnStepArgs a) {
         for (int u = 0; u < 8; u++) *(float4*)(vs + off[u]) = vb[u];
     }
     if (lane < C4) *(float4*)(qs + 4 * lane) = mine;
-    __syncthreads();
+    wave_lds_sync();
     float q[DH];
 #pragma unroll
     for (int i = 0; i < DH; i += 4) {
@@ -1067,26 +1075,68 @@ __global__ __launch_bounds__(64) void attention_step_rk_kernel(AttnStepArgs a) {
     const float sc = dot_ref_reg4<DH>(q, krow) * scale;
     const float mx = wave_max(lane < span ? sc : -3.40282347e38f);
     if (lane < span) es[lane] = fast_exp_ref(sc - mx);
-    __syncthreads();
+    wave_lds_sync();
     if (lane == 0) {
         float sum = 0.0f;  // nn.SoftmaxInPlaceF32's sequential sum
 #pragma unroll 8
         for (int jj = 0; jj < span; jj++) sum += es[jj];
-        rk_inv = 1.0f / sum;
+        inv_sh = 1.0f / sum;
     }
-    __syncthreads();
-    const float inv = rk_inv;
-    for (int i = lane; i < DH; i += 64) {
-        float o = 0.0f;
+    wave_lds_sync();
+    const float inv = inv_sh;
+    float o = 0.0f;
+    if (lane < DH) {
 #pragma unroll 8
-        for (int jj = 0; jj < span; jj++) o = axpy_ref<DH>(i, es[jj] * inv, vs[jj * DS + i], o);
-        a.att[(long long)s_ * a.Dp + h * DH + i] = o;
+        for (int jj = 0; jj < span; jj++) o = axpy_ref<DH>(lane, es[jj] * inv, vs[jj * DS + lane], o);
     }
     // record this position's key and value (slot pos % cap; the evicted key is outside the window)
     if (lane >= C4 && lane < 3 * C4) {
         float* ring = lane < 2 * C4 ? a.kring : a.vring;
         *(float4*)(ring + (((long long)s_ * a.heads + h) * cap + pos % cap) * DH + 4 * qc) = mine;
     }
+    return o;
+}
+
+// Decode attention, one wave per (session, head), key rows in registers (rk_head).
+template <int DH>
+__global__ __launch_bounds__(64) void attention_step_rk_kernel(AttnStepArgs a) {
+    extern __shared__ __align__(16) float rk_smem[];
+    __shared__ float rk_inv;
+    const int s_ = blockIdx.x / a.heads, h = blockIdx.x % a.heads;
+    const int lane = threadIdx.x;
+    const float o = rk_head<DH>(a, s_, h, lane, rk_smem, rk_inv);
+    if (lane < DH) a.att[(long long)s_ * a.Dp + h * DH + lane] = o;
+}
+
+// Decode attention of one session per workgroup, one wave per head (rk_head), fused with the limb
+// expansion of the attention output that the out projection reads: the row's absolute maximum over
+// all heads gives its scale, and each lane writes its element's three limbs (row_kernel's ROW_SRC
+// digits and scale, from the same values), so the output never goes through memory as fp32.
+template <int DH>
+__global__ __launch_bounds__(1024) void attention_step_rows_kernel(AttnStepArgs a) {
+    extern __shared__ __align__(16) float rows_smem[];
+    __shared__ float inv_sh[16], red[16];
+    const int s_ = blockIdx.x, h = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const float o = rk_head<DH>(a, s_, h, lane, rows_smem + h * rk_lds_floats(a.cap, DH), inv_sh[h]);
+    const float mx = wave_max(lane < DH ? fabsf(o) : 0.0f);
+    if (lane == 0) red[h] = mx;
+    __syncthreads();
+    float amax = red[0];
+    for (int i = 1; i < a.heads; i++) amax = fmaxf(amax, red[i]);
+    float sc, inv;
+    limb_scale(amax, sc, inv);
+    const int kc = a.Dp >> 6;
+    if (lane < DH) {
+        const Limbs L = split_limbs(o, inv);
+        const int k = h * DH + lane;
+        a.xl[frag_off_a(s_, k, 0, kc)] = L.q0;
+        a.xl[frag_off_a(s_, k, 1, kc)] = L.q1;
+        a.xl[frag_off_a(s_, k, 2, kc)] = L.q2;
+    }
+    for (int k = a.D + (int)threadIdx.x; k < a.Dp; k += blockDim.x)  // padding channels read as zero
+#pragma unroll
+        for (int l = 0; l < 3; l++) a.xl[frag_off_a(s_, k, l, kc)] = 0;
+    if (threadIdx.x == 0) a.xs[s_] = sc;
 }
 
 // Decode attention, staged: the span's key and value head slices go to LDS with 16-byte loads (eight
@@ -1369,7 +1419,7 @@ template <int DH>
 hipError_t attn_step_t(const AttnStepArgs& a, hipStream_t s) {
     if constexpr (DH % 4 == 0 && DH <= 64) {
         if (a.cap <= 64) {
-            const size_t lds = ((size_t)a.cap * (DH + 4) + DH + a.cap) * sizeof(float);
+            const size_t lds = (size_t)rk_lds_floats(a.cap, DH) * sizeof(float);
             hipLaunchKernelGGL(attention_step_rk_kernel<DH>, dim3(a.S * a.heads), dim3(64), lds, s, a);
             return hipGetLastError();
         }
@@ -1383,6 +1433,20 @@ hipError_t attn_step_t(const AttnStepArgs& a, hipStream_t s) {
     }
     hipLaunchKernelGGL(attention_step_kernel<DH>, dim3(a.S * a.heads), dim3(64), 0, s, a);
     return hipGetLastError();
+}
+
+template <int DH>
+hipError_t attn_step_rows_t(const AttnStepArgs& a, hipStream_t s) {
+    if constexpr (DH % 4 == 0 && DH <= 64) {
+        const size_t lds = (size_t)a.heads * rk_lds_floats(a.cap, DH) * sizeof(float);
+        static const hipError_t attr = hipFuncSetAttribute((const void*)attention_step_rows_kernel<DH>,
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                           (int)kStepRowsMaxLds);
+        if (attr != hipSuccess) return attr;
+        hipLaunchKernelGGL(attention_step_rows_kernel<DH>, dim3(a.S), dim3(64 * a.heads), lds, s, a);
+        return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
 }
 
 template <int NS4>
@@ -1473,6 +1537,23 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
     const int mode = option(OPT_ATTENTION_KERNEL);
     if (mode != ATTN_EXACT && attn_mfma_fits(a, dh)) return attn_mfma(a, dh, s);
     DH_SWITCH(dh, attn_t, a, s)
+}
+
+bool attention_step_rows_fits(const AttnStepArgs& a) {
+    if (a.heads <= 0 || a.heads > 16 || a.D % a.heads) return false;
+    const int dh = a.D / a.heads;
+    if (dh % 4 || dh > 64 || a.cap > 64 || a.Dp % 64) return false;
+    switch (dh) {  // the widths DH_SWITCH instantiates
+        case 4: case 8: case 12: case 16: case 20: case 24: case 32: case 40: case 48: case 64: break;
+        default: return false;
+    }
+    return (size_t)a.heads * rk_lds_floats(a.cap, dh) * sizeof(float) <= kStepRowsMaxLds;
+}
+
+hipError_t launch_attention_step_rows(const AttnStepArgs& a, hipStream_t s) {
+    if (a.S <= 0) return hipSuccess;
+    if (!attention_step_rows_fits(a) || !a.xl || !a.xs) return hipErrorInvalidValue;
+    DH_SWITCH(a.D / a.heads, attn_step_rows_t, a, s)
 }
 
 hipError_t launch_attention_step(const AttnStepArgs& a, hipStream_t s) {

@@ -82,8 +82,16 @@ struct AttnStepArgs {
     float* kring = nullptr;        // [S][heads][cap][D / heads]
     float* vring = nullptr;        // [S][heads][cap][D / heads]
     float* att = nullptr;          // [S][Dp]
+    int8_t* xl = nullptr;          // attention_step_rows: limbs of the output, fragment layout, K = Dp
+    float* xs = nullptr;           // attention_step_rows: [S] row scales
 };
 hipError_t launch_attention_step(const AttnStepArgs& a, hipStream_t s);
+// Decode attention fused with the limb expansion of its output (one workgroup per session, one wave per
+// head): writes xl/xs, as the row kernel would from att, instead of att. For head widths that are a
+// multiple of 4 up to 64, caches of at most 64 positions and at most 16 heads.
+constexpr size_t kStepRowsMaxLds = 156 * 1024;  // dynamic LDS; the static part and the 160 KiB total
+bool attention_step_rows_fits(const AttnStepArgs& a);
+hipError_t launch_attention_step_rows(const AttnStepArgs& a, hipStream_t s);
 
 // Per-row combination of the head GEMM's per-tile statistics.
 struct HeadCombineArgs {
