@@ -512,52 +512,107 @@ __global__ __launch_bounds__(64) void sample_pick_kernel(SampleArgs a) {
 // beside 63 others instead of alone in a workgroup): sums[row] = e[0] + e[1] + ... in index order. For
 // pure temperature sampling (pure != 0) the lane also draws: the first index whose running sum reaches
 // u * sum (the same sums again), or 0 when none does.
-__global__ __launch_bounds__(64) void sample_sum_kernel(SampleArgs a, int pure) {
-    const int row = blockIdx.x * blockDim.x + threadIdx.x;
-    if (row >= a.n) return;
-    const int V = a.V;
-    const double* e = a.scratch + (long long)row * V;
-    // batches of 16 in two register sets that alternate: a batch's loads are issued a whole batch of
-    // additions before they are needed (scheduling barriers keep them there)
-    constexpr int B = 16;
-    double s = 0.0;
-    const int nb = V / (2 * B) * (2 * B);
-    if (nb) {
-        double v0[B], v1[B];
+//
+// The wave's 64 rows pass through LDS in blocks of kSumCols columns: the block is loaded with
+// coalesced 16-byte loads (row by row), the next block's loads are in flight while each lane adds its
+// own row's values from LDS in index order. Rows are padded by one double, so the lanes' reads of one
+// column fall in different banks.
+constexpr int kSumCols = 32;
+constexpr int kSumLd = kSumCols + 1;
+constexpr int kSumLoads = 64 * kSumCols / 2 / 64;  // 16-byte loads per lane and block
+
+// Block cb of the wave's rows r0.. into registers: load u of lane L covers the double pair
+// (row (u*64 + L) / (kSumCols/2), columns 2*((u*64 + L) % (kSumCols/2)) + {0, 1}), clamped into the
+// arrays (clamped lanes load valid memory that nobody reads).
+__device__ __forceinline__ void sum_block_load(const double* e, int n, int V, int r0, int cb, int lane,
+                                               double2 (&buf)[kSumLoads]) {
 #pragma unroll
-        for (int k = 0; k < B; k++) v0[k] = e[k];
-        for (int i = 0; i < nb; i += 2 * B) {
-#pragma unroll
-            for (int k = 0; k < B; k++) v1[k] = e[i + B + k];
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int k = 0; k < B; k++) s += v0[k];
-            __builtin_amdgcn_sched_barrier(0);
-            const int j = min(i + 2 * B, nb - B);  // the next pair's first batch (past the end: a batch again)
-#pragma unroll
-            for (int k = 0; k < B; k++) v0[k] = e[j + k];
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int k = 0; k < B; k++) s += v1[k];
-            __builtin_amdgcn_sched_barrier(0);
-        }
+    for (int u = 0; u < kSumLoads; u++) {
+        const int q = u * 64 + lane;
+        const int r = min(r0 + q / (kSumCols / 2), n - 1);
+        const int c = min(cb * kSumCols + 2 * (q % (kSumCols / 2)), V - 2);
+        buf[u] = *(const double2*)(e + (long long)r * V + c);
     }
-    for (int i = nb; i < V; i++) s += e[i];
-    if (!pure) {
-        a.sums[row] = s;
+}
+
+__device__ __forceinline__ void sum_block_store(double* blk, int lane, const double2 (&buf)[kSumLoads]) {
+#pragma unroll
+    for (int u = 0; u < kSumLoads; u++) {
+        const int q = u * 64 + lane;
+        double* d = blk + (q / (kSumCols / 2)) * kSumLd + 2 * (q % (kSumCols / 2));
+        d[0] = buf[u].x;
+        d[1] = buf[u].y;
+    }
+}
+
+// Visits e[row][0], e[row][1], ... in order for the wave's rows (lane L: row r0 + L), f(index, value)
+// per element; stops after the block in which every lane's f has returned true.
+template <class F>
+__device__ __forceinline__ void sum_rows_scan(const double* e, int n, int V, int r0, int lane, double* blk, F&& f) {
+    if (V & 1) {  // rows not 16-byte aligned: each lane reads its own row
+        const double* rowp = e + (long long)min(r0 + lane, n - 1) * V;
+        for (int c = 0; c < V; c++)
+            if (f(c, rowp[c])) break;
         return;
     }
-    const double u = a.u ? a.u[row] : uniform_draw(a.seeds[row], a.step);
+    const int nb = (V + kSumCols - 1) / kSumCols;
+    double2 buf[kSumLoads];
+    sum_block_load(e, n, V, r0, 0, lane, buf);
+    bool done = false;
+    for (int cb = 0; cb < nb; cb++) {
+        sum_block_store(blk, lane, buf);
+        if (cb + 1 < nb) sum_block_load(e, n, V, r0, cb + 1, lane, buf);
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the block is in LDS
+        __builtin_amdgcn_wave_barrier();
+        const double* mine = blk + lane * kSumLd;
+        const int c0 = cb * kSumCols;
+        if (!done) {
+            // the last block of a vocabulary that is not a multiple of kSumCols was loaded from clamped
+            // columns: its values are read from their true columns
+            if (c0 + kSumCols <= V) {
+#pragma unroll 8
+                for (int c = 0; c < kSumCols; c++)
+                    if (!done && f(c0 + c, mine[c])) done = true;
+            } else {
+                const double* rowp = e + (long long)min(r0 + lane, n - 1) * V;
+                for (int c = c0; c < V; c++)
+                    if (!done && f(c, rowp[c])) done = true;
+            }
+        }
+        if (__builtin_amdgcn_ballot_w64(!done) == 0) break;
+        __builtin_amdgcn_wave_barrier();  // every lane's reads of this block come before the next store
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+    }
+}
+
+__global__ __launch_bounds__(64) void sample_sum_kernel(SampleArgs a, int pure) {
+    __shared__ double blk[64 * kSumLd];
+    const int lane = threadIdx.x, r0 = blockIdx.x * 64, row = r0 + lane;
+    const int V = a.V, n = a.n;
+    double s = 0.0;
+    sum_rows_scan(a.scratch, n, V, r0, lane, blk, [&](int, double v) {
+        s += v;
+        return false;
+    });
+    if (!pure) {
+        if (row < n) a.sums[row] = s;
+        return;
+    }
+    // every lane stays for the second pass: the blocks are stored into LDS by all 64 lanes together
+    const int rc = min(row, n - 1);
+    const double u = a.u ? a.u[rc] : uniform_draw(a.seeds[rc], a.step);
     const double r = u * s;
     double c = 0.0;
     int t = V;
-    for (int i = 0; i < V; i++) {
-        c += e[i];
+    sum_rows_scan(a.scratch, n, V, r0, lane, blk, [&](int i, double v) {
+        c += v;
         if (c >= r) {
             t = i;
-            break;
+            return true;
         }
-    }
+        return false;
+    });
+    if (row >= n) return;
     const int chosen = t < V ? t : 0;
     a.out[(long long)row * a.out_ld + a.out_col] = chosen;
     if (a.next_ids) a.next_ids[row] = chosen;

@@ -22,7 +22,7 @@ PARAMS = [  # temperature, top_k, top_p, rep_penalty
 ]
 
 
-@pytest.mark.parametrize("V", [4, 300, 2048, 8192])
+@pytest.mark.parametrize("V", [4, 300, 301, 2048, 8192])
 def test_sampler_matches_oracle(V):
     rng = np.random.default_rng(V)
     n = 24
