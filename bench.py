@@ -265,6 +265,7 @@ def run(args):
         raise SystemExit("bench.py needs a GPU")
     engine_option("gemm", args.gemm)
     engine_option("attention", args.attention)
+    engine_option("scan", args.scan)
     torch.cuda.set_device(0)
     # Everything runs on one non-default stream: the engine's launches, its HIP-event kernel timing and
     # the torch events bracketing the timed region.
@@ -464,7 +465,7 @@ def run(args):
                                                                                       key=lambda kv: -kv[1][1])}
         out["wall_s"] = round(wall, 3)
     out["cpu_baseline"] = cpu
-    out["kernels"] = {"gemm": args.gemm, "attention": args.attention}
+    out["kernels"] = {"gemm": args.gemm, "attention": args.attention, "scan": args.scan}
     return out
 
 
@@ -481,6 +482,9 @@ def main():
                     help="limb-expanded GEMM kernel (mg_engine_option); both give identical results")
     ap.add_argument("--attention", default="auto", choices=["auto", "exact", "mfma"],
                     help="attention kernel (mg_engine_option): reference order or matrix cores")
+    ap.add_argument("--scan", default="auto", choices=["auto", "separate", "fused"],
+                    help="latch scan and rule-input packing as two kernels or one (mg_engine_option); both "
+                         "give identical results")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

@@ -572,9 +572,10 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                 }
                 // rule input [n | left | g] (stream.go:180-184), limb-expanded with one scale per row
                 // The fused kernel runs one workgroup per sequence: automatic selection wants enough of
-                // them (at least 2048 waves) to cover the latency of its sequential rounds.
+                // them (at least 1024 waves: c3's 1024 sequences run faster fused, c1's 64 separate) to cover
+                // the latency of its sequential rounds.
                 const int sk = option(OPT_SCAN_KERNEL);
-                const bool many = (long long)c.B * ((Dp / 2 + 63) / 64) >= 2048;
+                const bool many = (long long)c.B * ((Dp / 2 + 63) / 64) >= 1024;
                 if (scan_rule_fits(c.T, Dp, dil) && (sk == 2 || (sk == 0 && many))) {
                     sa.dil = dil; sa.xl = w.xl.as<int8_t>(); sa.xs = w.xs.as<float>();
                     ProfScope ps(m->prof, K_SCAN, s);
