@@ -702,6 +702,39 @@ __global__ __launch_bounds__(256) void gemm_c2_kernel(GemmArgs g) {
     }
 
     const int nb = n0 + wn * 64 + 4 * lgrp;
+    if (m0 + GEMM_BM <= g.M && n0 + GEMM_BN <= g.nvalid && (g.ldo & 3) == 0 && !g.out_i32) {
+        // A whole tile: each half (tj) of the 64 x 128 fp32 result goes through LDS (the operand buffers
+        // are free once the loop's last barrier has passed) and out as 512-byte row segments with
+        // streaming stores, instead of 64-byte pieces of 16 rows per store.
+        constexpr int OLD = GEMM_BN + 4;  // staged row stride (floats)
+        float* ot = (float*)&Ws[0][0];    // 32 rows: 16.9 KB of the 20 KB buffer
+        float* const out0 = g.out + (long long)m0 * g.ldo + n0;
+#pragma unroll
+        for (int tj = 0; tj < 2; tj++) {
+#pragma unroll
+            for (int ti = 0; ti < 4; ti++) {
+                const int n = nb + ti * 16;
+                float4 v;
+                v.x = (float)acc[ti][tj][0] * g.wscale_n[n];
+                v.y = (float)acc[ti][tj][1] * g.wscale_n[n + 1];
+                v.z = (float)acc[ti][tj][2] * g.wscale_n[n + 2];
+                v.w = (float)acc[ti][tj][3] * g.wscale_n[n + 3];
+                *(float4*)(ot + (wm * 16 + lrow) * OLD + wn * 64 + ti * 16 + 4 * lgrp) = v;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int c = tid + 256 * i;
+                const int row = c >> 5, col = 4 * (c & 31);  // staged row = wm * 16 + lrow
+                const float4 v = *(const float4*)(ot + row * OLD + col);
+                const f4v t = {v.x, v.y, v.z, v.w};
+                float* dst = out0 + (long long)((row >> 4) * 32 + tj * 16 + (row & 15)) * g.ldo + col;
+                asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1 nt" ::"v"(dst), "v"(t) : "memory");
+            }
+            __syncthreads();  // the staged half is read before the next one is written
+        }
+        return;
+    }
 #pragma unroll
     for (int tj = 0; tj < 2; tj++) {
         const int m = m0 + wm * 32 + tj * 16 + lrow;

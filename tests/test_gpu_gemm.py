@@ -57,3 +57,14 @@ def test_gemm_config2_full():
     colsum = acc.astype(np.int64).sum(axis=0)
     want = A.astype(np.int64).sum(axis=0) @ W.astype(np.int64).T
     assert np.array_equal(colsum, want)
+
+
+@pytest.mark.parametrize("M,K,N", [(1000, 384, 512), (256, 64, 130), (128, 1152, 256)])
+def test_gemm_fp32_only(M, K, N):
+    """Without the int32 output, whole 64 x 128 tiles leave through LDS as row segments (the config-2
+    bench's call); partial tiles (the last rows, the last channels) take the direct stores. Both
+    bit-exact."""
+    A, W, s = _operands(M, K, N, 17 + M + N)
+    C = gemm_i8(A, W, s)
+    Cr, _ = O.gemm_i8_exact(A, W, s)
+    assert np.array_equal(C.view(np.uint32), Cr.view(np.uint32))
