@@ -95,8 +95,9 @@ __device__ __forceinline__ void stg_put(float* stg, int lane, int ti, const floa
 // Rows mt0..mt0+15, channels n0 + [0, 128) of `out` (row stride ldo) from the staged tile, as whole
 // 512-byte row segments. Store kinds: ST_PLAIN; ST_NT non-temporal, for outputs far larger than the L2
 // that the next kernel reads back from memory in any case; ST_STREAM non-temporal with both coherence
-// scope bits set (sc0 sc1 nt), for a final output no kernel reads again (measured on the probabilities
-// GEMM: 21.0 ms per c5 step against 22.0 with ST_NT and 23.7 with ST_PLAIN).
+// scope bits set (sc0 sc1 nt). Chosen per output by measurement: the probabilities take ST_STREAM (21.0 ms
+// per c5 step against 22.0 with ST_NT and 23.7 with ST_PLAIN); the logits (0.291 ms per c3 launch
+// against 0.308 with ST_STREAM) and the config-2 GEMM take ST_NT.
 enum StoreKind : int { ST_PLAIN = 0, ST_NT = 1, ST_STREAM = 2 };
 
 template <int SK = ST_PLAIN>
@@ -366,7 +367,7 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
             dst[0] = bmax; dst[1] = bsum; dst[2] = __int_as_float(bidx);
         }
         if constexpr (STG) {
-            if (orow) stg_flush<ST_STREAM>(g, stg, lane, mt0, n0, g.out, g.ldo);
+            if (orow) stg_flush<ST_NT>(g, stg, lane, mt0, n0, g.out, g.ldo);
         }
     }
 }
