@@ -25,6 +25,14 @@ namespace {
 // which is then written out with 16-byte stores.
 // ------------------------------------------------------------------------------------------------
 constexpr int ROW_TILE = 16;
+// The row and scan kernels' outputs (normalised rows, limb fragments) are far larger than the caches at
+// the sizes that matter and are read back by the next kernel from memory in any case: non-temporal
+// stores (c5: latch scan 11.59 -> 11.32 ms per step, row kernels 31.1 -> 30.9).
+__device__ __forceinline__ void nt_store4(float* dst, float4 v) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4 t = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(t, (f4*)dst);
+}
 // LDS staging of one 16-row tile in the fragment layout: each 1 KiB fragment padded to 1088 bytes and
 // each 256-byte column group inside it to 272, so that a wave's dword writes of one row spread over
 // the banks.
@@ -247,7 +255,7 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
 #pragma unroll
                 for (int i = 0; i < NS4; i++) {
                     const int c = lane + 64 * i;
-                    if (c < C4) *(float4*)(a.nout + (long long)m * Dp + 4 * c) = x[j][i];
+                    if (c < C4) nt_store4(a.nout + (long long)m * Dp + 4 * c, x[j][i]);
                 }
             }
             if (a.limbs) {
@@ -280,7 +288,8 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
         __syncthreads();
         const int bytes = 3 * Dp * ROW_TILE;  // Dp/64 K steps x 3 limbs x 1 KiB
         int8_t* dst = a.limbs + (long long)blockIdx.x * bytes;
-        for (int o = threadIdx.x * 16; o < bytes; o += 256 * 16) *(v4i*)(dst + o) = *(const v4i*)(stage + stage_off(o));
+        for (int o = threadIdx.x * 16; o < bytes; o += 256 * 16)
+            __builtin_nontemporal_store(*(const v4i*)(stage + stage_off(o)), (v4i*)(dst + o));
     }
 }
 
@@ -494,7 +503,7 @@ __global__ __launch_bounds__(512) void scan_rule_kernel(ScanArgs a) {
             }
             __syncthreads();
             for (int o = j * 16; o < seg_bytes; o += blockDim.x * 16)
-                *(v4i*)(dst + sg * seg_bytes + o) = *(const v4i*)(stage + stage_off(o));
+                __builtin_nontemporal_store(*(const v4i*)(stage + stage_off(o)), (v4i*)(dst + sg * seg_bytes + o));
             __syncthreads();
         };
         segment(nv, 0);
