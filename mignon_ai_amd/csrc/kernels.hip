@@ -802,6 +802,43 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 // over all banks instead of two.
 __device__ __forceinline__ int vswz(int r) { return 4 * ((r >> 3) & 3); }
 
+// S^T for key blocks SKIP..NKB-1 of one wave; the SKIP leading blocks hold only keys before the
+// sequence start (masked in the softmax), so their scores stay zero and no MFMA is spent on them.
+template <int ND, int NKB, int KS, int SKIP>
+__device__ __forceinline__ void attn_scores(v4f (&s)[NKB], const float* att_lds, int w, int qi, int kg,
+                                            const v4f (&qv)[ND]) {
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++) {
+        s[kb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        if (kb < SKIP) continue;
+#pragma unroll
+        for (int g = 0; g < ND; g++) {
+            const v4f kv = *(const v4f*)(att_lds + (16 * (w + kb) + qi) * KS + 16 * g + 4 * kg);
+#pragma unroll
+            for (int e = 0; e < 4; e++) s[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[e], qv[g][e], s[kb], 0, 0, 0);
+        }
+    }
+}
+
+// out = P V over key blocks SKIP..NKB-1 (the skipped blocks' probabilities are zero: leaving them out
+// adds nothing, bit for bit).
+template <int ND, int NKB, int VS, int SKIP>
+__device__ __forceinline__ void attn_pv(v4f (&o)[ND], const v4f (&s)[NKB], float inv, const float* att_lds, int w,
+                                        int qi, int kg) {
+#pragma unroll
+    for (int g = 0; g < ND; g++) o[g] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++) {
+        if (kb < SKIP) continue;
+#pragma unroll
+        for (int g = 0; g < ND; g++) {
+            const v4f vv = *(const v4f*)(att_lds + (16 * g + qi) * VS + ((16 * (w + kb) + 4 * kg) ^ vswz(16 * g + qi)));
+#pragma unroll
+            for (int r = 0; r < 4; r++) o[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(s[kb][r] * inv, vv[r], o[g], 0, 0, 0);
+        }
+    }
+}
+
 // Windowed causal attention on the fp32 matrix cores. A workgroup is G waves; wave w takes the 16
 // queries of tile G*grp + w for head blockIdx.y. The 16*(NKB+G-1) keys the G tiles attend are staged in
 // LDS once: keys first (row-major), then, over the same buffer, values transposed, so that every matrix
@@ -870,17 +907,21 @@ __global__ __launch_bounds__(64 * G) void attention_mfma_kernel(AttnArgs a, int 
         }
     }
     __syncthreads();
-    // s[kb][r] = q.k for query t0 + qi and key kbase + 16(w + kb) + 4kg + r
+    // s[kb][r] = q.k for query t0 + qi and key kbase + 16(w + kb) + 4kg + r. The leading blocks whose keys
+    // all lie before the sequence start (the first tiles of a sequence) are skipped; the count is
+    // uniform per wave and selects one of a few unrolled variants (more than 4 such blocks: 4 skipped).
+    int skip = 0;
+#pragma unroll
+    for (int kb = 0; kb < NKB - 1; kb++)
+        if (kbase + 16 * (w + kb) + 15 < 0) skip = kb + 1;
+    skip = min(skip, 4);
     v4f s[NKB];
-#pragma unroll
-    for (int kb = 0; kb < NKB; kb++) {
-        s[kb] = zero4;
-#pragma unroll
-        for (int g = 0; g < ND; g++) {
-            const v4f kv = *(const v4f*)(att_lds + (16 * (w + kb) + qi) * KS + 16 * g + 4 * kg);
-#pragma unroll
-            for (int e = 0; e < 4; e++) s[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[e], qv[g][e], s[kb], 0, 0, 0);
-        }
+    switch (skip) {
+        case 0: attn_scores<ND, NKB, KS, 0>(s, att_lds, w, qi, kg, qv); break;
+        case 1: attn_scores<ND, NKB, KS, 1>(s, att_lds, w, qi, kg, qv); break;
+        case 2: attn_scores<ND, NKB, KS, 2>(s, att_lds, w, qi, kg, qv); break;
+        case 3: attn_scores<ND, NKB, KS, 3>(s, att_lds, w, qi, kg, qv); break;
+        default: attn_scores<ND, NKB, KS, 4>(s, att_lds, w, qi, kg, qv); break;
     }
     __syncthreads();  // every wave's keys are read: the buffer takes the values
 #pragma unroll
@@ -923,16 +964,13 @@ __global__ __launch_bounds__(64 * G) void attention_mfma_kernel(AttnArgs a, int 
     __syncthreads();
     // out = P V: A = P (query qi, key jb + 4kg + r), B = V (key jb + 4kg + r, dim 16g + qi)
     v4f o[ND];
-#pragma unroll
-    for (int g = 0; g < ND; g++) o[g] = zero4;
-#pragma unroll
-    for (int kb = 0; kb < NKB; kb++)
-#pragma unroll
-        for (int g = 0; g < ND; g++) {
-            const v4f vv = *(const v4f*)(att_lds + (16 * g + qi) * VS + ((16 * (w + kb) + 4 * kg) ^ vswz(16 * g + qi)));
-#pragma unroll
-            for (int r = 0; r < 4; r++) o[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(s[kb][r] * inv, vv[r], o[g], 0, 0, 0);
-        }
+    switch (skip) {
+        case 0: attn_pv<ND, NKB, VS, 0>(o, s, inv, att_lds, w, qi, kg); break;
+        case 1: attn_pv<ND, NKB, VS, 1>(o, s, inv, att_lds, w, qi, kg); break;
+        case 2: attn_pv<ND, NKB, VS, 2>(o, s, inv, att_lds, w, qi, kg); break;
+        case 3: attn_pv<ND, NKB, VS, 3>(o, s, inv, att_lds, w, qi, kg); break;
+        default: attn_pv<ND, NKB, VS, 4>(o, s, inv, att_lds, w, qi, kg); break;
+    }
     if (tile >= qtiles) return;
     // o[g][r] = out[query t0 + 4kg + r][dim 16g + qi]
 #pragma unroll
