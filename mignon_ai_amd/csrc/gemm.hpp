@@ -73,9 +73,11 @@ struct GemmArgs {
 
 // Values of OPT_GEMM_KERNEL.
 enum GemmKernel : int { GEMM_AUTO = 0, GEMM_STREAM = 1, GEMM_SLAB = 2 };
-// Token rows from which the weight-stationary kernel is used when its slab fits in LDS (c4's decode
-// steps of 4096 rows: 41.2 ms per step with it against 43.3 with the streaming kernel).
-constexpr int kSlabMinRows = 2048;
+// Token rows from which the weight-stationary kernel is used when its slab fits in LDS: from 8192 rows
+// always, from 2048 rows when K is at least 256 (c4's decode steps of 4096 rows: 41.2 ms per step with
+// it against 43.3 with the streaming kernel; the chat model's K = 128 GEMMs stay faster streaming).
+constexpr int kSlabMinRows = 8192;
+constexpr int kSlabMinRowsWideK = 2048;
 // Largest dynamic LDS allocation of one workgroup on the current device (bytes).
 int slab_lds_limit();
 
