@@ -252,14 +252,6 @@ std::vector<float> latch_base_logits(int D) {
     return base;
 }
 
-// Head widths with a compiled attention kernel (kernels.hip, DH_SWITCH).
-bool attention_width_supported(int dh) {
-    static const int widths[] = {1, 2, 4, 8, 12, 16, 20, 24, 32, 40, 48, 64, 80, 96, 128};
-    for (int w : widths)
-        if (w == dh) return true;
-    return false;
-}
-
 void build_device_model(mg_model* m, const HostModel& hm, int max_context) {
     const int V = hm.V, D = hm.D, H = hm.H;
     m->V = V; m->D = D; m->H = H;
@@ -359,10 +351,11 @@ void build_device_model(mg_model* m, const HostModel& hm, int max_context) {
     }
     if (m->nattn > 0) {
         if (m->heads <= 0 || D % m->heads) throw Error(MG_ERR_FORMAT, "model file: attention heads must divide the state size");
-        int dh = D / m->heads;
-        if (!attention_width_supported(dh))
-            throw Error(MG_ERR_UNSUPPORTED, "attention head width " + std::to_string(dh) + " is not compiled");
-        if (m->cap > 256) throw Error(MG_ERR_UNSUPPORTED, "attention cache above 256 positions is not supported");
+        // every head width up to kMaxHeadWidth runs (the state size is at most 1024); the fallback attention
+        // kernel keeps a query's scores in LDS, which bounds the cache
+        if (m->cap > kMaxAttnSpan)
+            throw Error(MG_ERR_UNSUPPORTED, "attention cache of " + std::to_string(m->cap) + " positions is above the " +
+                                                std::to_string(kMaxAttnSpan) + " supported");
     }
 }
 

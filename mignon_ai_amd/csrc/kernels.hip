@@ -1274,6 +1274,184 @@ __global__ __launch_bounds__(64) void attention_step_lds_kernel(AttnStepArgs a) 
 }
 
 // ------------------------------------------------------------------------------------------------
+// Attention of any head width and any span (the fallback where no kernel above applies): one wave
+// per (row, head), batched rows reading their keys and values from the QKV rows of their sequence,
+// decode rows from their ring. Bit-identical to the reference order, like the kernels above:
+//   - Scores. DotF32's sixteen accumulator chains (vec_amd64.s:4-63) run on the sixteen lanes of a
+//     group, one key per group and four keys per wave step: lane u takes elements 16c + u of every
+//     16-chunk (u < 8 accumulator 0, u >= 8 accumulator 1) and, for u < 8, the trailing 8-chunk.
+//     The fold (a0 + a1, the high half onto the low, then the two shuffles) is the same additions
+//     through shuffles, and lane 0 of the group adds the unfused tail products in element order.
+//   - Softmax. Scores in LDS; max over the wave, FastExp, the sum in index order by one lane.
+//   - P.V. Lane i accumulates output elements i, i + 64, ... over the keys in order (AddScaledF32:
+//     fused inside the 16- and 8-chunks, unfused in the tail).
+// Keys and values pass through LDS in chunks of at most kWaveStage floats, all of a chunk's loads
+// issued before its first store.
+// ------------------------------------------------------------------------------------------------
+constexpr int kWaveStage = 4096;  // floats of one staged chunk of key or value rows
+
+__host__ __device__ inline int wave_chunk_keys(int dh) {
+    const int k = kWaveStage / dh / 4 * 4;
+    return k < 4 ? 4 : (k > 256 ? 256 : k);
+}
+
+// Copies rows j0 .. j0+nk-1 (dh floats each, rowp(j) gives row j) to stage[(j - j0)*dh ..]. nk*dh
+// is at most kWaveStage, so a lane moves at most 64 floats.
+template <class RowFn>
+__device__ __forceinline__ void wave_stage(float* stage, const RowFn& rowp, int j0, int nk, int dh, int lane) {
+    const int n = nk * dh;
+    const float inv_dh = 1.0f / (float)dh;
+    for (int e0 = 0; e0 < n; e0 += 16 * 64) {
+        float buf[16];
+        int off[16];
+#pragma unroll
+        for (int t = 0; t < 16; t++) {
+            const int e = min(e0 + t * 64 + lane, n - 1);  // lanes past the end repeat the last element
+            int key = (int)(((float)e + 0.5f) * inv_dh);   // e < 4096: one correction step suffices
+            if (key * dh > e) key--;
+            else if ((key + 1) * dh <= e) key++;
+            buf[t] = rowp(j0 + key)[e - key * dh];
+            off[t] = e;
+        }
+#pragma unroll
+        for (int t = 0; t < 16; t++) stage[off[t]] = buf[t];
+    }
+}
+
+// LDS floats of attention_wave_kernel for spans of at most `span` keys.
+__host__ __device__ inline int wave_lds_floats(int span) { return kWaveStage + span; }
+
+// NC = 16-element chunk slots per lane: dh <= 16*NC.
+template <int NC>
+__global__ __launch_bounds__(64) void attention_wave_kernel(AttnWaveArgs a) {
+    constexpr int NO = (NC + 3) / 4;  // output elements per lane
+    extern __shared__ __align__(16) float wv_smem[];
+    float* stage = wv_smem;            // [kWaveStage]
+    float* sc = wv_smem + kWaveStage;  // [span]
+    const int row = blockIdx.x, h = blockIdx.y;
+    const int lane = threadIdx.x, u = lane & 15, grp = lane >> 4;
+    const int dh = a.dh, D = a.D, cap = a.cap;
+    int pos;
+    long long seq0 = 0;  // batched: first row of the sequence
+    if (a.step) {
+        pos = a.pos[row];
+    } else {
+        const int b = row / a.T;
+        pos = row - b * a.T;
+        seq0 = (long long)b * a.T;
+    }
+    const int lo = max(window_start(pos, a.window), pos - cap + 1);
+    const int span = pos - lo + 1;
+    const float* qrow = a.qkv + (long long)row * 3 * D + h * dh;
+    const long long ring0 = ((long long)row * a.heads + h) * cap;
+    auto krow = [&](int j) -> const float* {
+        if (a.step) return j == pos ? qrow + D : a.kring + (ring0 + j % cap) * dh;
+        return a.qkv + (seq0 + j) * 3 * D + D + h * dh;
+    };
+    auto vrow = [&](int j) -> const float* {
+        if (a.step) return j == pos ? qrow + 2 * D : a.vring + (ring0 + j % cap) * dh;
+        return a.qkv + (seq0 + j) * 3 * D + 2 * D + h * dh;
+    };
+    const int n16 = dh >> 4;
+    const bool has8 = (dh & 15) >= 8;
+    const int t0 = (has8 ? 8 : 0), ntail = dh - 16 * n16 - t0;  // tail lanes t0 .. t0+ntail-1 of slot n16
+    float qr[NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) qr[c] = (16 * c + u < dh) ? qrow[16 * c + u] : 0.0f;
+    const float scale = (float)(1.0 / sqrt((double)dh));
+    const int KC = wave_chunk_keys(dh);
+
+    float mx = -3.40282347e38f;
+    for (int c0 = 0; c0 < span; c0 += KC) {
+        const int nk = min(KC, span - c0);
+        wave_stage(stage, krow, lo + c0, nk, dh, lane);
+        wave_lds_sync();
+        for (int k4 = 0; k4 < nk; k4 += 4) {
+            const int kk = min(k4 + grp, nk - 1);
+            const float* kr = stage + kk * dh;
+            float acc = 0.0f, tailp = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                if (c < n16) acc = fmaf(qr[c], kr[16 * c + u], acc);
+                if (c == n16) {
+                    const float kv = kr[min(16 * c + u, dh - 1)];
+                    if (has8 && u < 8) acc = fmaf(qr[c], kv, acc);
+                    tailp = qr[c] * kv;
+                }
+            }
+            float v = acc + __shfl_xor(acc, 8, 16);
+            v = v + __shfl_xor(v, 4, 16);
+            v = v + __shfl_xor(v, 2, 16);
+            float s = v + __shfl_xor(v, 1, 16);
+            for (int t = 0; t < ntail; t++) {
+                const float p = __shfl(tailp, t0 + t, 16);
+                s = s + p;
+            }
+            s = s * scale;
+            if (u == 0 && k4 + grp < nk) {
+                sc[c0 + k4 + grp] = s;
+                mx = fmaxf(mx, s);
+            }
+        }
+        wave_lds_sync();  // the stage is rewritten by the next chunk
+    }
+    // nn.SoftmaxInPlaceF32 (internal/nn/head.go:91-112)
+    mx = wave_max(mx);
+    for (int jj = lane; jj < span; jj += 64) sc[jj] = fast_exp_ref(sc[jj] - mx);
+    wave_lds_sync();
+    float inv = 0.0f;
+    if (lane == 0) {
+        float sum = 0.0f;
+#pragma unroll 8
+        for (int jj = 0; jj < span; jj++) sum += sc[jj];
+        inv = 1.0f / sum;
+    }
+    inv = __shfl(inv, 0, 64);
+
+    const int fused = dh / 8 * 8;
+    float o[NO];
+#pragma unroll
+    for (int r = 0; r < NO; r++) o[r] = 0.0f;
+    for (int c0 = 0; c0 < span; c0 += KC) {
+        const int nk = min(KC, span - c0);
+        wave_stage(stage, vrow, lo + c0, nk, dh, lane);
+        wave_lds_sync();
+        for (int kk = 0; kk < nk; kk++) {
+            const float p = sc[c0 + kk] * inv;
+            const float* vr = stage + kk * dh;
+#pragma unroll
+            for (int r = 0; r < NO; r++) {
+                const int i = lane + 64 * r;
+                if (i < dh) {
+                    const float x = vr[i];
+                    if (i < fused) {
+                        o[r] = fmaf(p, x, o[r]);
+                    } else {
+                        const float t = x * p;
+                        o[r] = t + o[r];
+                    }
+                }
+            }
+        }
+        wave_lds_sync();
+    }
+    float* dst = a.att + (long long)row * a.Dp + h * dh;
+#pragma unroll
+    for (int r = 0; r < NO; r++) {
+        const int i = lane + 64 * r;
+        if (i < dh) dst[i] = o[r];
+    }
+    if (a.step) {  // record this position's key and value (slot pos % cap lies outside the window)
+        float* kw = a.kring + (ring0 + pos % cap) * dh;
+        float* vw = a.vring + (ring0 + pos % cap) * dh;
+        for (int i = lane; i < dh; i += 64) {
+            kw[i] = qrow[D + i];
+            vw[i] = qrow[2 * D + i];
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
 // Head statistics, log-probs, bits
 // ------------------------------------------------------------------------------------------------
 // Per-row softmax statistics from the logits GEMM's per-tile (max, sum exp(l - max), first argmax).
@@ -1404,11 +1582,20 @@ __global__ void fill_f32_kernel(float* p, long long n, float v) {
         p[i] = v;
 }
 
+// LDS bytes of attention_kernel: the staged rows of a 64-query tile's window and the scores.
+size_t attn_exact_lds(const AttnArgs& a, int dh) {
+    const int stride = dh % 4 == 0 ? dh + 4 : dh + 1;
+    return (size_t)((ATT_QT + a.cap - 1) * stride + a.cap * 64) * sizeof(float);
+}
+
 template <int DH>
 hipError_t attn_t(const AttnArgs& a, hipStream_t s) {
     const int nqt = (a.T + ATT_QT - 1) / ATT_QT;
-    size_t lds = (size_t)((ATT_QT + a.cap - 1) * att_stride<DH>() + a.cap * 64) * sizeof(float);
+    const size_t lds = attn_exact_lds(a, DH);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
+    static const hipError_t attr = hipFuncSetAttribute((const void*)attention_kernel<DH>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return attr;
     hipLaunchKernelGGL(attention_kernel<DH>, dim3(a.B * nqt, a.heads), dim3(64), lds, s, a);
     return hipGetLastError();
 }
@@ -1434,17 +1621,21 @@ hipError_t attn_mfma_t(const AttnArgs& a, int dh, hipStream_t s) {
 }
 
 // Key blocks per 16-query tile: the widest span any query attends is W = min(window, cap) keys, so the
-// tile's keys fit in 1 + ceil((W - 1)/16) blocks of 16. The kernel keeps every block's keys and values
-// in registers, so it runs where ND*NKB <= 20 (head width up to 64 with spans up to 64 keys, narrower
-// heads with longer spans); other shapes take the reference-order kernel.
+// tile's keys fit in 1 + ceil((W - 1)/16) blocks of 16 (at most 17 variants' worth: spans up to 257
+// keys). The kernel keeps every block's scores in registers, so it runs where ND*NKB <= 20 (head width up
+// to 64 with spans up to 64 keys, narrower heads with longer spans) and for widths 68..128 with spans up
+// to 64 keys; other shapes take the reference-order kernels.
 int attn_mfma_blocks(const AttnArgs& a) {
     const int W = a.window > 0 ? std::min(a.window, a.cap) : a.cap;
     const int nkb = 1 + (W - 1 + 15) / 16;
-    return nkb <= 3 ? 3 : nkb <= 5 ? 5 : nkb <= 9 ? 9 : 17;
+    return nkb <= 3 ? 3 : nkb <= 5 ? 5 : nkb <= 9 ? 9 : nkb <= 17 ? 17 : 0;  // 0: longer than any variant
 }
-int attn_mfma_nd(int dh) { return dh <= 16 ? 1 : dh <= 32 ? 2 : 4; }
+int attn_mfma_nd(int dh) { return dh <= 16 ? 1 : dh <= 32 ? 2 : dh <= 64 ? 4 : dh <= 80 ? 5 : dh <= 96 ? 6 : 8; }
 bool attn_mfma_fits(const AttnArgs& a, int dh) {
-    return dh % 4 == 0 && dh <= 64 && attn_mfma_nd(dh) * attn_mfma_blocks(a) <= 20;
+    if (dh % 4 || dh > 128) return false;
+    const int nd = attn_mfma_nd(dh), nkb = attn_mfma_blocks(a);
+    if (nkb == 0) return false;
+    return nd <= 4 ? nd * nkb <= 20 : nkb <= 5;  // widths past 64: windows of up to 64 keys
 }
 
 hipError_t attn_mfma(const AttnArgs& a, int dh, hipStream_t s) {
@@ -1458,6 +1649,12 @@ hipError_t attn_mfma(const AttnArgs& a, int dh, hipStream_t s) {
         case 209: return attn_mfma_t<2, 9>(a, dh, s);
         case 403: return attn_mfma_t<4, 3>(a, dh, s);
         case 405: return attn_mfma_t<4, 5>(a, dh, s);
+        case 503: return attn_mfma_t<5, 3>(a, dh, s);
+        case 505: return attn_mfma_t<5, 5>(a, dh, s);
+        case 603: return attn_mfma_t<6, 3>(a, dh, s);
+        case 605: return attn_mfma_t<6, 5>(a, dh, s);
+        case 803: return attn_mfma_t<8, 3>(a, dh, s);
+        case 805: return attn_mfma_t<8, 5>(a, dh, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -1577,13 +1774,26 @@ hipError_t launch_latch_step(const LatchStepArgs& a, hipStream_t s) {
         default: return hipErrorInvalidValue; \
     }
 
+// Head widths with instantiated width-specific kernels (DH_SWITCH).
+bool dh_compiled(int dh) {
+    switch (dh) {
+        case 1: case 2: case 4: case 8: case 12: case 16: case 20: case 24: case 32: case 40: case 48: case 64:
+        case 80: case 96: case 128: return true;
+        default: return false;
+    }
+}
+
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
     if (a.B <= 0 || a.T <= 0) return hipSuccess;
-    if (a.heads <= 0 || a.D % a.heads || a.cap <= 0 || a.cap > 256) return hipErrorInvalidValue;
+    if (a.heads <= 0 || a.D % a.heads || a.cap <= 0) return hipErrorInvalidValue;
     const int dh = a.D / a.heads;
     const int mode = option(OPT_ATTENTION_KERNEL);
     if (mode != ATTN_EXACT && attn_mfma_fits(a, dh)) return attn_mfma(a, dh, s);
-    DH_SWITCH(dh, attn_t, a, s)
+    if (dh_compiled(dh) && attn_exact_lds(a, dh) <= 160 * 1024) DH_SWITCH(dh, attn_t, a, s)
+    AttnWaveArgs w;
+    w.rows = a.B * a.T; w.T = a.T; w.D = a.D; w.Dp = a.Dp; w.heads = a.heads; w.dh = dh;
+    w.window = a.window; w.cap = a.cap; w.qkv = a.qkv; w.att = a.att;
+    return launch_attention_wave(w, s);
 }
 
 bool attention_step_rows_fits(const AttnStepArgs& a) {
@@ -1605,8 +1815,42 @@ hipError_t launch_attention_step_rows(const AttnStepArgs& a, hipStream_t s) {
 
 hipError_t launch_attention_step(const AttnStepArgs& a, hipStream_t s) {
     if (a.S <= 0) return hipSuccess;
-    if (a.heads <= 0 || a.D % a.heads || a.cap <= 0 || a.cap > 256) return hipErrorInvalidValue;
-    DH_SWITCH(a.D / a.heads, attn_step_t, a, s)
+    if (a.heads <= 0 || a.D % a.heads || a.cap <= 0) return hipErrorInvalidValue;
+    const int dh = a.D / a.heads;
+    if (dh_compiled(dh) && a.cap <= 256) DH_SWITCH(dh, attn_step_t, a, s)
+    AttnWaveArgs w;
+    w.rows = a.S; w.D = a.D; w.Dp = a.Dp; w.heads = a.heads; w.dh = dh; w.window = a.window; w.cap = a.cap;
+    w.step = true; w.qkv = a.qkv; w.pos = a.pos; w.kring = a.kring; w.vring = a.vring; w.att = a.att;
+    return launch_attention_wave(w, s);
+}
+
+template <int NC>
+hipError_t attn_wave_t(const AttnWaveArgs& a, int span_max, hipStream_t s) {
+    const size_t lds = (size_t)wave_lds_floats(span_max) * sizeof(float);
+    static const hipError_t attr = hipFuncSetAttribute((const void*)attention_wave_kernel<NC>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL(attention_wave_kernel<NC>, dim3(a.rows, a.heads), dim3(64), lds, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_wave(const AttnWaveArgs& a, hipStream_t s) {
+    if (a.rows <= 0) return hipSuccess;
+    if (a.heads <= 0 || a.dh <= 0 || a.dh > kMaxHeadWidth || a.D != a.heads * a.dh || a.cap <= 0 || a.T <= 0)
+        return hipErrorInvalidValue;
+    if (a.step ? (!a.pos || !a.kring || !a.vring) : a.rows % a.T) return hipErrorInvalidValue;
+    // the widest span a query attends: min(window, cap) keys, and at most T in a batch
+    int span_max = a.window > 0 ? std::min(a.window, a.cap) : a.cap;
+    if (!a.step) span_max = std::min(span_max, a.T);
+    if (span_max > kMaxAttnSpan) return hipErrorInvalidValue;
+    const int nc = (a.dh + 15) / 16;
+    if (nc <= 1) return attn_wave_t<1>(a, span_max, s);
+    if (nc <= 2) return attn_wave_t<2>(a, span_max, s);
+    if (nc <= 4) return attn_wave_t<4>(a, span_max, s);
+    if (nc <= 8) return attn_wave_t<8>(a, span_max, s);
+    if (nc <= 16) return attn_wave_t<16>(a, span_max, s);
+    if (nc <= 32) return attn_wave_t<32>(a, span_max, s);
+    return attn_wave_t<64>(a, span_max, s);
 }
 
 hipError_t launch_head_combine(const HeadCombineArgs& a, hipStream_t s) {

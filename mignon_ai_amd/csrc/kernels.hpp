@@ -93,6 +93,25 @@ constexpr size_t kStepRowsMaxLds = 156 * 1024;  // dynamic LDS; the static part 
 bool attention_step_rows_fits(const AttnStepArgs& a);
 hipError_t launch_attention_step_rows(const AttnStepArgs& a, hipStream_t s);
 
+// Attention of any head width and span, one wave per (row, head): the fallback of launch_attention and
+// launch_attention_step where no specialised kernel applies (same results, reference order).
+struct AttnWaveArgs {
+    int rows = 0;   // batched: B*T; decode: sessions
+    int T = 1;      // batched: positions per sequence
+    int D = 0, Dp = 0, heads = 0, dh = 0, window = 0, cap = 0;
+    bool step = false;             // decode: keys and values from the rings, position pos[row]
+    const float* qkv = nullptr;    // [rows][3D]
+    const int32_t* pos = nullptr;  // decode [S]
+    float* kring = nullptr;        // decode [S][heads][cap][dh]
+    float* vring = nullptr;
+    float* att = nullptr;          // [rows][Dp]
+};
+// Longest span (keys per query) the fallback kernel takes: its scores live in LDS.
+constexpr int kMaxAttnSpan = 32768;
+// Largest head width of any attention kernel.
+constexpr int kMaxHeadWidth = 1024;
+hipError_t launch_attention_wave(const AttnWaveArgs& a, hipStream_t s);
+
 // Per-row combination of the head GEMM's per-tile statistics.
 struct HeadCombineArgs {
     int M = 0, ntiles = 0;
