@@ -43,7 +43,7 @@ sys.path.insert(0, ROOT)
 METRIC = "INT8 tokens/sec (batched forward + decode); % of int8-MFMA / HBM roofline"
 PEAK_MFMA_TOPS = 5000.0   # MI355X dense int8 MFMA, TOP/s
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, GB/s
-# What back-to-back independent int8 MFMAs sustain on this part (mignon_ai_amd/_build/calib_mfma, the
+# What back-to-back independent int8 MFMAs sustain on this part (calib_mfma.hip, the
 # median of the runs recorded in profiles/mfma_ceiling.md): the clock under full matrix-core load stays
 # below the one the published peak assumes.
 SUSTAINED_MFMA_TOPS = 4015.0

@@ -1,6 +1,6 @@
 """Plain device-to-device copy of a known size: the calibration kernel for HBM traffic counters.
 
-    python -m mignon_ai_amd.calib_copy --mib 1024 --reps 4
+    python calib_copy.py --mib 1024 --reps 4
 
 Under `rocprofv3 --pmc FETCH_SIZE` (then `--pmc WRITE_SIZE`) each copy dispatch must read and write
 exactly mib MiB; the ratio of the counter to that size is the factor by which the same counters of the

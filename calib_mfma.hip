@@ -3,7 +3,8 @@
 // register operands (no memory traffic but one checksum store per lane), enough waves to fill every
 // SIMD several times over.
 //
-//     mignon_ai_amd/_build/calib_mfma [iterations]
+//     hipcc --offload-arch=gfx950 -O3 -std=c++17 -Xclang -target-feature -Xclang -packed-fp32-ops \
+//         calib_mfma.hip -o gpurun_out/calib_mfma && gpurun_out/calib_mfma [iterations]
 //
 // Prints the achieved TOP/s (2 ops per multiply-accumulate) of three timed launches.
 #include <hip/hip_runtime.h>

@@ -78,6 +78,16 @@ typedef struct {
 } mg_kernel_time_t;
 int mg_model_profile(mg_model* m, int on);
 int mg_model_profile_read(mg_model* m, mg_kernel_time_t* out, int max);
+
+/* Cancellation: generate's Cancel hook, checked before each token (internal/generate/greedy.go:29,68-70,
+ * internal/generate/sample.go:204-206), which pkg/infer.Generate wires to its context
+ * (pkg/infer/infer.go:73-95). flag is caller-owned memory (NULL removes it) that any thread may set at any
+ * time, also while a call on m runs; this call takes no lock. While *flag is nonzero, a batched decode on
+ * m (mg_sessions_decode_greedy_until, mg_sessions_decode_sample, mg_generate_greedy, mg_generate_sample)
+ * enqueues no further token: every reply is cut before the first column not yet started, and the call
+ * returns MG_OK with out_counts giving the lengths of the replies produced so far. A flag already set when
+ * the call starts gives empty replies (after the prefill, as the reference's loop). */
+int mg_model_set_cancel(mg_model* m, const volatile int32_t* flag);
 int mg_model_sync(mg_model* m);
 void mg_model_free(mg_model* m);
 
@@ -165,7 +175,8 @@ void mg_sessions_free(mg_sessions* s);
  * tokens[offsets[q] .. offsets[q+1]); each of its targets t = 1..len-1 is scored from
  * window(seq[:t], context) (then Call's truncation to max_context), as log-softmax of seq[t].
  * logprob receives, sequence after sequence, max(len-1, 0) fp32 values; NaN marks a target that is not
- * scored (id outside [0, V), or context <= 0). offsets has n_seq+1 entries. Host pointers. */
+ * scored (id outside [0, V), or context 0). A negative context is MG_ERR_INVALID (the reference's window()
+ * panics on it). offsets has n_seq+1 entries. Host pointers. */
 int mg_score_sequences(mg_model* m, const int32_t* tokens, const long long* offsets, int n_seq, int context,
                        float* logprob);
 

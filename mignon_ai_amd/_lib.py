@@ -62,6 +62,7 @@ SIGNATURES = {
     "mg_model_set_stream": (_int, [_vp, _vp]),
     "mg_model_stream": (_vp, [_vp]),
     "mg_model_sync": (_int, [_vp]),
+    "mg_model_set_cancel": (_int, [_vp, _vp]),
     "mg_model_profile": (_int, [_vp, _int]),
     "mg_model_profile_read": (_int, [_vp, _vp, _int]),
     "mg_model_free": (None, [_vp]),

@@ -49,14 +49,6 @@ def build(verbose: bool = False) -> str:
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError("hipcc link failed")
     os.replace(tmp, LIB)
-    # the matrix-core ceiling probe (a standalone program, not part of the library)
-    probe = os.path.join(OUT_DIR, "calib_mfma")
-    cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
-           "-packed-fp32-ops", os.path.join(CSRC, "calib_mfma.hip"), "-o", probe]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        sys.stderr.write(r.stdout + r.stderr)
-        raise RuntimeError("hipcc failed on calib_mfma.hip")
     return LIB
 
 

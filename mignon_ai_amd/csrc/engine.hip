@@ -188,6 +188,8 @@ struct mg_model {
     float* latch_base = nullptr;
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
+    // caller-owned cancellation flag polled by batched decodes (mg_model_set_cancel); set without the lock
+    std::atomic<const volatile int32_t*> cancel{nullptr};
     mg::Workspace ws;
     mg::Profile prof;
     std::mutex mu;
@@ -486,9 +488,11 @@ __global__ void stop_scan_kernel(int S, int col, const int32_t* ids, int ld, Sto
     }
 }
 
-__global__ void stop_finish_kernel(int S, int max_tokens, int32_t* count) {
+// Sessions without a stop token among the produced columns 0..cut-1 get reply length cut (max_tokens, or
+// the column before which a cancellation stopped the decode).
+__global__ void stop_finish_kernel(int S, int cut, int32_t* count) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < S && count[i] < 0) count[i] = max_tokens;
+    if (i < S && (count[i] < 0 || count[i] > cut)) count[i] = cut;
 }
 
 // Scoring windows: row r of a [B][T] token matrix is tokens[start[r] .. start[r] + len[r]), padded with id 0
@@ -718,11 +722,15 @@ constexpr long long kMaxChunkTokens = 1 << 20;  // tokens per workspace pass of 
 
 // Stop tokens of a batched decode: after each column is written, scan() marks the sessions whose token is
 // a stop token and copies the stopped count into a pinned host slot behind an event; keep_going(k) holds
-// the host at most kLag steps ahead of the device and says whether step k is still needed.
+// the host at most kLag steps ahead of the device and says whether step k is still needed: not when every
+// session has stopped, nor when the model's cancellation flag is set (generate's Cancel, checked before each
+// token: internal/generate/greedy.go:68-70, internal/generate/sample.go:204-206), which cuts every reply
+// before column k.
 struct StopTracker {
     static constexpr int kLag = 2;
     mg_sessions* s;
     int S, max_tokens;
+    int cut;  // columns produced: max_tokens unless cancelled
     StopSet set;
     const int32_t* ids;
     int32_t *cnt, *stopped;
@@ -730,7 +738,7 @@ struct StopTracker {
 
     StopTracker(mg_sessions* ss, int max_tok, const int32_t* stops, int n_stops, const int32_t* out_ids_d,
                 hipStream_t stream)
-        : s(ss), S(ss->n), max_tokens(max_tok), set{}, ids(out_ids_d), st(stream) {
+        : s(ss), S(ss->n), max_tokens(max_tok), cut(max_tok), set{}, ids(out_ids_d), st(stream) {
         set.n = n_stops;
         for (int k = 0; k < n_stops; k++) set.id[k] = stops[k];
         if (!s->stop_host) {
@@ -752,15 +760,25 @@ struct StopTracker {
         HIPCHECK(hipMemcpyAsync(s->stop_host + slot, stopped, 4, hipMemcpyDeviceToHost, st));
         HIPCHECK(hipEventRecord(s->stop_ev[slot], st));
     }
+    bool cancelled() const {
+        const volatile int32_t* f = s->m->cancel.load(std::memory_order_acquire);
+        return f && *f != 0;
+    }
     bool keep_going(int k) {
         const int c = k - 1 - kLag;
-        if (c < 0) return true;
-        const int slot = c % mg_sessions::kStopRing;
-        HIPCHECK(hipEventSynchronize(s->stop_ev[slot]));
-        return s->stop_host[slot] < S;
+        if (c >= 0) {
+            const int slot = c % mg_sessions::kStopRing;
+            HIPCHECK(hipEventSynchronize(s->stop_ev[slot]));
+            if (s->stop_host[slot] >= S) return false;
+        }
+        if (cancelled()) {
+            cut = k;
+            return false;
+        }
+        return true;
     }
     void finish() {
-        hipLaunchKernelGGL(stop_finish_kernel, dim3((S + 255) / 256), dim3(256), 0, st, S, max_tokens, cnt);
+        hipLaunchKernelGGL(stop_finish_kernel, dim3((S + 255) / 256), dim3(256), 0, st, S, cut, cnt);
         HIPCHECK(hipGetLastError());
     }
 };
@@ -897,6 +915,14 @@ int mg_model_profile_read(mg_model* m, mg_kernel_time_t* out, int max) {
     });
 }
 
+int mg_model_set_cancel(mg_model* m, const volatile int32_t* flag) {
+    return guarded([&] {
+        require(m != nullptr, "mg_model_set_cancel: null model");
+        m->cancel.store(flag, std::memory_order_release);  // no lock: a decode in progress may hold it
+        return MG_OK;
+    });
+}
+
 int mg_model_sync(mg_model* m) {
     return guarded([&] {
         require(m != nullptr, "mg_model_sync: null model");
@@ -978,6 +1004,9 @@ int mg_score_sequences(mg_model* m, const int32_t* tokens, const long long* offs
     return guarded([&] {
         require(m && offsets && logprob, "mg_score_sequences: null argument");
         require(n_seq >= 0, "mg_score_sequences: negative sequence count");
+        // window() slices tokens[len-contextSize:], which panics in the reference for a negative size
+        // (internal/eval/suite.go:196-198); a context of 0 scores nothing
+        require(context >= 0, "mg_score_sequences: negative context");
         require(offsets[0] >= 0, "mg_score_sequences: negative offset");
         long long n_targets = 0;
         for (int q = 0; q < n_seq; q++) {
@@ -1277,7 +1306,8 @@ int mg_sessions_decode_greedy_until(mg_sessions* s, const int32_t* prompts, cons
         hc.out_ids = oi; hc.out_probs = op; hc.out_ld = max_tokens; hc.out_col = 0;
         prefill_device(s, p_d, l_d, max_len, nullptr, hc, st);
         tr.scan(0);
-        for (int k = 1; k < max_tokens && tr.keep_going(k); k++) {
+        const bool first = tr.keep_going(0);  // false: cancelled before the first token
+        for (int k = 1; first && k < max_tokens && tr.keep_going(k); k++) {
             hc.out_col = k;
             step_device(s, s->next_ids.as<int32_t>(), nullptr, hc, st);
             tr.scan(k);
@@ -1345,7 +1375,8 @@ int mg_sessions_decode_sample(mg_sessions* s, const int32_t* prompts, const int3
         HeadCombineArgs hc;  // the sampler, not the argmax, picks each token
         prefill_device(s, p_d, l_d, max_len, lg, hc, st);
         pick(0);
-        for (int k = 1; k < max_tokens && tr.keep_going(k); k++) {
+        const bool first = tr.keep_going(0);  // false: cancelled before the first token
+        for (int k = 1; first && k < max_tokens && tr.keep_going(k); k++) {
             step_device(s, s->next_ids.as<int32_t>(), lg, hc, st);
             pick(k);
         }

@@ -87,6 +87,13 @@ class Model:
     def sync(self):
         check(lib().mg_model_sync(self._h))
 
+    def set_cancel(self, flag: "ctypes.c_int32 | None"):
+        """mg_model_set_cancel: while flag.value is nonzero (any thread may set it), a batched decode on this
+        model stops before its next token and returns the replies produced so far. The model keeps the
+        flag alive; None removes it."""
+        self._cancel = flag
+        check(lib().mg_model_set_cancel(self._h, ctypes.addressof(flag) if flag is not None else None))
+
     def profile(self, on: bool):
         """Start (clearing earlier records) or stop per-kernel HIP-event timing on the model's stream."""
         check(lib().mg_model_profile(self._h, 1 if on else 0))

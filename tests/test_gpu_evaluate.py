@@ -93,6 +93,10 @@ def test_score_sequences_edges(orders):
         got = score_sequences(gm, seqs, context)
         for s, g in zip(seqs, got):
             _terms_close(g, T.score(om.call, [int(x) for x in s], context))
+    # the reference's window() panics on a negative context: an error here, not a silent NaN result
+    from mignon_ai_amd import MignonError
+    with pytest.raises(MignonError):
+        score_sequences(gm, seqs, -1)
 
 
 @pytest.mark.parametrize("case", list(EQUIV_CASES))

@@ -73,6 +73,17 @@ def test_kernels_identical_c3_batch(restore_selection):
     assert_close(b["logits"][sub], oracle_model(data).forward_all(ids[sub]), what="c3 slab")
 
 
+def test_kernels_identical_c5_shape(restore_selection):
+    """c5's widths: the GLU GEMM's 18 K steps (K 1152), the highway's 16 (K 1024), the 6-step latch, QKV,
+    out, logits and probabilities GEMMs, and a vocabulary of 64 channel slabs."""
+    data = model_bytes("c5")
+    m = Model(data)
+    ids = synth.token_ids(26, "kern-c5", (3, 128), 8192)
+    a, b = _both(m, ids, logits=True, logprob=True, probs=True, bits=True)
+    _same(a, b)
+    assert_close(b["logits"][:1], oracle_model(data).forward_all(ids[:1]), what="c5 slab")
+
+
 def test_sessions_identical(restore_selection):
     data = model_bytes("c4")
     prompts = synth.token_ids(25, "kern-c4", (64, 9), 4096)
