@@ -18,14 +18,21 @@ is already resident in HBM:
   chat          infer.Generate (greedy, chat template, at most 80 tokens) for the 168 order-search requests
                 x 24 on the reference's trained orders.mgn, all in one batch (mg_generate_greedy; value
                 counts requests)
+  append        one session's streaming latency (BenchmarkAppend of the reference's genbench on the medium
+                shape, c3's model): microseconds per Append with host logits
 
 Timing: W warmup steps, then K steps timed with HIP events and nothing else on the stream (value,
 ms_per_step); then K more steps with HIP events around every launch on the model's stream (the per-kernel
-breakdown, kernels_ms_per_step, and profiled_ms_per_step: per-launch events slow launch-bound configurations
+breakdown, kernel_classes, and profiled_ms_per_step: per-launch events slow launch-bound configurations
 down, so they stay out of the timed steps).
-roofline: the kernel class with the largest share of the profiled steps, its algorithmic work per launch
-(int8 MACs x 2 for GEMMs, compulsory bytes for memory-bound kernels) over its average launch time. cpu_baseline: the CPU restatement of the reference
-engine (oracle/, AVX2 dot kernels) timed on this host on a bounded sample of the same workload.
+kernel_classes: every kernel class of the profiled steps with its algorithmic work per launch as the
+engine states it (bytes its operands and results must move; int8 MACs x 2 for GEMMs), its bound (the
+larger of the issued-MFMA and HBM floors at the published peaks) and the achieved fraction of that peak.
+roofline: the same for the class with the largest share of the profiled time.
+cpu_baseline: the CPU restatement of the reference engine (oracle/, AVX2 dot kernels) timed on this host
+on a bounded sample of the same workload.
+single_session_append (c5 line) and --config append: one session's Append latency beside the reference's
+published figure for that shape.
 """
 from __future__ import annotations
 
@@ -83,33 +90,72 @@ def measured_traffic(config, cls):
     return (None, None) if v is None else (round(v), f"profiles/{config}_hbm_traffic.md")
 
 
-def roofline_for(prof, work_per_step, steps, config=None):
-    """Dominant kernel class by time; work_per_step maps class -> (bound, algorithmic units per step)."""
-    total = {k: v[1] for k, v in prof.items()}
-    cands = [k for k in total if k in work_per_step]
+def class_work(prof, extra=None):
+    """Per kernel class: (launches, ms, algorithmic bytes, algorithmic int8 ops), summed over the profiled
+    steps. The engine states bytes and ops per launch (mg_kernel_time_t); `extra` supplies the bytes of
+    classes whose work the host cannot know (decode attention's spans): {class: bytes over the steps}."""
+    out = {}
+    for k, v in prof.items():
+        launches, ms, by, ops = v
+        if extra and k in extra:
+            by = extra[k]
+        out[k] = (launches, ms, by, ops)
+    return out
+
+
+def class_roofline(cls, launches, ms, by, ops):
+    """Roofline of one kernel class from its algorithmic work. The bound is whichever floor is larger at
+    the published peaks: issued int8 MFMA ops (every limb GEMM issues each algorithmic op once per
+    activation limb plane) against 5.0 POP/s, or bytes against 8 TB/s. Returns None without stated work."""
+    if ms <= 0 or (by <= 0 and ops <= 0):
+        return None
+    planes = LIMB_PLANES if cls in LIMB_GEMMS else 1
+    t_mfma = ops * planes / (PEAK_MFMA_TOPS * 1e12)
+    t_hbm = by / (PEAK_HBM_GBS * 1e9)
+    secs = ms / 1e3
+    if t_mfma >= t_hbm:
+        achieved = ops / secs / 1e12
+        r = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_TOPS, "unit": "TFLOP/s",
+             "frac": round(achieved / PEAK_MFMA_TOPS, 4)}
+        if planes > 1:
+            r["issued"] = round(achieved * planes, 2)
+            r["issued_frac"] = round(achieved * planes / PEAK_MFMA_TOPS, 4)
+            r["issued_frac_of_sustained"] = round(achieved * planes / SUSTAINED_MFMA_TOPS, 4)
+    else:
+        achieved = by / secs / 1e9
+        r = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+             "frac": round(achieved / PEAK_HBM_GBS, 4)}
+    r["bytes_per_launch"] = round(by / launches)
+    r["ops_per_launch"] = round(ops / launches)
+    r["avg_launch_ms"] = round(ms / launches, 4)
+    return r
+
+
+def class_table(work, steps):
+    """Every kernel class of the profiled steps: launches and ms per step, and its roofline."""
+    table = {}
+    for k, (launches, ms, by, ops) in sorted(work.items(), key=lambda kv: -kv[1][1]):
+        row = {"launches_per_step": round(launches / steps, 2), "ms_per_step": round(ms / steps, 3)}
+        r = class_roofline(k, launches, ms, by, ops)
+        if r:
+            row.update({x: r[x] for x in ("bound", "achieved", "unit", "frac", "bytes_per_launch", "ops_per_launch")})
+            if "issued_frac_of_sustained" in r:
+                row["issued_frac_of_sustained"] = r["issued_frac_of_sustained"]
+        table[k] = row
+    return table
+
+
+def roofline_for(work, config=None):
+    """The roofline of the kernel class with the largest share of the profiled time (among classes whose
+    work is stated), with the HBM traffic its counters measured where a summary is committed."""
+    cands = [k for k, v in work.items() if v[2] > 0 or v[3] > 0]
     if not cands:
         return None, None
-    dom = max(cands, key=lambda k: total[k])
-    launches, ms = prof[dom]
-    bound, units = work_per_step[dom]
-    per_launch = units * steps / launches
-    avg_s = ms / launches / 1e3
-    if bound == "mfma":
-        achieved = per_launch / avg_s / 1e12
-        r = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_TOPS, "unit": "TFLOP/s",
-             "frac": round(achieved / PEAK_MFMA_TOPS, 4), "traffic": None}
-        if dom in LIMB_GEMMS:
-            # every algorithmic op is issued once per activation limb plane
-            r["issued"] = round(achieved * LIMB_PLANES, 2)
-            r["issued_frac"] = round(achieved * LIMB_PLANES / PEAK_MFMA_TOPS, 4)
-            r["issued_frac_of_sustained"] = round(achieved * LIMB_PLANES / SUSTAINED_MFMA_TOPS, 4)
-    else:
-        achieved = per_launch / avg_s / 1e9
-        r = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-             "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None}
+    dom = max(cands, key=lambda k: work[k][1])
+    launches, ms, by, ops = work[dom]
+    r = class_roofline(dom, launches, ms, by, ops)
     r["kernel"] = dom
-    r["per_launch"] = per_launch
-    r["avg_launch_ms"] = round(ms / launches, 4)
+    r["traffic"] = None
     if config:
         r["traffic"], src = measured_traffic(config, dom)
         if src:
@@ -251,6 +297,56 @@ def cpu_baseline_chat(data, requests, max_tokens, seconds):
                       f"tokenizer and greedy loop over the C++ restatement of the reference Go engine"}
 
 
+APPEND_CONTEXT, APPEND_TOKENS, APPEND_REPEATS = 128, 64, 20  # genbench's ctx=128 run, appendTokens
+APPEND_PUBLISHED_US = 125.0  # medium preset, INT8 generation (internal/train/presets.go:95)
+
+
+def append_latency(seed, repeats=APPEND_REPEATS, cpu_seconds=0.0):
+    """Single-session streaming latency as the reference's BenchmarkAppend measures it
+    (internal/genbench/genbench_test.go:88-123): the `medium` shape (c3's model: D128 H256, 2 blocks x 1
+    step, 4 heads, window 64, V2048) at context 128, a session prefilled with 64 ids in [0, 1000) outside
+    the timed region, then 64 Appends timed, each returning the position's logits to the host (one
+    mg_sessions_step of one session with host pointers). Reported as microseconds per token: the median
+    over `repeats` prefill + 64-append rounds, and the oracle's (the CPU restatement, one core) beside it."""
+    from mignon_ai_amd import Model, mgnn, quantize_f32, synth
+    spec = synth.CONFIGS["c3"]["spec"]
+    data = mgnn.build_model_file(spec, seed, quantize_f32)
+    m = Model(data)
+    rng = np.random.default_rng(seed)
+    prompt = rng.integers(0, 1000, APPEND_CONTEXT - APPEND_TOKENS)
+    toks = rng.integers(0, 1000, (repeats + 1, APPEND_TOKENS))
+    sess = m.new_session(APPEND_CONTEXT)
+    rounds = []
+    for r in range(repeats + 1):  # the first round warms up
+        sess.prefill(prompt)
+        t0 = time.perf_counter()
+        for t in toks[r]:
+            sess.append(int(t))
+        rounds.append((time.perf_counter() - t0) / APPEND_TOKENS * 1e6)
+    us = float(np.median(rounds[1:]))
+    out = {"us_per_token": round(us, 2), "us_per_token_min": round(float(min(rounds[1:])), 2),
+           "reference_published_us_per_token": APPEND_PUBLISHED_US,
+           "workload": f"BenchmarkAppend, medium shape (D{spec.D} H{spec.H} {len(spec.blocks)} blocks heads "
+                       f"{spec.heads} window {spec.window} V{spec.V}), context {APPEND_CONTEXT}: prefill "
+                       f"{APPEND_CONTEXT - APPEND_TOKENS} ids, then {APPEND_TOKENS} Appends with host logits; median "
+                       f"of {repeats} rounds"}
+    if cpu_seconds > 0:
+        from oracle import oracle as O
+        om = O.OracleModel(O.read_model(data))
+        osess = om.new_session(APPEND_CONTEXT)
+        n, t_total = 0, 0.0
+        while t_total < cpu_seconds:
+            osess.prefill([int(x) for x in prompt])
+            t0 = time.perf_counter()
+            for t in toks[n % len(toks)]:
+                osess.append(int(t))
+            t_total += time.perf_counter() - t0
+            n += 1
+        out["cpu_us_per_token"] = round(t_total / (n * APPEND_TOKENS) * 1e6, 2)
+        out["cpu_kind"] = "port: the oracle's session (C++ restatement of the reference Go engine), one core"
+    return out
+
+
 def synth_ids(seed, tag, shape, V):
     from mignon_ai_amd import synth
     return synth.token_ids(seed, tag, shape, V)
@@ -276,7 +372,18 @@ def run(args):
            "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic"}
     cpu = None
 
-    if name == "c2":
+    if name == "append":
+        a = append_latency(args.seed, cpu_seconds=0 if args.no_cpu_baseline else min(args.cpu_seconds, 10.0))
+        us = a["us_per_token"]
+        out.update(metric="single-session INT8 Append latency", value=us, unit="us/token", ms_per_step=round(us / 1e3, 5),
+                   higher_is_better=False, config={"workload": a.pop("workload"), "context": APPEND_CONTEXT,
+                                                   "appended": APPEND_TOKENS})
+        out.update(a)
+        out["roofline"] = None
+        if "cpu_us_per_token" in a:
+            cpu = {"value": a["cpu_us_per_token"], "unit": "us/token", "cores": 1, "kind": "port",
+                   "sample": "the same prefill + 64 Appends through the oracle's session, repeated for up to 10 s"}
+    elif name == "c2":
         c = synth.C2
         M, K, N = c["M"], c["K"], c["N"]
         A = (synth.u64_stream(args.seed, "A", M * K) % np.uint64(255)).astype(np.int64) - 127
@@ -326,19 +433,16 @@ def run(args):
         targets = N - 1
         rows = 1 + (N - 1 - W)
         positions = W + (rows - 1) * W
-        macs = per_token_macs(spec)
-        work = {k: ("mfma", 2 * v * positions) for k, v in macs.items() if v and k not in ("gemm_logits", "gemm_probs")}
-        work["gemm_logits"] = ("mfma", 2 * macs["gemm_logits"] * targets)
         out.update(value=round(targets / (ms / 1e3), 1), unit="targets/s", ms_per_step=round(ms, 4))
         out["config"] = {"workload": f"score: eval.Perplexity over a {N}-token stream, context {W}, of the c3 model "
                                      f"(D{spec.D} H{spec.H} {len(spec.blocks)} blocks heads {spec.heads} window "
                                      f"{spec.window} V{spec.V}); host token stream in, per-target log-probs out",
                          "tokens": N, "context": W, "window_rows": rows, "body_positions": positions,
                          "params": spec.n_params}
-        dom, roof = roofline_for(prof, work, args.steps, None)
+        work = class_work(prof)
+        dom, roof = roofline_for(work, None)
         out["roofline"] = roof
-        out["kernels_ms_per_step"] = {k: round(v[1] / args.steps, 3) for k, v in sorted(prof.items(),
-                                                                                      key=lambda kv: -kv[1][1])}
+        out["kernel_classes"] = class_table(work, args.steps)
         out["wall_s"] = round(wall, 3)
         if not args.no_cpu_baseline:
             cpu = cpu_baseline_score(data, stream_ids, W, args.cpu_seconds)
@@ -368,9 +472,9 @@ def run(args):
                          "requests": len(batch), "generated_tokens": gen,
                          "generated_tokens_per_s": round(gen / (ms / 1e3), 1)}
         out["data"] = "the reference's order-search requests (tests/golden/orders_handwritten.json)"
-        out["kernels_ms_per_step"] = {k: round(v[1] / args.steps, 3) for k, v in sorted(prof.items(),
-                                                                                      key=lambda kv: -kv[1][1])}
-        out["roofline"] = None
+        work = class_work(prof)
+        out["kernel_classes"] = class_table(work, args.steps)
+        out["roofline"] = roofline_for(work, None)[1]
         out["wall_s"] = round(wall, 3)
         if not args.no_cpu_baseline:
             cpu = cpu_baseline_chat(data, requests, CHAT_MAX_TOKENS, args.cpu_seconds)
@@ -401,9 +505,7 @@ def run(args):
                 m.forward_batch_device(ids, **kw)
 
             tokens = B * T
-            work = {k: ("mfma", 2 * v * tokens) for k, v in macs.items() if v}
-            if "probs" not in kw:
-                work.pop("gemm_probs", None)
+            extra = None
             ms, wall, ms_prof = timed(step, args.warmup, args.steps, torch, before=lambda: m.profile(True))
             prof = m.profile_read()
             out["profiled_ms_per_step"] = round(ms_prof, 4)  # the second, instrumented pass
@@ -432,11 +534,12 @@ def run(args):
                 def step():
                     sess.decode_greedy_device(prompts, lens, G, oid, opb)
 
-            positions = S * (P + G - 1)
-            work = {k: ("mfma", 2 * v * positions) for k, v in macs.items() if v and k != "gemm_probs"}
-            # K/V ring reads of the decode steps: sum over appended positions of the attended span
+            # decode attention's bytes (the engine cannot state them: the spans live on the device): per
+            # session, block and appended position, the K/V ring rows of the attended span, the new K/V row
+            # and q in, the output row out
             span = sum(min(p + 1, spec.window) for p in range(P, P + G - 1))
-            work["attention_step"] = ("hbm", S * len(spec.blocks) * 2 * span * spec.D * 4)
+            extra = {"attention_step": (args.steps * S * len(spec.blocks) *
+                                        (2 * span + (G - 1) * 4) * spec.D * 4)}
             ms, wall, ms_prof = timed(step, args.warmup, args.steps, torch, before=lambda: m.profile(True))
             prof = m.profile_read()
             out["profiled_ms_per_step"] = round(ms_prof, 4)  # the second, instrumented pass
@@ -452,7 +555,8 @@ def run(args):
                 cpu = cpu_baseline_decode(data, spec, S, P, G, args.cpu_seconds, args.seed)
                 if name == "sample":
                     cpu["sample"] += "; greedy choice in place of sampling (a lower bound of the reference's time)"
-        dom, roof = roofline_for(prof, work, args.steps, name)
+        work = class_work(prof, extra)
+        dom, roof = roofline_for(work, name)
         out["roofline"] = roof
         total_macs = sum(v for k, v in macs.items() if k != "gemm_probs")
         tok = (cfg["B"] * cfg["T"]) if name not in ("c4", "sample") else cfg["B"] * (cfg["P"] + cfg["G"] - 1)
@@ -461,9 +565,11 @@ def run(args):
                                 "unit": "TFLOP/s", "frac": round(path_tops / PEAK_MFMA_TOPS, 4),
                                 "note": "whole step: algorithmic int8 MACs x 2 (one pass of every weight "
                                         "GEMM; the probability head's recompute not counted)"}
-        out["kernels_ms_per_step"] = {k: round(v[1] / args.steps, 3) for k, v in sorted(prof.items(),
-                                                                                      key=lambda kv: -kv[1][1])}
+        out["kernel_classes"] = class_table(work, args.steps)
         out["wall_s"] = round(wall, 3)
+        if name == "c5":
+            # the one latency figure the reference publishes for this path, measured beside the headline
+            out["single_session_append"] = append_latency(args.seed, repeats=10)
     out["cpu_baseline"] = cpu
     out["kernels"] = {"gemm": args.gemm, "attention": args.attention, "scan": args.scan}
     return out
@@ -474,7 +580,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--config", default="c5", choices=["c1", "c2", "c3", "c4", "c5", "score", "chat", "sample"])
+    ap.add_argument("--config", default="c5", choices=["c1", "c2", "c3", "c4", "c5", "score", "chat", "sample",
+                                                       "append"])
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)

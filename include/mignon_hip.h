@@ -70,11 +70,16 @@ void* mg_model_stream(const mg_model* m);
 
 /* Kernel timing (no reference counterpart; measurement support). While on, every kernel launch of the
  * handle is bracketed by HIP events on its stream; mg_model_profile_read waits for the stream and
- * returns per-class launch counts and summed durations (at most max entries; returns the class count). */
+ * returns per-class launch counts, summed durations and the summed algorithmic work of those launches:
+ * bytes = HBM bytes each launch must move (its operands read once, its results written once; 0 where the
+ * host cannot know it, e.g. decode attention's spans), ops = int8 multiply-accumulates x 2 (GEMMs only,
+ * unpadded shapes, one pass per weight matrix). At most max entries; returns the class count. */
 typedef struct {
     char name[32];
     long long launches;
     double total_ms;
+    double bytes;
+    double ops;
 } mg_kernel_time_t;
 int mg_model_profile(mg_model* m, int on);
 int mg_model_profile_read(mg_model* m, mg_kernel_time_t* out, int max);
@@ -274,10 +279,16 @@ int mg_quantize_f32(const float* w, long long n, int8_t* q, float* scale, int fl
  *     sequence length is a multiple of 16 and the padded width at most 1024; elsewhere the separate
  *     kernels run whatever the option says. Automatic fuses where it applies to batches of many
  *     sequences (one workgroup per sequence).
+ *   MG_OPT_STEP_GRAPH: MG_STEP_EAGER launches a decode step's kernels one at a time; MG_STEP_GRAPH
+ *     captures a step's launches as a HIP graph once and replays it while the step's buffers and
+ *     arguments are unchanged (identical results, less host time per step). Automatic uses the graph.
  * value < 0 only reads the option. Returns the previous value, or MG_ERR_INVALID. */
 #define MG_OPT_GEMM_KERNEL 0
 #define MG_OPT_ATTENTION_KERNEL 1
 #define MG_OPT_SCAN_KERNEL 2
+#define MG_OPT_STEP_GRAPH 3
+#define MG_STEP_EAGER 1
+#define MG_STEP_GRAPH 2
 #define MG_SCAN_SEPARATE 1
 #define MG_SCAN_FUSED 2
 #define MG_GEMM_STREAM 1

@@ -21,6 +21,7 @@ MG_OPT_GEMM_KERNEL, MG_OPT_ATTENTION_KERNEL, MG_OPT_SCAN_KERNEL = 0, 1, 2
 MG_GEMM_STREAM, MG_GEMM_SLAB = 1, 2
 MG_ATTN_EXACT, MG_ATTN_MFMA = 1, 2
 MG_SCAN_SEPARATE, MG_SCAN_FUSED = 1, 2
+MG_OPT_STEP_GRAPH, MG_STEP_EAGER, MG_STEP_GRAPH = 3, 1, 2
 
 _vp = ctypes.c_void_p
 _i32p = ctypes.POINTER(ctypes.c_int32)
@@ -50,7 +51,8 @@ class HeldOut(ctypes.Structure):
 
 
 class KernelTime(ctypes.Structure):
-    _fields_ = [("name", ctypes.c_char * 32), ("launches", _ll), ("total_ms", ctypes.c_double)]
+    _fields_ = [("name", ctypes.c_char * 32), ("launches", _ll), ("total_ms", ctypes.c_double),
+                ("bytes", ctypes.c_double), ("ops", ctypes.c_double)]
 
 
 # name -> (restype, argtypes); the exported set of include/mignon_hip.h

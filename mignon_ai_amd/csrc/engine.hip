@@ -39,6 +39,12 @@ std::atomic<int> g_options[OPT_COUNT];
 
 int option(int opt) { return (opt >= 0 && opt < OPT_COUNT) ? g_options[opt].load(std::memory_order_relaxed) : 0; }
 
+int options_key() {
+    int k = 0;
+    for (int o = 0; o < OPT_COUNT; o++) k = k * 4 + g_options[o].load(std::memory_order_relaxed);
+    return k;
+}
+
 int set_option(int opt, int value) {
     if (opt < 0 || opt >= OPT_COUNT) return -1;
     if (value < 0) return g_options[opt].load();
@@ -127,7 +133,12 @@ struct Profile {
     bool on = false;
     std::vector<hipEvent_t> pool;
     size_t used = 0;
-    std::vector<std::pair<int, size_t>> recs;  // class, index of the start event (end = start + 1)
+    struct Rec {
+        int cls;
+        size_t start;        // index of the start event (end = start + 1)
+        double bytes, ops;   // algorithmic HBM bytes and int8 ops of the launch (0: not stated)
+    };
+    std::vector<Rec> recs;
     ~Profile() {
         for (hipEvent_t e : pool) (void)hipEventDestroy(e);
     }
@@ -141,13 +152,17 @@ struct Profile {
     }
 };
 
-// Records start/end events around the launches in its scope when the model's profiler is on.
+// Records start/end events around the launches in its scope when the model's profiler is on, with the
+// algorithmic work the caller states for them: the HBM bytes the launches must move (operands read once,
+// results written once) and their int8 multiply-accumulates x 2.
 struct ProfScope {
     Profile* p;
     hipStream_t s;
     int cls;
     size_t start = 0;
-    ProfScope(Profile& pr, int c, hipStream_t st) : p(pr.on ? &pr : nullptr), s(st), cls(c) {
+    double bytes = 0, ops = 0;
+    ProfScope(Profile& pr, int c, hipStream_t st, double b = 0, double o = 0)
+        : p(pr.on ? &pr : nullptr), s(st), cls(c), bytes(b), ops(o) {
         if (p) {
             start = p->used;
             (void)hipEventRecord(p->next(), s);
@@ -156,7 +171,7 @@ struct ProfScope {
     ~ProfScope() {
         if (p) {
             (void)hipEventRecord(p->next(), s);
-            p->recs.emplace_back(cls, start);
+            p->recs.push_back({cls, start, bytes, ops});
         }
     }
 };
@@ -164,6 +179,7 @@ struct ProfScope {
 // Workspace for a batch of tokens in flight.
 struct Workspace {
     int cap_tokens = 0;
+    long long gen = 0;  // bumped whenever the buffers below are reallocated (captured graphs hold their addresses)
     DevBuf cur, bin, nf, lam, nl, ns, xl, xs, h, hl, hs, qkv, att, stats, lse, tlog, logprob, argmax, prob, ids, tgt,
         rowmap, lens, tmp;
 };
@@ -206,10 +222,30 @@ struct mg_sessions {
     mg::DevBuf stop_count, stopped;
     int32_t* stop_host = nullptr;
     hipEvent_t stop_ev[kStopRing] = {};
+    // mg_sessions_step with host pointers: device buffers for its ids and outputs and a pinned host
+    // mirror, kept for the life of the set (no allocation per step)
+    mg::DevBuf io;
+    uint8_t* io_host = nullptr;
+    // The last step captured as a HIP graph, replayed while what its launches captured is unchanged:
+    // the workspace's buffers, the engine options and the output pointers.
+    struct StepGraph {
+        hipGraphExec_t exec = nullptr;
+        long long ws_gen = -1;
+        int opts = -1;
+        const void* ptrs[4] = {};
+        bool failed = false;  // capture is not possible here: launch one kernel at a time
+        void reset() {
+            if (exec) (void)hipGraphExecDestroy(exec);
+            exec = nullptr;
+            ws_gen = -1;
+        }
+    } graph;
     ~mg_sessions() {
+        graph.reset();
         for (hipEvent_t& e : stop_ev)
             if (e) (void)hipEventDestroy(e);
         if (stop_host) (void)hipHostFree(stop_host);
+        if (io_host) (void)hipHostFree(io_host);
     }
 };
 
@@ -367,6 +403,7 @@ void build_device_model(mg_model* m, const HostModel& hm, int max_context) {
 void ensure_ws(mg_model* m, int tokens) {
     Workspace& w = m->ws;
     if (tokens <= w.cap_tokens) return;
+    w.gen++;
     size_t M = (size_t)tokens;
     const size_t Mp = (size_t)round_up(tokens, LX_ROWS);  // limb operands are read in whole row tiles
     const size_t Dp = m->Dp, Hp = m->Hp, D = m->D;
@@ -418,9 +455,54 @@ int gemm_class(int epi) {
     }
 }
 
+// Algorithmic work of one limb-expanded GEMM launch over g.M token rows: int8 MACs x 2 at the model's
+// unpadded shape (one pass of the weight matrix), and the bytes it must move: the three limb planes and
+// row scales of A, the weights and bias once, and what its epilogue reads and writes.
+void gemm_work(const mg_model* m, int epi, const GemmArgs& g, double& bytes, double& ops) {
+    const double M = g.M, D = m->D, H = m->H, V = m->V;
+    double k = 0, rows = 0;
+    switch (epi) {
+        case EPI_LATCH: k = D; rows = D; break;
+        case EPI_GLU: k = 3 * D; rows = 2 * H; break;
+        case EPI_HIGHWAY: k = H; rows = 2 * D; break;
+        case EPI_F32: k = D; rows = 3 * D; break;
+        case EPI_RESID: k = D; rows = D; break;
+        default: k = D; rows = V; break;  // EPI_LOGITS, EPI_PROBS
+    }
+    ops = 2.0 * M * k * rows;
+    bytes = M * (3.0 * g.Kp + 4) + (double)g.Kp * g.Np + (g.bias ? 4.0 * g.Np : 0);
+    const double nv = g.nvalid;
+    switch (epi) {
+        case EPI_HIGHWAY:
+        case EPI_RESID: bytes += (g.resid ? 12.0 : 8.0) * M * nv; break;  // state read, (blockIn read,) write
+        case EPI_LOGITS: bytes += (g.out ? 4.0 * M * nv : 0) + 12.0 * M * g.stats_ld + (g.tgt ? 8.0 * M : 0); break;
+        case EPI_PROBS: bytes += 4.0 * M * nv + 4.0 * M; break;
+        default: bytes += 4.0 * M * nv; break;
+    }
+}
+
 void gemm(mg_model* m, int epi, const GemmArgs& g, hipStream_t s) {
-    ProfScope ps(m->prof, gemm_class(epi), s);
+    double bytes = 0, ops = 0;
+    if (m->prof.on) gemm_work(m, epi, g, bytes, ops);
+    ProfScope ps(m->prof, gemm_class(epi), s, bytes, ops);
     HIPCHECK(launch_gemm_lx(epi, g, s));
+}
+
+// Bytes a row-kernel launch must move: its source rows (the embedding's int8 rows and ids; cur and
+// blockIn for the residual; two fp32 rows per position for the rule input, whose left neighbour is a
+// re-read of a row already fetched), then its fp32 outputs and the limb planes with their row scales.
+double row_bytes(const RowArgs& r) {
+    const double M = r.M, D = r.D;
+    double b = 0;
+    switch (r.mode) {
+        case ROW_EMBED: b = M * (4 + D + 8 * D); break;
+        case ROW_RESID: b = M * 16 * D; break;
+        case ROW_RULE: b = M * 8 * D; break;
+        default: b = M * 4 * D + (r.row_map ? 4 * M : 0); break;
+    }
+    if (r.nout) b += M * 4 * D;
+    if (r.limbs) b += M * (3.0 * r.Dp + 4);
+    return b;
 }
 
 // Row kernel helper: mode + optional norm, writes n (fp32) and the limb-expanded copy into ws.nl/ns.
@@ -435,7 +517,7 @@ void row_call(mg_model* m, int M, int mode, const int32_t* ids, const float* src
     if (limbs) {
         r.limbs = w.nl.as<int8_t>(); r.lscale = w.ns.as<float>();
     }
-    ProfScope ps(m->prof, K_ROW, s);
+    ProfScope ps(m->prof, K_ROW, s, row_bytes(r));
     HIPCHECK(launch_row(r, s));
 }
 
@@ -553,7 +635,9 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                 la.g = c.sess->g.as<float>() + (size_t)bs * c.B * Dp;
                 la.norm_ring = c.sess->norm_ring.as<float>() + (size_t)bs * c.B * m->ring * Dp;
                 la.xl = w.xl.as<int8_t>(); la.xs = w.xs.as<float>();
-                ProfScope ps(m->prof, K_LATCH_STEP, s);
+                // per session: lambda, n, g and the ring's left row in; g, the ring slot and the rule
+                // input's limbs out
+                ProfScope ps(m->prof, K_LATCH_STEP, s, (double)M * (24.0 * D + 9.0 * Dp + 8));
                 HIPCHECK(launch_latch_step(la, s));
             } else {
                 // g for every position, written over lambda (each element is read before it is replaced)
@@ -575,18 +659,19 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                 const bool many = (long long)c.B * ((Dp / 2 + 63) / 64) >= 1024;
                 if (scan_rule_fits(c.T, Dp, dil) && (sk == 2 || (sk == 0 && many))) {
                     sa.dil = dil; sa.xl = w.xl.as<int8_t>(); sa.xs = w.xs.as<float>();
-                    ProfScope ps(m->prof, K_SCAN, s);
+                    // lambda and n in (the left neighbour is a re-read), the rule input's limbs out
+                    ProfScope ps(m->prof, K_SCAN, s, (double)M * (8.0 * D + 9.0 * Dp + 4));
                     HIPCHECK(launch_scan_rule(sa, s));
                 } else {
                     {
-                        ProfScope ps(m->prof, K_SCAN, s);
+                        ProfScope ps(m->prof, K_SCAN, s, (double)M * 12.0 * D);
                         HIPCHECK(launch_scan(sa, s));
                     }
                     RowArgs r;
                     r.M = M; r.mode = ROW_RULE; r.D = D; r.Dp = 3 * Dp; r.seg = Dp; r.dil = dil; r.T = c.T;
                     r.src = w.nf.as<float>(); r.src2 = w.lam.as<float>();
                     r.limbs = w.xl.as<int8_t>(); r.lscale = w.xs.as<float>();
-                    ProfScope ps(m->prof, K_SCAN, s);
+                    ProfScope ps(m->prof, K_SCAN, s, row_bytes(r));
                     HIPCHECK(launch_row(r, s));
                 }
             }
@@ -598,7 +683,7 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                 RowArgs r;
                 r.M = M; r.D = m->H; r.Dp = Hp; r.mode = ROW_SRC; r.src = w.h.as<float>(); r.lds = Hp;
                 r.limbs = w.hl.as<int8_t>(); r.lscale = w.hs.as<float>();
-                ProfScope ps(m->prof, K_ROW, s);
+                ProfScope ps(m->prof, K_ROW, s, row_bytes(r));
                 HIPCHECK(launch_row(r, s));
             }
             // cur = highway(cur, W2 h) (stream.go:222-229)
@@ -641,7 +726,8 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                 AttnArgs aa;
                 aa.B = c.B; aa.T = c.T; aa.D = D; aa.Dp = Dp; aa.heads = m->heads; aa.window = m->window; aa.cap = m->cap;
                 aa.qkv = w.qkv.as<float>(); aa.att = w.att.as<float>();
-                ProfScope ps(m->prof, K_ATTN, s);
+                // q, k and v of every position in, the output row out
+                ProfScope ps(m->prof, K_ATTN, s, (double)M * 16.0 * D);
                 HIPCHECK(launch_attention(aa, s));
             }
             if (!att_limbs) row_call(m, M, ROW_SRC, nullptr, w.att.as<float>(), Dp, nullptr, nullptr, nullptr, true, s);
@@ -671,7 +757,10 @@ void run_head(mg_model* m, int M, const int32_t* row_map, const int32_t* tgt, fl
     gemm(m, EPI_LOGITS, g, s);
     hc.M = M; hc.ntiles = m->Vp / LX_BN; hc.stats = w.stats.as<float>(); hc.V = m->V;
     hc.tgt = tgt; hc.tlog = w.tlog.as<float>();
-    ProfScope ps(m->prof, K_HEAD_COMBINE, s);
+    // the per-tile statistics (and target logits) in; per-row results out
+    const double outs = 4.0 * (!!hc.lse + !!hc.argmax + !!hc.logprob + !!hc.next_ids + !!hc.out_ids) +
+                        8.0 * (!!hc.prob + !!hc.out_probs);
+    ProfScope ps(m->prof, K_HEAD_COMBINE, s, (double)M * (12.0 * hc.ntiles + (tgt ? 8.0 : 0) + outs));
     HIPCHECK(launch_head_combine(hc, s));
 }
 
@@ -892,13 +981,15 @@ int mg_model_profile_read(mg_model* m, mg_kernel_time_t* out, int max) {
         require(m != nullptr && (out != nullptr || max == 0), "mg_model_profile_read: null argument");
         Guard g(m);
         HIPCHECK(hipStreamSynchronize(m->stream));
-        double ms[K_NCLASS] = {0};
+        double ms[K_NCLASS] = {0}, by[K_NCLASS] = {0}, op[K_NCLASS] = {0};
         long long n[K_NCLASS] = {0};
         for (auto& r : m->prof.recs) {
             float t = 0;
-            HIPCHECK(hipEventElapsedTime(&t, m->prof.pool[r.second], m->prof.pool[r.second + 1]));
-            ms[r.first] += t;
-            n[r.first]++;
+            HIPCHECK(hipEventElapsedTime(&t, m->prof.pool[r.start], m->prof.pool[r.start + 1]));
+            ms[r.cls] += t;
+            by[r.cls] += r.bytes;
+            op[r.cls] += r.ops;
+            n[r.cls]++;
         }
         int k = 0;
         for (int c = 0; c < K_NCLASS; c++) {
@@ -908,6 +999,8 @@ int mg_model_profile_read(mg_model* m, mg_kernel_time_t* out, int max) {
                 std::strncpy(out[k].name, kClassNames[c], sizeof(out[k].name) - 1);
                 out[k].launches = n[c];
                 out[k].total_ms = ms[c];
+                out[k].bytes = by[c];
+                out[k].ops = op[c];
             }
             k++;
         }
@@ -978,7 +1071,7 @@ int mg_forward_batch(mg_model* m, const int32_t* ids, int B, int T, float* logit
             }
             if (bits) {
                 float* bd = dev ? bits + b0 : st.out<float>((size_t)Bc);
-                ProfScope ps(m->prof, K_BITS, s);
+                ProfScope ps(m->prof, K_BITS, s, (double)M * 8.0 + 4.0 * Bc);
                 HIPCHECK(launch_bits(Bc, T, w.logprob.as<float>(), ids_d, V, bd, s));
                 if (!dev) HIPCHECK(hipMemcpyAsync(bits + b0, bd, (size_t)Bc * 4, hipMemcpyDeviceToHost, s));
             }
@@ -1212,6 +1305,55 @@ int mg_sessions_prefill(mg_sessions* s, const int32_t* prompts, const int32_t* l
     });
 }
 
+namespace {
+
+// One decode step of every session (step_device), replayed from a captured HIP graph when the options
+// allow it and the profiler is off: a step is ~10 launches per block of a few microseconds each at small
+// batches, and the graph removes their host-side enqueue cost. The graph is captured again when the
+// workspace was reallocated, an option changed or the argument pointers differ; if capture fails the set
+// falls back to launching kernel by kernel.
+void step_graphed(mg_sessions* s, const int32_t* ids_d, float* logits_d, const HeadCombineArgs& hc, hipStream_t st) {
+    mg_model* m = s->m;
+    const int mode = option(OPT_STEP_GRAPH);
+    auto& G = s->graph;
+    if (mode == 1 || m->prof.on || G.failed) {
+        step_device(s, ids_d, logits_d, hc, st);
+        return;
+    }
+    ensure_ws(m, s->n);  // before any capture: no allocation may happen inside one
+    const void* ptrs[4] = {ids_d, logits_d, hc.argmax, hc.prob};
+    const bool same = G.exec && G.ws_gen == m->ws.gen && G.opts == options_key() &&
+                      std::equal(ptrs, ptrs + 4, G.ptrs);
+    if (!same) {
+        G.reset();
+        hipGraph_t graph = nullptr;
+        bool ok = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) == hipSuccess;
+        if (ok) {
+            try {
+                step_device(s, ids_d, logits_d, hc, st);
+            } catch (const Error&) {
+                ok = false;
+            }
+            ok = hipStreamEndCapture(st, &graph) == hipSuccess && ok && graph;
+        }
+        if (ok) ok = hipGraphInstantiateWithFlags(&G.exec, graph, 0) == hipSuccess;
+        if (graph) (void)hipGraphDestroy(graph);
+        if (!ok) {
+            (void)hipGetLastError();
+            G.reset();
+            G.failed = true;
+            step_device(s, ids_d, logits_d, hc, st);
+            return;
+        }
+        G.ws_gen = m->ws.gen;
+        G.opts = options_key();
+        std::copy(ptrs, ptrs + 4, G.ptrs);
+    }
+    HIPCHECK(hipGraphLaunch(G.exec, st));
+}
+
+}  // namespace
+
 int mg_sessions_step(mg_sessions* s, const int32_t* ids, float* logits, int32_t* argmax, double* prob, int flags) {
     return guarded([&] {
         require(s && ids, "mg_sessions_step: null argument");
@@ -1220,19 +1362,39 @@ int mg_sessions_step(mg_sessions* s, const int32_t* ids, float* logits, int32_t*
         hipStream_t st = m->stream;
         const bool dev = flags & MG_PTR_DEVICE;
         const int S = s->n;
-        Staging sg;
-        const int32_t* i_d = dev ? ids : sg.in(ids, (size_t)S, st);
-        float* lg = logits ? (dev ? logits : sg.out<float>((size_t)S * m->V)) : nullptr;
-        HeadCombineArgs hc;
-        hc.argmax = argmax ? (dev ? argmax : sg.out<int32_t>(S)) : nullptr;
-        hc.prob = prob ? (dev ? prob : sg.out<double>(S)) : nullptr;
-        step_device(s, i_d, lg, hc, st);
-        if (!dev) {
-            if (logits) HIPCHECK(hipMemcpyAsync(logits, lg, (size_t)S * m->V * 4, hipMemcpyDeviceToHost, st));
-            if (argmax) HIPCHECK(hipMemcpyAsync(argmax, hc.argmax, (size_t)S * 4, hipMemcpyDeviceToHost, st));
-            if (prob) HIPCHECK(hipMemcpyAsync(prob, hc.prob, (size_t)S * 8, hipMemcpyDeviceToHost, st));
-            HIPCHECK(hipStreamSynchronize(st));
+        if (dev) {
+            HeadCombineArgs hc;
+            hc.argmax = argmax;
+            hc.prob = prob;
+            step_graphed(s, ids, logits, hc, st);
+            return MG_OK;
         }
+        // host pointers: the set's own device buffers and pinned mirror [ids | logits | argmax | prob]
+        auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+        const size_t o_lg = up((size_t)S * 4), o_am = o_lg + up((size_t)S * m->V * 4), o_pb = o_am + up((size_t)S * 4),
+                     total = o_pb + (size_t)S * 8;
+        if (s->io.n < total) {
+            s->io.ensure(total);
+            if (s->io_host) (void)hipHostFree(s->io_host);
+            s->io_host = nullptr;
+            HIPCHECK(hipHostMalloc((void**)&s->io_host, total, 0));
+        }
+        uint8_t* d = s->io.as<uint8_t>();
+        uint8_t* h = s->io_host;
+        std::memcpy(h, ids, (size_t)S * 4);
+        HIPCHECK(hipMemcpyAsync(d, h, (size_t)S * 4, hipMemcpyHostToDevice, st));
+        HeadCombineArgs hc;
+        hc.argmax = argmax ? (int32_t*)(d + o_am) : nullptr;
+        hc.prob = prob ? (double*)(d + o_pb) : nullptr;
+        float* lg = logits ? (float*)(d + o_lg) : nullptr;
+        step_graphed(s, (const int32_t*)d, lg, hc, st);
+        if (logits) HIPCHECK(hipMemcpyAsync(h + o_lg, lg, (size_t)S * m->V * 4, hipMemcpyDeviceToHost, st));
+        if (argmax) HIPCHECK(hipMemcpyAsync(h + o_am, hc.argmax, (size_t)S * 4, hipMemcpyDeviceToHost, st));
+        if (prob) HIPCHECK(hipMemcpyAsync(h + o_pb, hc.prob, (size_t)S * 8, hipMemcpyDeviceToHost, st));
+        HIPCHECK(hipStreamSynchronize(st));
+        if (logits) std::memcpy(logits, h + o_lg, (size_t)S * m->V * 4);
+        if (argmax) std::memcpy(argmax, h + o_am, (size_t)S * 4);
+        if (prob) std::memcpy(prob, h + o_pb, (size_t)S * 8);
         return MG_OK;
     });
 }

@@ -7,11 +7,15 @@ enum Option : int {
     OPT_GEMM_KERNEL = 0,       // 0 automatic, 1 streaming, 2 weight-stationary
     OPT_ATTENTION_KERNEL = 1,  // 0 automatic, 1 reference order (VALU), 2 matrix cores
     OPT_SCAN_KERNEL = 2,       // 0 automatic, 1 latch scan then rule-input packing, 2 fused
+    OPT_STEP_GRAPH = 3,        // decode steps: 0 automatic (replayed from a captured HIP graph), 1 launched
+                               // one kernel at a time, 2 graph
     OPT_COUNT
 };
 
 // Current value of an option.
 int option(int opt);
+// All options packed into one value (changes whenever any option does).
+int options_key();
 // Sets an option (value < 0 only reads it); returns the previous value, or -1 for an unknown option or
 // value.
 int set_option(int opt, int value);

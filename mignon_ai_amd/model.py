@@ -99,11 +99,13 @@ class Model:
         check(lib().mg_model_profile(self._h, 1 if on else 0))
 
     def profile_read(self) -> dict:
-        """{kernel class: (launches, total ms)} of the launches recorded while profiling was on."""
+        """{kernel class: (launches, total ms, algorithmic bytes, algorithmic int8 ops)} of the launches
+        recorded while profiling was on (bytes and ops summed over the launches; 0 where not stated)."""
         from ._lib import KernelTime
         buf = (KernelTime * 32)()
         n = check(lib().mg_model_profile_read(self._h, buf, 32))
-        return {buf[i].name.decode(): (buf[i].launches, buf[i].total_ms) for i in range(min(n, 32))}
+        return {buf[i].name.decode(): (buf[i].launches, buf[i].total_ms, buf[i].bytes, buf[i].ops)
+                for i in range(min(n, 32))}
 
     # quant.Model.Call / Forward (LogitsFn)
     def call(self, ids):
@@ -285,7 +287,7 @@ def quantize_f32(w):
 
 
 _OPTIONS = {"gemm": (0, ["auto", "stream", "slab"]), "attention": (1, ["auto", "exact", "mfma"]),
-            "scan": (2, ["auto", "separate", "fused"])}
+            "scan": (2, ["auto", "separate", "fused"]), "step_graph": (3, ["auto", "off", "on"])}
 
 
 def sample_logits(logits, recent=None, temperature=1.0, top_k=0, top_p=1.0, rep_penalty=1.0, u=None):
@@ -312,8 +314,9 @@ def sample_logits(logits, recent=None, temperature=1.0, top_k=0, top_p=1.0, rep_
 
 def engine_option(name: str, value: str | None = None) -> str:
     """mg_engine_option: which implementation runs for "gemm" ("auto", "stream", "slab"), "attention"
-    ("auto", "exact", "mfma") or "scan" ("auto", "separate", "fused"), for the whole process. Returns the previous value (value None only
-    reads it)."""
+    ("auto", "exact", "mfma"), "scan" ("auto", "separate", "fused") or "step_graph" (decode steps replayed
+    from a captured HIP graph: "auto", "off", "on"), for the whole process. Returns the previous value
+    (value None only reads it)."""
     opt, names = _OPTIONS[name]
     prev = lib().mg_engine_option(opt, -1 if value is None else names.index(value))
     check(prev if prev < 0 else 0)
