@@ -127,6 +127,16 @@ int mg_sessions_prefill(mg_sessions* s, const int32_t* prompts, const int32_t* l
 /* quantSession.Append for every session (internal/quant/session.go:41-56): ids [n]. */
 int mg_sessions_step(mg_sessions* s, const int32_t* ids, float* logits, int32_t* argmax, double* prob, int flags);
 
+/* No counterpart in the reference: mg_sessions_step for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same kernels and results as
+ * mg_sessions_step with MG_PTR_DEVICE, but it allocates nothing: its workspace is a static 64 MiB array
+ * per GPU (held until the process ends) instead of the model's workspace. All pointers are device
+ * pointers; logits, argmax and prob may be NULL. A set whose sessions need more than 64 MiB of workspace
+ * (about 4300 sessions of c4's D256/H512/V4096 model, fewer for wider models) is MG_ERR_INVALID. Calls on
+ * one GPU share the array: calls that overlap in time on one GPU (other streams, other models) race;
+ * calls on one model's stream are ordered. The step is enqueued on the model's stream and not waited for. */
+int mg_sessions_step_noalloc(mg_sessions* s, const int32_t* ids, float* logits, int32_t* argmax, double* prob);
+
 /* generate.greedyLoop for every session without stop tokens (internal/generate/greedy.go:63-87):
  * Prefill(prompt), then max_tokens tokens, each the first-maximum argmax with its probability, with
  * Append after every token but the last. out_ids [n][max_tokens], out_probs [n][max_tokens]. */

@@ -73,6 +73,7 @@ SIGNATURES = {
     "mg_sessions_create": (_int, [_vp, _int, _int, ctypes.POINTER(_vp)]),
     "mg_sessions_prefill": (_int, [_vp, _vp, _vp, _int, _vp, _vp, _vp, _int]),
     "mg_sessions_step": (_int, [_vp, _vp, _vp, _vp, _vp, _int]),
+    "mg_sessions_step_noalloc": (_int, [_vp, _vp, _vp, _vp, _vp]),
     "mg_sessions_decode_greedy": (_int, [_vp, _vp, _vp, _int, _int, _vp, _vp, _int]),
     "mg_sessions_decode_greedy_until": (_int, [_vp, _vp, _vp, _int, _int, _vp, _int, _vp, _vp, _vp, _int]),
     "mg_sessions_state_bytes": (_ll, [_vp]),

@@ -76,17 +76,20 @@ void require(bool ok, const std::string& msg) {
 struct DevBuf {
     void* p = nullptr;
     size_t n = 0;
+    bool borrowed = false;  // points into memory the buffer does not own (never freed or grown)
     DevBuf() = default;
     DevBuf(const DevBuf&) = delete;
     DevBuf& operator=(const DevBuf&) = delete;
     ~DevBuf() { release(); }
     void release() {
-        if (p) (void)hipFree(p);
+        if (p && !borrowed) (void)hipFree(p);
         p = nullptr;
         n = 0;
+        borrowed = false;
     }
     void ensure(size_t bytes) {
         if (bytes <= n) return;
+        if (borrowed) throw Error(MG_ERR_INVALID, "internal: a borrowed buffer cannot grow");
         release();
         if (bytes == 0) return;
         hipError_t e = hipMalloc(&p, bytes);
@@ -207,6 +210,7 @@ struct mg_model {
     // caller-owned cancellation flag polled by batched decodes (mg_model_set_cancel); set without the lock
     std::atomic<const volatile int32_t*> cancel{nullptr};
     mg::Workspace ws;
+    mg::Workspace* wsp = nullptr;  // while set (an allocation-free call), the workspace in use instead of ws
     mg::Profile prof;
     std::mutex mu;
 };
@@ -400,39 +404,67 @@ void build_device_model(mg_model* m, const HostModel& hm, int max_context) {
 // ------------------------------------------------------------------------------------------------
 // Workspace sizing: every per-token buffer for up to `tokens` rows.
 // ------------------------------------------------------------------------------------------------
-void ensure_ws(mg_model* m, int tokens) {
-    Workspace& w = m->ws;
-    if (tokens <= w.cap_tokens) return;
-    w.gen++;
+// The workspace in use: the model's own, or the view of the static scratch an allocation-free call
+// installs for its duration.
+Workspace& ws_of(mg_model* m) { return m->wsp ? *m->wsp : m->ws; }
+
+// Calls f(buffer, bytes) for every workspace buffer that `tokens` rows need.
+template <class F>
+void ws_sizes(const mg_model* m, Workspace& w, int tokens, F&& f) {
     size_t M = (size_t)tokens;
     const size_t Mp = (size_t)round_up(tokens, LX_ROWS);  // limb operands are read in whole row tiles
     const size_t Dp = m->Dp, Hp = m->Hp, D = m->D;
-    w.cur.ensure(M * Dp * 4);
-    w.bin.ensure(M * Dp * 4);
-    w.nf.ensure(M * Dp * 4);
-    w.lam.ensure(M * Dp * 4);
-    w.nl.ensure(Mp * 3 * Dp);
-    w.ns.ensure(Mp * 4);
-    w.xl.ensure(Mp * 9 * Dp);
-    w.xs.ensure(Mp * 4);
-    w.h.ensure(M * Hp * 4);
-    w.hl.ensure(Mp * 3 * Hp);
-    w.hs.ensure(Mp * 4);
+    f(w.cur, M * Dp * 4);
+    f(w.bin, M * Dp * 4);
+    f(w.nf, M * Dp * 4);
+    f(w.lam, M * Dp * 4);
+    f(w.nl, Mp * 3 * Dp);
+    f(w.ns, Mp * 4);
+    f(w.xl, Mp * 9 * Dp);
+    f(w.xs, Mp * 4);
+    f(w.h, M * Hp * 4);
+    f(w.hl, Mp * 3 * Hp);
+    f(w.hs, Mp * 4);
     if (m->nattn) {
-        w.qkv.ensure(M * 3 * D * 4);
-        w.att.ensure(M * Dp * 4);
+        f(w.qkv, M * 3 * D * 4);
+        f(w.att, M * Dp * 4);
     }
-    w.stats.ensure(M * (m->Vp / LX_BN) * 12);
-    w.lse.ensure(M * 4);
-    w.tlog.ensure(M * 4);
-    w.logprob.ensure(M * 4);
-    w.argmax.ensure(M * 4);
-    w.prob.ensure(M * 8);
-    w.ids.ensure(M * 4);
-    w.tgt.ensure(M * 4);
-    w.rowmap.ensure(M * 4);
-    w.lens.ensure(M * 4);
+    f(w.stats, M * (m->Vp / LX_BN) * 12);
+    f(w.lse, M * 4);
+    f(w.tlog, M * 4);
+    f(w.logprob, M * 4);
+    f(w.argmax, M * 4);
+    f(w.prob, M * 8);
+    f(w.ids, M * 4);
+    f(w.tgt, M * 4);
+    f(w.rowmap, M * 4);
+    f(w.lens, M * 4);
+}
+
+void ensure_ws(mg_model* m, int tokens) {
+    Workspace& w = ws_of(m);
+    if (tokens <= w.cap_tokens) return;
+    w.gen++;
+    ws_sizes(m, w, tokens, [](DevBuf& b, size_t bytes) { b.ensure(bytes); });
     w.cap_tokens = tokens;
+}
+
+// Lays the buffers `tokens` rows need out in one region, each at a 256-byte boundary: returns the region's
+// size, and with base set makes every buffer of w a borrowed view into [base, base + size).
+size_t carve_ws(const mg_model* m, Workspace& w, int tokens, uint8_t* base) {
+    size_t off = 0;
+    ws_sizes(m, w, tokens, [&](DevBuf& b, size_t bytes) {
+        off = (off + 255) / 256 * 256;
+        if (base) {
+            b.release();
+            b.p = base + off;
+            b.n = bytes;
+            b.borrowed = true;
+        }
+        off += bytes;
+    });
+    if (base) w.cap_tokens = tokens;
+    return off;
 }
 
 GemmArgs lx_args(const int8_t* A, const float* As, const int8_t* W, int Np, int Kp, int M, int nvalid, float wscale) {
@@ -508,7 +540,7 @@ double row_bytes(const RowArgs& r) {
 // Row kernel helper: mode + optional norm, writes n (fp32) and the limb-expanded copy into ws.nl/ns.
 void row_call(mg_model* m, int M, int mode, const int32_t* ids, const float* src, int lds, const int32_t* row_map,
               const float* gamma, float* nout, bool limbs, hipStream_t s) {
-    Workspace& w = m->ws;
+    Workspace& w = ws_of(m);
     RowArgs r;
     r.M = M; r.D = m->D; r.Dp = m->Dp; r.mode = mode;
     r.ids = ids; r.emb = m->emb; r.emb_scale = m->emb_scale; r.V = m->V;
@@ -602,7 +634,7 @@ struct BodyCtx {
 };
 
 void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
-    Workspace& w = m->ws;
+    Workspace& w = ws_of(m);
     const int M = c.B * c.T;
     const int Dp = m->Dp, Hp = m->Hp, D = m->D;
     int bs = 0, ab = 0;
@@ -746,7 +778,7 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
 // per-tile softmax statistics, then the per-row combination.
 void run_head(mg_model* m, int M, const int32_t* row_map, const int32_t* tgt, float* logits_out, HeadCombineArgs hc,
               hipStream_t s) {
-    Workspace& w = m->ws;
+    Workspace& w = ws_of(m);
     // headLogits (internal/quant/stream.go:232-248)
     row_call(m, M, ROW_SRC, nullptr, nullptr, 0, row_map, m->final_norm, nullptr, true, s);
     GemmArgs g = lx_args(w.nl.as<int8_t>(), w.ns.as<float>(), m->headw, m->Vp, m->Dp, M, m->V, m->head_scale);
@@ -891,6 +923,36 @@ void copy_decode_outputs(bool dev, int S, int max_tokens, const int32_t* oi, con
 
 using namespace mg;
 
+// Workspace of the allocation-free decode step (mg_sessions_step_noalloc): one copy of this array per GPU
+// the library runs on, held until the process ends. Host code never uses its name as an address (the
+// name is a host-side stand-in): kernels get the per-device address scratch_setup resolves.
+constexpr size_t kScratchBytes = 64ull << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Resolves this device's copy of `scratch`, once per device, with that device current (mg_model_load).
+void scratch_setup(int device) {
+    require(device >= 0 && device < kMaxScratchDevices, "device index beyond the scratch table");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[device]) return;
+    void* p = nullptr;
+    HIPCHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    require(p != nullptr, "hipGetSymbolAddress returned no address for the scratch array");
+    g_scratch_ptr[device] = (uint8_t*)p;
+}
+
+uint8_t* scratch_ptr(int device) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    return (device >= 0 && device < kMaxScratchDevices) ? g_scratch_ptr[device] : nullptr;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* mg_last_error(void) { return g_last_error.c_str(); }
@@ -909,6 +971,7 @@ int mg_model_load(const uint8_t* data, size_t n, int max_context, mg_model** out
         validate_for_engine(hm);
         std::unique_ptr<mg_model> m(new mg_model());
         HIPCHECK(hipGetDevice(&m->device));
+        scratch_setup(m->device);
         build_device_model(m.get(), hm, max_context);
         HIPCHECK(hipStreamCreateWithFlags(&m->own_stream, hipStreamNonBlocking));
         m->stream = m->own_stream;
@@ -1045,7 +1108,7 @@ int mg_forward_batch(mg_model* m, const int32_t* ids, int B, int T, float* logit
         const int V = m->V;
         int chunk = (int)std::max<long long>(1, std::min<long long>(B, kMaxChunkTokens / std::max(T, 1)));
         ensure_ws(m, chunk * T);
-        Workspace& w = m->ws;
+        Workspace& w = ws_of(m);
         Staging st;
         for (int b0 = 0; b0 < B; b0 += chunk) {
             const int Bc = std::min(chunk, B - b0);
@@ -1143,7 +1206,7 @@ int mg_score_sequences(mg_model* m, const int32_t* tokens, const long long* offs
         Guard gd(m);
         hipStream_t s = m->stream;
         ensure_ws(m, (int)cap);
-        Workspace& w = m->ws;
+        Workspace& w = ws_of(m);
         Staging st;
         int32_t* tok_d = st.in(tokens, (size_t)n_tok, s);
         long long* start_d = st.out<long long>(max_rows);
@@ -1246,7 +1309,7 @@ void prefill_device(mg_sessions* s, const int32_t* prompts_d, const int32_t* len
     const int S = s->n;
     const int Tw = std::min(max_len, s->window);
     ensure_ws(m, S * Tw);
-    Workspace& w = m->ws;
+    Workspace& w = ws_of(m);
     w.tmp.ensure((size_t)S * Tw * 4);
     int32_t* ids_w = w.tmp.as<int32_t>();
     int32_t* lens_w = w.lens.as<int32_t>();
@@ -1322,7 +1385,7 @@ void step_graphed(mg_sessions* s, const int32_t* ids_d, float* logits_d, const H
     }
     ensure_ws(m, s->n);  // before any capture: no allocation may happen inside one
     const void* ptrs[4] = {ids_d, logits_d, hc.argmax, hc.prob};
-    const bool same = G.exec && G.ws_gen == m->ws.gen && G.opts == options_key() &&
+    const bool same = G.exec && G.ws_gen == ws_of(m).gen && G.opts == options_key() &&
                       std::equal(ptrs, ptrs + 4, G.ptrs);
     if (!same) {
         G.reset();
@@ -1345,7 +1408,7 @@ void step_graphed(mg_sessions* s, const int32_t* ids_d, float* logits_d, const H
             step_device(s, ids_d, logits_d, hc, st);
             return;
         }
-        G.ws_gen = m->ws.gen;
+        G.ws_gen = ws_of(m).gen;
         G.opts = options_key();
         std::copy(ptrs, ptrs + 4, G.ptrs);
     }
@@ -1395,6 +1458,40 @@ int mg_sessions_step(mg_sessions* s, const int32_t* ids, float* logits, int32_t*
         if (logits) std::memcpy(logits, h + o_lg, (size_t)S * m->V * 4);
         if (argmax) std::memcpy(argmax, h + o_am, (size_t)S * 4);
         if (prob) std::memcpy(prob, h + o_pb, (size_t)S * 8);
+        return MG_OK;
+    });
+}
+
+int mg_sessions_step_noalloc(mg_sessions* s, const int32_t* ids, float* logits, int32_t* argmax, double* prob) {
+    return guarded([&] {
+        require(s && ids, "mg_sessions_step_noalloc: null argument");
+        mg_model* m = s->m;
+        Guard gd(m);
+        uint8_t* base = scratch_ptr(m->device);
+        require(base != nullptr, "mg_sessions_step_noalloc: the scratch array of this device is not set up");
+        Workspace view;
+        const size_t need = carve_ws(m, view, s->n, nullptr);
+        if (need > kScratchBytes)
+            throw Error(MG_ERR_INVALID, "mg_sessions_step_noalloc: " + std::to_string(s->n) + " sessions of this model need " +
+                                            std::to_string(need) + " bytes of scratch; it holds " +
+                                            std::to_string(kScratchBytes) + " (use mg_sessions_step)");
+        carve_ws(m, view, s->n, base);
+        // the view replaces the model's workspace for this call only; the profiler (which creates events)
+        // is paused
+        struct Use {
+            mg_model* m;
+            bool prof;
+            ~Use() {
+                m->wsp = nullptr;
+                m->prof.on = prof;
+            }
+        } use{m, m->prof.on};
+        m->wsp = &view;
+        m->prof.on = false;
+        HeadCombineArgs hc;
+        hc.argmax = argmax;
+        hc.prob = prob;
+        step_device(s, ids, logits, hc, m->stream);
         return MG_OK;
     });
 }

@@ -185,6 +185,16 @@ class Sessions:
         check(lib().mg_sessions_step(self._h, ptr(ids), ptr(lg), ptr(am), ptr(pb), 0))
         return lg, am, pb
 
+    def step_device(self, ids, logits=None, argmax=None, prob=None):
+        """mg_sessions_step on device arrays (ids [n] int32; logits [n][V] fp32, argmax [n] int32, prob [n]
+        float64, each optional); enqueued on the model's stream."""
+        check(lib().mg_sessions_step(self._h, ptr(ids), ptr(logits), ptr(argmax), ptr(prob), MG_PTR_DEVICE))
+
+    def step_noalloc(self, ids, logits=None, argmax=None, prob=None):
+        """mg_sessions_step_noalloc: step_device without any allocation (the library's static per-GPU
+        scratch holds the workspace); device arrays only."""
+        check(lib().mg_sessions_step_noalloc(self._h, ptr(ids), ptr(logits), ptr(argmax), ptr(prob)))
+
     def decode_greedy(self, prompts2d, max_tokens, lens=None):
         p = _i32(prompts2d)
         n, L = p.shape

@@ -40,6 +40,7 @@ def test_null_arguments_are_errors():
     assert L.mg_forward_batch(None, None, 1, 1, None, None, None, None, 0) == _lib.MG_ERR_INVALID
     assert L.mg_sessions_state_bytes(None) == -1
     assert L.mg_model_set_cancel(None, None) == _lib.MG_ERR_INVALID
+    assert L.mg_sessions_step_noalloc(None, None, None, None, None) == _lib.MG_ERR_INVALID
 
 
 def _has_gpu():
