@@ -232,11 +232,13 @@ struct mg_sessions {
     uint8_t* io_host = nullptr;
     // The last step captured as a HIP graph, replayed while what its launches captured is unchanged:
     // the workspace's buffers, the engine options and the output pointers.
+    mg::DevBuf col;  // decode column of the graph-replayed steps (advanced by each step on the device)
     struct StepGraph {
         hipGraphExec_t exec = nullptr;
         long long ws_gen = -1;
         int opts = -1;
-        const void* ptrs[4] = {};
+        static constexpr int kKey = 11;
+        const void* ptrs[kKey] = {};
         bool failed = false;  // capture is not possible here: launch one kernel at a time
         void reset() {
             if (exec) (void)hipGraphExecDestroy(exec);
@@ -1332,7 +1334,7 @@ void step_device(mg_sessions* s, const int32_t* ids_d, float* logits_d, HeadComb
     c.B = S; c.T = 1; c.ids = ids_d; c.sess = s; c.step = true;
     run_body(m, c, st);
     run_head(m, S, nullptr, nullptr, logits_d, hc, st);
-    HIPCHECK(launch_set_pos(S, nullptr, s->pos.as<int32_t>(), 1, st));
+    HIPCHECK(launch_set_pos(S, nullptr, s->pos.as<int32_t>(), 1, st, const_cast<int32_t*>(hc.col)));
 }
 
 }  // namespace
@@ -1370,11 +1372,19 @@ int mg_sessions_prefill(mg_sessions* s, const int32_t* prompts, const int32_t* l
 
 namespace {
 
+// The device column counter of a batched decode, set to 1 (the prefill wrote column 0).
+const int32_t* start_columns(mg_sessions* s, hipStream_t st) {
+    s->col.ensure(4);
+    HIPCHECK(launch_fill_i32(s->col.as<int32_t>(), 1, 1, st));
+    return s->col.as<int32_t>();
+}
+
 // One decode step of every session (step_device), replayed from a captured HIP graph when the options
 // allow it and the profiler is off: a step is ~10 launches per block of a few microseconds each at small
-// batches, and the graph removes their host-side enqueue cost. The graph is captured again when the
-// workspace was reallocated, an option changed or the argument pointers differ; if capture fails the set
-// falls back to launching kernel by kernel.
+// batches, and the graph removes their host-side enqueue cost. Batched decodes pass the output column
+// through hc.col (device memory the step advances), so one graph serves every column. The graph is
+// captured again when the workspace was reallocated, an option changed or the arguments differ; if
+// capture fails the set falls back to launching kernel by kernel.
 void step_graphed(mg_sessions* s, const int32_t* ids_d, float* logits_d, const HeadCombineArgs& hc, hipStream_t st) {
     mg_model* m = s->m;
     const int mode = option(OPT_STEP_GRAPH);
@@ -1384,9 +1394,11 @@ void step_graphed(mg_sessions* s, const int32_t* ids_d, float* logits_d, const H
         return;
     }
     ensure_ws(m, s->n);  // before any capture: no allocation may happen inside one
-    const void* ptrs[4] = {ids_d, logits_d, hc.argmax, hc.prob};
+    const void* ptrs[mg_sessions::StepGraph::kKey] = {ids_d, logits_d, hc.argmax, hc.prob, hc.next_ids, hc.out_ids, hc.out_probs,
+                                hc.col, (const void*)(intptr_t)hc.out_ld, (const void*)(intptr_t)hc.out_col,
+                                hc.lse};
     const bool same = G.exec && G.ws_gen == ws_of(m).gen && G.opts == options_key() &&
-                      std::equal(ptrs, ptrs + 4, G.ptrs);
+                      std::equal(ptrs, ptrs + G.kKey, G.ptrs);
     if (!same) {
         G.reset();
         hipGraph_t graph = nullptr;
@@ -1410,7 +1422,7 @@ void step_graphed(mg_sessions* s, const int32_t* ids_d, float* logits_d, const H
         }
         G.ws_gen = ws_of(m).gen;
         G.opts = options_key();
-        std::copy(ptrs, ptrs + 4, G.ptrs);
+        std::copy(ptrs, ptrs + G.kKey, G.ptrs);
     }
     HIPCHECK(hipGraphLaunch(G.exec, st));
 }
@@ -1519,10 +1531,8 @@ int mg_sessions_decode_greedy(mg_sessions* s, const int32_t* prompts, const int3
         hc.next_ids = s->next_ids.as<int32_t>();
         hc.out_ids = oi; hc.out_probs = op; hc.out_ld = max_tokens; hc.out_col = 0;
         prefill_device(s, p_d, l_d, max_len, nullptr, hc, st);
-        for (int k = 1; k < max_tokens; k++) {
-            hc.out_col = k;
-            step_device(s, s->next_ids.as<int32_t>(), nullptr, hc, st);
-        }
+        hc.col = start_columns(s, st);
+        for (int k = 1; k < max_tokens; k++) step_graphed(s, s->next_ids.as<int32_t>(), nullptr, hc, st);
         if (!dev) {
             HIPCHECK(hipMemcpyAsync(out_ids, oi, (size_t)S * max_tokens * 4, hipMemcpyDeviceToHost, st));
             if (out_probs) HIPCHECK(hipMemcpyAsync(out_probs, op, (size_t)S * max_tokens * 8, hipMemcpyDeviceToHost, st));
@@ -1566,9 +1576,9 @@ int mg_sessions_decode_greedy_until(mg_sessions* s, const int32_t* prompts, cons
         prefill_device(s, p_d, l_d, max_len, nullptr, hc, st);
         tr.scan(0);
         const bool first = tr.keep_going(0);  // false: cancelled before the first token
+        hc.col = start_columns(s, st);
         for (int k = 1; first && k < max_tokens && tr.keep_going(k); k++) {
-            hc.out_col = k;
-            step_device(s, s->next_ids.as<int32_t>(), nullptr, hc, st);
+            step_graphed(s, s->next_ids.as<int32_t>(), nullptr, hc, st);
             tr.scan(k);
         }
         tr.finish();
@@ -1636,7 +1646,7 @@ int mg_sessions_decode_sample(mg_sessions* s, const int32_t* prompts, const int3
         pick(0);
         const bool first = tr.keep_going(0);  // false: cancelled before the first token
         for (int k = 1; first && k < max_tokens && tr.keep_going(k); k++) {
-            step_device(s, s->next_ids.as<int32_t>(), lg, hc, st);
+            step_graphed(s, s->next_ids.as<int32_t>(), lg, hc, st);
             pick(k);
         }
         tr.finish();

@@ -307,7 +307,6 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
         // logits are -inf): their max, then the sum of exp(l - max) and the first channel holding the max.
         // Two passes over registers: no running rescale, and the argmax only when it is wanted.
         const float l2e = 1.4426950408889634f;
-        const int t = row.tgt - nb;  // the target's position among this lane's channels
         float* orow = g.out ? g.out + (long long)m * g.ldo : nullptr;
         float y[8][4];
 #pragma unroll
@@ -318,14 +317,28 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
 #pragma unroll
             for (int r = 0; r < 4; r++) y[ti][r] = fmaf(limb_dot(acc, ti, r), sw, bb[r]);
             if constexpr (STG) {
-                if (orow) stg_put(stg, lane, ti, y[ti]);
+                if (orow || g.tgt) stg_put(stg, lane, ti, y[ti]);
             } else if (orow && mok) {
                 const int nv = g.nvalid - n;
                 if (nv > 0) store4(orow + n, y[ti], nv, vec);
             }
-            if (mok && t >= ti * 16 && t < ti * 16 + 4) {
-                const int r = t & 3;
-                g.tlog[m] = r == 0 ? y[ti][0] : r == 1 ? y[ti][1] : r == 2 ? y[ti][2] : y[ti][3];
+        }
+        // the target logit of each token row: from the staged tile, one lane per row; without staging,
+        // the lane holding it selects it without branches
+        if (g.tgt) {
+            if constexpr (STG) {
+                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the staged tile has landed
+                __builtin_amdgcn_wave_barrier();
+                const int t0 = row.tgt - n0;
+                if (lane < 16 && mok && t0 >= 0 && t0 < LX_BN) g.tlog[m] = stg[lane * STG_LD + t0];
+            } else {
+                const int t = row.tgt - nb;  // the target's position among this lane's channels
+                float tv = 0.0f;
+#pragma unroll
+                for (int ti = 0; ti < 8; ti++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) tv = t == ti * 16 + r ? y[ti][r] : tv;
+                if (mok && t >= 0 && t < LX_BN && (t & 12) == 0) g.tlog[m] = tv;
             }
         }
         float mx = y[0][0];

@@ -1491,8 +1491,9 @@ __global__ __launch_bounds__(256) void head_combine_kernel(HeadCombineArgs a) {
         a.logprob[m] = (tg >= 0 && tg < a.V) ? a.tlog[m] - lse : __int_as_float(0x7fc00000);
     }
     if (a.next_ids) a.next_ids[m] = bi;
-    if (a.out_ids) a.out_ids[(long long)m * a.out_ld + a.out_col] = bi;
-    if (a.out_probs) a.out_probs[(long long)m * a.out_ld + a.out_col] = p;
+    const int oc = a.col ? *a.col : a.out_col;
+    if (a.out_ids) a.out_ids[(long long)m * a.out_ld + oc] = bi;
+    if (a.out_probs) a.out_probs[(long long)m * a.out_ld + oc] = p;
 }
 
 // eval's nll.score accumulates nats in float64 target by target (internal/eval/eval.go:25-48);
@@ -1567,9 +1568,10 @@ __global__ void export_kv_kernel(int B, int T, int D, int heads, int cap, const 
         }
 }
 
-__global__ void set_pos_kernel(int S, const int32_t* lens, int32_t* pos, int add) {
+__global__ void set_pos_kernel(int S, const int32_t* lens, int32_t* pos, int add, int32_t* col) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < S) pos[i] = (lens ? lens[i] : pos[i]) + add;
+    if (i == 0 && col) *col += 1;
 }
 
 __global__ void fill_i32_kernel(int32_t* p, int n, int v) {
@@ -1891,9 +1893,9 @@ hipError_t launch_export_kv(int B, int T, int D, int heads, int cap, const int32
     return hipGetLastError();
 }
 
-hipError_t launch_set_pos(int S, const int32_t* lens, int32_t* pos, int add, hipStream_t s) {
+hipError_t launch_set_pos(int S, const int32_t* lens, int32_t* pos, int add, hipStream_t s, int32_t* col) {
     if (S <= 0) return hipSuccess;
-    hipLaunchKernelGGL(set_pos_kernel, dim3((S + 255) / 256), dim3(256), 0, s, S, lens, pos, add);
+    hipLaunchKernelGGL(set_pos_kernel, dim3((S + 255) / 256), dim3(256), 0, s, S, lens, pos, add, col);
     return hipGetLastError();
 }
 

@@ -128,6 +128,8 @@ struct HeadCombineArgs {
     int32_t* out_ids = nullptr;    // [M][out_ld] at column out_col
     double* out_probs = nullptr;
     int out_ld = 0, out_col = 0;
+    const int32_t* col = nullptr;  // when set, the output column is *col instead of out_col (one captured
+                                   // decode step serves every column)
 };
 hipError_t launch_head_combine(const HeadCombineArgs& a, hipStream_t s);
 
@@ -142,7 +144,8 @@ hipError_t launch_export_ring(int B, int T, int Dp, int ring, const int32_t* len
                               hipStream_t s);
 hipError_t launch_export_kv(int B, int T, int D, int heads, int cap, const int32_t* lens, const float* qkv,
                             float* kring, float* vring, hipStream_t s);
-hipError_t launch_set_pos(int S, const int32_t* lens, int32_t* pos, int add, hipStream_t s);
+// pos[i] = (lens ? lens[i] : pos[i]) + add; with col set, also advances the decode column *col by one.
+hipError_t launch_set_pos(int S, const int32_t* lens, int32_t* pos, int add, hipStream_t s, int32_t* col = nullptr);
 hipError_t launch_fill_i32(int32_t* p, int n, int v, hipStream_t s);
 hipError_t launch_fill_f32(float* p, long long n, float v, hipStream_t s);
 

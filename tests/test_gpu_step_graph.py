@@ -60,3 +60,35 @@ def test_graph_single_session_matches_oracle(restore_graph):
     assert_close(gs.prefill(toks[:5]), os_.prefill(toks[:5]), what="prefill")
     for i in range(5, 40):
         assert_close(gs.append(toks[i]), os_.append(toks[i]), what=f"append {i}")
+
+
+@pytest.mark.parametrize("cfg", ["c4", "c3"])
+def test_graph_decodes_equal_eager(restore_graph, cfg):
+    """Batched decodes (greedy, greedy with stop tokens, sampled) replay one captured step for every column
+    (the column advances in device memory): the same tokens, probabilities and reply lengths as launching
+    each step kernel by kernel, with eager work on the model between the calls."""
+    data = model_bytes(cfg)
+    spec = synth.CONFIGS[cfg]["spec"]
+    prompts = synth.token_ids(11, f"graph-dec:{cfg}", (24, 7), spec.V)
+    lens = (np.arange(24) % 7 + 1).astype(np.int32)
+    res = {}
+    for mode in ("off", "on"):
+        engine_option("step_graph", mode)
+        m = Model(data)
+        ss = m.sessions(24)
+        a = ss.decode_greedy(prompts, 30, lens)
+        m.forward_batch(synth.token_ids(12, "graph-dec:batch", (40, 16), spec.V))
+        stops = [int(x) for x in a[0][:3, 5]]  # tokens that do occur, so some replies stop early
+        b = ss.decode_greedy_until(prompts, 30, stops, lens)
+        c = ss.decode_sample(prompts, 30, list(range(24)), temperature=0.8, top_k=20, top_p=0.9, rep_penalty=1.1,
+                             stops=stops, lens=lens)
+        res[mode] = (a, b, c)
+    (ea, eb, ec), (ga, gb, gc) = res["off"], res["on"]
+    assert np.array_equal(ea[0], ga[0]) and np.array_equal(ea[1].view(np.uint64), ga[1].view(np.uint64))
+    assert np.array_equal(eb[2], gb[2]) and (eb[2] < 30).any()
+    for i in range(24):
+        k = eb[2][i]
+        assert np.array_equal(eb[0][i, :k], gb[0][i, :k])
+        assert np.array_equal(eb[1][i, :k].view(np.uint64), gb[1][i, :k].view(np.uint64))
+        assert np.array_equal(ec[0][i, :ec[1][i]], gc[0][i, :gc[1][i]])
+    assert np.array_equal(ec[1], gc[1])
