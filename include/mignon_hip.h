@@ -281,8 +281,11 @@ int mg_quantize_f32(const float* w, long long n, int8_t* q, float* scale, int fl
  *     fits). Both give bit-identical results; automatic picks the slab kernel for large batches.
  *   MG_OPT_ATTENTION_KERNEL: MG_ATTN_EXACT keeps the reference's sequential dot-product and softmax
  *     order (bit-identical given equal inputs); MG_ATTN_MFMA computes scores and P.V on the matrix
- *     cores (fp32, other summation order). Automatic picks the matrix cores where they apply (head width
- *     a multiple of 4 up to 64, attended span up to 64 keys, or longer spans for narrower heads).
+ *     cores (fp32, other summation order); MG_ATTN_FUSED also computes the attention projection inside
+ *     the attention kernel, per sequence and head (teacher-forced batches of 128-token sequences, head
+ *     width 32 or 64), with results bit-identical to MG_ATTN_MFMA. Automatic fuses where that applies,
+ *     else picks the matrix cores where they apply (head width a multiple of 4 up to 64, attended span
+ *     up to 64 keys, or longer spans for narrower heads).
  *   MG_OPT_SCAN_KERNEL: MG_SCAN_SEPARATE writes the latch state of every position, then limb-expands
  *     the rule input [n | left | g] in a second kernel; MG_SCAN_FUSED does both in one pass without
  *     writing the latch state. Both give byte-identical operands. The fused kernel applies where the
@@ -305,6 +308,7 @@ int mg_quantize_f32(const float* w, long long n, int8_t* q, float* scale, int fl
 #define MG_GEMM_SLAB 2
 #define MG_ATTN_EXACT 1
 #define MG_ATTN_MFMA 2
+#define MG_ATTN_FUSED 3
 int mg_engine_option(int option, int value);
 
 #ifdef __cplusplus

@@ -19,7 +19,7 @@ MG_ERR_UNSUPPORTED = -5
 MG_PTR_DEVICE = 1
 MG_OPT_GEMM_KERNEL, MG_OPT_ATTENTION_KERNEL, MG_OPT_SCAN_KERNEL = 0, 1, 2
 MG_GEMM_STREAM, MG_GEMM_SLAB = 1, 2
-MG_ATTN_EXACT, MG_ATTN_MFMA = 1, 2
+MG_ATTN_EXACT, MG_ATTN_MFMA, MG_ATTN_FUSED = 1, 2, 3
 MG_SCAN_SEPARATE, MG_SCAN_FUSED = 1, 2
 MG_OPT_STEP_GRAPH, MG_STEP_EAGER, MG_STEP_GRAPH = 3, 1, 2
 

@@ -48,7 +48,7 @@ int options_key() {
 int set_option(int opt, int value) {
     if (opt < 0 || opt >= OPT_COUNT) return -1;
     if (value < 0) return g_options[opt].load();
-    if (value > 2) return -1;
+    if (value > (opt == OPT_ATTENTION_KERNEL ? 3 : 2)) return -1;
     return g_options[opt].exchange(value);
 }
 
@@ -125,12 +125,13 @@ struct DevBlock {
 // Kernel classes timed by the optional profiler (HIP events around every launch on the launch stream).
 enum KClass : int {
     K_ROW = 0, K_GEMM_LATCH, K_SCAN, K_LATCH_STEP, K_GEMM_GLU, K_GEMM_HIGHWAY, K_GEMM_QKV, K_ATTN, K_ATTN_STEP,
-    K_GEMM_OUT, K_GEMM_LOGITS, K_HEAD_COMBINE, K_GEMM_PROBS, K_BITS, K_EXPORT, K_GEMM_I8, K_SAMPLE, K_NCLASS
+    K_GEMM_OUT, K_GEMM_LOGITS, K_HEAD_COMBINE, K_GEMM_PROBS, K_BITS, K_EXPORT, K_GEMM_I8, K_SAMPLE, K_QKV_ATTN,
+    K_NCLASS
 };
 const char* const kClassNames[K_NCLASS] = {
     "row_norm_pack", "gemm_latch", "latch_scan", "latch_step", "gemm_glu", "gemm_highway", "gemm_qkv",
     "attention", "attention_step", "gemm_out", "gemm_logits", "head_combine", "gemm_probs", "bits",
-    "state_export", "gemm_i8", "sample"};
+    "state_export", "gemm_i8", "sample", "qkv_attention"};
 
 struct Profile {
     bool on = false;
@@ -731,10 +732,28 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
             // attendPosition (internal/quant/attention.go:69-104)
             bool att_limbs = false;  // the attention kernel wrote the out projection's operand itself
             row_call(m, M, ROW_SRC, nullptr, nullptr, 0, nullptr, blk.anorm, nullptr, true, s);
+            // teacher-forced batches without a session export: the projection fused with attention, when
+            // the shapes fit (q, k and v never go through memory)
+            QkvAttnArgs qa;
+            qa.B = c.B; qa.T = c.T; qa.D = D; qa.Dp = Dp; qa.heads = m->heads; qa.window = m->window; qa.cap = m->cap;
+            qa.A = w.nl.as<int8_t>(); qa.As = w.ns.as<float>(); qa.W = blk.qkv; qa.Np3 = m->Np3; qa.wscale = blk.sqkv;
+            qa.att = w.att.as<float>();
+            const int am = option(OPT_ATTENTION_KERNEL);
+            const bool fused = !c.step && !c.sess && (am == ATTN_AUTO || am == ATTN_FUSED) && qkv_attention_fits(qa);
             GemmArgs g = lx_args(w.nl.as<int8_t>(), w.ns.as<float>(), blk.qkv, m->Np3, Dp, M, 3 * D, blk.sqkv);
             g.out = w.qkv.as<float>(); g.ldo = 3 * D;
-            gemm(m, EPI_F32, g, s);
-            if (c.step) {
+            if (fused) {
+                double bytes = 0, ops = 0;
+                if (m->prof.on) {
+                    gemm_work(m, EPI_F32, g, bytes, ops);
+                    bytes += (double)M * (4.0 * D - 4.0 * 3 * D);  // the attention output instead of q, k, v
+                }
+                ProfScope ps(m->prof, K_QKV_ATTN, s, bytes, ops);
+                HIPCHECK(launch_qkv_attention(qa, s));
+            } else {
+                gemm(m, EPI_F32, g, s);
+            }
+            if (!fused && c.step) {
                 AttnStepArgs aa;
                 aa.S = M; aa.D = D; aa.Dp = Dp; aa.heads = m->heads; aa.window = m->window; aa.cap = m->cap;
                 aa.pos = c.sess->pos.as<int32_t>(); aa.qkv = w.qkv.as<float>();
@@ -750,7 +769,7 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                 } else {
                     HIPCHECK(launch_attention_step(aa, s));
                 }
-            } else {
+            } else if (!fused) {
                 if (c.sess) {
                     ProfScope ps(m->prof, K_EXPORT, s);
                     HIPCHECK(launch_export_kv(c.B, c.T, D, m->heads, m->cap, c.lens, w.qkv.as<float>(),

@@ -986,6 +986,175 @@ __global__ __launch_bounds__(64 * G) void attention_mfma_kernel(AttnArgs a, int 
     }
 }
 
+// ------------------------------------------------------------------------------------------------
+// Attention projection fused with windowed attention (teacher-forced forward, 128-token sequences)
+// ------------------------------------------------------------------------------------------------
+// A workgroup of 8 waves holds head h's slab of the QKV weights in LDS (per K step: the head's q, k and v
+// fragments, 3*ND KiB) and streams a run of sequences through it. Per sequence, wave w takes tokens
+// 16w..16w+15: its limb fragments (all K steps, fetched while the previous sequence's attention runs)
+// meet the slab on v_mfma_i32_16x16x64_i8 once for k, once for v, once for q. The epilogue is the QKV
+// GEMM's (EPI_F32: three digit sums combined, times row scale and weight scale), and its layout (lane L:
+// token L & 15, channels 16i + 4(L >> 4) + r) is already the Q^T operand of attention_mfma_kernel, whose
+// key layout the k rows are written in (LDS row = key - kbase) and whose value transpose the v registers
+// are written in after the scores. Scores, softmax and P.V then run exactly as in attention_mfma_kernel
+// with one group of G = 8 tiles, so the output is the same bit for bit, without the fp32 q/k/v round trip
+// through memory.
+template <int ND, int NKB, int KC>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void qkv_attention_kernel(
+    QkvAttnArgs a, int run_seqs, int n_runs) {
+    constexpr int G = 8;
+    constexpr int DP = 16 * ND;               // head width
+    constexpr int KEYS = 16 * (NKB + G - 1);  // key rows of attention_mfma_kernel: keys kbase .. kbase + KEYS - 1
+    constexpr int ZROWS = 16 * (NKB - 1);     // its leading rows: keys before the sequence start, never read
+                                              // (every key block holding them is skipped)
+    constexpr int KS = DP + 4;                // K row stride (floats), as attention_mfma_kernel
+    constexpr int VS = KEYS - ZROWS + 4;      // V^T row stride: the allocated keys, +4 as there
+    constexpr int NF = 3 * ND;                // weight fragments per K step
+    constexpr int SLAB = KC * NF * 1024;
+    constexpr int KBYTES = (KEYS - ZROWS) * KS * 4;
+    extern __shared__ __align__(16) int8_t qa_smem[];
+    int8_t* slab = qa_smem;
+    // K rows and V^T columns of keys 0..127 only, addressed as attention_mfma_kernel addresses its buffer
+    // (key row / column key - kbase, never below ZROWS), so that its score and P.V routines run unchanged
+    float* klds = (float*)(qa_smem + SLAB) - ZROWS * KS;
+    float* vlds = (float*)(qa_smem + SLAB + KBYTES) - ZROWS;
+    const int slot = blockIdx.x >> 3;
+    const int h = slot % a.heads;
+    const int run = (slot / a.heads) * 8 + (blockIdx.x & 7);  // all heads of a run on one XCD
+    if (run >= n_runs) return;
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int qi = lane & 15, kg = lane >> 4;
+    const int D = a.D, T = 16 * G;
+    {
+        // slab[ks][f][1 KiB], f = part*ND + i: fragment (part*D + h*DP)/16 + i of K step ks (part 0 q, 1 k, 2 v)
+        const long long np16 = a.Np3 >> 4;
+        for (int c = tid; c < KC * NF * 64; c += 512) {
+            const int ks = c / (NF * 64), f = (c >> 6) % NF, o = (c & 63) << 4;
+            const int part = f / ND, i = f - part * ND;
+            const long long frag = ((part * D + h * DP) >> 4) + i;
+            *(v4i*)(slab + ((long long)c << 4)) = *(const v4i*)(a.W + (ks * np16 + frag) * 1024 + o);
+        }
+    }
+    const float scale = (float)(1.0 / sqrt((double)DP));
+    const int kbase = 16 - 16 * NKB;
+    int skip = 0;  // leading key blocks of this wave wholly before the sequence start (as attention_mfma_kernel)
+#pragma unroll
+    for (int kb = 0; kb < NKB - 1; kb++)
+        if (kbase + 16 * (w + kb) + 15 < 0) skip = kb + 1;
+    skip = min(skip, 4);
+    const int t = 16 * w + qi;
+    const int lo = max(window_start(t, a.window), t - a.cap + 1);
+    const int jstart = kbase + 16 * w;
+    const int key = t - kbase;  // this lane's token as a key row
+    const int s_begin = run * run_seqs, s_end = min(s_begin + run_seqs, a.B);
+    v4i af[KC][3];
+    auto load_a = [&](int b) {
+        const int8_t* ap = a.A + ((long long)b * (T / 16) + w) * (KC * 3 * 1024) + lane * 16;
+#pragma unroll
+        for (int ks = 0; ks < KC; ks++)
+#pragma unroll
+            for (int l = 0; l < 3; l++) af[ks][l] = *(const v4i*)(ap + (ks * 3 + l) * 1024);
+    };
+    load_a(s_begin);
+    __syncthreads();
+    const int8_t* wl = slab + lane * 16;
+    for (int b = s_begin; b < s_end; b++) {
+        const long long m0 = (long long)b * T + 16 * w;
+        const float sw = a.As[m0 + qi] * a.wscale;
+        v4f qv[ND];
+        // parts in the order k, v (both to LDS), q (kept in registers)
+#pragma unroll
+        for (int pi = 0; pi < 3; pi++) {
+            const int part = pi == 0 ? 1 : pi == 1 ? 2 : 0;
+            v4i acc[3][ND];
+#pragma unroll
+            for (int ks = 0; ks < KC; ks++) {
+                v4i wf[ND];
+#pragma unroll
+                for (int i = 0; i < ND; i++) wf[i] = *(const v4i*)(wl + ((ks * NF + part * ND + i) << 10));
+#pragma unroll
+                for (int i = 0; i < ND; i++)
+#pragma unroll
+                    for (int l = 0; l < 3; l++)
+                        acc[l][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[i], af[ks][l],
+                                                                          ks == 0 ? v4i{0, 0, 0, 0} : acc[l][i], 0, 0, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, ND, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 3 * ND, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < ND; i++) {
+                v4f v;
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    v[r] = fmaf((float)acc[2][i][r], kInvLimb2, fmaf((float)acc[1][i][r], kInvLimb1, (float)acc[0][i][r])) * sw;
+                if (pi == 0) {
+                    *(v4f*)(klds + key * KS + 16 * i + 4 * kg) = v;
+                } else if (pi == 1) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int d = 16 * i + 4 * kg + r;
+                        vlds[d * VS + (key ^ vswz(d))] = v[r];
+                    }
+                } else {
+                    qv[i] = v;
+                }
+            }
+        }
+        // the next sequence's fragments load during this one's attention
+        if (b + 1 < s_end) load_a(b + 1);
+        __syncthreads();  // every key row and value column is written
+        v4f s[NKB];
+        switch (skip) {
+            case 0: attn_scores<ND, NKB, KS, 0>(s, klds, w, qi, kg, qv); break;
+            case 1: attn_scores<ND, NKB, KS, 1>(s, klds, w, qi, kg, qv); break;
+            case 2: attn_scores<ND, NKB, KS, 2>(s, klds, w, qi, kg, qv); break;
+            case 3: attn_scores<ND, NKB, KS, 3>(s, klds, w, qi, kg, qv); break;
+            default: attn_scores<ND, NKB, KS, 4>(s, klds, w, qi, kg, qv); break;
+        }
+        float mx = -3.40282347e38f;
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int j = jstart + 16 * kb + 4 * kg + r;
+                const float v = s[kb][r] * scale;
+                s[kb][r] = v;
+                if (j >= lo && j <= t && v > mx) mx = v;
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        float sum = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int j = jstart + 16 * kb + 4 * kg + r;
+                const float e = (j >= lo && j <= t) ? fast_exp_ref(s[kb][r] - mx) : 0.0f;
+                s[kb][r] = e;
+                sum += e;
+            }
+        sum += __shfl_xor(sum, 16, 64);
+        sum += __shfl_xor(sum, 32, 64);
+        const float inv = 1.0f / sum;
+        v4f o[ND];
+        switch (skip) {
+            case 0: attn_pv<ND, NKB, VS, 0>(o, s, inv, vlds, w, qi, kg); break;
+            case 1: attn_pv<ND, NKB, VS, 1>(o, s, inv, vlds, w, qi, kg); break;
+            case 2: attn_pv<ND, NKB, VS, 2>(o, s, inv, vlds, w, qi, kg); break;
+            case 3: attn_pv<ND, NKB, VS, 3>(o, s, inv, vlds, w, qi, kg); break;
+            default: attn_pv<ND, NKB, VS, 4>(o, s, inv, vlds, w, qi, kg); break;
+        }
+        // o[g][r] = out[query 16w + 4kg + r][dim 16g + qi]
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float* dst = a.att + (m0 + 4 * kg + r) * a.Dp + h * DP;
+#pragma unroll
+            for (int g = 0; g < ND; g++) dst[16 * g + qi] = o[g][r];
+        }
+        __syncthreads();  // every wave's keys and values are read before the next sequence's are written
+    }
+}
+
 // One wavefront per (session, head): lane j scores key j of the ring, lane i accumulates output i.
 template <int DH>
 __global__ __launch_bounds__(64) void attention_step_kernel(AttnStepArgs a) {
@@ -1661,6 +1830,31 @@ hipError_t attn_mfma(const AttnArgs& a, int dh, hipStream_t s) {
     }
 }
 
+template <int ND, int NKB, int KC>
+hipError_t qkv_attn_t(const QkvAttnArgs& a, hipStream_t s) {
+    constexpr int G = 8, DP = 16 * ND, KEYS = 16 * (NKB + G - 1), ZROWS = 16 * (NKB - 1);
+    constexpr size_t lds = (size_t)KC * 3 * ND * 1024 + sizeof(float) * ((KEYS - ZROWS) * (DP + 4) + DP * (KEYS + 4 - ZROWS));
+    static const hipError_t attr = hipFuncSetAttribute((const void*)qkv_attention_kernel<ND, NKB, KC>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
+    // runs of sequences per workgroup: long enough to amortise the slab copy, short enough that every
+    // XCD's CUs get several workgroups
+    const int R = std::max(1, std::min(32, a.B * a.heads / 2048));
+    const int n_runs = (a.B + R - 1) / R;
+    const int grid = 8 * a.heads * ((n_runs + 7) / 8);
+    hipLaunchKernelGGL((qkv_attention_kernel<ND, NKB, KC>), dim3(grid), dim3(512), lds, s, a, R, n_runs);
+    return hipGetLastError();
+}
+
+template <int ND, int NKB>
+hipError_t qkv_attn_k(const QkvAttnArgs& a, hipStream_t s) {
+    switch (a.Dp / 64) {
+        case 2: return qkv_attn_t<ND, NKB, 2>(a, s);
+        case 4: return qkv_attn_t<ND, NKB, 4>(a, s);
+        default: return qkv_attn_t<ND, NKB, 6>(a, s);
+    }
+}
+
 template <int DH>
 hipError_t attn_step_t(const AttnStepArgs& a, hipStream_t s) {
     if constexpr (DH % 4 == 0 && DH <= 64) {
@@ -1796,6 +1990,31 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
     w.rows = a.B * a.T; w.T = a.T; w.D = a.D; w.Dp = a.Dp; w.heads = a.heads; w.dh = dh;
     w.window = a.window; w.cap = a.cap; w.qkv = a.qkv; w.att = a.att;
     return launch_attention_wave(w, s);
+}
+
+bool qkv_attention_fits(const QkvAttnArgs& a) {
+    if (a.heads <= 0 || a.D % a.heads || a.T != 128 || a.cap <= 0) return false;
+    const int dh = a.D / a.heads;
+    if ((dh != 32 && dh != 64) || (a.Dp != 128 && a.Dp != 256 && a.Dp != 384) || a.Np3 % 16) return false;
+    AttnArgs t;
+    t.T = a.T; t.window = a.window; t.cap = a.cap;
+    const int nkb = attn_mfma_blocks(t);
+    return dh == 32 ? (nkb == 3 || nkb == 5 || nkb == 9) : (nkb == 3 || nkb == 5);
+}
+
+hipError_t launch_qkv_attention(const QkvAttnArgs& a, hipStream_t s) {
+    if (a.B <= 0) return hipSuccess;
+    if (!qkv_attention_fits(a)) return hipErrorInvalidValue;
+    AttnArgs t;
+    t.T = a.T; t.window = a.window; t.cap = a.cap;
+    const int nkb = attn_mfma_blocks(t), dh = a.D / a.heads;
+    switch ((dh / 16) * 100 + nkb) {
+        case 203: return qkv_attn_k<2, 3>(a, s);
+        case 205: return qkv_attn_k<2, 5>(a, s);
+        case 209: return qkv_attn_k<2, 9>(a, s);
+        case 403: return qkv_attn_k<4, 3>(a, s);
+        default: return qkv_attn_k<4, 5>(a, s);
+    }
 }
 
 bool attention_step_rows_fits(const AttnStepArgs& a) {

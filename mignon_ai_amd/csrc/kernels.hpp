@@ -9,7 +9,7 @@ namespace mg {
 enum RowMode : int { ROW_SRC = 0, ROW_EMBED = 1, ROW_RESID = 2, ROW_RULE = 3 };
 
 // Values of OPT_ATTENTION_KERNEL.
-enum AttnKernel : int { ATTN_AUTO = 0, ATTN_EXACT = 1, ATTN_MFMA = 2 };
+enum AttnKernel : int { ATTN_AUTO = 0, ATTN_EXACT = 1, ATTN_MFMA = 2, ATTN_FUSED = 3 };
 
 struct RowArgs {
     int M = 0, D = 0, Dp = 0;
@@ -73,6 +73,25 @@ struct AttnArgs {
     float* att = nullptr;        // [B*T][Dp]
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
+
+// The attention projection fused with windowed attention (teacher-forced forward): per sequence and head,
+// the head's q, k and v come from the limb-expanded normalised rows and the QKV weights on the int8 matrix
+// cores and stay on chip (k and v in LDS, q in registers); only the attention output is written. The
+// q, k, v values and the attention arithmetic are those of the separate QKV GEMM (EPI_F32) followed by
+// attention_mfma_kernel, so the output is bit-identical to that pair.
+struct QkvAttnArgs {
+    int B = 0, T = 0, D = 0, Dp = 0, heads = 0, window = 0, cap = 0;
+    const int8_t* A = nullptr;   // limb-expanded rows, GEMM fragment layout (K = Dp)
+    const float* As = nullptr;   // [B*T] row scales
+    const int8_t* W = nullptr;   // QKV weights, fragment layout [Dp/64][Np3/16][1 KiB], rows q | k | v
+    int Np3 = 0;
+    float wscale = 1.0f;
+    float* att = nullptr;        // [B*T][Dp]
+};
+// Whether the fused kernel takes these shapes: 128-token sequences, head width 32 or 64, Dp of 128, 256
+// or 384, and attended spans the matrix-core attention kernel covers.
+bool qkv_attention_fits(const QkvAttnArgs& a);
+hipError_t launch_qkv_attention(const QkvAttnArgs& a, hipStream_t s);
 
 // Attention for one streaming position per session over its key/value ring.
 struct AttnStepArgs {

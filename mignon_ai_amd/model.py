@@ -296,7 +296,7 @@ def quantize_f32(w):
     return q, np.float32(s[0])
 
 
-_OPTIONS = {"gemm": (0, ["auto", "stream", "slab"]), "attention": (1, ["auto", "exact", "mfma"]),
+_OPTIONS = {"gemm": (0, ["auto", "stream", "slab"]), "attention": (1, ["auto", "exact", "mfma", "fused"]),
             "scan": (2, ["auto", "separate", "fused"]), "step_graph": (3, ["auto", "off", "on"])}
 
 
@@ -324,7 +324,7 @@ def sample_logits(logits, recent=None, temperature=1.0, top_k=0, top_p=1.0, rep_
 
 def engine_option(name: str, value: str | None = None) -> str:
     """mg_engine_option: which implementation runs for "gemm" ("auto", "stream", "slab"), "attention"
-    ("auto", "exact", "mfma"), "scan" ("auto", "separate", "fused") or "step_graph" (decode steps replayed
+    ("auto", "exact", "mfma", "fused": the projection fused with matrix-core attention), "scan" ("auto", "separate", "fused") or "step_graph" (decode steps replayed
     from a captured HIP graph: "auto", "off", "on"), for the whole process. Returns the previous value
     (value None only reads it)."""
     opt, names = _OPTIONS[name]
