@@ -120,7 +120,9 @@ int mg_sessions_create(mg_model* m, int n, int context, mg_sessions** out);
  * [n][max_len] with lengths lens[n] (1..max_len); prompts longer than the window keep their last
  * window tokens. Outputs describe the next token after each prompt:
  *   logits [n][V] fp32, argmax [n] (first maximum, internal/generate/greedy.go:89-102),
- *   prob [n] double = 1 / sum exp(l - max). */
+ *   prob [n] double = 1 / sum exp(l - max) (argmaxProb, internal/generate/greedy.go:89-102; the sum is
+ *   accumulated in fp32 from the head's per-tile statistics, so the value has fp32 accuracy, about 1e-6
+ *   relative, where the reference sums math.Exp in float64). */
 int mg_sessions_prefill(mg_sessions* s, const int32_t* prompts, const int32_t* lens, int max_len, float* logits,
                         int32_t* argmax, double* prob, int flags);
 
@@ -146,7 +148,9 @@ int mg_sessions_decode_greedy(mg_sessions* s, const int32_t* prompts, const int3
 /* generate.greedyLoop with stop tokens (internal/generate/greedy.go:63-87) for every session: as
  * mg_sessions_decode_greedy, and each session's reply ends before the first of its n_stops (<= 8) stop
  * ids; out_counts[n] receives the reply lengths. Entries of out_ids / out_probs past a session's count
- * are unspecified: decoding ends once every session has stopped. */
+ * are unspecified: decoding ends once every session has stopped. Sessions that stopped are still stepped
+ * until all have (the reference's loop never Appends the stop token), so the set's state afterwards is
+ * unspecified: Prefill again before reusing it (as mg_generate_greedy does with a fresh set). */
 int mg_sessions_decode_greedy_until(mg_sessions* s, const int32_t* prompts, const int32_t* lens, int max_len,
                                     int max_tokens, const int32_t* stops, int n_stops, int32_t* out_ids,
                                     double* out_probs, int32_t* out_counts, int flags);
@@ -173,7 +177,8 @@ int mg_sample_logits(const double* logits, int n, int V, const int32_t* recent, 
  * penalize_prompt) + reply, a stop before any of the n_stops (<= 8) stop ids, Append. The reference
  * draws from Go's global math/rand, randomly seeded; here session i's draw at step k is the (k+1)-th
  * output of SplitMix64 seeded with seeds[i], top 53 bits over 2^53. out_ids [n][max_tokens],
- * out_counts[n] as mg_sessions_decode_greedy_until. Vocabularies up to 8192 tokens. */
+ * out_counts[n] and the set's state afterwards as mg_sessions_decode_greedy_until. Vocabularies up to
+ * 8192 tokens. */
 int mg_sessions_decode_sample(mg_sessions* s, const int32_t* prompts, const int32_t* lens, int max_len, int max_tokens,
                               const mg_sampling_t* sp, const uint64_t* seeds, const int32_t* stops, int n_stops,
                               int32_t* out_ids, int32_t* out_counts, int flags);
