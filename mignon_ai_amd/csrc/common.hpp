@@ -119,6 +119,18 @@ __device__ __forceinline__ float sigmoid_clamped_f32(float x) {
     return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
 }
 
+// sigmoidClamped from 2^x and the hardware reciprocal (see sigmoid_clamped_f32), as the GEMM epilogues
+// compute it; exactly 0 and 1 beyond |x| > 15 as in the reference.
+// The empty volatile asm pins the exponential and reciprocal before the saturation test: otherwise the
+// compiler moves them into a branch of their own, one divergent branch per element.
+__device__ __forceinline__ float sigmoid_epi(float x) {
+    const float e = __builtin_amdgcn_exp2f(x * -1.4426950408889634f);
+    float v = __builtin_amdgcn_rcpf(1.0f + e);
+    asm volatile("" : "+v"(v));
+    const float sat = x > 0.0f ? 1.0f : 0.0f;
+    return fabsf(x) > 15.0f ? sat : v;
+}
+
 // One element of the reference's vectorised e^x (vecExpASM_F32, internal/kernels/vec_amd64.s:281-430):
 // clamp to [-88, 88], k = nearest-even(x*log2e), two-constant ln2 reduction with FMA, degree-5
 // polynomial as an FMA chain, 2^k from exponent bits. Bit-identical to the reference on IEEE FMA.

@@ -126,12 +126,12 @@ struct DevBlock {
 enum KClass : int {
     K_ROW = 0, K_GEMM_LATCH, K_SCAN, K_LATCH_STEP, K_GEMM_GLU, K_GEMM_HIGHWAY, K_GEMM_QKV, K_ATTN, K_ATTN_STEP,
     K_GEMM_OUT, K_GEMM_LOGITS, K_HEAD_COMBINE, K_GEMM_PROBS, K_BITS, K_EXPORT, K_GEMM_I8, K_SAMPLE, K_QKV_ATTN,
-    K_NCLASS
+    K_STEP1, K_NCLASS
 };
 const char* const kClassNames[K_NCLASS] = {
     "row_norm_pack", "gemm_latch", "latch_scan", "latch_step", "gemm_glu", "gemm_highway", "gemm_qkv",
     "attention", "attention_step", "gemm_out", "gemm_logits", "head_combine", "gemm_probs", "bits",
-    "state_export", "gemm_i8", "sample", "qkv_attention"};
+    "state_export", "gemm_i8", "sample", "qkv_attention", "session_step"};
 
 struct Profile {
     bool on = false;
@@ -210,6 +210,7 @@ struct mg_model {
     hipStream_t stream = nullptr;
     // caller-owned cancellation flag polled by batched decodes (mg_model_set_cancel); set without the lock
     std::atomic<const volatile int32_t*> cancel{nullptr};
+    mg::Step1Block* s1blocks = nullptr;  // device copy of the blocks for step1_kernel
     mg::Workspace ws;
     mg::Workspace* wsp = nullptr;  // while set (an allocation-free call), the workspace in use instead of ws
     mg::Profile prof;
@@ -228,9 +229,11 @@ struct mg_sessions {
     int32_t* stop_host = nullptr;
     hipEvent_t stop_ev[kStopRing] = {};
     // mg_sessions_step with host pointers: device buffers for its ids and outputs and a pinned host
-    // mirror, kept for the life of the set (no allocation per step)
+    // mirror (coherent, mapped: io_host_dev is its device address), kept for the life of the set (no
+    // allocation per step)
     mg::DevBuf io;
     uint8_t* io_host = nullptr;
+    uint8_t* io_host_dev = nullptr;
     // The last step captured as a HIP graph, replayed while what its launches captured is unchanged:
     // the workspace's buffers, the engine options and the output pointers.
     mg::DevBuf col;  // decode column of the graph-replayed steps (advanced by each step on the device)
@@ -393,6 +396,18 @@ void build_device_model(mg_model* m, const HostModel& hm, int max_context) {
         std::vector<float> fn(hm.final_norm);
         fn.resize(Dp, 0.0f);
         m->final_norm = upload(m, fn);
+    }
+    {
+        std::vector<Step1Block> sb(m->blocks.size());
+        for (size_t b = 0; b < m->blocks.size(); b++) {
+            const DevBlock& db = m->blocks[b];
+            Step1Block& x = sb[b];
+            x.steps = db.steps; x.dil_base = db.dil_base; x.init_dil = db.init_dil; x.attn = db.attn ? 1 : 0;
+            x.w1 = db.w1; x.b1 = db.b1; x.s1 = db.s1; x.w2 = db.w2; x.b2 = db.b2; x.s2 = db.s2;
+            x.wsel = db.wsel; x.ssel = db.ssel; x.gamma = db.gamma; x.anorm = db.anorm;
+            x.qkv = db.qkv; x.sqkv = db.sqkv; x.wo = db.wo; x.so = db.so;
+        }
+        if (!sb.empty()) m->s1blocks = upload(m, sb);
     }
     if (m->nattn > 0) {
         if (m->heads <= 0 || D % m->heads) throw Error(MG_ERR_FORMAT, "model file: attention heads must divide the state size");
@@ -1345,9 +1360,36 @@ void prefill_device(mg_sessions* s, const int32_t* prompts_d, const int32_t* len
     HIPCHECK(launch_set_pos(S, lens_w, s->pos.as<int32_t>(), 0, st));
 }
 
+// The one-workgroup-per-session step for this set, when the option and the shapes allow it.
+constexpr int kStep1MaxSessions = 256;  // automatic selection: sets up to this size
+bool step1_args(mg_sessions* s, const int32_t* ids_d, float* logits_d, const HeadCombineArgs& hc, Step1Args& a) {
+    mg_model* m = s->m;
+    const int mode = option(OPT_STEP_KERNEL);
+    if (mode == 1 || (mode == 0 && s->n > kStep1MaxSessions) || !m->s1blocks) return false;
+    a.S = s->n; a.D = m->D; a.Dp = m->Dp; a.H = m->H; a.Hp = m->Hp; a.V = m->V; a.Vp = m->Vp;
+    a.NpD = m->NpD; a.Np3 = m->Np3; a.heads = m->nattn ? m->heads : 0; a.window = m->window; a.cap = m->cap;
+    a.ring = m->ring; a.nblocks = (int)m->blocks.size(); a.blocks = m->s1blocks;
+    a.emb = m->emb; a.emb_scale = m->emb_scale; a.headw = m->headw; a.headb = m->headb; a.head_scale = m->head_scale;
+    a.final_norm = m->final_norm; a.latch_base = m->latch_base;
+    a.pos = s->pos.as<int32_t>(); a.g = s->g.as<float>(); a.norm_ring = s->norm_ring.as<float>();
+    a.kring = s->kring.as<float>(); a.vring = s->vring.as<float>();
+    a.ids = ids_d; a.logits = logits_d; a.argmax = hc.argmax; a.prob = hc.prob; a.next_ids = hc.next_ids;
+    a.out_ids = hc.out_ids; a.out_probs = hc.out_probs; a.out_ld = hc.out_ld; a.out_col = hc.out_col; a.col = hc.col;
+    return step1_fits(a);
+}
+
 void step_device(mg_sessions* s, const int32_t* ids_d, float* logits_d, HeadCombineArgs hc, hipStream_t st) {
     mg_model* m = s->m;
     const int S = s->n;
+    Step1Args s1;
+    if (!hc.lse && !hc.logprob && step1_args(s, ids_d, logits_d, hc, s1)) {
+        {
+            ProfScope ps(m->prof, K_STEP1, st);
+            HIPCHECK(launch_step1(s1, st));
+        }
+        if (hc.col) HIPCHECK(launch_advance(const_cast<int32_t*>(hc.col), st));
+        return;
+    }
     ensure_ws(m, S);
     BodyCtx c;
     c.B = S; c.T = 1; c.ids = ids_d; c.sess = s; c.step = true;
@@ -1463,28 +1505,35 @@ int mg_sessions_step(mg_sessions* s, const int32_t* ids, float* logits, int32_t*
             step_graphed(s, ids, logits, hc, st);
             return MG_OK;
         }
-        // host pointers: the set's own device buffers and pinned mirror [ids | logits | argmax | prob]
+        // host pointers: the set's own device buffers and pinned mirror [ids | logits | argmax | prob].
+        // When the one-workgroup step runs, its single kernel reads the ids from and writes the outputs to
+        // the pinned mirror itself (no copies); otherwise the mirror is staged through the device buffers.
         auto up = [](size_t b) { return (b + 255) / 256 * 256; };
         const size_t o_lg = up((size_t)S * 4), o_am = o_lg + up((size_t)S * m->V * 4), o_pb = o_am + up((size_t)S * 4),
                      total = o_pb + (size_t)S * 8;
         if (s->io.n < total) {
             s->io.ensure(total);
             if (s->io_host) (void)hipHostFree(s->io_host);
-            s->io_host = nullptr;
-            HIPCHECK(hipHostMalloc((void**)&s->io_host, total, 0));
+            s->io_host = s->io_host_dev = nullptr;
+            HIPCHECK(hipHostMalloc((void**)&s->io_host, total, hipHostMallocCoherent | hipHostMallocMapped));
+            HIPCHECK(hipHostGetDevicePointer((void**)&s->io_host_dev, s->io_host, 0));
         }
-        uint8_t* d = s->io.as<uint8_t>();
         uint8_t* h = s->io_host;
         std::memcpy(h, ids, (size_t)S * 4);
-        HIPCHECK(hipMemcpyAsync(d, h, (size_t)S * 4, hipMemcpyHostToDevice, st));
+        Step1Args probe;
+        const bool direct = step1_args(s, nullptr, nullptr, HeadCombineArgs{}, probe);
+        uint8_t* d = direct ? s->io_host_dev : s->io.as<uint8_t>();
+        if (!direct) HIPCHECK(hipMemcpyAsync(d, h, (size_t)S * 4, hipMemcpyHostToDevice, st));
         HeadCombineArgs hc;
         hc.argmax = argmax ? (int32_t*)(d + o_am) : nullptr;
         hc.prob = prob ? (double*)(d + o_pb) : nullptr;
         float* lg = logits ? (float*)(d + o_lg) : nullptr;
         step_graphed(s, (const int32_t*)d, lg, hc, st);
-        if (logits) HIPCHECK(hipMemcpyAsync(h + o_lg, lg, (size_t)S * m->V * 4, hipMemcpyDeviceToHost, st));
-        if (argmax) HIPCHECK(hipMemcpyAsync(h + o_am, hc.argmax, (size_t)S * 4, hipMemcpyDeviceToHost, st));
-        if (prob) HIPCHECK(hipMemcpyAsync(h + o_pb, hc.prob, (size_t)S * 8, hipMemcpyDeviceToHost, st));
+        if (!direct) {
+            if (logits) HIPCHECK(hipMemcpyAsync(h + o_lg, lg, (size_t)S * m->V * 4, hipMemcpyDeviceToHost, st));
+            if (argmax) HIPCHECK(hipMemcpyAsync(h + o_am, hc.argmax, (size_t)S * 4, hipMemcpyDeviceToHost, st));
+            if (prob) HIPCHECK(hipMemcpyAsync(h + o_pb, hc.prob, (size_t)S * 8, hipMemcpyDeviceToHost, st));
+        }
         HIPCHECK(hipStreamSynchronize(st));
         if (logits) std::memcpy(logits, h + o_lg, (size_t)S * m->V * 4);
         if (argmax) std::memcpy(argmax, h + o_am, (size_t)S * 4);

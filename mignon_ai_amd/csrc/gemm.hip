@@ -48,18 +48,6 @@ __device__ __forceinline__ float limb_dot(const v4i (&acc)[3][8], int ti, int r)
     return fmaf((float)acc[2][ti][r], kInvLimb2, fmaf((float)acc[1][ti][r], kInvLimb1, (float)acc[0][ti][r]));
 }
 
-// sigmoidClamped from 2^x and the hardware reciprocal (see sigmoid_clamped_f32); exactly 0 and 1 beyond
-// |x| > 15 as in the reference.
-// The empty volatile asm pins the exponential and reciprocal before the saturation test: otherwise the
-// compiler moves them into a branch of their own, one divergent branch per element.
-__device__ __forceinline__ float sigmoid_epi(float x) {
-    const float e = __builtin_amdgcn_exp2f(x * -1.4426950408889634f);
-    float v = __builtin_amdgcn_rcpf(1.0f + e);
-    asm volatile("" : "+v"(v));
-    const float sat = x > 0.0f ? 1.0f : 0.0f;
-    return fabsf(x) > 15.0f ? sat : v;
-}
-
 // Per-token values the epilogue needs, loaded when the tile starts so that their latency hides behind
 // the tile's MFMAs.
 // (Only loads here: any arithmetic on a loaded value would make the compiler wait for it at once.)

@@ -1635,6 +1635,437 @@ __device__ __forceinline__ void merge_stats(float& bm, float& bs, int& bi, float
     bm = nm; bs = ns; bi = ni;
 }
 
+// ------------------------------------------------------------------------------------------------
+// One session's decode step in one workgroup (step1_kernel)
+// ------------------------------------------------------------------------------------------------
+constexpr int S1_THREADS = 512;
+
+// The row kernel's RMSNorm scale (1/rms) of one row x[0..D), by one wave: 16 partial sums in DotF32's
+// order, their fold, the unfused tail, then float32(sqrt(float64(ss/D + 1e-5))) (row_kernel).
+__device__ __forceinline__ float s1_rms_inv(const float* x, int D, int lane) {
+    const int p = lane & 15;
+    float part = 0.0f;
+    const int c16 = D >> 4;
+#pragma unroll 8
+    for (int c = 0; c < c16; c++) {
+        const float v = x[16 * c + p];
+        part = fmaf(v, v, part);
+    }
+    if (p < 8 && D - 16 * c16 >= 8) {
+        const float v = x[16 * c16 + p];
+        part = fmaf(v, v, part);
+    }
+    float v8[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) v8[q] = __shfl(part, q, 64) + __shfl(part, q + 8, 64);
+    float ss = hreduce8(v8);
+    for (int e = (D >> 3) << 3; e < D; e++) {
+        const float t = x[e];
+        const float pp = t * t;
+        ss = ss + pp;
+    }
+    const float rms = (float)sqrt((double)(ss / (float)D + 1e-5f));
+    return 1.0f / rms;
+}
+
+// Workgroup maximum of per-thread values (every thread gets it). red: 8 floats of LDS.
+__device__ __forceinline__ float s1_block_max(float v, float* red, int lane, int w) {
+    v = wave_max(v);
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    float m = red[0];
+#pragma unroll
+    for (int i = 1; i < S1_THREADS / 64; i++) m = fmaxf(m, red[i]);
+    __syncthreads();  // red is reused by the next reduction
+    return m;
+}
+
+// Limb planes of one row (values x[d] for d < Dvalid, zero up to Kp) in the single-row operand layout
+// xl[k >> 6][limb][k & 63]; returns the row scale. The digits and scale are the row kernel's.
+__device__ __forceinline__ float s1_limbs(const float* x, int Dvalid, int Kp, int8_t* xl, float* red, int tid,
+                                          int lane, int w) {
+    float m = 0.0f;
+    for (int d = tid; d < Dvalid; d += S1_THREADS) m = fmaxf(m, fabsf(x[d]));
+    const float amax = s1_block_max(m, red, lane, w);
+    float sc, inv;
+    limb_scale(amax, sc, inv);
+    for (int k = tid; k < Kp; k += S1_THREADS) {
+        const Limbs L = split_limbs(k < Dvalid ? x[k] : 0.0f, inv);
+        int8_t* o = xl + (k >> 6) * 192 + (k & 63);
+        o[0] = L.q0;
+        o[64] = L.q1;
+        o[128] = L.q2;
+    }
+    return sc;
+}
+
+// Fragments f[0..nf) (16 output channels each, nf <= 4) of an int8 weight matrix in the GEMM fragment
+// layout times the row's limb planes: the B operand of v_mfma_i32_16x16x64_i8 is the row in token column
+// 0, so only lanes with (lane & 15) == 0 take it; their accumulators hold channels 16f + 4(lane >> 4) + r,
+// one sum per plane. The weights of four K steps of all nf fragments are requested together, so a wave
+// waits for memory once per four K steps rather than once per fragment and step.
+__device__ __forceinline__ void s1_frags(const int8_t* W, int np16, int kc, const int (&f)[4], int nf,
+                                         const int8_t* xl, int lane, v4i (&acc)[4][3]) {
+#pragma unroll
+    for (int g = 0; g < 4; g++) acc[g][0] = acc[g][1] = acc[g][2] = v4i{0, 0, 0, 0};
+    const bool tok = (lane & 15) == 0;
+    const int8_t* xp = xl + (lane >> 4) * 16;
+    for (int k0 = 0; k0 < kc; k0 += 4) {
+        v4i wv[4][4];
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (g < nf && k0 + j < kc)
+                    wv[g][j] = *(const v4i*)(W + ((((long long)(k0 + j) * np16 + f[g]) << 10) + lane * 16));
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (k0 + j >= kc) break;
+            v4i xv[3];
+#pragma unroll
+            for (int l = 0; l < 3; l++) xv[l] = tok ? *(const v4i*)(xp + (k0 + j) * 192 + l * 64) : v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                if (g < nf)
+#pragma unroll
+                    for (int l = 0; l < 3; l++) acc[g][l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wv[g][j], xv[l], acc[g][l], 0, 0, 0);
+        }
+    }
+}
+
+__device__ __forceinline__ float s1_dot(const v4i (&acc)[3], int r) {
+    return fmaf((float)acc[2][r], kInvLimb2, fmaf((float)acc[1][r], kInvLimb1, (float)acc[0][r]));
+}
+
+// Matrix-vector phases of step1_kernel: wave w takes fragments w, w + 8, ... in groups of four
+// (S1_FRAGS, with `f`, `r` and the combined dot product `v` in scope of BODY for each channel its lane
+// holds) or fragment pairs (value 2q, gate 2q + 1) in groups of two (S1_PAIRS: `q`, `g4`, `r`, `vv`,
+// `vg`).
+#define S1_FRAGS(W, NP16, KC, BODY)                                                                  \
+    for (int f0 = w; f0 < (NP16); f0 += 4 * (S1_THREADS / 64)) {                                    \
+        int fl[4];                                                                                   \
+        int nf = 0;                                                                                  \
+        for (int g = 0; g < 4; g++) {                                                                \
+            fl[g] = f0 + g * (S1_THREADS / 64);                                                      \
+            if (fl[g] < (NP16)) nf = g + 1;                                                          \
+        }                                                                                            \
+        v4i acc[4][3];                                                                               \
+        s1_frags((W), (NP16), (KC), fl, nf, xl, lane, acc);                                          \
+        if ((lane & 15) == 0) {                                                                      \
+            _Pragma("unroll") for (int g = 0; g < 4; g++) {                                          \
+                if (g >= nf) break;                                                                  \
+                const int f = fl[g];                                                                 \
+                _Pragma("unroll") for (int r = 0; r < 4; r++) {                                      \
+                    const float v = s1_dot(acc[g], r);                                               \
+                    BODY                                                                             \
+                }                                                                                    \
+            }                                                                                        \
+        }                                                                                            \
+    }
+#define S1_PAIRS(W, NP16, KC, BODY)                                                                  \
+    for (int q0 = w; q0 < (NP16) / 2; q0 += 2 * (S1_THREADS / 64)) {                                \
+        const int q1 = q0 + S1_THREADS / 64;                                                         \
+        const int np = q1 < (NP16) / 2 ? 2 : 1;                                                      \
+        int fl[4] = {2 * q0, 2 * q0 + 1, 2 * q1, 2 * q1 + 1};                                        \
+        v4i acc[4][3];                                                                               \
+        s1_frags((W), (NP16), (KC), fl, 2 * np, xl, lane, acc);                                      \
+        if ((lane & 15) == 0) {                                                                      \
+            const int g4 = lane >> 4;                                                                \
+            _Pragma("unroll") for (int pp = 0; pp < 2; pp++) {                                       \
+                if (pp >= np) break;                                                                 \
+                const int q = pp == 0 ? q0 : q1;                                                     \
+                _Pragma("unroll") for (int r = 0; r < 4; r++) {                                      \
+                    const float vv = s1_dot(acc[2 * pp], r), vg = s1_dot(acc[2 * pp + 1], r);        \
+                    BODY                                                                             \
+                }                                                                                    \
+            }                                                                                        \
+        }                                                                                            \
+    }
+
+template <int DH>
+__global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
+    extern __shared__ __align__(16) float s1_smem[];
+    __shared__ float red[16];
+    __shared__ float rk_inv[8];
+    __shared__ float bcast[4];
+    const int s_ = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int D = a.D, Dp = a.Dp, H = a.H, Hp = a.Hp, V = a.V, Vp = a.Vp;
+    const int ntiles = Vp / LX_BN;
+    float* cur = s1_smem;
+    float* bin = cur + Dp;
+    float* nrm = bin + Dp;
+    float* lam = nrm + Dp;
+    float* hbuf = lam + Dp;
+    float* qkv = hbuf + Hp;
+    float* att = qkv + 3 * Dp;
+    float* logit = att + Dp;
+    float* tstats = logit + Vp;
+    float* rk = tstats + 4 * ntiles;
+    const int rkf = (rk_lds_floats(a.cap, DH) + 3) & ~3;  // per head, 16-byte aligned
+    int8_t* xl = (int8_t*)(rk + a.heads * rkf);
+    const int pos = a.pos[s_];
+    {
+        int id = a.ids[s_];
+        id = (id < 0 || id >= V) ? 0 : id;  // quant.Model.appendPosition clamps (stream.go:144-146)
+        for (int d = tid; d < Dp; d += S1_THREADS) {
+            const float v = d < D ? (float)a.emb[(long long)id * D + d] * a.emb_scale : 0.0f;
+            cur[d] = v;
+            bin[d] = v;
+        }
+    }
+    __syncthreads();
+    int bs = 0, ab = 0;
+    for (int b = 0; b < a.nblocks; b++) {
+        const Step1Block& B = a.blocks[b];
+        if (b > 0) {
+            // blockIn += cur; cur = blockIn (stream.go:157-163)
+            for (int d = tid; d < Dp; d += S1_THREADS) {
+                const float v = bin[d] + cur[d];
+                bin[d] = v;
+                cur[d] = v;
+            }
+            __syncthreads();
+        }
+        for (int st = 0; st < B.steps; st++, bs++) {
+            int dil = B.init_dil;
+            for (int q = 0; q < st && dil < 32; q++) dil *= B.dil_base;
+            dil = min(dil, 32);
+            // n = RMSNorm(cur; gamma) (stream.go:166-171)
+            if (B.gamma) {
+                if (w == 0) {
+                    const float inv = s1_rms_inv(cur, D, lane);
+                    if (lane == 0) bcast[0] = inv;
+                }
+                __syncthreads();
+                const float inv = bcast[0];
+                for (int d = tid; d < Dp; d += S1_THREADS) nrm[d] = d < D ? (cur[d] * inv) * B.gamma[d] : 0.0f;
+            } else {
+                for (int d = tid; d < Dp; d += S1_THREADS) nrm[d] = d < D ? cur[d] : 0.0f;
+            }
+            __syncthreads();
+            const float sn = s1_limbs(nrm, D, Dp, xl, red, tid, lane, w);
+            __syncthreads();
+            // lambda = sigmoid_clamped(n.W_sel*s + base) (stream.go:195-205)
+            {
+                const float sw = sn * B.ssel;
+                S1_FRAGS(B.wsel, a.NpD / 16, Dp / 64, {
+                    const int c = 16 * f + 4 * (lane >> 4) + r;
+                    if (c < D) lam[c] = sigmoid_epi(fmaf(v, sw, a.latch_base[c]));
+                });
+            }
+            __syncthreads();
+            // latch update, norm ring and the rule input [n | left | g] (latch_step_kernel)
+            float nv = 0.0f, lv = 0.0f, gv = 0.0f;
+            const int d = tid;
+            if (d < D) {
+                nv = nrm[d];
+                const float l = lam[d];
+                float* gp = a.g + ((long long)bs * a.S + s_) * Dp + d;
+                gv = *gp;
+                const float p1 = l * gv;
+                const float p2 = (1.0f - l) * nv;
+                gv = p1 + p2;
+                *gp = gv;
+                float* ring = a.norm_ring + ((long long)bs * a.S + s_) * a.ring * Dp;
+                ring[(long long)(pos % a.ring) * Dp + d] = nv;
+                if (pos >= dil) lv = ring[(long long)((pos - dil) % a.ring) * Dp + d];
+            }
+            const float amax = s1_block_max(fmaxf(fabsf(nv), fmaxf(fabsf(lv), fabsf(gv))), red, lane, w);
+            float sx, ix;
+            limb_scale(amax, sx, ix);
+            {
+                const float v3[3] = {nv, lv, gv};
+                if (d < Dp) {
+#pragma unroll
+                    for (int sg = 0; sg < 3; sg++) {
+                        const Limbs L = split_limbs(v3[sg], ix);
+                        const int k = sg * Dp + d;
+                        int8_t* o = xl + (k >> 6) * 192 + (k & 63);
+                        o[0] = L.q0;
+                        o[64] = L.q1;
+                        o[128] = L.q2;
+                    }
+                }
+            }
+            __syncthreads();
+            // h = GLU(x) (stream.go:214-220): fragment pairs (value 2q, gate 2q + 1)
+            {
+                const float sw = sx * B.s1;
+                S1_PAIRS(B.w1, 2 * Hp / 16, 3 * Dp / 64, {
+                    const int c = 16 * q + 4 * g4 + r;
+                    const float ov = fmaf(vv, sw, B.b1[32 * q + 4 * g4 + r]);
+                    const float gt = sigmoid_epi(fmaf(vg, sw, B.b1[32 * q + 16 + 4 * g4 + r]));
+                    hbuf[c] = c < H ? ov * gt : 0.0f;
+                });
+            }
+            __syncthreads();
+            const float sh = s1_limbs(hbuf, H, Hp, xl, red, tid, lane, w);
+            __syncthreads();
+            // cur = highway(cur, W2 h) (stream.go:222-229)
+            {
+                const float sw = sh * B.s2;
+                S1_PAIRS(B.w2, 2 * Dp / 16, Hp / 64, {
+                    const int c = 16 * q + 4 * g4 + r;
+                    if (c < D) {
+                        const float ov = fmaf(vv, sw, B.b2[32 * q + 4 * g4 + r]);
+                        const float gt = sigmoid_epi(fmaf(vg, sw, B.b2[32 * q + 16 + 4 * g4 + r]));
+                        const float x1 = (1.0f - gt) * cur[c];
+                        const float x2 = gt * ov;
+                        cur[c] = x1 + x2;
+                    }
+                });
+            }
+            __syncthreads();
+        }
+        if (B.attn) {
+            // attendPosition (internal/quant/attention.go:69-104)
+            if (w == 0) {
+                const float inv = s1_rms_inv(cur, D, lane);
+                if (lane == 0) bcast[0] = inv;
+            }
+            __syncthreads();
+            {
+                const float inv = bcast[0];
+                for (int d = tid; d < Dp; d += S1_THREADS) nrm[d] = d < D ? (cur[d] * inv) * B.anorm[d] : 0.0f;
+            }
+            __syncthreads();
+            const float sa = s1_limbs(nrm, D, Dp, xl, red, tid, lane, w);
+            __syncthreads();
+            {
+                const float sw = sa * B.sqkv;
+                S1_FRAGS(B.qkv, a.Np3 / 16, Dp / 64, {
+                    const int c = 16 * f + 4 * (lane >> 4) + r;
+                    if (c < 3 * D) qkv[c] = v * sw;
+                });
+            }
+            __syncthreads();
+            if (w < a.heads) {
+                AttnStepArgs sa_;
+                sa_.S = 1; sa_.D = D; sa_.Dp = Dp; sa_.heads = a.heads; sa_.window = a.window; sa_.cap = a.cap;
+                sa_.pos = a.pos + s_;
+                sa_.qkv = qkv;
+                const long long ring0 = ((long long)ab * a.S + s_) * a.heads * a.cap * DH;
+                sa_.kring = a.kring + ring0;
+                sa_.vring = a.vring + ring0;
+                const float o = rk_head<DH>(sa_, 0, w, lane, rk + w * rkf, rk_inv[w]);
+                if (lane < DH) att[w * DH + lane] = o;
+            }
+            __syncthreads();
+            const float so_ = s1_limbs(att, D, Dp, xl, red, tid, lane, w);
+            __syncthreads();
+            {
+                const float sw = so_ * B.so;
+                S1_FRAGS(B.wo, a.NpD / 16, Dp / 64, {
+                    const int c = 16 * f + 4 * (lane >> 4) + r;
+                    if (c < D) cur[c] = cur[c] + v * sw;
+                });
+            }
+            __syncthreads();
+            ab++;
+        }
+    }
+    // headLogits (internal/quant/stream.go:232-248)
+    if (a.final_norm) {
+        if (w == 0) {
+            const float inv = s1_rms_inv(cur, D, lane);
+            if (lane == 0) bcast[0] = inv;
+        }
+        __syncthreads();
+        const float inv = bcast[0];
+        for (int d = tid; d < Dp; d += S1_THREADS) nrm[d] = d < D ? (cur[d] * inv) * a.final_norm[d] : 0.0f;
+    } else {
+        for (int d = tid; d < Dp; d += S1_THREADS) nrm[d] = d < D ? cur[d] : 0.0f;
+    }
+    __syncthreads();
+    const float sf = s1_limbs(nrm, D, Dp, xl, red, tid, lane, w);
+    __syncthreads();
+    {
+        const float sw = sf * a.head_scale;
+        S1_FRAGS(a.headw, Vp / 16, Dp / 64, {
+            const int c = 16 * f + 4 * (lane >> 4) + r;
+            logit[c] = fmaf(v, sw, a.headb[c]);
+        });
+    }
+    __syncthreads();
+    if (a.logits) {  // coalesced: the row may live in host memory
+        float* lo = a.logits + (long long)s_ * V;
+        for (int c = tid; c < V; c += S1_THREADS) lo[c] = logit[c];
+    }
+    // per 128-channel tile: the logits epilogue's statistics (max, sum exp(l - max), first argmax), with
+    // its lane structure (lane group g4 = lane >> 4 holds channels 4g4 + 16ti + r)
+    const bool want_argmax = a.argmax || a.next_ids || a.out_ids;
+    for (int t = w; t < ntiles; t += S1_THREADS / 64) {
+        const float l2e = 1.4426950408889634f;
+        const int nb = t * LX_BN + 4 * (lane >> 4);
+        float y[8][4];
+#pragma unroll
+        for (int ti = 0; ti < 8; ti++) {
+            const float4 v = *(const float4*)(logit + nb + 16 * ti);
+            y[ti][0] = v.x; y[ti][1] = v.y; y[ti][2] = v.z; y[ti][3] = v.w;
+        }
+        float mx = y[0][0];
+#pragma unroll
+        for (int ti = 0; ti < 8; ti++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) mx = fmaxf(mx, y[ti][r]);
+        const float ml = mx == -INFINITY ? 0.0f : mx * l2e;
+        float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ti = 0; ti < 8; ti++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) s4[r] += __builtin_amdgcn_exp2f(fmaf(y[ti][r], l2e, -ml));
+        float bmax = mx, bsum = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+        int bidx = 0x7fffffff;
+        if (want_argmax && mx > -INFINITY) {
+            int off = 0;
+#pragma unroll
+            for (int ti = 7; ti >= 0; ti--)
+#pragma unroll
+                for (int r = 3; r >= 0; r--) off = y[ti][r] == mx ? ti * 16 + r : off;
+            bidx = nb + off;
+        }
+#pragma unroll
+        for (int o = 16; o <= 32; o <<= 1) {
+            float om = __shfl_xor(bmax, o, 64), os = __shfl_xor(bsum, o, 64);
+            int oi = __shfl_xor(bidx, o, 64);
+            float nm = fmaxf(bmax, om);
+            float ns = (bmax == -INFINITY ? 0.0f : bsum * __expf(bmax - nm)) +
+                       (om == -INFINITY ? 0.0f : os * __expf(om - nm));
+            int ni = (om > bmax) ? oi : (bmax > om) ? bidx : min(bidx, oi);
+            bmax = nm; bsum = ns; bidx = ni;
+        }
+        if (lane == 0) {
+            tstats[3 * t] = bmax;
+            tstats[3 * t + 1] = bsum;
+            tstats[3 * t + 2] = __int_as_float(bidx);
+        }
+    }
+    __syncthreads();
+    // their combination (head_combine_kernel), 16 lanes of wave 0
+    if (w == 0 && lane < 16) {
+        const int l = lane;
+        float bm = -INFINITY, bsm = 0.0f;
+        int bi = 0x7fffffff;
+        for (int t = l; t < ntiles; t += 16) merge_stats(bm, bsm, bi, tstats[3 * t], tstats[3 * t + 1], __float_as_int(tstats[3 * t + 2]));
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) {
+            const float om = __shfl_xor(bm, o, 16), os = __shfl_xor(bsm, o, 16);
+            const int oi = __shfl_xor(bi, o, 16);
+            merge_stats(bm, bsm, bi, om, os, oi);
+        }
+        if (l == 0) {
+            const double p = 1.0 / (double)bsm;
+            if (a.argmax) a.argmax[s_] = bi;
+            if (a.prob) a.prob[s_] = p;
+            if (a.next_ids) a.next_ids[s_] = bi;
+            const int oc = a.col ? *a.col : a.out_col;
+            if (a.out_ids) a.out_ids[(long long)s_ * a.out_ld + oc] = bi;
+            if (a.out_probs) a.out_probs[(long long)s_ * a.out_ld + oc] = p;
+            a.pos[s_] = pos + 1;
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void head_combine_kernel(HeadCombineArgs a) {
     const int l = threadIdx.x & 15;
     const int m = blockIdx.x * 16 + (threadIdx.x >> 4);
@@ -2074,6 +2505,41 @@ hipError_t launch_attention_wave(const AttnWaveArgs& a, hipStream_t s) {
     return attn_wave_t<64>(a, span_max, s);
 }
 
+size_t step1_lds_bytes(const Step1Args& a, int dh) {
+    const size_t floats = (size_t)8 * a.Dp + a.Hp + a.Vp + 4 * (a.Vp / LX_BN) +
+                          (size_t)a.heads * ((rk_lds_floats(a.cap, dh) + 3) & ~3);
+    const size_t xl = (size_t)std::max(9 * a.Dp, 3 * a.Hp);
+    return floats * sizeof(float) + xl;
+}
+
+bool step1_fits(const Step1Args& a) {
+    if (a.S <= 0 || a.D > 512 || a.Dp > 512 || a.Hp > 1024 || a.Vp > 16384 || a.nblocks <= 0) return false;
+    const int dh = a.heads > 0 ? a.D / a.heads : 16;
+    if (a.heads > 0 && (a.heads > S1_THREADS / 64 || a.D % a.heads || (dh != 16 && dh != 32 && dh != 64) ||
+                        a.cap > 64 || a.cap <= 0))
+        return false;
+    return step1_lds_bytes(a, dh) <= 150 * 1024;
+}
+
+template <int DH>
+hipError_t step1_t(const Step1Args& a, hipStream_t s) {
+    const size_t lds = step1_lds_bytes(a, DH);
+    static const hipError_t attr = hipFuncSetAttribute((const void*)step1_kernel<DH>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL(step1_kernel<DH>, dim3(a.S), dim3(S1_THREADS), lds, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_step1(const Step1Args& a, hipStream_t s) {
+    if (!step1_fits(a)) return hipErrorInvalidValue;
+    switch (a.heads > 0 ? a.D / a.heads : 16) {
+        case 16: return step1_t<16>(a, s);
+        case 32: return step1_t<32>(a, s);
+        default: return step1_t<64>(a, s);
+    }
+}
+
 hipError_t launch_head_combine(const HeadCombineArgs& a, hipStream_t s) {
     if (a.M <= 0) return hipSuccess;
     hipLaunchKernelGGL(head_combine_kernel, dim3((a.M + 15) / 16), dim3(256), 0, s, a);
@@ -2115,6 +2581,13 @@ hipError_t launch_export_kv(int B, int T, int D, int heads, int cap, const int32
 hipError_t launch_set_pos(int S, const int32_t* lens, int32_t* pos, int add, hipStream_t s, int32_t* col) {
     if (S <= 0) return hipSuccess;
     hipLaunchKernelGGL(set_pos_kernel, dim3((S + 255) / 256), dim3(256), 0, s, S, lens, pos, add, col);
+    return hipGetLastError();
+}
+
+__global__ void advance_kernel(int32_t* p) { *p += 1; }
+
+hipError_t launch_advance(int32_t* p, hipStream_t s) {
+    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, p);
     return hipGetLastError();
 }
 

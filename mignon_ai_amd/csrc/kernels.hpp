@@ -131,6 +131,46 @@ constexpr int kMaxAttnSpan = 32768;
 constexpr int kMaxHeadWidth = 1024;
 hipError_t launch_attention_wave(const AttnWaveArgs& a, hipStream_t s);
 
+// One decode step of a few sessions, each session's whole model step (norms, latch, rule, attention,
+// head) in one workgroup: for small sets, where the batched step's ~10 launches per block, each a few
+// microseconds at one row, dominate. Same arithmetic as the batched step (limb-expanded int8 MFMA with
+// the GEMM epilogues' formulas, the row kernels' and latch step's reductions, rk_head's attention, the
+// head's per-tile statistics and their combination), so its outputs equal the batched step's bit for bit.
+struct Step1Block {
+    int steps = 0, dil_base = 2, init_dil = 1, attn = 0;
+    const int8_t* w1 = nullptr; const float* b1 = nullptr; float s1 = 0;   // fragment layout, rows paired
+    const int8_t* w2 = nullptr; const float* b2 = nullptr; float s2 = 0;
+    const int8_t* wsel = nullptr; float ssel = 0;
+    const float* gamma = nullptr;                                          // or null: no normalisation
+    const float* anorm = nullptr;
+    const int8_t* qkv = nullptr; float sqkv = 0;
+    const int8_t* wo = nullptr; float so = 0;
+};
+struct Step1Args {
+    int S = 0, D = 0, Dp = 0, H = 0, Hp = 0, V = 0, Vp = 0, NpD = 0, Np3 = 0;
+    int heads = 0, window = 0, cap = 0, ring = 1, nblocks = 0;
+    const Step1Block* blocks = nullptr;  // device array [nblocks]
+    const int8_t* emb = nullptr; float emb_scale = 0;
+    const int8_t* headw = nullptr; const float* headb = nullptr; float head_scale = 0;
+    const float* final_norm = nullptr; const float* latch_base = nullptr;
+    // session state (the engine's layouts): pos [S]; g [nbs][S][Dp]; norm ring [nbs][S][ring][Dp];
+    // K/V rings [nattn][S][heads][cap][dh]
+    int32_t* pos = nullptr; float* g = nullptr; float* norm_ring = nullptr; float* kring = nullptr; float* vring = nullptr;
+    const int32_t* ids = nullptr;        // [S]
+    float* logits = nullptr;             // [S][V] or null
+    int32_t* argmax = nullptr;           // [S] or null
+    double* prob = nullptr;              // [S] or null
+    int32_t* next_ids = nullptr;         // [S] or null
+    int32_t* out_ids = nullptr;          // [S][out_ld] at column *col (or out_col)
+    double* out_probs = nullptr;
+    int out_ld = 0, out_col = 0;
+    const int32_t* col = nullptr;
+};
+// Whether the one-workgroup step takes this model (state size up to 512, hidden size up to 1024, at most
+// 8 attention heads of width 16, 32 or 64 over caches of at most 64 positions, vocabulary up to 16384).
+bool step1_fits(const Step1Args& a);
+hipError_t launch_step1(const Step1Args& a, hipStream_t s);
+
 // Per-row combination of the head GEMM's per-tile statistics.
 struct HeadCombineArgs {
     int M = 0, ntiles = 0;
@@ -166,6 +206,8 @@ hipError_t launch_export_kv(int B, int T, int D, int heads, int cap, const int32
 // pos[i] = (lens ? lens[i] : pos[i]) + add; with col set, also advances the decode column *col by one.
 hipError_t launch_set_pos(int S, const int32_t* lens, int32_t* pos, int add, hipStream_t s, int32_t* col = nullptr);
 hipError_t launch_fill_i32(int32_t* p, int n, int v, hipStream_t s);
+// *p += 1 (one thread).
+hipError_t launch_advance(int32_t* p, hipStream_t s);
 hipError_t launch_fill_f32(float* p, long long n, float v, hipStream_t s);
 
 }  // namespace mg

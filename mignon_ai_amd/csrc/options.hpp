@@ -9,6 +9,8 @@ enum Option : int {
     OPT_SCAN_KERNEL = 2,       // 0 automatic, 1 latch scan then rule-input packing, 2 fused
     OPT_STEP_GRAPH = 3,        // decode steps: 0 automatic (replayed from a captured HIP graph), 1 launched
                                // one kernel at a time, 2 graph
+    OPT_STEP_KERNEL = 4,       // decode steps of small session sets: 0 automatic, 1 layer by layer, 2 one
+                               // workgroup per session (step1_kernel) wherever the model fits it
     OPT_COUNT
 };
 
