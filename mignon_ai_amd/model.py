@@ -325,10 +325,10 @@ def sample_logits(logits, recent=None, temperature=1.0, top_k=0, top_p=1.0, rep_
 
 def engine_option(name: str, value: str | None = None) -> str:
     """mg_engine_option: which implementation runs for "gemm" ("auto", "stream", "slab"), "attention"
-    ("auto", "exact", "mfma", "fused": the projection fused with matrix-core attention), "step_kernel"
-    (decode steps of small session sets: "auto", "layered", "fused": one workgroup per session), "scan" ("auto", "separate", "fused") or "step_graph" (decode steps replayed
-    from a captured HIP graph: "auto", "off", "on"), for the whole process. Returns the previous value
-    (value None only reads it)."""
+    ("auto", "exact", "mfma", "fused": the projection fused with matrix-core attention), "scan" ("auto",
+    "separate", "fused"), "step_graph" (decode steps replayed from a captured HIP graph: "auto", "off",
+    "on") or "step_kernel" (decode steps of small session sets: "auto", "layered", "fused": one workgroup
+    per session), for the whole process. Returns the previous value (value None only reads it)."""
     opt, names = _OPTIONS[name]
     prev = lib().mg_engine_option(opt, -1 if value is None else names.index(value))
     check(prev if prev < 0 else 0)
