@@ -303,7 +303,10 @@ int mg_quantize_f32(const float* w, long long n, int8_t* q, float* scale, int fl
  *   MG_OPT_STEP_KERNEL: MG_STEP_LAYERED runs a decode step layer by layer (about ten kernels per block,
  *     each over all sessions); MG_STEP_FUSED runs each session's whole step in one workgroup, where the
  *     model fits it (state size up to 512, at most 8 heads of width 16, 32 or 64, caches of at most 64
- *     positions); identical results. Automatic fuses sets of up to 256 sessions. The fused step's one
+ *     positions); MG_STEP_TILED runs the step for 16 sessions per workgroup, one kernel per stretch
+ *     between attention blocks and the decode attention kernel between them (state size up to 512, hidden
+ *     size up to 1024, caches of at most 64 positions); identical results. Automatic fuses sets of up to
+ *     256 sessions and tiles larger ones, where the model fits. The fused step's one
  *     kernel reads the ids of an mg_sessions_step call with host pointers from, and writes its outputs
  *     to, the set's pinned host buffers directly (no copies between host and device buffers).
  * value < 0 only reads the option. Returns the previous value, or MG_ERR_INVALID. */
@@ -316,6 +319,7 @@ int mg_quantize_f32(const float* w, long long n, int8_t* q, float* scale, int fl
 #define MG_OPT_STEP_KERNEL 4
 #define MG_STEP_LAYERED 1
 #define MG_STEP_FUSED 2
+#define MG_STEP_TILED 3
 #define MG_SCAN_SEPARATE 1
 #define MG_SCAN_FUSED 2
 #define MG_GEMM_STREAM 1

@@ -12,6 +12,28 @@ namespace mg {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
+// A load through the global address space. Pointers read from device memory (the per-block weight
+// tables of the one-workgroup decode steps) are generic, and generic (flat) loads count against both
+// the memory and the LDS counters, so the compiler waits for every outstanding load and LDS access at
+// each use: one fragment in flight instead of a batch.
+template <class T>
+__device__ __forceinline__ T ldg(const T* p) {
+    return *(const __attribute__((address_space(1))) T*)p;
+}
+template <class T>
+__device__ __forceinline__ void stg(T* p, T v) {
+    *(__attribute__((address_space(1))) T*)p = v;
+}
+// float4 is a class type: through the native vector type
+typedef float v4f_ __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ldg(const float4* p) {
+    const v4f_ v = *(const __attribute__((address_space(1))) v4f_*)p;
+    return float4{v.x, v.y, v.z, v.w};
+}
+__device__ __forceinline__ void stg(float4* p, float4 v) {
+    *(__attribute__((address_space(1))) v4f_*)p = v4f_{v.x, v.y, v.z, v.w};
+}
+
 constexpr int WAVE = 64;
 
 // Limb expansion of fp32 activations for int8 MFMA. A row segment x with scale s = amax/127 is held as

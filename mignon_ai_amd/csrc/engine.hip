@@ -48,7 +48,7 @@ int options_key() {
 int set_option(int opt, int value) {
     if (opt < 0 || opt >= OPT_COUNT) return -1;
     if (value < 0) return g_options[opt].load();
-    if (value > (opt == OPT_ATTENTION_KERNEL ? 3 : 2)) return -1;
+    if (value > (opt == OPT_ATTENTION_KERNEL || opt == OPT_STEP_KERNEL ? 3 : 2)) return -1;
     return g_options[opt].exchange(value);
 }
 
@@ -126,12 +126,12 @@ struct DevBlock {
 enum KClass : int {
     K_ROW = 0, K_GEMM_LATCH, K_SCAN, K_LATCH_STEP, K_GEMM_GLU, K_GEMM_HIGHWAY, K_GEMM_QKV, K_ATTN, K_ATTN_STEP,
     K_GEMM_OUT, K_GEMM_LOGITS, K_HEAD_COMBINE, K_GEMM_PROBS, K_BITS, K_EXPORT, K_GEMM_I8, K_SAMPLE, K_QKV_ATTN,
-    K_STEP1, K_NCLASS
+    K_STEP1, K_TILE_STEP, K_NCLASS
 };
 const char* const kClassNames[K_NCLASS] = {
     "row_norm_pack", "gemm_latch", "latch_scan", "latch_step", "gemm_glu", "gemm_highway", "gemm_qkv",
     "attention", "attention_step", "gemm_out", "gemm_logits", "head_combine", "gemm_probs", "bits",
-    "state_export", "gemm_i8", "sample", "qkv_attention", "session_step"};
+    "state_export", "gemm_i8", "sample", "qkv_attention", "session_step", "tile_step"};
 
 struct Profile {
     bool on = false;
@@ -1362,10 +1362,9 @@ void prefill_device(mg_sessions* s, const int32_t* prompts_d, const int32_t* len
 
 // The one-workgroup-per-session step for this set, when the option and the shapes allow it.
 constexpr int kStep1MaxSessions = 256;  // automatic selection: sets up to this size
-bool step1_args(mg_sessions* s, const int32_t* ids_d, float* logits_d, const HeadCombineArgs& hc, Step1Args& a) {
+// The arguments both single-kernel steps share.
+bool step1_args_fill(mg_sessions* s, const int32_t* ids_d, float* logits_d, const HeadCombineArgs& hc, Step1Args& a) {
     mg_model* m = s->m;
-    const int mode = option(OPT_STEP_KERNEL);
-    if (mode == 1 || (mode == 0 && s->n > kStep1MaxSessions) || !m->s1blocks) return false;
     a.S = s->n; a.D = m->D; a.Dp = m->Dp; a.H = m->H; a.Hp = m->Hp; a.V = m->V; a.Vp = m->Vp;
     a.NpD = m->NpD; a.Np3 = m->Np3; a.heads = m->nattn ? m->heads : 0; a.window = m->window; a.cap = m->cap;
     a.ring = m->ring; a.nblocks = (int)m->blocks.size(); a.blocks = m->s1blocks;
@@ -1375,7 +1374,39 @@ bool step1_args(mg_sessions* s, const int32_t* ids_d, float* logits_d, const Hea
     a.kring = s->kring.as<float>(); a.vring = s->vring.as<float>();
     a.ids = ids_d; a.logits = logits_d; a.argmax = hc.argmax; a.prob = hc.prob; a.next_ids = hc.next_ids;
     a.out_ids = hc.out_ids; a.out_probs = hc.out_probs; a.out_ld = hc.out_ld; a.out_col = hc.out_col; a.col = hc.col;
-    return step1_fits(a);
+    return true;
+}
+
+bool step1_args(mg_sessions* s, const int32_t* ids_d, float* logits_d, const HeadCombineArgs& hc, Step1Args& a) {
+    mg_model* m = s->m;
+    const int mode = option(OPT_STEP_KERNEL);
+    if (mode == 1 || mode == 3 || (mode == 0 && s->n > kStep1MaxSessions) || !m->s1blocks) return false;
+    return step1_args_fill(s, ids_d, logits_d, hc, a) && step1_fits(a);
+}
+
+// The decode attention of the tiled step (between its segments): its shape, for the fit check.
+AttnStepArgs step_attn_args(mg_sessions* s, int ab) {
+    mg_model* m = s->m;
+    Workspace& w = ws_of(m);
+    AttnStepArgs aa;
+    aa.S = s->n; aa.D = m->D; aa.Dp = m->Dp; aa.heads = m->heads; aa.window = m->window; aa.cap = m->cap;
+    aa.pos = s->pos.as<int32_t>(); aa.qkv = w.qkv.as<float>();
+    aa.kring = s->kring.as<float>() + (size_t)ab * s->n * m->cap * m->D;
+    aa.vring = s->vring.as<float>() + (size_t)ab * s->n * m->cap * m->D;
+    aa.xl = w.nl.as<int8_t>(); aa.xs = w.ns.as<float>();
+    return aa;
+}
+
+// The tiled step (16 sessions per workgroup), when the option and the shapes allow it: automatic for
+// sets larger than the fused step takes.
+bool tile_args(mg_sessions* s, const int32_t* ids_d, float* logits_d, const HeadCombineArgs& hc, TileStepArgs& a) {
+    mg_model* m = s->m;
+    const int mode = option(OPT_STEP_KERNEL);
+    if (!(mode == 3 || mode == 0) || !m->s1blocks) return false;
+    Step1Args& b = a;
+    if (!step1_args_fill(s, ids_d, logits_d, hc, b)) return false;
+    if (m->nattn && !attention_step_rows_fits(step_attn_args(s, 0))) return false;
+    return tile_step_fits(a);
 }
 
 void step_device(mg_sessions* s, const int32_t* ids_d, float* logits_d, HeadCombineArgs hc, hipStream_t st) {
@@ -1386,6 +1417,34 @@ void step_device(mg_sessions* s, const int32_t* ids_d, float* logits_d, HeadComb
         {
             ProfScope ps(m->prof, K_STEP1, st);
             HIPCHECK(launch_step1(s1, st));
+        }
+        if (hc.col) HIPCHECK(launch_advance(const_cast<int32_t*>(hc.col), st));
+        return;
+    }
+    TileStepArgs ta;
+    if (!hc.lse && !hc.logprob && tile_args(s, ids_d, logits_d, hc, ta)) {
+        ensure_ws(m, S);
+        Workspace& w = ws_of(m);
+        ta.cur = w.cur.as<float>(); ta.bin = w.bin.as<float>(); ta.qkv = w.qkv.as<float>();
+        ta.att_xl = w.nl.as<int8_t>(); ta.att_xs = w.ns.as<float>();
+        int ab = 0;
+        for (;;) {
+            {
+                ProfScope ps(m->prof, K_TILE_STEP, st);
+                HIPCHECK(launch_tile_step(ta, st));
+            }
+            int next = ta.seg_out ? ta.seg_block + 1 : ta.seg_block;
+            while (next < (int)m->blocks.size() && !m->blocks[next].attn) next++;
+            if (next >= (int)m->blocks.size()) break;
+            {
+                // the segment ended with block next's projection: its attention, output limbs to w.nl/w.ns
+                AttnStepArgs aa = step_attn_args(s, ab);
+                ProfScope ps(m->prof, K_ATTN_STEP, st);
+                HIPCHECK(launch_attention_step_rows(aa, st));
+            }
+            ab++;
+            ta.seg_block = next;
+            ta.seg_out = 1;
         }
         if (hc.col) HIPCHECK(launch_advance(const_cast<int32_t*>(hc.col), st));
         return;

@@ -1717,7 +1717,9 @@ __device__ __forceinline__ void s1_frags(const int8_t* W, int np16, int kc, cons
 #pragma unroll
             for (int j = 0; j < 4; j++)
                 if (g < nf && k0 + j < kc)
-                    wv[g][j] = *(const v4i*)(W + ((((long long)(k0 + j) * np16 + f[g]) << 10) + lane * 16));
+                    wv[g][j] = ldg((const v4i*)(W + ((((long long)(k0 + j) * np16 + f[g]) << 10) + lane * 16)));
+        // keep the batch together: the scheduler would otherwise sink each load to its first MFMA
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             if (k0 + j >= kc) break;
@@ -1838,7 +1840,7 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
                 }
                 __syncthreads();
                 const float inv = bcast[0];
-                for (int d = tid; d < Dp; d += S1_THREADS) nrm[d] = d < D ? (cur[d] * inv) * B.gamma[d] : 0.0f;
+                for (int d = tid; d < Dp; d += S1_THREADS) nrm[d] = d < D ? (cur[d] * inv) * ldg(B.gamma + d) : 0.0f;
             } else {
                 for (int d = tid; d < Dp; d += S1_THREADS) nrm[d] = d < D ? cur[d] : 0.0f;
             }
@@ -1850,7 +1852,7 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
                 const float sw = sn * B.ssel;
                 S1_FRAGS(B.wsel, a.NpD / 16, Dp / 64, {
                     const int c = 16 * f + 4 * (lane >> 4) + r;
-                    if (c < D) lam[c] = sigmoid_epi(fmaf(v, sw, a.latch_base[c]));
+                    if (c < D) lam[c] = sigmoid_epi(fmaf(v, sw, ldg(a.latch_base + c)));
                 });
             }
             __syncthreads();
@@ -1893,8 +1895,8 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
                 const float sw = sx * B.s1;
                 S1_PAIRS(B.w1, 2 * Hp / 16, 3 * Dp / 64, {
                     const int c = 16 * q + 4 * g4 + r;
-                    const float ov = fmaf(vv, sw, B.b1[32 * q + 4 * g4 + r]);
-                    const float gt = sigmoid_epi(fmaf(vg, sw, B.b1[32 * q + 16 + 4 * g4 + r]));
+                    const float ov = fmaf(vv, sw, ldg(B.b1 + 32 * q + 4 * g4 + r));
+                    const float gt = sigmoid_epi(fmaf(vg, sw, ldg(B.b1 + 32 * q + 16 + 4 * g4 + r)));
                     hbuf[c] = c < H ? ov * gt : 0.0f;
                 });
             }
@@ -1907,8 +1909,8 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
                 S1_PAIRS(B.w2, 2 * Dp / 16, Hp / 64, {
                     const int c = 16 * q + 4 * g4 + r;
                     if (c < D) {
-                        const float ov = fmaf(vv, sw, B.b2[32 * q + 4 * g4 + r]);
-                        const float gt = sigmoid_epi(fmaf(vg, sw, B.b2[32 * q + 16 + 4 * g4 + r]));
+                        const float ov = fmaf(vv, sw, ldg(B.b2 + 32 * q + 4 * g4 + r));
+                        const float gt = sigmoid_epi(fmaf(vg, sw, ldg(B.b2 + 32 * q + 16 + 4 * g4 + r)));
                         const float x1 = (1.0f - gt) * cur[c];
                         const float x2 = gt * ov;
                         cur[c] = x1 + x2;
@@ -1926,7 +1928,7 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
             __syncthreads();
             {
                 const float inv = bcast[0];
-                for (int d = tid; d < Dp; d += S1_THREADS) nrm[d] = d < D ? (cur[d] * inv) * B.anorm[d] : 0.0f;
+                for (int d = tid; d < Dp; d += S1_THREADS) nrm[d] = d < D ? (cur[d] * inv) * ldg(B.anorm + d) : 0.0f;
             }
             __syncthreads();
             const float sa = s1_limbs(nrm, D, Dp, xl, red, tid, lane, w);
@@ -2062,6 +2064,631 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
             if (a.out_ids) a.out_ids[(long long)s_ * a.out_ld + oc] = bi;
             if (a.out_probs) a.out_probs[(long long)s_ * a.out_ld + oc] = p;
             a.pos[s_] = pos + 1;
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Decode step of a tile of 16 sessions per workgroup (tile_step_kernel)
+// ------------------------------------------------------------------------------------------------
+// The 16 sessions of a tile are the 16 token columns of v_mfma_i32_16x16x64_i8, so every weight
+// fragment, loaded once per workgroup, serves all of them. The step runs in segments: a segment ends
+// once an attention block's projection q, k, v is written; that block's attention (with the limb
+// expansion of its output, attention_step_rows_kernel) runs between segments, and the next segment
+// starts with the block's out projection. cur and blockIn go through memory between segments. In the
+// row phases (residual, norms, limb planes, the latch update) wave w owns rows w and w + 8, lane L
+// channels 4L + 256i .. +3. Every operation is the layered step's, in its order: results are
+// bit-identical.
+constexpr int TS_NS = 16;
+constexpr int TS_THREADS = 512;
+constexpr int TS_NI = 2;  // float4 chunks of a state row per lane (state size up to 512)
+
+// Workgroup barrier over LDS only: the waves exchange data through LDS alone (the global stores of a
+// segment are read by later kernels), so outstanding global loads and stores need not drain.
+__device__ __forceinline__ void ts_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// LDS of tile_step_kernel (offsets in floats, the limb operand's in bytes): cur and blockIn [16][Dp + 4];
+// one region reused by n and lambda [2][16][Dp + 4], h [16][Hp + 4] and the head's tile statistics
+// [16][Vp/128][3]; then the limb operand xl [K/64][3 planes][1 KiB] for K up to max(3 Dp, Hp).
+struct TsLds {
+    int ld, hld, cur, bin, nrm, lam, h, ts, xl_off, bytes;
+};
+__host__ __device__ inline TsLds ts_lds(int Dp, int Hp, int Vp) {
+    TsLds L;
+    L.ld = Dp + 4;
+    L.hld = Hp + 4;
+    L.cur = 0;
+    L.bin = TS_NS * L.ld;
+    const int u = 2 * TS_NS * L.ld;
+    L.nrm = u;
+    L.lam = u + TS_NS * L.ld;
+    L.h = u;
+    L.ts = u;
+    int usz = 2 * TS_NS * L.ld;
+    usz = usz > TS_NS * L.hld ? usz : TS_NS * L.hld;
+    usz = usz > TS_NS * (Vp / 128) * 3 ? usz : TS_NS * (Vp / 128) * 3;
+    L.xl_off = ((u + usz) * 4 + 15) & ~15;
+    const int kmax = 3 * Dp > Hp ? 3 * Dp : Hp;
+    L.bytes = L.xl_off + (kmax / 64) * 3072;
+    return L;
+}
+
+// Byte offset in xl of channel k (a multiple of 4) of token column t: fragment (K step k/64, plane 0),
+// lane t + 16*((k >> 4) & 3), byte k & 15.
+__device__ __forceinline__ int ts_xoff(int k, int t) { return (k >> 6) * 3072 + ((t + 16 * ((k >> 4) & 3)) << 4) + (k & 15); }
+
+// The three limb planes of chunk v (channels k .. k + 3 of token column t) into xl.
+__device__ __forceinline__ void ts_put_limbs(int8_t* xl, int k, int t, float4 v, float inv) {
+    uint32_t w0, w1, w2;
+    split4_pack(v, inv, w0, w1, w2);
+    int8_t* o = xl + ts_xoff(k, t);
+    *(uint32_t*)o = w0;
+    *(uint32_t*)(o + 1024) = w1;
+    *(uint32_t*)(o + 2048) = w2;
+}
+
+__device__ __forceinline__ float ts_amax4(float m, float4 v) {
+    return fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+}
+
+// Limb planes of one row (chunks v[i] = channels 4*lane + 256*i .. +3, zero at and past the row's valid
+// channels) into column t of xl, for channels below Kp; returns the row scale. One wave: the row
+// kernel's scale (the row's absolute maximum) and digits.
+template <int NI>
+__device__ __forceinline__ float ts_row_limbs(const float4 (&v)[NI], int Kp, int t, int8_t* xl, int lane) {
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NI; i++) m = ts_amax4(m, v[i]);
+    float sc, inv;
+    limb_scale(wave_max(m), sc, inv);
+#pragma unroll
+    for (int i = 0; i < NI; i++)
+        if (4 * lane + 256 * i < Kp) ts_put_limbs(xl, 4 * lane + 256 * i, t, v[i], inv);
+    return sc;
+}
+
+__device__ __forceinline__ float4 ts_ld4(const float* p, int k, int valid) {
+    if (k + 4 <= valid) return *(const float4*)(p + k);
+    float4 r = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (k < valid) r.x = p[k];
+    if (k + 1 < valid) r.y = p[k + 1];
+    if (k + 2 < valid) r.z = p[k + 2];
+    return r;
+}
+
+// Row t: with `resid`, first blockIn += cur; cur = blockIn (stream.go:157-163); then n = RMSNorm(cur;
+// gamma) (cur itself without gamma), kept in `keep` when given, and its limb planes (K = Dp); returns
+// the row scale. One wave (s1_rms_inv, the row kernel's order).
+__device__ __forceinline__ float ts_norm_row(float* x, float* bin, bool resid, const float* gamma, int D, int Dp,
+                                             float* keep, int8_t* xl, int t, int lane) {
+    // gamma first: its memory latency runs under the residual and the sum of squares
+    float4 gm[TS_NI];
+#pragma unroll
+    for (int i = 0; i < TS_NI; i++) {
+        const int k = 4 * lane + 256 * i;
+        gm[i] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (gamma) {
+            if (k + 4 <= D) {
+                gm[i] = ldg((const float4*)(gamma + k));
+            } else {
+#pragma unroll
+                for (int u = 0; u < 3; u++)
+                    if (k + u < D) (&gm[i].x)[u] = ldg(gamma + k + u);
+            }
+        }
+    }
+    if (resid) {
+#pragma unroll
+        for (int i = 0; i < TS_NI; i++) {
+            const int k = 4 * lane + 256 * i;
+            if (k < Dp) {
+                const float4 c = *(const float4*)(x + k), b = *(const float4*)(bin + k);
+                const float4 v = {b.x + c.x, b.y + c.y, b.z + c.z, b.w + c.w};
+                *(float4*)(x + k) = v;
+                *(float4*)(bin + k) = v;
+            }
+        }
+        wave_lds_sync();
+    }
+    const float inv = gamma ? s1_rms_inv(x, D, lane) : 1.0f;
+    float4 v[TS_NI];
+#pragma unroll
+    for (int i = 0; i < TS_NI; i++) {
+        const int k = 4 * lane + 256 * i;
+        float4 u = ts_ld4(x, k, D);
+        if (gamma) {
+            u.x = (u.x * inv) * gm[i].x;
+            u.y = (u.y * inv) * gm[i].y;
+            u.z = (u.z * inv) * gm[i].z;
+            u.w = (u.w * inv) * gm[i].w;
+        }
+        v[i] = u;
+        if (keep && k < Dp) *(float4*)(keep + k) = u;
+    }
+    return ts_row_limbs<TS_NI>(v, Dp, t, xl, lane);
+}
+
+// Matrix phases of tile_step_kernel. Wave w takes units w, w + 8, ... of the phase: with TS_FRAG one
+// 16-channel fragment (GF units per group), with TS_PAIR the fragment pair 2q (value), 2q + 1 (gate)
+// (GF/2 per group), with TS_TILE the GF consecutive fragments GF*u .. GF*u + GF - 1 (one per group).
+// A group's weights are requested KB K steps at a time (GF * KB loads in flight; loads past the wave's
+// units or past the last K step repeat a valid address and go unused), with the group's bias values
+// (`bias`, indexed by output row, or null), then multiplied by the tile's limb planes (all 16 token
+// columns). After a group's last K step `epi` gets, for each unit, the combined dot products of token
+// lane & 15, channels c0 .. c0 + 3 with c0 = 16 f + 4 (lane >> 4), and the bias of those rows:
+// epi(f, v[4], b) (TS_FRAG), epi(q, vv[4], vg[4], bv, bg) (TS_PAIR), or epi(u, acc, b[GF]) (TS_TILE).
+enum { TS_FRAG = 0, TS_PAIR = 1, TS_TILE = 2 };
+template <int MODE, int GF, int KB, class Epi>
+__device__ __forceinline__ void ts_matvec(const int8_t* W, const float* bias, int np16, int kc, int nunits,
+                                          const int8_t* xl, int lane, int w, Epi&& epi) {
+    constexpr int UPG = MODE == TS_FRAG ? GF : MODE == TS_PAIR ? GF / 2 : 1;  // units per group
+    const int mine = nunits > w ? (nunits - 1 - w) / 8 + 1 : 0;
+    const int8_t* wl = W + lane * 16;
+    const int8_t* xp = xl + lane * 16;
+    for (int gi = 0; gi * UPG < mine; gi++) {
+        int fr[GF];
+        bool ok[GF];
+#pragma unroll
+        for (int g = 0; g < GF; g++) {
+            const int u0 = UPG * gi + (MODE == TS_FRAG ? g : MODE == TS_PAIR ? g / 2 : 0);
+            ok[g] = u0 < mine;
+            const int un = w + 8 * min(u0, mine - 1);
+            fr[g] = MODE == TS_FRAG ? un : MODE == TS_PAIR ? 2 * un + (g & 1) : GF * un + g;
+        }
+        // the bias with the weights (after the MFMAs for whole tiles, whose accumulators fill the registers)
+        float4 b4[GF];
+        auto load_bias = [&] {
+#pragma unroll
+            for (int g = 0; g < GF; g++)
+                b4[g] = bias ? ldg((const float4*)(bias + 16 * fr[g] + 4 * (lane >> 4))) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        };
+        if constexpr (MODE != TS_TILE) load_bias();
+        v4i acc[GF][3];
+#pragma unroll
+        for (int g = 0; g < GF; g++) acc[g][0] = acc[g][1] = acc[g][2] = v4i{0, 0, 0, 0};
+        for (int k0 = 0; k0 < kc; k0 += KB) {
+            v4i wv[GF][KB];
+#pragma unroll
+            for (int g = 0; g < GF; g++)
+#pragma unroll
+                for (int j = 0; j < KB; j++)
+                    wv[g][j] = ldg((const v4i*)(wl + (((long long)min(k0 + j, kc - 1) * np16 + fr[g]) << 10)));
+            // keep the batch together: the scheduler would otherwise sink each load to its first MFMA
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < KB; j++) {
+                if (k0 + j >= kc) break;
+                v4i xv[3];
+#pragma unroll
+                for (int l = 0; l < 3; l++) xv[l] = *(const v4i*)(xp + (k0 + j) * 3072 + l * 1024);
+#pragma unroll
+                for (int g = 0; g < GF; g++)
+                    if (ok[g])
+#pragma unroll
+                        for (int l = 0; l < 3; l++)
+                            acc[g][l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wv[g][j], xv[l], acc[g][l], 0, 0, 0);
+            }
+        }
+        if constexpr (MODE == TS_TILE) {
+            load_bias();
+            epi(w + 8 * gi, acc, b4);
+        } else if constexpr (MODE == TS_PAIR) {
+#pragma unroll
+            for (int p = 0; p < GF / 2; p++)
+                if (ok[2 * p]) {
+                    float vv[4], vg[4];
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        vv[r] = s1_dot(acc[2 * p], r);
+                        vg[r] = s1_dot(acc[2 * p + 1], r);
+                    }
+                    epi(fr[2 * p] >> 1, vv, vg, b4[2 * p], b4[2 * p + 1]);
+                }
+        } else {
+#pragma unroll
+            for (int g = 0; g < GF; g++)
+                if (ok[g]) {
+                    float v[4];
+#pragma unroll
+                    for (int r = 0; r < 4; r++) v[r] = s1_dot(acc[g], r);
+                    epi(fr[g], v, b4[g]);
+                }
+        }
+    }
+}
+
+__global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
+    extern __shared__ __align__(16) float ts_smem[];
+    __shared__ float rsc[TS_NS];  // row scales of the current limb operand
+    const int s0 = blockIdx.x * TS_NS, ns = min(TS_NS, a.S - s0);
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int D = a.D, Dp = a.Dp, H = a.H, Hp = a.Hp, V = a.V, Vp = a.Vp;
+    const TsLds L = ts_lds(Dp, Hp, Vp);
+    const int ld = L.ld, hld = L.hld;
+    float* cur = ts_smem + L.cur;
+    float* bin = ts_smem + L.bin;
+    float* nrm = ts_smem + L.nrm;
+    float* lam = ts_smem + L.lam;
+    float* hb = ts_smem + L.h;
+    float* tst = ts_smem + L.ts;
+    int8_t* xl = (int8_t*)ts_smem + L.xl_off;
+    const int kcD = Dp >> 6;
+
+    // state rows (each wave its own): the embedding (quant.Model.appendPosition, ids clamped as
+    // stream.go:144-146), or the previous segment's cur and blockIn; rows past the set are zero
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int t = w + 8 * i;
+        const bool ok = t < ns;
+        int id = 0;
+        if (ok && a.seg_block == 0 && !a.seg_out) {
+            id = a.ids[s0 + t];
+            id = (id < 0 || id >= V) ? 0 : id;
+        }
+#pragma unroll
+        for (int ii = 0; ii < TS_NI; ii++) {
+            const int k = 4 * lane + 256 * ii;
+            if (k >= Dp) continue;
+            float4 c = {0.0f, 0.0f, 0.0f, 0.0f}, bi = c;
+            if (ok) {
+                if (a.seg_block == 0 && !a.seg_out) {
+                    const int8_t* e = a.emb + (long long)id * D;
+#pragma unroll
+                    for (int u = 0; u < 4; u++)
+                        if (k + u < D) (&c.x)[u] = (float)e[k + u] * a.emb_scale;
+                    bi = c;
+                } else {
+                    const long long row = (long long)(s0 + t) * Dp;
+                    c = *(const float4*)(a.cur + row + k);
+                    bi = *(const float4*)(a.bin + row + k);
+                }
+            }
+            *(float4*)(cur + t * ld + k) = c;
+            *(float4*)(bin + t * ld + k) = bi;
+        }
+    }
+    int b = a.seg_block;
+    if (a.seg_out) {
+        // the out projection of block b, whose attention has run: cur += att.W_o * s (attention.go:100-103)
+        const int8_t* src = a.att_xl + (long long)blockIdx.x * kcD * 3072;
+        for (int c = tid; c < kcD * 192; c += TS_THREADS) *(v4i*)(xl + c * 16) = *(const v4i*)(src + c * 16);
+        if (tid < TS_NS) rsc[tid] = tid < ns ? a.att_xs[s0 + tid] : 0.0f;
+        ts_barrier();
+        const Step1Block& B = a.blocks[b];
+        ts_matvec<TS_FRAG, 4, 2>(B.wo, nullptr, a.NpD / 16, kcD, a.NpD / 16, xl, lane, w, [&](int f, const float (&v)[4], float4) {
+            const int c0 = 16 * f + 4 * (lane >> 4), t = lane & 15;
+            const float sw = rsc[t] * B.so;
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                if (c0 + r < D) cur[t * ld + c0 + r] = cur[t * ld + c0 + r] + v[r] * sw;
+        });
+        b++;
+    }
+    ts_barrier();
+    int bs = 0;  // block steps before block b: the index of its latch state and norm ring
+    for (int q = 0; q < b; q++) bs += a.blocks[q].steps;
+    for (; b < a.nblocks; b++) {
+        const Step1Block& B = a.blocks[b];
+        bool resid = b > 0;  // blockIn += cur; cur = blockIn at the block's start, by each row's wave
+        if (B.steps == 0 && resid) {
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int t = w + 8 * i;
+#pragma unroll
+                for (int ii = 0; ii < TS_NI; ii++) {
+                    const int k = 4 * lane + 256 * ii;
+                    if (k < Dp) {
+                        float* x = cur + t * ld + k;
+                        float* bb = bin + t * ld + k;
+                        const float4 c = *(const float4*)x, bv = *(const float4*)bb;
+                        const float4 v = {bv.x + c.x, bv.y + c.y, bv.z + c.z, bv.w + c.w};
+                        *(float4*)x = v;
+                        *(float4*)bb = v;
+                    }
+                }
+            }
+            resid = false;
+            ts_barrier();
+        }
+        for (int st = 0; st < B.steps; st++, bs++) {
+            int dil = B.init_dil;
+            for (int q = 0; q < st && dil < 32; q++) dil *= B.dil_base;
+            dil = min(dil, 32);
+            // n = RMSNorm(cur; gamma) (stream.go:166-171) and its limbs
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int t = w + 8 * i;
+                const float sc = ts_norm_row(cur + t * ld, bin + t * ld, resid && st == 0, B.gamma, D, Dp, nrm + t * ld,
+                                             xl, t, lane);
+                if (lane == 0) rsc[t] = sc;
+            }
+            ts_barrier();
+            // lambda = sigmoid_clamped(n.W_sel*s + base) (stream.go:195-205)
+            ts_matvec<TS_FRAG, 4, 2>(B.wsel, a.latch_base, a.NpD / 16, kcD, a.NpD / 16, xl, lane, w,
+                                     [&](int f, const float (&v)[4], float4 b) {
+                const int c0 = 16 * f + 4 * (lane >> 4), t = lane & 15;
+                const float sw = rsc[t] * B.ssel;
+                const float bb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (c0 + r < D) lam[t * ld + c0 + r] = sigmoid_epi(fmaf(v[r], sw, bb[r]));
+            });
+            ts_barrier();
+            // latch update, norm ring and the rule input [n | left | g] (latch_step_kernel): both rows'
+            // memory reads are issued before either row is computed
+            {
+                float4 gq[2][TS_NI], lq[2][TS_NI];
+                int posr[2];
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    const int t = w + 8 * i;
+                    const bool ok = t < ns;
+                    const int s = s0 + (ok ? t : 0);
+                    posr[i] = a.pos[s];
+                    const float* gbase = a.g + ((long long)bs * a.S + s) * Dp;
+                    const float* ring = a.norm_ring + ((long long)bs * a.S + s) * a.ring * Dp;
+                    const int p = posr[i];
+                    const float* lslot = ring + (long long)((p >= dil ? p - dil : 0) % a.ring) * Dp;
+#pragma unroll
+                    for (int ii = 0; ii < TS_NI; ii++) {
+                        const int k = min(4 * lane + 256 * ii, Dp - 4);
+                        gq[i][ii] = ok ? ldg((const float4*)(gbase + k)) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+                        lq[i][ii] = ok && p >= dil ? ldg((const float4*)(lslot + k)) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    const int t = w + 8 * i;
+                    const bool ok = t < ns;
+                    const int s = s0 + (ok ? t : 0);
+                    const int p = posr[i];
+                    float* gbase = a.g + ((long long)bs * a.S + s) * Dp;
+                    float* ring = a.norm_ring + ((long long)bs * a.S + s) * a.ring * Dp;
+                    float* wslot = ring + (long long)(p % a.ring) * Dp;
+                    float4 nv[TS_NI], lv[TS_NI], gv[TS_NI];
+                    float m = 0.0f;
+#pragma unroll
+                    for (int ii = 0; ii < TS_NI; ii++) {
+                        const int k = 4 * lane + 256 * ii;
+                        float ne[4] = {0.0f, 0.0f, 0.0f, 0.0f}, le[4] = {0.0f, 0.0f, 0.0f, 0.0f},
+                              ge[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                        if (ok && k < Dp) {
+                            const float4 n4 = *(const float4*)(nrm + t * ld + k), l4 = *(const float4*)(lam + t * ld + k);
+                            const float nn[4] = {n4.x, n4.y, n4.z, n4.w}, ll[4] = {l4.x, l4.y, l4.z, l4.w};
+                            const float gg[4] = {gq[i][ii].x, gq[i][ii].y, gq[i][ii].z, gq[i][ii].w};
+                            const float lf[4] = {lq[i][ii].x, lq[i][ii].y, lq[i][ii].z, lq[i][ii].w};
+#pragma unroll
+                            for (int e = 0; e < 4; e++) {
+                                if (k + e < D) {
+                                    ne[e] = nn[e];
+                                    const float p1 = ll[e] * gg[e];
+                                    const float p2 = (1.0f - ll[e]) * nn[e];
+                                    ge[e] = p1 + p2;
+                                    le[e] = lf[e];
+                                }
+                            }
+                            if (k + 4 <= D) {
+                                stg((float4*)(gbase + k), float4{ge[0], ge[1], ge[2], ge[3]});
+                                stg((float4*)(wslot + k), float4{ne[0], ne[1], ne[2], ne[3]});
+                            } else {
+#pragma unroll
+                                for (int e = 0; e < 4; e++)
+                                    if (k + e < D) {
+                                        stg(gbase + k + e, ge[e]);
+                                        stg(wslot + k + e, ne[e]);
+                                    }
+                            }
+                        }
+                        nv[ii] = float4{ne[0], ne[1], ne[2], ne[3]};
+                        lv[ii] = float4{le[0], le[1], le[2], le[3]};
+                        gv[ii] = float4{ge[0], ge[1], ge[2], ge[3]};
+                        m = ts_amax4(ts_amax4(ts_amax4(m, nv[ii]), lv[ii]), gv[ii]);
+                    }
+                    float sx, ix;
+                    limb_scale(wave_max(m), sx, ix);
+#pragma unroll
+                    for (int ii = 0; ii < TS_NI; ii++) {
+                        const int k = 4 * lane + 256 * ii;
+                        if (k < Dp) {
+                            ts_put_limbs(xl, k, t, nv[ii], ix);
+                            ts_put_limbs(xl, Dp + k, t, lv[ii], ix);
+                            ts_put_limbs(xl, 2 * Dp + k, t, gv[ii], ix);
+                        }
+                    }
+                    if (lane == 0) rsc[t] = sx;
+                }
+            }
+            ts_barrier();
+            // h = GLU(x) (stream.go:214-220): fragment pairs (value 2q, gate 2q + 1)
+            ts_matvec<TS_PAIR, 4, 2>(B.w1, B.b1, 2 * Hp / 16, 3 * kcD, Hp / 16, xl, lane, w,
+                                     [&](int q, const float (&vv)[4], const float (&vg)[4], float4 bv, float4 bg) {
+                const int c0 = 16 * q + 4 * (lane >> 4), t = lane & 15;
+                const float sw = rsc[t] * B.s1;
+                const float bvv[4] = {bv.x, bv.y, bv.z, bv.w}, bgg[4] = {bg.x, bg.y, bg.z, bg.w};
+                float h[4];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float ov = fmaf(vv[r], sw, bvv[r]);
+                    const float gt = sigmoid_epi(fmaf(vg[r], sw, bgg[r]));
+                    h[r] = c0 + r < H ? ov * gt : 0.0f;
+                }
+                *(float4*)(hb + t * hld + c0) = float4{h[0], h[1], h[2], h[3]};
+            });
+            ts_barrier();
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int t = w + 8 * i;
+                float4 v[4];
+#pragma unroll
+                for (int ii = 0; ii < 4; ii++) v[ii] = ts_ld4(hb + t * hld, 4 * lane + 256 * ii, H);
+                const float sc = ts_row_limbs<4>(v, Hp, t, xl, lane);
+                if (lane == 0) rsc[t] = sc;
+            }
+            ts_barrier();
+            // cur = highway(cur, W2 h) (stream.go:222-229)
+            ts_matvec<TS_PAIR, 4, 2>(B.w2, B.b2, 2 * Dp / 16, Hp / 64, Dp / 16, xl, lane, w,
+                                     [&](int q, const float (&vv)[4], const float (&vg)[4], float4 bv, float4 bg) {
+                const int c0 = 16 * q + 4 * (lane >> 4), t = lane & 15;
+                const float sw = rsc[t] * B.s2;
+                const float bvv[4] = {bv.x, bv.y, bv.z, bv.w}, bgg[4] = {bg.x, bg.y, bg.z, bg.w};
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int c = c0 + r;
+                    if (c < D) {
+                        const float ov = fmaf(vv[r], sw, bvv[r]);
+                        const float gt = sigmoid_epi(fmaf(vg[r], sw, bgg[r]));
+                        const float x1 = (1.0f - gt) * cur[t * ld + c];
+                        const float x2 = gt * ov;
+                        cur[t * ld + c] = x1 + x2;
+                    }
+                }
+            });
+            ts_barrier();
+        }
+        if (B.attn) {
+            // attendPosition's projection (internal/quant/attention.go:69-80): q, k, v of every session to
+            // memory for the attention kernel; cur and blockIn for the next segment
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int t = w + 8 * i;
+                const float sc = ts_norm_row(cur + t * ld, bin + t * ld, resid && B.steps == 0, B.anorm, D, Dp, nullptr, xl, t, lane);
+                if (lane == 0) rsc[t] = sc;
+                if (t < ns) {
+                    const long long row = (long long)(s0 + t) * Dp;
+#pragma unroll
+                    for (int ii = 0; ii < TS_NI; ii++) {
+                        const int k = 4 * lane + 256 * ii;
+                        if (k < Dp) {
+                            *(float4*)(a.cur + row + k) = *(const float4*)(cur + t * ld + k);
+                            *(float4*)(a.bin + row + k) = *(const float4*)(bin + t * ld + k);
+                        }
+                    }
+                }
+            }
+            ts_barrier();
+            ts_matvec<TS_FRAG, 4, 2>(B.qkv, nullptr, a.Np3 / 16, kcD, a.Np3 / 16, xl, lane, w,
+                                     [&](int f, const float (&v)[4], float4) {
+                const int c0 = 16 * f + 4 * (lane >> 4), t = lane & 15;
+                const float sw = rsc[t] * B.sqkv;
+                if (t < ns) {
+                    float* o = a.qkv + (long long)(s0 + t) * 3 * D + c0;
+                    if (c0 + 4 <= 3 * D && (D & 3) == 0) {
+                        stg((float4*)o, float4{v[0] * sw, v[1] * sw, v[2] * sw, v[3] * sw});
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; r++)
+                            if (c0 + r < 3 * D) o[r] = v[r] * sw;
+                    }
+                }
+            });
+            return;
+        }
+    }
+    // headLogits (internal/quant/stream.go:232-248)
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int t = w + 8 * i;
+        const float sc = ts_norm_row(cur + t * ld, bin + t * ld, false, a.final_norm, D, Dp, nullptr, xl, t, lane);
+        if (lane == 0) rsc[t] = sc;
+    }
+    ts_barrier();
+    // 128-channel tiles of the vocabulary, wave w taking tiles w, w + 8, ...: the logits epilogue's
+    // statistics per token (max, sum exp(l - max), first argmax) with its lane structure
+    const int ntiles = Vp / LX_BN;
+    const bool want_argmax = a.argmax || a.next_ids || a.out_ids;
+    const int t = lane & 15, g4 = lane >> 4;
+    const float sw = rsc[t] * a.head_scale;
+    ts_matvec<TS_TILE, 8, 1>(a.headw, a.headb, Vp / 16, kcD, ntiles, xl, lane, w,
+                             [&](int tt, const v4i (&acc)[8][3], const float4 (&b4)[8]) {
+        float y[8][4];
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const float bb[4] = {b4[g].x, b4[g].y, b4[g].z, b4[g].w};
+#pragma unroll
+            for (int r = 0; r < 4; r++) y[g][r] = fmaf(s1_dot(acc[g], r), sw, bb[r]);
+        }
+        const int nb = tt * LX_BN + 4 * g4;
+        if (a.logits && t < ns) {
+            float* lo = a.logits + (long long)(s0 + t) * V;
+#pragma unroll
+            for (int ti = 0; ti < 8; ti++) {
+                const int c = nb + 16 * ti;
+                if ((V & 3) == 0 && c + 4 <= V) {
+                    *(float4*)(lo + c) = float4{y[ti][0], y[ti][1], y[ti][2], y[ti][3]};
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        if (c + r < V) lo[c + r] = y[ti][r];
+                }
+            }
+        }
+        const float l2e = 1.4426950408889634f;
+        float mx = y[0][0];
+#pragma unroll
+        for (int ti = 0; ti < 8; ti++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) mx = fmaxf(mx, y[ti][r]);
+        const float ml = mx == -INFINITY ? 0.0f : mx * l2e;
+        float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ti = 0; ti < 8; ti++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) s4[r] += __builtin_amdgcn_exp2f(fmaf(y[ti][r], l2e, -ml));
+        float bmax = mx, bsum = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+        int bidx = 0x7fffffff;
+        if (want_argmax && mx > -INFINITY) {
+            int off = 0;
+#pragma unroll
+            for (int ti = 7; ti >= 0; ti--)
+#pragma unroll
+                for (int r = 3; r >= 0; r--) off = y[ti][r] == mx ? ti * 16 + r : off;
+            bidx = nb + off;
+        }
+#pragma unroll
+        for (int o = 16; o <= 32; o <<= 1) {
+            float om = __shfl_xor(bmax, o, 64), os = __shfl_xor(bsum, o, 64);
+            int oi = __shfl_xor(bidx, o, 64);
+            float nm = fmaxf(bmax, om);
+            float ns_ = (bmax == -INFINITY ? 0.0f : bsum * __expf(bmax - nm)) +
+                        (om == -INFINITY ? 0.0f : os * __expf(om - nm));
+            int ni = (om > bmax) ? oi : (bmax > om) ? bidx : min(bidx, oi);
+            bmax = nm; bsum = ns_; bidx = ni;
+        }
+        if (g4 == 0) {
+            float* d = tst + (t * ntiles + tt) * 3;
+            d[0] = bmax;
+            d[1] = bsum;
+            d[2] = __int_as_float(bidx);
+        }
+    });
+    ts_barrier();
+    // their combination (head_combine_kernel): 16 lanes per session, waves 0..3
+    if (w < 4) {
+        const int tk = 4 * w + (lane >> 4), l = lane & 15;
+        const float* st = tst + tk * ntiles * 3;
+        float bm = -INFINITY, bsm = 0.0f;
+        int bi = 0x7fffffff;
+        for (int u = l; u < ntiles; u += 16) merge_stats(bm, bsm, bi, st[3 * u], st[3 * u + 1], __float_as_int(st[3 * u + 2]));
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) {
+            const float om = __shfl_xor(bm, o, 16), os = __shfl_xor(bsm, o, 16);
+            const int oi = __shfl_xor(bi, o, 16);
+            merge_stats(bm, bsm, bi, om, os, oi);
+        }
+        if (l == 0 && tk < ns) {
+            const int s = s0 + tk;
+            const double p = 1.0 / (double)bsm;
+            if (a.argmax) a.argmax[s] = bi;
+            if (a.prob) a.prob[s] = p;
+            if (a.next_ids) a.next_ids[s] = bi;
+            const int oc = a.col ? *a.col : a.out_col;
+            if (a.out_ids) a.out_ids[(long long)s * a.out_ld + oc] = bi;
+            if (a.out_probs) a.out_probs[(long long)s * a.out_ld + oc] = p;
+            a.pos[s] = a.pos[s] + 1;
         }
     }
 }
@@ -2528,6 +3155,22 @@ hipError_t step1_t(const Step1Args& a, hipStream_t s) {
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
     if (attr != hipSuccess) return attr;
     hipLaunchKernelGGL(step1_kernel<DH>, dim3(a.S), dim3(S1_THREADS), lds, s, a);
+    return hipGetLastError();
+}
+
+bool tile_step_fits(const TileStepArgs& a) {
+    if (a.S <= 0 || a.nblocks <= 0 || a.D > 512 || a.Dp > 512 || a.Hp > 1024 || a.Dp % 64 || a.Hp % 64 || a.Vp % LX_BN)
+        return false;
+    return (size_t)ts_lds(a.Dp, a.Hp, a.Vp).bytes <= kTileStepMaxLds;
+}
+
+hipError_t launch_tile_step(const TileStepArgs& a, hipStream_t s) {
+    if (!tile_step_fits(a)) return hipErrorInvalidValue;
+    static const hipError_t attr = hipFuncSetAttribute((const void*)tile_step_kernel,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kTileStepMaxLds);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL(tile_step_kernel, dim3((a.S + TS_NS - 1) / TS_NS), dim3(TS_THREADS),
+                       (size_t)ts_lds(a.Dp, a.Hp, a.Vp).bytes, s, a);
     return hipGetLastError();
 }
 

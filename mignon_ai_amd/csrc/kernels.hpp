@@ -171,6 +171,25 @@ struct Step1Args {
 bool step1_fits(const Step1Args& a);
 hipError_t launch_step1(const Step1Args& a, hipStream_t s);
 
+// A decode step for tiles of 16 sessions, one workgroup each (the 16 token columns of the matrix cores),
+// in segments: segment 0 runs from the embedding to the first attention block's projection q, k, v;
+// segment k > 0 starts with the out projection of the block whose attention just ran
+// (attention_step_rows_kernel, which writes the out projection's operand) and runs to the next
+// attention block's projection or through the head. Same session state and outputs as Step1Args.
+struct TileStepArgs : Step1Args {
+    int seg_block = 0;               // first block of the segment
+    int seg_out = 0;                 // 1: the segment starts with that block's out projection
+    float* cur = nullptr;            // [S][Dp] cur and blockIn between segments
+    float* bin = nullptr;
+    float* qkv = nullptr;            // [S][3D]: the projection that ends a segment
+    const int8_t* att_xl = nullptr;  // the attention output's limb planes (fragment layout, K = Dp)
+    const float* att_xs = nullptr;   // and their row scales [S]
+};
+constexpr size_t kTileStepMaxLds = 150 * 1024;
+// Whether the tiled step takes this model (state size up to 512, hidden size up to 1024, and its LDS).
+bool tile_step_fits(const TileStepArgs& a);
+hipError_t launch_tile_step(const TileStepArgs& a, hipStream_t s);
+
 // Per-row combination of the head GEMM's per-tile statistics.
 struct HeadCombineArgs {
     int M = 0, ntiles = 0;

@@ -5,12 +5,13 @@ namespace mg {
 
 enum Option : int {
     OPT_GEMM_KERNEL = 0,       // 0 automatic, 1 streaming, 2 weight-stationary
-    OPT_ATTENTION_KERNEL = 1,  // 0 automatic, 1 reference order (VALU), 2 matrix cores
+    OPT_ATTENTION_KERNEL = 1,  // 0 automatic, 1 reference order (VALU), 2 matrix cores, 3 projection fused in
     OPT_SCAN_KERNEL = 2,       // 0 automatic, 1 latch scan then rule-input packing, 2 fused
     OPT_STEP_GRAPH = 3,        // decode steps: 0 automatic (replayed from a captured HIP graph), 1 launched
                                // one kernel at a time, 2 graph
-    OPT_STEP_KERNEL = 4,       // decode steps of small session sets: 0 automatic, 1 layer by layer, 2 one
-                               // workgroup per session (step1_kernel) wherever the model fits it
+    OPT_STEP_KERNEL = 4,       // decode steps: 0 automatic, 1 layer by layer, 2 one workgroup per session
+                               // (step1_kernel), 3 one workgroup per 16 sessions (tile_step_kernel),
+                               // wherever the model fits them
     OPT_COUNT
 };
 
