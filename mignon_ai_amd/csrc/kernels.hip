@@ -1231,7 +1231,7 @@ __host__ __device__ constexpr int rk_lds_floats(int cap, int dh) { return cap * 
 // so a wave makes one memory round trip. `sm` (rk_lds_floats) and `inv_sh` are private to the wave.
 // Returns output element `lane` of the head (lanes < DH) and records this position's key and value in
 // the ring.
-template <int DH>
+template <int DH, bool QL = false>
 __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, int lane, float* sm, float& inv_sh) {
     constexpr int DS = DH + 4;
     constexpr int C4 = DH / 4;
@@ -1247,19 +1247,35 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
     const float* qkv = a.qkv + (long long)s_ * 3 * D;
     const float* kr = a.kring + ((long long)s_ * a.heads + h) * cap * DH;
     const float* vr = a.vring + ((long long)s_ * a.heads + h) * cap * DH;
+    // q, k, v of this position: in LDS (QL) or global memory; the rings in global memory. Typed loads, so
+    // that the compiler need not treat them as generic (flat) accesses, which it serialises.
+    auto qkv4 = [&](const float* p) -> float4 {
+        if constexpr (QL) {
+            typedef float f4 __attribute__((ext_vector_type(4)));
+            const f4 v = *(const __attribute__((address_space(3))) f4*)p;
+            return float4{v.x, v.y, v.z, v.w};
+        } else {
+            return ldg((const float4*)p);
+        }
+    };
     // lanes 0..3*C4-1: one float4 each of this position's q, k and v (part lane / C4, chunk lane % C4)
     const int qpart = min(lane / C4, 2), qc = lane % C4;
-    const float4 mine = *(const float4*)(qkv + qpart * D + h * DH + 4 * qc);
+    const float4 mine = qkv4(qkv + qpart * D + h * DH + 4 * qc);
     // ring slot of key lo + jj (jj < span <= cap): one wrap, no division per key
     const int lo_slot = lo % cap;
     auto slot = [&](int jj) { const int r = lo_slot + jj; return r >= cap ? r - cap : r; };
     // this lane's key row (key lo + lane; the current position's from qkv, not yet in the ring)
     float4 krow[C4];
     {
+        // (the current position's ring slot is read too, in bounds, and its value discarded)
         const int jj = min(lane, span - 1);
-        const float* kp = jj == span - 1 ? qkv + D + h * DH : kr + (long long)slot(jj) * DH;
+        const float* kp = kr + (long long)slot(jj) * DH;
 #pragma unroll
-        for (int c = 0; c < C4; c++) krow[c] = *(const float4*)(kp + 4 * c);
+        for (int c = 0; c < C4; c++) krow[c] = ldg((const float4*)(kp + 4 * c));
+        if (jj == span - 1) {
+#pragma unroll
+            for (int c = 0; c < C4; c++) krow[c] = qkv4(qkv + D + h * DH + 4 * c);
+        }
     }
     // values: rows jj = 0..span-1 into LDS, every load issued before the first store. Lanes past the
     // end repeat the last element (the same bytes to the same address), so no store is conditional and
@@ -1272,8 +1288,8 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
         for (int u = 0; u < 8; u++) {
             const int e = min(e0 + u * 64 + lane, n4 - 1);
             const int jj = e / C4, c = e - jj * C4;
-            const float* vp = jj == span - 1 ? qkv + 2 * D + h * DH : vr + (long long)slot(jj) * DH;
-            vb[u] = *(const float4*)(vp + 4 * c);
+            vb[u] = ldg((const float4*)(vr + (long long)slot(jj) * DH + 4 * c));
+            if (jj == span - 1) vb[u] = qkv4(qkv + 2 * D + h * DH + 4 * c);
             off[u] = jj * DS + 4 * c;
         }
 #pragma unroll
@@ -1308,7 +1324,7 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
     // record this position's key and value (slot pos % cap; the evicted key is outside the window)
     if (lane >= C4 && lane < 3 * C4) {
         float* ring = lane < 2 * C4 ? a.kring : a.vring;
-        *(float4*)(ring + (((long long)s_ * a.heads + h) * cap + pos % cap) * DH + 4 * qc) = mine;
+        stg((float4*)(ring + (((long long)s_ * a.heads + h) * cap + pos % cap) * DH + 4 * qc), mine);
     }
     return o;
 }
@@ -1635,6 +1651,15 @@ __device__ __forceinline__ void merge_stats(float& bm, float& bs, int& bi, float
     bm = nm; bs = ns; bi = ni;
 }
 
+// Workgroup barrier over LDS only, for the one-workgroup decode steps: their waves exchange data through
+// LDS alone (what they store to global memory is read by later kernels, or by the storing lane), so
+// outstanding global loads and stores need not drain at each phase boundary.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // ------------------------------------------------------------------------------------------------
 // One session's decode step in one workgroup (step1_kernel)
 // ------------------------------------------------------------------------------------------------
@@ -1672,11 +1697,11 @@ __device__ __forceinline__ float s1_rms_inv(const float* x, int D, int lane) {
 __device__ __forceinline__ float s1_block_max(float v, float* red, int lane, int w) {
     v = wave_max(v);
     if (lane == 0) red[w] = v;
-    __syncthreads();
+    lds_barrier();
     float m = red[0];
 #pragma unroll
     for (int i = 1; i < S1_THREADS / 64; i++) m = fmaxf(m, red[i]);
-    __syncthreads();  // red is reused by the next reduction
+    lds_barrier();  // red is reused by the next reduction
     return m;
 }
 
@@ -1691,98 +1716,107 @@ __device__ __forceinline__ float s1_limbs(const float* x, int Dvalid, int Kp, in
     limb_scale(amax, sc, inv);
     for (int k = tid; k < Kp; k += S1_THREADS) {
         const Limbs L = split_limbs(k < Dvalid ? x[k] : 0.0f, inv);
-        int8_t* o = xl + (k >> 6) * 192 + (k & 63);
+        int8_t* o = xl + (k >> 6) * 3072 + ((16 * ((k >> 4) & 3)) << 4) + (k & 15);
         o[0] = L.q0;
-        o[64] = L.q1;
-        o[128] = L.q2;
+        o[1024] = L.q1;
+        o[2048] = L.q2;
     }
     return sc;
-}
-
-// Fragments f[0..nf) (16 output channels each, nf <= 4) of an int8 weight matrix in the GEMM fragment
-// layout times the row's limb planes: the B operand of v_mfma_i32_16x16x64_i8 is the row in token column
-// 0, so only lanes with (lane & 15) == 0 take it; their accumulators hold channels 16f + 4(lane >> 4) + r,
-// one sum per plane. The weights of four K steps of all nf fragments are requested together, so a wave
-// waits for memory once per four K steps rather than once per fragment and step.
-__device__ __forceinline__ void s1_frags(const int8_t* W, int np16, int kc, const int (&f)[4], int nf,
-                                         const int8_t* xl, int lane, v4i (&acc)[4][3]) {
-#pragma unroll
-    for (int g = 0; g < 4; g++) acc[g][0] = acc[g][1] = acc[g][2] = v4i{0, 0, 0, 0};
-    const bool tok = (lane & 15) == 0;
-    const int8_t* xp = xl + (lane >> 4) * 16;
-    for (int k0 = 0; k0 < kc; k0 += 4) {
-        v4i wv[4][4];
-#pragma unroll
-        for (int g = 0; g < 4; g++)
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                if (g < nf && k0 + j < kc)
-                    wv[g][j] = ldg((const v4i*)(W + ((((long long)(k0 + j) * np16 + f[g]) << 10) + lane * 16)));
-        // keep the batch together: the scheduler would otherwise sink each load to its first MFMA
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            if (k0 + j >= kc) break;
-            v4i xv[3];
-#pragma unroll
-            for (int l = 0; l < 3; l++) xv[l] = tok ? *(const v4i*)(xp + (k0 + j) * 192 + l * 64) : v4i{0, 0, 0, 0};
-#pragma unroll
-            for (int g = 0; g < 4; g++)
-                if (g < nf)
-#pragma unroll
-                    for (int l = 0; l < 3; l++) acc[g][l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wv[g][j], xv[l], acc[g][l], 0, 0, 0);
-        }
-    }
 }
 
 __device__ __forceinline__ float s1_dot(const v4i (&acc)[3], int r) {
     return fmaf((float)acc[2][r], kInvLimb2, fmaf((float)acc[1][r], kInvLimb1, (float)acc[0][r]));
 }
 
-// Matrix-vector phases of step1_kernel: wave w takes fragments w, w + 8, ... in groups of four
-// (S1_FRAGS, with `f`, `r` and the combined dot product `v` in scope of BODY for each channel its lane
-// holds) or fragment pairs (value 2q, gate 2q + 1) in groups of two (S1_PAIRS: `q`, `g4`, `r`, `vv`,
-// `vg`).
-#define S1_FRAGS(W, NP16, KC, BODY)                                                                  \
-    for (int f0 = w; f0 < (NP16); f0 += 4 * (S1_THREADS / 64)) {                                    \
-        int fl[4];                                                                                   \
-        int nf = 0;                                                                                  \
-        for (int g = 0; g < 4; g++) {                                                                \
-            fl[g] = f0 + g * (S1_THREADS / 64);                                                      \
-            if (fl[g] < (NP16)) nf = g + 1;                                                          \
-        }                                                                                            \
-        v4i acc[4][3];                                                                               \
-        s1_frags((W), (NP16), (KC), fl, nf, xl, lane, acc);                                          \
-        if ((lane & 15) == 0) {                                                                      \
-            _Pragma("unroll") for (int g = 0; g < 4; g++) {                                          \
-                if (g >= nf) break;                                                                  \
-                const int f = fl[g];                                                                 \
-                _Pragma("unroll") for (int r = 0; r < 4; r++) {                                      \
-                    const float v = s1_dot(acc[g], r);                                               \
-                    BODY                                                                             \
-                }                                                                                    \
-            }                                                                                        \
-        }                                                                                            \
+// Matrix phases of the one-workgroup decode steps (8 waves; the limb operand xl holds the rows of up to
+// 16 sessions in the MFMA's token columns). Wave w takes units w, w + 8, ... of the phase: with TS_FRAG one
+// 16-channel fragment (GF units per group), with TS_PAIR the fragment pair 2q (value), 2q + 1 (gate)
+// (GF/2 per group), with TS_TILE the GF consecutive fragments GF*u .. GF*u + GF - 1 (one per group).
+// A group's weights are requested KB K steps at a time (GF * KB loads in flight; loads past the wave's
+// units or past the last K step repeat a valid address and go unused), with the group's bias values
+// (`bias`, indexed by output row, or null), then multiplied by the tile's limb planes (all 16 token
+// columns). After a group's last K step `epi` gets, for each unit, the combined dot products of token
+// lane & 15, channels c0 .. c0 + 3 with c0 = 16 f + 4 (lane >> 4), and the bias of those rows:
+// epi(f, v[4], b) (TS_FRAG), epi(q, vv[4], vg[4], bv, bg) (TS_PAIR), or epi(u, acc, b[GF]) (TS_TILE).
+enum { TS_FRAG = 0, TS_PAIR = 1, TS_TILE = 2 };
+template <int MODE, int GF, int KB, class Epi>
+__device__ __forceinline__ void ts_matvec(const int8_t* W, const float* bias, int np16, int kc, int nunits,
+                                          const int8_t* xl, int lane, int w, Epi&& epi) {
+    constexpr int UPG = MODE == TS_FRAG ? GF : MODE == TS_PAIR ? GF / 2 : 1;  // units per group
+    const int mine = nunits > w ? (nunits - 1 - w) / 8 + 1 : 0;
+    const int8_t* wl = W + lane * 16;
+    const int8_t* xp = xl + lane * 16;
+    for (int gi = 0; gi * UPG < mine; gi++) {
+        int fr[GF];
+        bool ok[GF];
+#pragma unroll
+        for (int g = 0; g < GF; g++) {
+            const int u0 = UPG * gi + (MODE == TS_FRAG ? g : MODE == TS_PAIR ? g / 2 : 0);
+            ok[g] = u0 < mine;
+            const int un = w + 8 * min(u0, mine - 1);
+            fr[g] = MODE == TS_FRAG ? un : MODE == TS_PAIR ? 2 * un + (g & 1) : GF * un + g;
+        }
+        // the bias with the weights (after the MFMAs for whole tiles, whose accumulators fill the registers)
+        float4 b4[GF];
+        auto load_bias = [&] {
+#pragma unroll
+            for (int g = 0; g < GF; g++)
+                b4[g] = bias ? ldg((const float4*)(bias + 16 * fr[g] + 4 * (lane >> 4))) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        };
+        if constexpr (MODE != TS_TILE) load_bias();
+        v4i acc[GF][3];
+#pragma unroll
+        for (int g = 0; g < GF; g++) acc[g][0] = acc[g][1] = acc[g][2] = v4i{0, 0, 0, 0};
+        for (int k0 = 0; k0 < kc; k0 += KB) {
+            v4i wv[GF][KB];
+#pragma unroll
+            for (int g = 0; g < GF; g++)
+#pragma unroll
+                for (int j = 0; j < KB; j++)
+                    wv[g][j] = ldg((const v4i*)(wl + (((long long)min(k0 + j, kc - 1) * np16 + fr[g]) << 10)));
+            // keep the batch together: the scheduler would otherwise sink each load to its first MFMA
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < KB; j++) {
+                if (k0 + j >= kc) break;
+                v4i xv[3];
+#pragma unroll
+                for (int l = 0; l < 3; l++) xv[l] = *(const v4i*)(xp + (k0 + j) * 3072 + l * 1024);
+#pragma unroll
+                for (int g = 0; g < GF; g++)
+                    if (ok[g])
+#pragma unroll
+                        for (int l = 0; l < 3; l++)
+                            acc[g][l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wv[g][j], xv[l], acc[g][l], 0, 0, 0);
+            }
+        }
+        if constexpr (MODE == TS_TILE) {
+            load_bias();
+            epi(w + 8 * gi, acc, b4);
+        } else if constexpr (MODE == TS_PAIR) {
+#pragma unroll
+            for (int p = 0; p < GF / 2; p++)
+                if (ok[2 * p]) {
+                    float vv[4], vg[4];
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        vv[r] = s1_dot(acc[2 * p], r);
+                        vg[r] = s1_dot(acc[2 * p + 1], r);
+                    }
+                    epi(fr[2 * p] >> 1, vv, vg, b4[2 * p], b4[2 * p + 1]);
+                }
+        } else {
+#pragma unroll
+            for (int g = 0; g < GF; g++)
+                if (ok[g]) {
+                    float v[4];
+#pragma unroll
+                    for (int r = 0; r < 4; r++) v[r] = s1_dot(acc[g], r);
+                    epi(fr[g], v, b4[g]);
+                }
+        }
     }
-#define S1_PAIRS(W, NP16, KC, BODY)                                                                  \
-    for (int q0 = w; q0 < (NP16) / 2; q0 += 2 * (S1_THREADS / 64)) {                                \
-        const int q1 = q0 + S1_THREADS / 64;                                                         \
-        const int np = q1 < (NP16) / 2 ? 2 : 1;                                                      \
-        int fl[4] = {2 * q0, 2 * q0 + 1, 2 * q1, 2 * q1 + 1};                                        \
-        v4i acc[4][3];                                                                               \
-        s1_frags((W), (NP16), (KC), fl, 2 * np, xl, lane, acc);                                      \
-        if ((lane & 15) == 0) {                                                                      \
-            const int g4 = lane >> 4;                                                                \
-            _Pragma("unroll") for (int pp = 0; pp < 2; pp++) {                                       \
-                if (pp >= np) break;                                                                 \
-                const int q = pp == 0 ? q0 : q1;                                                     \
-                _Pragma("unroll") for (int r = 0; r < 4; r++) {                                      \
-                    const float vv = s1_dot(acc[2 * pp], r), vg = s1_dot(acc[2 * pp + 1], r);        \
-                    BODY                                                                             \
-                }                                                                                    \
-            }                                                                                        \
-        }                                                                                            \
-    }
+}
 
 template <int DH>
 __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
@@ -1815,7 +1849,7 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
             bin[d] = v;
         }
     }
-    __syncthreads();
+    lds_barrier();
     int bs = 0, ab = 0;
     for (int b = 0; b < a.nblocks; b++) {
         const Step1Block& B = a.blocks[b];
@@ -1826,7 +1860,7 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
                 bin[d] = v;
                 cur[d] = v;
             }
-            __syncthreads();
+            lds_barrier();
         }
         for (int st = 0; st < B.steps; st++, bs++) {
             int dil = B.init_dil;
@@ -1838,24 +1872,29 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
                     const float inv = s1_rms_inv(cur, D, lane);
                     if (lane == 0) bcast[0] = inv;
                 }
-                __syncthreads();
+                lds_barrier();
                 const float inv = bcast[0];
                 for (int d = tid; d < Dp; d += S1_THREADS) nrm[d] = d < D ? (cur[d] * inv) * ldg(B.gamma + d) : 0.0f;
             } else {
                 for (int d = tid; d < Dp; d += S1_THREADS) nrm[d] = d < D ? cur[d] : 0.0f;
             }
-            __syncthreads();
+            lds_barrier();
             const float sn = s1_limbs(nrm, D, Dp, xl, red, tid, lane, w);
-            __syncthreads();
+            lds_barrier();
             // lambda = sigmoid_clamped(n.W_sel*s + base) (stream.go:195-205)
             {
                 const float sw = sn * B.ssel;
-                S1_FRAGS(B.wsel, a.NpD / 16, Dp / 64, {
-                    const int c = 16 * f + 4 * (lane >> 4) + r;
-                    if (c < D) lam[c] = sigmoid_epi(fmaf(v, sw, ldg(a.latch_base + c)));
+                ts_matvec<TS_FRAG, 4, 2>(B.wsel, a.latch_base, a.NpD / 16, Dp / 64, a.NpD / 16, xl, lane, w,
+                                         [&](int f, const float (&v)[4], float4 b) {
+                    if (lane & 15) return;
+                    const int c0 = 16 * f + 4 * (lane >> 4);
+                    const float bb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        if (c0 + r < D) lam[c0 + r] = sigmoid_epi(fmaf(v[r], sw, bb[r]));
                 });
             }
-            __syncthreads();
+            lds_barrier();
             // latch update, norm ring and the rule input [n | left | g] (latch_step_kernel)
             float nv = 0.0f, lv = 0.0f, gv = 0.0f;
             const int d = tid;
@@ -1882,42 +1921,55 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
                     for (int sg = 0; sg < 3; sg++) {
                         const Limbs L = split_limbs(v3[sg], ix);
                         const int k = sg * Dp + d;
-                        int8_t* o = xl + (k >> 6) * 192 + (k & 63);
+                        int8_t* o = xl + (k >> 6) * 3072 + ((16 * ((k >> 4) & 3)) << 4) + (k & 15);
                         o[0] = L.q0;
-                        o[64] = L.q1;
-                        o[128] = L.q2;
+                        o[1024] = L.q1;
+                        o[2048] = L.q2;
                     }
                 }
             }
-            __syncthreads();
+            lds_barrier();
             // h = GLU(x) (stream.go:214-220): fragment pairs (value 2q, gate 2q + 1)
             {
                 const float sw = sx * B.s1;
-                S1_PAIRS(B.w1, 2 * Hp / 16, 3 * Dp / 64, {
-                    const int c = 16 * q + 4 * g4 + r;
-                    const float ov = fmaf(vv, sw, ldg(B.b1 + 32 * q + 4 * g4 + r));
-                    const float gt = sigmoid_epi(fmaf(vg, sw, ldg(B.b1 + 32 * q + 16 + 4 * g4 + r)));
-                    hbuf[c] = c < H ? ov * gt : 0.0f;
-                });
-            }
-            __syncthreads();
-            const float sh = s1_limbs(hbuf, H, Hp, xl, red, tid, lane, w);
-            __syncthreads();
-            // cur = highway(cur, W2 h) (stream.go:222-229)
-            {
-                const float sw = sh * B.s2;
-                S1_PAIRS(B.w2, 2 * Dp / 16, Hp / 64, {
-                    const int c = 16 * q + 4 * g4 + r;
-                    if (c < D) {
-                        const float ov = fmaf(vv, sw, ldg(B.b2 + 32 * q + 4 * g4 + r));
-                        const float gt = sigmoid_epi(fmaf(vg, sw, ldg(B.b2 + 32 * q + 16 + 4 * g4 + r)));
-                        const float x1 = (1.0f - gt) * cur[c];
-                        const float x2 = gt * ov;
-                        cur[c] = x1 + x2;
+                ts_matvec<TS_PAIR, 4, 2>(B.w1, B.b1, 2 * Hp / 16, 3 * Dp / 64, Hp / 16, xl, lane, w,
+                                         [&](int q, const float (&vv)[4], const float (&vg)[4], float4 bv, float4 bg) {
+                    if (lane & 15) return;
+                    const int c0 = 16 * q + 4 * (lane >> 4);
+                    const float bvv[4] = {bv.x, bv.y, bv.z, bv.w}, bgg[4] = {bg.x, bg.y, bg.z, bg.w};
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const float ov = fmaf(vv[r], sw, bvv[r]);
+                        const float gt = sigmoid_epi(fmaf(vg[r], sw, bgg[r]));
+                        hbuf[c0 + r] = c0 + r < H ? ov * gt : 0.0f;
                     }
                 });
             }
-            __syncthreads();
+            lds_barrier();
+            const float sh = s1_limbs(hbuf, H, Hp, xl, red, tid, lane, w);
+            lds_barrier();
+            // cur = highway(cur, W2 h) (stream.go:222-229)
+            {
+                const float sw = sh * B.s2;
+                ts_matvec<TS_PAIR, 4, 2>(B.w2, B.b2, 2 * Dp / 16, Hp / 64, Dp / 16, xl, lane, w,
+                                         [&](int q, const float (&vv)[4], const float (&vg)[4], float4 bv, float4 bg) {
+                    if (lane & 15) return;
+                    const int c0 = 16 * q + 4 * (lane >> 4);
+                    const float bvv[4] = {bv.x, bv.y, bv.z, bv.w}, bgg[4] = {bg.x, bg.y, bg.z, bg.w};
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int c = c0 + r;
+                        if (c < D) {
+                            const float ov = fmaf(vv[r], sw, bvv[r]);
+                            const float gt = sigmoid_epi(fmaf(vg[r], sw, bgg[r]));
+                            const float x1 = (1.0f - gt) * cur[c];
+                            const float x2 = gt * ov;
+                            cur[c] = x1 + x2;
+                        }
+                    }
+                });
+            }
+            lds_barrier();
         }
         if (B.attn) {
             // attendPosition (internal/quant/attention.go:69-104)
@@ -1925,22 +1977,26 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
                 const float inv = s1_rms_inv(cur, D, lane);
                 if (lane == 0) bcast[0] = inv;
             }
-            __syncthreads();
+            lds_barrier();
             {
                 const float inv = bcast[0];
                 for (int d = tid; d < Dp; d += S1_THREADS) nrm[d] = d < D ? (cur[d] * inv) * ldg(B.anorm + d) : 0.0f;
             }
-            __syncthreads();
+            lds_barrier();
             const float sa = s1_limbs(nrm, D, Dp, xl, red, tid, lane, w);
-            __syncthreads();
+            lds_barrier();
             {
                 const float sw = sa * B.sqkv;
-                S1_FRAGS(B.qkv, a.Np3 / 16, Dp / 64, {
-                    const int c = 16 * f + 4 * (lane >> 4) + r;
-                    if (c < 3 * D) qkv[c] = v * sw;
+                ts_matvec<TS_FRAG, 4, 2>(B.qkv, nullptr, a.Np3 / 16, Dp / 64, a.Np3 / 16, xl, lane, w,
+                                         [&](int f, const float (&v)[4], float4) {
+                    if (lane & 15) return;
+                    const int c0 = 16 * f + 4 * (lane >> 4);
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        if (c0 + r < 3 * D) qkv[c0 + r] = v[r] * sw;
                 });
             }
-            __syncthreads();
+            lds_barrier();
             if (w < a.heads) {
                 AttnStepArgs sa_;
                 sa_.S = 1; sa_.D = D; sa_.Dp = Dp; sa_.heads = a.heads; sa_.window = a.window; sa_.cap = a.cap;
@@ -1949,20 +2005,24 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
                 const long long ring0 = ((long long)ab * a.S + s_) * a.heads * a.cap * DH;
                 sa_.kring = a.kring + ring0;
                 sa_.vring = a.vring + ring0;
-                const float o = rk_head<DH>(sa_, 0, w, lane, rk + w * rkf, rk_inv[w]);
+                const float o = rk_head<DH, true>(sa_, 0, w, lane, rk + w * rkf, rk_inv[w]);
                 if (lane < DH) att[w * DH + lane] = o;
             }
-            __syncthreads();
+            lds_barrier();
             const float so_ = s1_limbs(att, D, Dp, xl, red, tid, lane, w);
-            __syncthreads();
+            lds_barrier();
             {
                 const float sw = so_ * B.so;
-                S1_FRAGS(B.wo, a.NpD / 16, Dp / 64, {
-                    const int c = 16 * f + 4 * (lane >> 4) + r;
-                    if (c < D) cur[c] = cur[c] + v * sw;
+                ts_matvec<TS_FRAG, 4, 2>(B.wo, nullptr, a.NpD / 16, Dp / 64, a.NpD / 16, xl, lane, w,
+                                         [&](int f, const float (&v)[4], float4) {
+                    if (lane & 15) return;
+                    const int c0 = 16 * f + 4 * (lane >> 4);
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        if (c0 + r < D) cur[c0 + r] = cur[c0 + r] + v[r] * sw;
                 });
             }
-            __syncthreads();
+            lds_barrier();
             ab++;
         }
     }
@@ -1972,23 +2032,25 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
             const float inv = s1_rms_inv(cur, D, lane);
             if (lane == 0) bcast[0] = inv;
         }
-        __syncthreads();
+        lds_barrier();
         const float inv = bcast[0];
         for (int d = tid; d < Dp; d += S1_THREADS) nrm[d] = d < D ? (cur[d] * inv) * a.final_norm[d] : 0.0f;
     } else {
         for (int d = tid; d < Dp; d += S1_THREADS) nrm[d] = d < D ? cur[d] : 0.0f;
     }
-    __syncthreads();
+    lds_barrier();
     const float sf = s1_limbs(nrm, D, Dp, xl, red, tid, lane, w);
-    __syncthreads();
+    lds_barrier();
     {
         const float sw = sf * a.head_scale;
-        S1_FRAGS(a.headw, Vp / 16, Dp / 64, {
-            const int c = 16 * f + 4 * (lane >> 4) + r;
-            logit[c] = fmaf(v, sw, a.headb[c]);
+        ts_matvec<TS_FRAG, 4, 2>(a.headw, a.headb, Vp / 16, Dp / 64, Vp / 16, xl, lane, w,
+                                 [&](int f, const float (&v)[4], float4 b) {
+            if (lane & 15) return;
+            const int c0 = 16 * f + 4 * (lane >> 4);
+            *(float4*)(logit + c0) = float4{fmaf(v[0], sw, b.x), fmaf(v[1], sw, b.y), fmaf(v[2], sw, b.z), fmaf(v[3], sw, b.w)};
         });
     }
-    __syncthreads();
+    lds_barrier();
     if (a.logits) {  // coalesced: the row may live in host memory
         float* lo = a.logits + (long long)s_ * V;
         for (int c = tid; c < V; c += S1_THREADS) lo[c] = logit[c];
@@ -2042,7 +2104,7 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
             tstats[3 * t + 2] = __int_as_float(bidx);
         }
     }
-    __syncthreads();
+    lds_barrier();
     // their combination (head_combine_kernel), 16 lanes of wave 0
     if (w == 0 && lane < 16) {
         const int l = lane;
@@ -2082,14 +2144,6 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
 constexpr int TS_NS = 16;
 constexpr int TS_THREADS = 512;
 constexpr int TS_NI = 2;  // float4 chunks of a state row per lane (state size up to 512)
-
-// Workgroup barrier over LDS only: the waves exchange data through LDS alone (the global stores of a
-// segment are read by later kernels), so outstanding global loads and stores need not drain.
-__device__ __forceinline__ void ts_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 // LDS of tile_step_kernel (offsets in floats, the limb operand's in bytes): cur and blockIn [16][Dp + 4];
 // one region reused by n and lambda [2][16][Dp + 4], h [16][Hp + 4] and the head's tile statistics
@@ -2212,95 +2266,6 @@ __device__ __forceinline__ float ts_norm_row(float* x, float* bin, bool resid, c
     return ts_row_limbs<TS_NI>(v, Dp, t, xl, lane);
 }
 
-// Matrix phases of tile_step_kernel. Wave w takes units w, w + 8, ... of the phase: with TS_FRAG one
-// 16-channel fragment (GF units per group), with TS_PAIR the fragment pair 2q (value), 2q + 1 (gate)
-// (GF/2 per group), with TS_TILE the GF consecutive fragments GF*u .. GF*u + GF - 1 (one per group).
-// A group's weights are requested KB K steps at a time (GF * KB loads in flight; loads past the wave's
-// units or past the last K step repeat a valid address and go unused), with the group's bias values
-// (`bias`, indexed by output row, or null), then multiplied by the tile's limb planes (all 16 token
-// columns). After a group's last K step `epi` gets, for each unit, the combined dot products of token
-// lane & 15, channels c0 .. c0 + 3 with c0 = 16 f + 4 (lane >> 4), and the bias of those rows:
-// epi(f, v[4], b) (TS_FRAG), epi(q, vv[4], vg[4], bv, bg) (TS_PAIR), or epi(u, acc, b[GF]) (TS_TILE).
-enum { TS_FRAG = 0, TS_PAIR = 1, TS_TILE = 2 };
-template <int MODE, int GF, int KB, class Epi>
-__device__ __forceinline__ void ts_matvec(const int8_t* W, const float* bias, int np16, int kc, int nunits,
-                                          const int8_t* xl, int lane, int w, Epi&& epi) {
-    constexpr int UPG = MODE == TS_FRAG ? GF : MODE == TS_PAIR ? GF / 2 : 1;  // units per group
-    const int mine = nunits > w ? (nunits - 1 - w) / 8 + 1 : 0;
-    const int8_t* wl = W + lane * 16;
-    const int8_t* xp = xl + lane * 16;
-    for (int gi = 0; gi * UPG < mine; gi++) {
-        int fr[GF];
-        bool ok[GF];
-#pragma unroll
-        for (int g = 0; g < GF; g++) {
-            const int u0 = UPG * gi + (MODE == TS_FRAG ? g : MODE == TS_PAIR ? g / 2 : 0);
-            ok[g] = u0 < mine;
-            const int un = w + 8 * min(u0, mine - 1);
-            fr[g] = MODE == TS_FRAG ? un : MODE == TS_PAIR ? 2 * un + (g & 1) : GF * un + g;
-        }
-        // the bias with the weights (after the MFMAs for whole tiles, whose accumulators fill the registers)
-        float4 b4[GF];
-        auto load_bias = [&] {
-#pragma unroll
-            for (int g = 0; g < GF; g++)
-                b4[g] = bias ? ldg((const float4*)(bias + 16 * fr[g] + 4 * (lane >> 4))) : float4{0.0f, 0.0f, 0.0f, 0.0f};
-        };
-        if constexpr (MODE != TS_TILE) load_bias();
-        v4i acc[GF][3];
-#pragma unroll
-        for (int g = 0; g < GF; g++) acc[g][0] = acc[g][1] = acc[g][2] = v4i{0, 0, 0, 0};
-        for (int k0 = 0; k0 < kc; k0 += KB) {
-            v4i wv[GF][KB];
-#pragma unroll
-            for (int g = 0; g < GF; g++)
-#pragma unroll
-                for (int j = 0; j < KB; j++)
-                    wv[g][j] = ldg((const v4i*)(wl + (((long long)min(k0 + j, kc - 1) * np16 + fr[g]) << 10)));
-            // keep the batch together: the scheduler would otherwise sink each load to its first MFMA
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int j = 0; j < KB; j++) {
-                if (k0 + j >= kc) break;
-                v4i xv[3];
-#pragma unroll
-                for (int l = 0; l < 3; l++) xv[l] = *(const v4i*)(xp + (k0 + j) * 3072 + l * 1024);
-#pragma unroll
-                for (int g = 0; g < GF; g++)
-                    if (ok[g])
-#pragma unroll
-                        for (int l = 0; l < 3; l++)
-                            acc[g][l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wv[g][j], xv[l], acc[g][l], 0, 0, 0);
-            }
-        }
-        if constexpr (MODE == TS_TILE) {
-            load_bias();
-            epi(w + 8 * gi, acc, b4);
-        } else if constexpr (MODE == TS_PAIR) {
-#pragma unroll
-            for (int p = 0; p < GF / 2; p++)
-                if (ok[2 * p]) {
-                    float vv[4], vg[4];
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        vv[r] = s1_dot(acc[2 * p], r);
-                        vg[r] = s1_dot(acc[2 * p + 1], r);
-                    }
-                    epi(fr[2 * p] >> 1, vv, vg, b4[2 * p], b4[2 * p + 1]);
-                }
-        } else {
-#pragma unroll
-            for (int g = 0; g < GF; g++)
-                if (ok[g]) {
-                    float v[4];
-#pragma unroll
-                    for (int r = 0; r < 4; r++) v[r] = s1_dot(acc[g], r);
-                    epi(fr[g], v, b4[g]);
-                }
-        }
-    }
-}
-
 __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
     extern __shared__ __align__(16) float ts_smem[];
     __shared__ float rsc[TS_NS];  // row scales of the current limb operand
@@ -2357,7 +2322,7 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
         const int8_t* src = a.att_xl + (long long)blockIdx.x * kcD * 3072;
         for (int c = tid; c < kcD * 192; c += TS_THREADS) *(v4i*)(xl + c * 16) = *(const v4i*)(src + c * 16);
         if (tid < TS_NS) rsc[tid] = tid < ns ? a.att_xs[s0 + tid] : 0.0f;
-        ts_barrier();
+        lds_barrier();
         const Step1Block& B = a.blocks[b];
         ts_matvec<TS_FRAG, 4, 2>(B.wo, nullptr, a.NpD / 16, kcD, a.NpD / 16, xl, lane, w, [&](int f, const float (&v)[4], float4) {
             const int c0 = 16 * f + 4 * (lane >> 4), t = lane & 15;
@@ -2368,7 +2333,7 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
         });
         b++;
     }
-    ts_barrier();
+    lds_barrier();
     int bs = 0;  // block steps before block b: the index of its latch state and norm ring
     for (int q = 0; q < b; q++) bs += a.blocks[q].steps;
     for (; b < a.nblocks; b++) {
@@ -2392,7 +2357,7 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
                 }
             }
             resid = false;
-            ts_barrier();
+            lds_barrier();
         }
         for (int st = 0; st < B.steps; st++, bs++) {
             int dil = B.init_dil;
@@ -2406,7 +2371,7 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
                                              xl, t, lane);
                 if (lane == 0) rsc[t] = sc;
             }
-            ts_barrier();
+            lds_barrier();
             // lambda = sigmoid_clamped(n.W_sel*s + base) (stream.go:195-205)
             ts_matvec<TS_FRAG, 4, 2>(B.wsel, a.latch_base, a.NpD / 16, kcD, a.NpD / 16, xl, lane, w,
                                      [&](int f, const float (&v)[4], float4 b) {
@@ -2417,7 +2382,7 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
                 for (int r = 0; r < 4; r++)
                     if (c0 + r < D) lam[t * ld + c0 + r] = sigmoid_epi(fmaf(v[r], sw, bb[r]));
             });
-            ts_barrier();
+            lds_barrier();
             // latch update, norm ring and the rule input [n | left | g] (latch_step_kernel): both rows'
             // memory reads are issued before either row is computed
             {
@@ -2502,7 +2467,7 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
                     if (lane == 0) rsc[t] = sx;
                 }
             }
-            ts_barrier();
+            lds_barrier();
             // h = GLU(x) (stream.go:214-220): fragment pairs (value 2q, gate 2q + 1)
             ts_matvec<TS_PAIR, 4, 2>(B.w1, B.b1, 2 * Hp / 16, 3 * kcD, Hp / 16, xl, lane, w,
                                      [&](int q, const float (&vv)[4], const float (&vg)[4], float4 bv, float4 bg) {
@@ -2518,7 +2483,7 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
                 }
                 *(float4*)(hb + t * hld + c0) = float4{h[0], h[1], h[2], h[3]};
             });
-            ts_barrier();
+            lds_barrier();
 #pragma unroll
             for (int i = 0; i < 2; i++) {
                 const int t = w + 8 * i;
@@ -2528,7 +2493,7 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
                 const float sc = ts_row_limbs<4>(v, Hp, t, xl, lane);
                 if (lane == 0) rsc[t] = sc;
             }
-            ts_barrier();
+            lds_barrier();
             // cur = highway(cur, W2 h) (stream.go:222-229)
             ts_matvec<TS_PAIR, 4, 2>(B.w2, B.b2, 2 * Dp / 16, Hp / 64, Dp / 16, xl, lane, w,
                                      [&](int q, const float (&vv)[4], const float (&vg)[4], float4 bv, float4 bg) {
@@ -2547,7 +2512,7 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
                     }
                 }
             });
-            ts_barrier();
+            lds_barrier();
         }
         if (B.attn) {
             // attendPosition's projection (internal/quant/attention.go:69-80): q, k, v of every session to
@@ -2569,7 +2534,7 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
                     }
                 }
             }
-            ts_barrier();
+            lds_barrier();
             ts_matvec<TS_FRAG, 4, 2>(B.qkv, nullptr, a.Np3 / 16, kcD, a.Np3 / 16, xl, lane, w,
                                      [&](int f, const float (&v)[4], float4) {
                 const int c0 = 16 * f + 4 * (lane >> 4), t = lane & 15;
@@ -2595,7 +2560,7 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
         const float sc = ts_norm_row(cur + t * ld, bin + t * ld, false, a.final_norm, D, Dp, nullptr, xl, t, lane);
         if (lane == 0) rsc[t] = sc;
     }
-    ts_barrier();
+    lds_barrier();
     // 128-channel tiles of the vocabulary, wave w taking tiles w, w + 8, ...: the logits epilogue's
     // statistics per token (max, sum exp(l - max), first argmax) with its lane structure
     const int ntiles = Vp / LX_BN;
@@ -2665,7 +2630,7 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
             d[2] = __int_as_float(bidx);
         }
     });
-    ts_barrier();
+    lds_barrier();
     // their combination (head_combine_kernel): 16 lanes per session, waves 0..3
     if (w < 4) {
         const int tk = 4 * w + (lane >> 4), l = lane & 15;
@@ -3135,7 +3100,7 @@ hipError_t launch_attention_wave(const AttnWaveArgs& a, hipStream_t s) {
 size_t step1_lds_bytes(const Step1Args& a, int dh) {
     const size_t floats = (size_t)8 * a.Dp + a.Hp + a.Vp + 4 * (a.Vp / LX_BN) +
                           (size_t)a.heads * ((rk_lds_floats(a.cap, dh) + 3) & ~3);
-    const size_t xl = (size_t)std::max(9 * a.Dp, 3 * a.Hp);
+    const size_t xl = (size_t)(std::max(3 * a.Dp, a.Hp) / 64) * 3072;  // limb operand, MFMA fragment layout
     return floats * sizeof(float) + xl;
 }
 
