@@ -1267,14 +1267,21 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
     // this lane's key row (key lo + lane; the current position's from qkv, not yet in the ring)
     float4 krow[C4];
     {
-        // (the current position's ring slot is read too, in bounds, and its value discarded)
         const int jj = min(lane, span - 1);
-        const float* kp = kr + (long long)slot(jj) * DH;
+        if constexpr (QL) {
+            // q, k, v in LDS: the ring row and the LDS row are separate loads (the current position's
+            // ring slot is read too, in bounds, and its value discarded)
+            const float* kp = kr + (long long)slot(jj) * DH;
 #pragma unroll
-        for (int c = 0; c < C4; c++) krow[c] = ldg((const float4*)(kp + 4 * c));
-        if (jj == span - 1) {
+            for (int c = 0; c < C4; c++) krow[c] = ldg((const float4*)(kp + 4 * c));
+            if (jj == span - 1) {
 #pragma unroll
-            for (int c = 0; c < C4; c++) krow[c] = qkv4(qkv + D + h * DH + 4 * c);
+                for (int c = 0; c < C4; c++) krow[c] = qkv4(qkv + D + h * DH + 4 * c);
+            }
+        } else {
+            const float* kp = jj == span - 1 ? qkv + D + h * DH : kr + (long long)slot(jj) * DH;
+#pragma unroll
+            for (int c = 0; c < C4; c++) krow[c] = ldg((const float4*)(kp + 4 * c));
         }
     }
     // values: rows jj = 0..span-1 into LDS, every load issued before the first store. Lanes past the
@@ -1288,8 +1295,13 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
         for (int u = 0; u < 8; u++) {
             const int e = min(e0 + u * 64 + lane, n4 - 1);
             const int jj = e / C4, c = e - jj * C4;
-            vb[u] = ldg((const float4*)(vr + (long long)slot(jj) * DH + 4 * c));
-            if (jj == span - 1) vb[u] = qkv4(qkv + 2 * D + h * DH + 4 * c);
+            if constexpr (QL) {
+                vb[u] = ldg((const float4*)(vr + (long long)slot(jj) * DH + 4 * c));
+                if (jj == span - 1) vb[u] = qkv4(qkv + 2 * D + h * DH + 4 * c);
+            } else {
+                const float* vp = jj == span - 1 ? qkv + 2 * D + h * DH : vr + (long long)slot(jj) * DH;
+                vb[u] = ldg((const float4*)(vp + 4 * c));
+            }
             off[u] = jj * DS + 4 * c;
         }
 #pragma unroll
