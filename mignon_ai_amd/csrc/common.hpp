@@ -217,10 +217,24 @@ __device__ __forceinline__ float dot_f32_ref(const X& x, const Y& y) {
     return s;
 }
 
+// Lane-exchange move within rows of 16 lanes (DPP: a VALU operand modifier, no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_value(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Maximum over the 64 lanes (all active), returned to every lane: within each row of 16 by DPP (swap
+// neighbours, swap pairs, half-row mirror, row mirror), then the four rows' values read out. The maximum
+// does not depend on the order of the comparisons.
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = fmaxf(v, dpp_move<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+    v = fmaxf(v, dpp_move<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+    v = fmaxf(v, dpp_move<0x141>(v));  // row_half_mirror
+    v = fmaxf(v, dpp_move<0x140>(v));  // row_mirror
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
 __device__ __forceinline__ float wave_sum(float v) {

@@ -1694,7 +1694,7 @@ __device__ __forceinline__ float s1_rms_inv(const float* x, int D, int lane) {
     }
     float v8[8];
 #pragma unroll
-    for (int q = 0; q < 8; q++) v8[q] = __shfl(part, q, 64) + __shfl(part, q + 8, 64);
+    for (int q = 0; q < 8; q++) v8[q] = lane_value(part, q) + lane_value(part, q + 8);
     float ss = hreduce8(v8);
     for (int e = (D >> 3) << 3; e < D; e++) {
         const float t = x[e];
