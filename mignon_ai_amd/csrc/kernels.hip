@@ -2481,7 +2481,7 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
             }
             lds_barrier();
             // h = GLU(x) (stream.go:214-220): fragment pairs (value 2q, gate 2q + 1)
-            ts_matvec<TS_PAIR, 4, 2>(B.w1, B.b1, 2 * Hp / 16, 3 * kcD, Hp / 16, xl, lane, w,
+            ts_matvec<TS_PAIR, 4, 3>(B.w1, B.b1, 2 * Hp / 16, 3 * kcD, Hp / 16, xl, lane, w,
                                      [&](int q, const float (&vv)[4], const float (&vg)[4], float4 bv, float4 bg) {
                 const int c0 = 16 * q + 4 * (lane >> 4), t = lane & 15;
                 const float sw = rsc[t] * B.s1;
@@ -2547,7 +2547,7 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
                 }
             }
             lds_barrier();
-            ts_matvec<TS_FRAG, 4, 2>(B.qkv, nullptr, a.Np3 / 16, kcD, a.Np3 / 16, xl, lane, w,
+            ts_matvec<TS_FRAG, 6, 2>(B.qkv, nullptr, a.Np3 / 16, kcD, a.Np3 / 16, xl, lane, w,
                                      [&](int f, const float (&v)[4], float4) {
                 const int c0 = 16 * f + 4 * (lane >> 4), t = lane & 15;
                 const float sw = rsc[t] * B.sqkv;
