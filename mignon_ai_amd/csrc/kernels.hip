@@ -2226,12 +2226,46 @@ __device__ __forceinline__ float4 ts_ld4(const float* p, int k, int valid) {
     return r;
 }
 
-// Row t: with `resid`, first blockIn += cur; cur = blockIn (stream.go:157-163); then n = RMSNorm(cur;
-// gamma) (cur itself without gamma), kept in `keep` when given, and its limb planes (K = Dp); returns
-// the row scale. One wave (s1_rms_inv, the row kernel's order).
-__device__ __forceinline__ float ts_norm_row(float* x, float* bin, bool resid, const float* gamma, int D, int Dp,
-                                             float* keep, int8_t* xl, int t, int lane) {
-    // gamma first: its memory latency runs under the residual and the sum of squares
+// s1_rms_inv of two rows by one wave, their chains interleaved (the same operations per row).
+__device__ __forceinline__ void ts_rms_inv2(const float* x0, const float* x1, int D, int lane, float (&inv)[2]) {
+    const int p = lane & 15;
+    float part0 = 0.0f, part1 = 0.0f;
+    const int c16 = D >> 4;
+#pragma unroll 8
+    for (int c = 0; c < c16; c++) {
+        const float v0 = x0[16 * c + p], v1 = x1[16 * c + p];
+        part0 = fmaf(v0, v0, part0);
+        part1 = fmaf(v1, v1, part1);
+    }
+    if (p < 8 && D - 16 * c16 >= 8) {
+        const float v0 = x0[16 * c16 + p], v1 = x1[16 * c16 + p];
+        part0 = fmaf(v0, v0, part0);
+        part1 = fmaf(v1, v1, part1);
+    }
+    float a8[8], b8[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        a8[q] = lane_value(part0, q) + lane_value(part0, q + 8);
+        b8[q] = lane_value(part1, q) + lane_value(part1, q + 8);
+    }
+    float ss0 = hreduce8(a8), ss1 = hreduce8(b8);
+    for (int e = (D >> 3) << 3; e < D; e++) {
+        const float t0 = x0[e], t1 = x1[e];
+        const float p0 = t0 * t0, p1 = t1 * t1;
+        ss0 = ss0 + p0;
+        ss1 = ss1 + p1;
+    }
+    inv[0] = 1.0f / (float)sqrt((double)(ss0 / (float)D + 1e-5f));
+    inv[1] = 1.0f / (float)sqrt((double)(ss1 / (float)D + 1e-5f));
+}
+
+// Rows w and w + 8 by wave w: with `resid`, first blockIn += cur; cur = blockIn (stream.go:157-163);
+// then n = RMSNorm(cur; gamma) (cur itself without gamma; s1_rms_inv, the row kernel's order), kept when
+// `keep` is given, and its limb planes (K = Dp). gamma is loaded once for both rows, and the two rows'
+// dependent chains are interleaved. keep: the
+// n rows' base (row stride ld) or null. sc: the two row scales.
+__device__ __forceinline__ void ts_norm_rows(float* cur, float* bin, int ld, bool resid, const float* gamma, int D,
+                                             int Dp, float* keep, int8_t* xl, int w, int lane, float (&sc)[2]) {
     float4 gm[TS_NI];
 #pragma unroll
     for (int i = 0; i < TS_NI; i++) {
@@ -2247,35 +2281,54 @@ __device__ __forceinline__ float ts_norm_row(float* x, float* bin, bool resid, c
             }
         }
     }
+    const int tr[2] = {w, w + 8};
     if (resid) {
 #pragma unroll
         for (int i = 0; i < TS_NI; i++) {
             const int k = 4 * lane + 256 * i;
             if (k < Dp) {
-                const float4 c = *(const float4*)(x + k), b = *(const float4*)(bin + k);
-                const float4 v = {b.x + c.x, b.y + c.y, b.z + c.z, b.w + c.w};
-                *(float4*)(x + k) = v;
-                *(float4*)(bin + k) = v;
+#pragma unroll
+                for (int r = 0; r < 2; r++) {
+                    float* x = cur + tr[r] * ld + k;
+                    float* b = bin + tr[r] * ld + k;
+                    const float4 c = *(const float4*)x, bb = *(const float4*)b;
+                    const float4 v = {bb.x + c.x, bb.y + c.y, bb.z + c.z, bb.w + c.w};
+                    *(float4*)x = v;
+                    *(float4*)b = v;
+                }
             }
         }
         wave_lds_sync();
     }
-    const float inv = gamma ? s1_rms_inv(x, D, lane) : 1.0f;
-    float4 v[TS_NI];
+    float inv[2] = {1.0f, 1.0f};
+    if (gamma) ts_rms_inv2(cur + tr[0] * ld, cur + tr[1] * ld, D, lane, inv);
+    float4 v[2][TS_NI];
+    float m[2] = {0.0f, 0.0f};
 #pragma unroll
-    for (int i = 0; i < TS_NI; i++) {
-        const int k = 4 * lane + 256 * i;
-        float4 u = ts_ld4(x, k, D);
-        if (gamma) {
-            u.x = (u.x * inv) * gm[i].x;
-            u.y = (u.y * inv) * gm[i].y;
-            u.z = (u.z * inv) * gm[i].z;
-            u.w = (u.w * inv) * gm[i].w;
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+        for (int i = 0; i < TS_NI; i++) {
+            const int k = 4 * lane + 256 * i;
+            float4 u = ts_ld4(cur + tr[r] * ld, k, D);
+            if (gamma) {
+                u.x = (u.x * inv[r]) * gm[i].x;
+                u.y = (u.y * inv[r]) * gm[i].y;
+                u.z = (u.z * inv[r]) * gm[i].z;
+                u.w = (u.w * inv[r]) * gm[i].w;
+            }
+            v[r][i] = u;
+            if (keep && k < Dp) *(float4*)(keep + tr[r] * ld + k) = u;
+            m[r] = ts_amax4(m[r], u);
         }
-        v[i] = u;
-        if (keep && k < Dp) *(float4*)(keep + k) = u;
-    }
-    return ts_row_limbs<TS_NI>(v, Dp, t, xl, lane);
+    const float a0 = wave_max(m[0]), a1 = wave_max(m[1]);
+    float ix[2];
+    limb_scale(a0, sc[0], ix[0]);
+    limb_scale(a1, sc[1], ix[1]);
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+        for (int i = 0; i < TS_NI; i++)
+            if (4 * lane + 256 * i < Dp) ts_put_limbs(xl, 4 * lane + 256 * i, tr[r], v[r][i], ix[r]);
 }
 
 __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
@@ -2376,12 +2429,13 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
             for (int q = 0; q < st && dil < 32; q++) dil *= B.dil_base;
             dil = min(dil, 32);
             // n = RMSNorm(cur; gamma) (stream.go:166-171) and its limbs
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const int t = w + 8 * i;
-                const float sc = ts_norm_row(cur + t * ld, bin + t * ld, resid && st == 0, B.gamma, D, Dp, nrm + t * ld,
-                                             xl, t, lane);
-                if (lane == 0) rsc[t] = sc;
+            {
+                float sc[2];
+                ts_norm_rows(cur, bin, ld, resid && st == 0, B.gamma, D, Dp, nrm, xl, w, lane, sc);
+                if (lane == 0) {
+                    rsc[w] = sc[0];
+                    rsc[w + 8] = sc[1];
+                }
             }
             lds_barrier();
             // lambda = sigmoid_clamped(n.W_sel*s + base) (stream.go:195-205)
@@ -2417,6 +2471,8 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
                         lq[i][ii] = ok && p >= dil ? ldg((const float4*)(lslot + k)) : float4{0.0f, 0.0f, 0.0f, 0.0f};
                     }
                 }
+                float4 nv2[2][TS_NI], lv2[2][TS_NI], gv2[2][TS_NI];
+                float m2[2] = {0.0f, 0.0f};
 #pragma unroll
                 for (int i = 0; i < 2; i++) {
                     const int t = w + 8 * i;
@@ -2426,8 +2482,8 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
                     float* gbase = a.g + ((long long)bs * a.S + s) * Dp;
                     float* ring = a.norm_ring + ((long long)bs * a.S + s) * a.ring * Dp;
                     float* wslot = ring + (long long)(p % a.ring) * Dp;
-                    float4 nv[TS_NI], lv[TS_NI], gv[TS_NI];
-                    float m = 0.0f;
+                    float4 (&nv)[TS_NI] = nv2[i], (&lv)[TS_NI] = lv2[i], (&gv)[TS_NI] = gv2[i];
+                    float& m = m2[i];
 #pragma unroll
                     for (int ii = 0; ii < TS_NI; ii++) {
                         const int k = 4 * lane + 256 * ii;
@@ -2465,18 +2521,25 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
                         gv[ii] = float4{ge[0], ge[1], ge[2], ge[3]};
                         m = ts_amax4(ts_amax4(ts_amax4(m, nv[ii]), lv[ii]), gv[ii]);
                     }
-                    float sx, ix;
-                    limb_scale(wave_max(m), sx, ix);
+                }
+                // both rows' maxima, then their digits
+                const float a0 = wave_max(m2[0]), a1 = wave_max(m2[1]);
+                float sx[2], ix[2];
+                limb_scale(a0, sx[0], ix[0]);
+                limb_scale(a1, sx[1], ix[1]);
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    const int t = w + 8 * i;
 #pragma unroll
                     for (int ii = 0; ii < TS_NI; ii++) {
                         const int k = 4 * lane + 256 * ii;
                         if (k < Dp) {
-                            ts_put_limbs(xl, k, t, nv[ii], ix);
-                            ts_put_limbs(xl, Dp + k, t, lv[ii], ix);
-                            ts_put_limbs(xl, 2 * Dp + k, t, gv[ii], ix);
+                            ts_put_limbs(xl, k, t, nv2[i][ii], ix[i]);
+                            ts_put_limbs(xl, Dp + k, t, lv2[i][ii], ix[i]);
+                            ts_put_limbs(xl, 2 * Dp + k, t, gv2[i][ii], ix[i]);
                         }
                     }
-                    if (lane == 0) rsc[t] = sx;
+                    if (lane == 0) rsc[t] = sx[i];
                 }
             }
             lds_barrier();
@@ -2529,11 +2592,17 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
         if (B.attn) {
             // attendPosition's projection (internal/quant/attention.go:69-80): q, k, v of every session to
             // memory for the attention kernel; cur and blockIn for the next segment
+            {
+                float sc[2];
+                ts_norm_rows(cur, bin, ld, resid && B.steps == 0, B.anorm, D, Dp, nullptr, xl, w, lane, sc);
+                if (lane == 0) {
+                    rsc[w] = sc[0];
+                    rsc[w + 8] = sc[1];
+                }
+            }
 #pragma unroll
             for (int i = 0; i < 2; i++) {
                 const int t = w + 8 * i;
-                const float sc = ts_norm_row(cur + t * ld, bin + t * ld, resid && B.steps == 0, B.anorm, D, Dp, nullptr, xl, t, lane);
-                if (lane == 0) rsc[t] = sc;
                 if (t < ns) {
                     const long long row = (long long)(s0 + t) * Dp;
 #pragma unroll
@@ -2566,11 +2635,13 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
         }
     }
     // headLogits (internal/quant/stream.go:232-248)
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int t = w + 8 * i;
-        const float sc = ts_norm_row(cur + t * ld, bin + t * ld, false, a.final_norm, D, Dp, nullptr, xl, t, lane);
-        if (lane == 0) rsc[t] = sc;
+    {
+        float sc[2];
+        ts_norm_rows(cur, bin, ld, false, a.final_norm, D, Dp, nullptr, xl, w, lane, sc);
+        if (lane == 0) {
+            rsc[w] = sc[0];
+            rsc[w + 8] = sc[1];
+        }
     }
     lds_barrier();
     // 128-channel tiles of the vocabulary, wave w taking tiles w, w + 8, ...: the logits epilogue's
