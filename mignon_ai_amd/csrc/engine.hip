@@ -241,7 +241,7 @@ struct mg_sessions {
         hipGraphExec_t exec = nullptr;
         long long ws_gen = -1;
         int opts = -1;
-        static constexpr int kKey = 11;
+        static constexpr int kKey = 12;
         const void* ptrs[kKey] = {};
         bool failed = false;  // capture is not possible here: launch one kernel at a time
         void reset() {
@@ -1374,6 +1374,7 @@ bool step1_args_fill(mg_sessions* s, const int32_t* ids_d, float* logits_d, cons
     a.kring = s->kring.as<float>(); a.vring = s->vring.as<float>();
     a.ids = ids_d; a.logits = logits_d; a.argmax = hc.argmax; a.prob = hc.prob; a.next_ids = hc.next_ids;
     a.out_ids = hc.out_ids; a.out_probs = hc.out_probs; a.out_ld = hc.out_ld; a.out_col = hc.out_col; a.col = hc.col;
+    a.done = hc.done;
     return true;
 }
 
@@ -1439,6 +1440,7 @@ void step_device(mg_sessions* s, const int32_t* ids_d, float* logits_d, HeadComb
             {
                 // the segment ended with block next's projection: its attention, output limbs to w.nl/w.ns
                 AttnStepArgs aa = step_attn_args(s, ab);
+                aa.done = hc.done;
                 ProfScope ps(m->prof, K_ATTN_STEP, st);
                 HIPCHECK(launch_attention_step_rows(aa, st));
             }
@@ -1516,7 +1518,7 @@ void step_graphed(mg_sessions* s, const int32_t* ids_d, float* logits_d, const H
     ensure_ws(m, s->n);  // before any capture: no allocation may happen inside one
     const void* ptrs[mg_sessions::StepGraph::kKey] = {ids_d, logits_d, hc.argmax, hc.prob, hc.next_ids, hc.out_ids, hc.out_probs,
                                 hc.col, (const void*)(intptr_t)hc.out_ld, (const void*)(intptr_t)hc.out_col,
-                                hc.lse};
+                                hc.lse, hc.done};
     const bool same = G.exec && G.ws_gen == ws_of(m).gen && G.opts == options_key() &&
                       std::equal(ptrs, ptrs + G.kKey, G.ptrs);
     if (!same) {
@@ -1704,6 +1706,7 @@ int mg_sessions_decode_greedy_until(mg_sessions* s, const int32_t* prompts, cons
         tr.scan(0);
         const bool first = tr.keep_going(0);  // false: cancelled before the first token
         hc.col = start_columns(s, st);
+        hc.done = tr.cnt;  // sessions past their stop token need no further steps
         for (int k = 1; first && k < max_tokens && tr.keep_going(k); k++) {
             step_graphed(s, s->next_ids.as<int32_t>(), nullptr, hc, st);
             tr.scan(k);
@@ -1772,6 +1775,7 @@ int mg_sessions_decode_sample(mg_sessions* s, const int32_t* prompts, const int3
         prefill_device(s, p_d, l_d, max_len, lg, hc, st);
         pick(0);
         const bool first = tr.keep_going(0);  // false: cancelled before the first token
+        if (n_stops > 0) hc.done = tr.cnt;  // sessions past their stop token need no further steps
         for (int k = 1; first && k < max_tokens && tr.keep_going(k); k++) {
             step_graphed(s, s->next_ids.as<int32_t>(), lg, hc, st);
             pick(k);

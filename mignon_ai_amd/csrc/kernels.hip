@@ -1361,6 +1361,7 @@ __global__ __launch_bounds__(1024) void attention_step_rows_kernel(AttnStepArgs 
     extern __shared__ __align__(16) float rows_smem[];
     __shared__ float inv_sh[16], red[16];
     const int s_ = blockIdx.x, h = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (a.done && a.done[s_] >= 0) return;  // a finished session of a batched decode (the whole workgroup)
     const float o = rk_head<DH>(a, s_, h, lane, rows_smem + h * rk_lds_floats(a.cap, DH), inv_sh[h]);
     const float mx = wave_max(lane < DH ? fabsf(o) : 0.0f);
     if (lane == 0) red[h] = mx;
@@ -1851,6 +1852,7 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
     float* rk = tstats + 4 * ntiles;
     const int rkf = (rk_lds_floats(a.cap, DH) + 3) & ~3;  // per head, 16-byte aligned
     int8_t* xl = (int8_t*)(rk + a.heads * rkf);
+    if (a.done && a.done[s_] >= 0) return;  // a finished session of a batched decode
     const int pos = a.pos[s_];
     {
         int id = a.ids[s_];
@@ -2336,6 +2338,11 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
     __shared__ float rsc[TS_NS];  // row scales of the current limb operand
     const int s0 = blockIdx.x * TS_NS, ns = min(TS_NS, a.S - s0);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    if (a.done) {
+        // a tile whose sessions have all finished (a batched decode's stop tokens) is skipped
+        const bool run = lane < ns && a.done[s0 + lane] < 0;
+        if (!__any(run)) return;
+    }
     const int D = a.D, Dp = a.Dp, H = a.H, Hp = a.Hp, V = a.V, Vp = a.Vp;
     const TsLds L = ts_lds(Dp, Hp, Vp);
     const int ld = L.ld, hld = L.hld;

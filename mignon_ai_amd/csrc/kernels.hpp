@@ -103,6 +103,7 @@ struct AttnStepArgs {
     float* att = nullptr;          // [S][Dp]
     int8_t* xl = nullptr;          // attention_step_rows: limbs of the output, fragment layout, K = Dp
     float* xs = nullptr;           // attention_step_rows: [S] row scales
+    const int32_t* done = nullptr; // attention_step_rows: [S] or null: sessions with done[i] >= 0 are skipped
 };
 hipError_t launch_attention_step(const AttnStepArgs& a, hipStream_t s);
 // Decode attention fused with the limb expansion of its output (one workgroup per session, one wave per
@@ -165,6 +166,7 @@ struct Step1Args {
     double* out_probs = nullptr;
     int out_ld = 0, out_col = 0;
     const int32_t* col = nullptr;
+    const int32_t* done = nullptr;       // [S] or null: sessions with done[i] >= 0 are skipped (finished)
 };
 // Whether the one-workgroup step takes this model (state size up to 512, hidden size up to 1024, at most
 // 8 attention heads of width 16, 32 or 64 over caches of at most 64 positions, vocabulary up to 16384).
@@ -208,6 +210,8 @@ struct HeadCombineArgs {
     int out_ld = 0, out_col = 0;
     const int32_t* col = nullptr;  // when set, the output column is *col instead of out_col (one captured
                                    // decode step serves every column)
+    const int32_t* done = nullptr; // [M] or null: sessions with done[i] >= 0 have finished (a batched decode's
+                                   // stop token); the one-workgroup steps may skip them
 };
 hipError_t launch_head_combine(const HeadCombineArgs& a, hipStream_t s);
 
