@@ -104,3 +104,30 @@ def test_tiled_greedy_decode(restore_step):
     assert np.array_equal(res["layered"][1].view(np.uint64), res["tiled"][1].view(np.uint64))
     rid, _ = oracle_model(data).greedy(prompts[:2], 40)
     assert np.array_equal(res["tiled"][0][:2], rid)
+
+
+def test_zero_step_block_all_step_kernels(restore_step):
+    """A block with no rule steps (its input is the previous block's state plus the residual, then its
+    attention): the layered, fused and tiled steps, bit for bit, against the oracle's session; the batched
+    forward against the oracle's Call."""
+    from helpers import tiny_spec, uniform_model_bytes
+    spec = tiny_spec([(2, 2, 1), (0, 2, 1), (1, 2, 2)], heads=2, context=64)
+    data = uniform_model_bytes(spec)
+    om = oracle_model(data)
+    toks = np.random.default_rng(23).integers(0, 16, 40).astype(np.int32)
+    res = {}
+    for mode in ("layered", "fused", "tiled"):
+        engine_option("step_kernel", mode)
+        gs = Model(data).new_session(12)
+        out = [gs.prefill(toks[:5])]
+        out += [gs.append(t) for t in toks[5:]]
+        res[mode] = out
+    os_ = om.new_session(12)
+    ref = [os_.prefill(toks[:5])] + [os_.append(t) for t in toks[5:]]
+    for i, r in enumerate(ref):
+        assert np.array_equal(res["layered"][i].view(np.uint32), res["fused"][i].view(np.uint32)), f"fused {i}"
+        assert np.array_equal(res["layered"][i].view(np.uint32), res["tiled"][i].view(np.uint32)), f"tiled {i}"
+        assert_close(res["tiled"][i], r, what=f"position {i}")
+    ids = toks[:24].reshape(2, 12)
+    got = Model(data).call(ids[0])
+    assert_close(got, om.call(ids[0]), what="call")
