@@ -58,7 +58,7 @@ LIMB_PLANES = 3
 # kernel classes whose int8 work runs on limb-expanded activations (the fused attention class counts its
 # projection GEMM; its fp32 attention flops are not in ops)
 LIMB_GEMMS = ("gemm_glu", "gemm_highway", "gemm_latch", "gemm_qkv", "gemm_out", "gemm_logits", "gemm_probs",
-              "qkv_attention")
+              "qkv_attention", "tile_step")
 SCORE_TOKENS, SCORE_CONTEXT = 65536, 128
 CHAT_REPEAT, CHAT_MAX_TOKENS = 24, 80   # max reply tokens: examples/order-search/orders.js:20
 SAMPLE_PARAMS = dict(temperature=0.7, top_k=40, top_p=0.9, rep_penalty=1.2)

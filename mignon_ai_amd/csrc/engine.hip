@@ -1398,6 +1398,41 @@ AttnStepArgs step_attn_args(mg_sessions* s, int ab) {
     return aa;
 }
 
+// Algorithmic work of one segment of the tiled step over S sessions (the profiler's figures): int8 MACs x 2
+// of its matrix products at the unpadded shapes; the bytes memory must move: its weights once, and per
+// session the state rows in and out (cur, blockIn), the latch state and norm ring per block step, the
+// attention output's limbs in, q/k/v out, and the logits when they are written.
+void tile_work(const mg_model* m, int S, int seg_block, bool seg_out, bool logits, double& bytes, double& ops) {
+    const double D = m->D, H = m->H, V = m->V, Dp = m->Dp;
+    double macs = 0, wbytes = 0, per = 0;
+    int b = seg_block;
+    if (seg_out) {
+        macs += D * D; wbytes += (double)m->Dp * m->NpD;
+        per += 8.0 * Dp + 3.0 * Dp + 4;  // cur and blockIn in, attention limbs and scale in
+        b++;
+    }
+    bool ended = false;
+    for (; b < (int)m->blocks.size() && !ended; b++) {
+        const DevBlock& B = m->blocks[b];
+        for (int st = 0; st < B.steps; st++) {
+            macs += D * D + 3.0 * D * 2.0 * H + H * 2.0 * D;
+            wbytes += (double)m->Dp * m->NpD + 3.0 * m->Dp * 2.0 * m->Hp + (double)m->Hp * 2.0 * m->Dp;
+            per += 8.0 * D + 8.0 * D;  // g read and written, norm ring slot written and the left row read
+        }
+        if (B.attn) {
+            macs += 3.0 * D * D; wbytes += (double)m->Dp * m->Np3;
+            per += 12.0 * D + 8.0 * Dp;  // q, k, v and the state rows out
+            ended = true;
+        }
+    }
+    if (!ended) {
+        macs += D * V; wbytes += (double)m->Dp * m->Vp;
+        per += 24.0 + (logits ? 4.0 * V : 0.0);
+    }
+    ops = 2.0 * S * macs;
+    bytes = wbytes + S * per;
+}
+
 // The tiled step (16 sessions per workgroup), when the option and the shapes allow it: automatic for
 // sets larger than the fused step takes.
 bool tile_args(mg_sessions* s, const int32_t* ids_d, float* logits_d, const HeadCombineArgs& hc, TileStepArgs& a) {
@@ -1431,7 +1466,9 @@ void step_device(mg_sessions* s, const int32_t* ids_d, float* logits_d, HeadComb
         int ab = 0;
         for (;;) {
             {
-                ProfScope ps(m->prof, K_TILE_STEP, st);
+                double bytes = 0, ops = 0;
+                if (m->prof.on) tile_work(m, S, ta.seg_block, ta.seg_out != 0, logits_d != nullptr, bytes, ops);
+                ProfScope ps(m->prof, K_TILE_STEP, st, bytes, ops);
                 HIPCHECK(launch_tile_step(ta, st));
             }
             int next = ta.seg_out ? ta.seg_block + 1 : ta.seg_block;
