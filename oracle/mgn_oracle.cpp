@@ -368,16 +368,19 @@ struct SeqState {
     }
 };
 
+// The latch update of one channel (internal/quant/stream.go:202): lambda*g + (1 - lambda)*n, each
+// product rounded separately.
+inline float latch_combine(float lam, float g, float n) {
+    float a = lam * g;
+    float b = (1.0f - lam) * n;
+    return a + b;
+}
+
 // quant.Model.updateLatch (internal/quant/stream.go:195-205)
 float* update_latch(const OrModel& q, SeqState& st, float* gl, const Block& blk, const float* normCell) {
     int D = q.D;
     matvec_i8(st.latch_logit.data(), D, blk.wsel.data(), D, blk.ssel, normCell, D, q.latch_base.data());
-    for (int d = 0; d < D; d++) {
-        float lam = sigmoid_clamped(st.latch_logit[d]);
-        float a = lam * gl[d];
-        float b = (1.0f - lam) * normCell[d];
-        gl[d] = a + b;
-    }
+    for (int d = 0; d < D; d++) gl[d] = latch_combine(sigmoid_clamped(st.latch_logit[d]), gl[d], normCell[d]);
     return gl;
 }
 
@@ -409,9 +412,32 @@ inline int window_start(int i, int window) {
     return 0;
 }
 
+// The attention of one position over keys and values lo..pos (internal/quant/attention.go:82-101): per
+// head, scores q.k * (1/sqrt(dh)) in DotF32 order, SoftmaxInPlaceF32, then out += p_j * v_j with
+// AddScaledF32. Key and value row j sit at keys/values + (j % ring) * stride; out is [D] and zeroed first.
+void attend_heads(const float* query_row, const float* keys, const float* values, size_t stride, int ring, int lo,
+                  int pos, int D, int heads, float* scores, float* scratch, float* out) {
+    int dh = D / heads, span = pos - lo + 1;
+    float scale = (float)(1.0 / std::sqrt((double)dh));
+    std::fill(out, out + D, 0.0f);
+    for (int h = 0; h < heads; h++) {
+        const float* query = query_row + h * dh;
+        for (int j = lo; j <= pos; j++) {
+            size_t k = (size_t)(j % ring) * stride;
+            scores[j - lo] = dot_f32(query, keys + k + h * dh, dh) * scale;
+        }
+        softmax_inplace(scores, scratch, span);
+        float* o = out + h * dh;
+        for (int j = lo; j <= pos; j++) {
+            size_t v = (size_t)(j % ring) * stride;
+            add_scaled(o, values + v + h * dh, scores[j - lo], dh);
+        }
+    }
+}
+
 // quant.Model.attendPosition (internal/quant/attention.go:69-104)
 void attend_position(const OrModel& q, SeqState& st, int b, const Block& blk, int pos) {
-    int D = q.D, heads = q.heads, dh = D / heads;
+    int D = q.D, heads = q.heads;
     rmsnorm(st.cur.data(), blk.attn_norm.data(), st.a_norm.data(), D);
     matvec_i8(st.a_qkv.data(), 3 * D, blk.qkv.data(), D, blk.sqkv, st.a_norm.data(), D, nullptr);
     float* keys = st.attnK[b].data();
@@ -421,23 +447,8 @@ void attend_position(const OrModel& q, SeqState& st, int b, const Block& blk, in
     std::memcpy(keys + (size_t)slot * D, st.a_qkv.data() + D, D * sizeof(float));
     std::memcpy(values + (size_t)slot * D, st.a_qkv.data() + 2 * D, D * sizeof(float));
     int lo = std::max(window_start(pos, q.window), pos - ring + 1);
-    int span = pos - lo + 1;
-    float* scores = st.attn_scores.data();
-    float scale = (float)(1.0 / std::sqrt((double)dh));
-    std::fill(st.a_att.begin(), st.a_att.end(), 0.0f);
-    for (int h = 0; h < heads; h++) {
-        const float* query = st.a_qkv.data() + h * dh;
-        for (int j = lo; j <= pos; j++) {
-            size_t k = (size_t)(j % ring) * D;
-            scores[j - lo] = dot_f32(query, keys + k + h * dh, dh) * scale;
-        }
-        softmax_inplace(scores, st.attn_scratch.data(), span);
-        float* out = st.a_att.data() + h * dh;
-        for (int j = lo; j <= pos; j++) {
-            size_t v = (size_t)(j % ring) * D;
-            add_scaled(out, values + v + h * dh, scores[j - lo], dh);
-        }
-    }
+    attend_heads(st.a_qkv.data(), keys, values, D, ring, lo, pos, D, heads, st.attn_scores.data(),
+                 st.attn_scratch.data(), st.a_att.data());
     matvec_i8(st.a_proj.data(), D, blk.wo.data(), D, blk.so, st.a_att.data(), D, nullptr);
     for (int d = 0; d < D; d++) st.cur[d] += st.a_proj[d];
 }
@@ -698,6 +709,39 @@ void or_matvec_i8(float* y, int rows, const int8_t* w, int stride, float scale, 
                   const float* bias) {
     matvec_i8(y, rows, w, stride, scale, x, cols, bias);
 }
+// Stage-level pins for the engine's batched kernels. The latch recurrence of updateLatch
+// (internal/quant/stream.go:195-205) over B sequences of T positions given lambda (the sigmoid of the
+// latch logits) and the normalised cells, the latch starting from zero (quantSeqState.reset,
+// stream.go:115-121): g[b][t] = lambda*g[b][t-1] + (1 - lambda)*n. Rows of D values, stride ld.
+void or_latch_seq(const float* lam, const float* nf, int B, int T, int D, int ld, float* g) {
+    for (int b = 0; b < B; b++) {
+        std::vector<float> gl(D, 0.0f);
+        for (int t = 0; t < T; t++) {
+            size_t r = ((size_t)b * T + t) * ld;
+            for (int d = 0; d < D; d++) {
+                gl[d] = latch_combine(lam[r + d], gl[d], nf[r + d]);
+                g[r + d] = gl[d];
+            }
+        }
+    }
+}
+
+// attendPosition's attention (internal/quant/attention.go:82-101, without the norm and projections)
+// for every position of B sequences of T positions whose q, k, v rows are given ([B*T][3D]: q | k | v):
+// position t attends to lo..t with lo = max(WindowStart(t, window), t - cap + 1), as a session whose
+// ring holds cap positions. att: [B*T][ld].
+void or_attend_seq(const float* qkv, int B, int T, int D, int heads, int window, int cap, float* att, int ld) {
+    std::vector<float> scores(T), scratch(T);
+    for (int b = 0; b < B; b++) {
+        const float* rows = qkv + (size_t)b * T * 3 * D;
+        for (int t = 0; t < T; t++) {
+            int lo = std::max(window_start(t, window), t - cap + 1);
+            attend_heads(rows + (size_t)t * 3 * D, rows + D, rows + 2 * D, (size_t)3 * D, T, lo, t, D, heads,
+                         scores.data(), scratch.data(), att + ((size_t)b * T + t) * ld);
+        }
+    }
+}
+
 void or_latch_base(int D, float* out) {
     auto b = latch_base_logits(D);
     std::memcpy(out, b.data(), D * sizeof(float));

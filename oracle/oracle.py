@@ -77,6 +77,9 @@ def lib():
             "or_matvec_i8": (None, [_f32p, ctypes.c_int, _i8p, ctypes.c_int, ctypes.c_float, _f32p, ctypes.c_int,
                                     _f32p]),
             "or_latch_base": (None, [ctypes.c_int, _f32p]),
+            "or_latch_seq": (None, [_f32p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p]),
+            "or_attend_seq": (None, [_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_int, _f32p, ctypes.c_int]),
             "or_quantize": (None, [_f32p, ctypes.c_longlong, _i8p, _f32p]),
             "or_gemm_i8_ref": (ctypes.c_int, [_i8p, ctypes.c_int, ctypes.c_int, _i8p, ctypes.c_int, _f32p, _f32p,
                                               ctypes.c_int]),
@@ -164,6 +167,27 @@ def latch_base(D: int) -> np.ndarray:
     out = np.empty(D, np.float32)
     lib().or_latch_base(D, _p(out, _f32p))
     return out
+
+
+def latch_seq(lam, nf):
+    """updateLatch's recurrence (internal/quant/stream.go:195-205) over [B][T][D] lambda and normalised
+    cells, the latch starting from zero: the latch after every position, [B][T][D]."""
+    lam, nf = _c(lam, np.float32), _c(nf, np.float32)
+    B, T, D = lam.shape
+    g = np.empty_like(lam)
+    lib().or_latch_seq(_p(lam, _f32p), _p(nf, _f32p), B, T, D, D, _p(g, _f32p))
+    return g
+
+
+def attend_seq(qkv, heads, window, cap):
+    """attendPosition's attention (internal/quant/attention.go:82-101) for every position of [B][T][3D]
+    q | k | v rows, over a ring of cap positions: [B][T][D]."""
+    qkv = _c(qkv, np.float32)
+    B, T, D3 = qkv.shape
+    D = D3 // 3
+    att = np.empty((B, T, D), np.float32)
+    lib().or_attend_seq(_p(qkv, _f32p), B, T, D, heads, window, cap, _p(att, _f32p), D)
+    return att
 
 
 def quantize(w):

@@ -74,3 +74,13 @@ def test_engine_option_validates():
         assert prev in (0, 1, 2)
         assert L.mg_engine_option(opt, -1) == val
         assert L.mg_engine_option(opt, prev) == val
+
+
+def test_stage_hooks_load_against_the_engine():
+    """The stage-level parity tests' hooks (test infrastructure, not part of the ABI) load against the
+    engine library and export their entry points."""
+    import stage_hooks
+
+    L = stage_hooks.lib()
+    for name in ("mgt_row", "mgt_latch_scan", "mgt_attention", "mgt_attention_step"):
+        assert hasattr(L, name)

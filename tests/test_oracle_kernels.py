@@ -207,3 +207,90 @@ def test_avx2_dot_paths_match_scalar_restatement():
             assert bits(a) == bits(O.dot_f32(x, y)) and bits(b) == bits(O.dot_i8_f32(x, w)), n
     finally:
         O.force_scalar(False)
+
+
+# ---- the latch recurrence and attention over whole sequences (the stage-level pins' oracle) --------
+
+def test_latch_seq_closed_forms():
+    rng = np.random.default_rng(21)
+    B, T, D = 2, 19, 13
+    nf = rng.standard_normal((B, T, D)).astype(np.float32)
+    # lambda = 0: the latch is the normalised cell itself; lambda = 1: it stays at its zero start
+    assert np.array_equal(bits(O.latch_seq(np.zeros((B, T, D), np.float32), nf)), bits(nf))
+    assert not O.latch_seq(np.ones((B, T, D), np.float32), nf).any()
+    # constant lambda and cell: g_t = n (1 - lambda^(t+1))
+    lam = np.full((1, T, 1), 0.75, np.float32)
+    g = O.latch_seq(lam, np.full((1, T, 1), 2.0, np.float32))[0, :, 0]
+    assert np.allclose(g, 2.0 * (1 - 0.75 ** np.arange(1, T + 1)), rtol=1e-6)
+    # random inputs against the float64 recurrence
+    lam = rng.uniform(0, 1, (B, T, D)).astype(np.float32)
+    g = O.latch_seq(lam, nf)
+    ref = np.zeros((B, D))
+    for t in range(T):
+        ref = lam[:, t] * ref + (1 - lam[:, t].astype(np.float64)) * nf[:, t]
+        assert np.allclose(g[:, t], ref, rtol=1e-5, atol=1e-6)
+
+
+def test_latch_seq_rounds_each_product():
+    # updateLatch rounds lam*g and (1-lam)*n separately (stream.go:202; Go fuses nothing on amd64): on
+    # these inputs a fused multiply-add gives a different float32
+    rng = np.random.default_rng(5)
+    hits = 0
+    for _ in range(200):
+        lam = rng.uniform(0, 1, (1, 2, 1)).astype(np.float32)
+        n = rng.standard_normal((1, 2, 1)).astype(np.float32)
+        g0 = F(F(F(1) - lam[0, 0, 0]) * n[0, 0, 0])
+        b = F(F(F(1) - lam[0, 1, 0]) * n[0, 1, 0])
+        sep = F(F(lam[0, 1, 0] * g0) + b)
+        fused = F(float(lam[0, 1, 0]) * float(g0) + float(b))
+        got = O.latch_seq(lam, n)[0, 1, 0]
+        assert bits(got) == bits(sep)
+        hits += bits(sep) != bits(fused)
+    assert hits > 0
+
+
+def _attn_f64(qkv, heads, window, cap):
+    B, T, D3 = qkv.shape
+    D = D3 // 3
+    dh = D // heads
+    out = np.zeros((B, T, D))
+    for b in range(B):
+        for t in range(T):
+            lo = max(t - window + 1 if window > 0 else 0, t - cap + 1, 0)
+            for h in range(heads):
+                sl = slice(h * dh, (h + 1) * dh)
+                q = qkv[b, t, sl].astype(np.float64)
+                k = qkv[b, lo:t + 1, D:2 * D][:, sl].astype(np.float64)
+                v = qkv[b, lo:t + 1, 2 * D:][:, sl].astype(np.float64)
+                s = k @ q / np.sqrt(dh)
+                p = np.exp(s - s.max())
+                out[b, t, sl] = (p / p.sum()) @ v
+    return out
+
+
+@pytest.mark.parametrize("D,heads,T,window,cap", [(16, 2, 12, 0, 128), (24, 3, 20, 4, 128), (12, 1, 30, 0, 8),
+                                                 (56, 1, 9, 0, 128), (72, 4, 15, 6, 10)])
+def test_attend_seq_against_float64(D, heads, T, window, cap):
+    rng = np.random.default_rng(D + T)
+    qkv = rng.standard_normal((2, T, 3 * D)).astype(np.float32)
+    got = O.attend_seq(qkv, heads, window, cap)
+    assert np.allclose(got, _attn_f64(qkv, heads, window, cap), rtol=2e-5, atol=2e-6)
+
+
+def test_attend_seq_special_cases():
+    rng = np.random.default_rng(8)
+    D, T = 24, 11
+    qkv = rng.standard_normal((1, T, 3 * D)).astype(np.float32)
+    v = qkv[:, :, 2 * D:]
+    # one attended position (position 0, window 1, a ring of 1): the output is that value, bit for bit
+    assert np.array_equal(bits(O.attend_seq(qkv, 2, 0, 128)[:, 0]), bits(v[:, 0]))
+    for window, cap in ((1, 128), (0, 1)):
+        assert np.array_equal(bits(O.attend_seq(qkv, 3, window, cap)), bits(v))
+    # equal keys: uniform weights, the output is the mean of the attended values
+    same = qkv.copy()
+    same[:, :, D:2 * D] = same[:, :1, D:2 * D]
+    got = O.attend_seq(same, 2, 0, 128)
+    mean = np.cumsum(v.astype(np.float64), axis=1) / np.arange(1, T + 1)[None, :, None]
+    assert np.allclose(got, mean, rtol=1e-5, atol=1e-6)
+    # a window of w equals a ring of w positions
+    assert np.array_equal(bits(O.attend_seq(qkv, 2, 4, 128)), bits(O.attend_seq(qkv, 2, 0, 4)))
