@@ -184,8 +184,8 @@ struct ProfScope {
 struct Workspace {
     int cap_tokens = 0;
     long long gen = 0;  // bumped whenever the buffers below are reallocated (captured graphs hold their addresses)
-    DevBuf cur, bin, nf, lam, nl, ns, xl, xs, h, hl, hs, qkv, att, stats, lse, tlog, logprob, argmax, prob, ids, tgt,
-        rowmap, lens, tmp;
+    DevBuf cur, bin, nf, rinv, lam, nl, ns, xl, xs, h, hl, hs, qkv, att, stats, lse, tlog, logprob, argmax, prob, ids,
+        tgt, rowmap, lens, tmp;
 };
 
 }  // namespace
@@ -435,6 +435,7 @@ void ws_sizes(const mg_model* m, Workspace& w, int tokens, F&& f) {
     f(w.cur, M * Dp * 4);
     f(w.bin, M * Dp * 4);
     f(w.nf, M * Dp * 4);
+    f(w.rinv, M * 4);
     f(w.lam, M * Dp * 4);
     f(w.nl, Mp * 3 * Dp);
     f(w.ns, Mp * 4);
@@ -551,19 +552,20 @@ double row_bytes(const RowArgs& r) {
         default: b = M * 4 * D + (r.row_map ? 4 * M : 0); break;
     }
     if (r.nout) b += M * 4 * D;
+    if (r.rinv) b += M * 4;
     if (r.limbs) b += M * (3.0 * r.Dp + 4);
     return b;
 }
 
 // Row kernel helper: mode + optional norm, writes n (fp32) and the limb-expanded copy into ws.nl/ns.
 void row_call(mg_model* m, int M, int mode, const int32_t* ids, const float* src, int lds, const int32_t* row_map,
-              const float* gamma, float* nout, bool limbs, hipStream_t s) {
+              const float* gamma, float* nout, bool limbs, hipStream_t s, float* rinv = nullptr) {
     Workspace& w = ws_of(m);
     RowArgs r;
     r.M = M; r.D = m->D; r.Dp = m->Dp; r.mode = mode;
     r.ids = ids; r.emb = m->emb; r.emb_scale = m->emb_scale; r.V = m->V;
     r.cur = w.cur.as<float>(); r.block_in = w.bin.as<float>();
-    r.src = src; r.lds = lds; r.row_map = row_map; r.gamma = gamma; r.nout = nout;
+    r.src = src; r.lds = lds; r.row_map = row_map; r.gamma = gamma; r.nout = nout; r.rinv = rinv;
     if (limbs) {
         r.limbs = w.nl.as<int8_t>(); r.lscale = w.ns.as<float>();
     }
@@ -668,12 +670,25 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
         if (blk.steps == 0) row_call(m, M, mode, c.ids, nullptr, 0, nullptr, nullptr, nullptr, false, s);
         for (int st = 0; st < blk.steps; st++, bs++) {
             const int dil = blk.dilation(st);
+            // The rule input's latch scan: fused with the rule-input packing when it fits and there are
+            // enough sequences (one workgroup each; at least 1024 waves: c3's 1024 sequences run faster
+            // fused, c1's 64 separate) to cover the latency of its sequential rounds. Without a session
+            // export (and with a norm) it recomputes n from the norm's source rows and 1/rms, so n is
+            // never stored.
+            const int sk = option(OPT_SCAN_KERNEL);
+            const bool many = (long long)c.B * ((Dp / 2 + 63) / 64) >= 1024;
+            const bool fused_scan = !c.step && scan_rule_fits(c.T, Dp, dil) && (sk == 2 || (sk == 0 && many));
+            const bool keep_n = c.step || c.sess || !fused_scan || !blk.gamma;
+            float* nout = keep_n ? w.nf.as<float>() : nullptr;
+            float* rinv = keep_n ? nullptr : w.rinv.as<float>();
+            // the rows the norm reads: blockIn when the previous block added its state there, else cur
+            // (the embedding and the residual write both)
+            const float* nsrc = (st == 0 && in_bin) ? w.bin.as<float>() : w.cur.as<float>();
             // n = RMSNorm(cur; gamma) (stream.go:166-171), fused with the embedding / residual at step 0
             if (st == 0 && in_bin)
-                row_call(m, M, ROW_SRC, nullptr, w.bin.as<float>(), Dp, nullptr, blk.gamma, w.nf.as<float>(), true, s);
+                row_call(m, M, ROW_SRC, nullptr, w.bin.as<float>(), Dp, nullptr, blk.gamma, nout, true, s, rinv);
             else
-                row_call(m, M, st == 0 ? mode : ROW_SRC, c.ids, nullptr, 0, nullptr, blk.gamma, w.nf.as<float>(), true,
-                         s);
+                row_call(m, M, st == 0 ? mode : ROW_SRC, c.ids, nullptr, 0, nullptr, blk.gamma, nout, true, s, rinv);
             // lambda = sigmoid_clamped(n.W_sel*s + base) (stream.go:195-205)
             GemmArgs g = lx_args(w.nl.as<int8_t>(), w.ns.as<float>(), blk.wsel, m->NpD, Dp, M, D, blk.ssel);
             g.bias = m->latch_base; g.out = w.lam.as<float>(); g.ldo = Dp;
@@ -702,13 +717,11 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                                                 c.sess->norm_ring.as<float>() + (size_t)bs * c.B * m->ring * Dp, s));
                 }
                 // rule input [n | left | g] (stream.go:180-184), limb-expanded with one scale per row
-                // The fused kernel runs one workgroup per sequence: automatic selection wants enough of
-                // them (at least 1024 waves: c3's 1024 sequences run faster fused, c1's 64 separate) to cover
-                // the latency of its sequential rounds.
-                const int sk = option(OPT_SCAN_KERNEL);
-                const bool many = (long long)c.B * ((Dp / 2 + 63) / 64) >= 1024;
-                if (scan_rule_fits(c.T, Dp, dil) && (sk == 2 || (sk == 0 && many))) {
+                if (fused_scan) {
                     sa.dil = dil; sa.xl = w.xl.as<int8_t>(); sa.xs = w.xs.as<float>();
+                    if (!keep_n) {
+                        sa.nf = nullptr; sa.xn = nsrc; sa.rinv = rinv; sa.gamma = blk.gamma;
+                    }
                     // lambda and n in (the left neighbour is a re-read), the rule input's limbs out
                     ProfScope ps(m->prof, K_SCAN, s, (double)M * (8.0 * D + 9.0 * Dp + 4));
                     HIPCHECK(launch_scan_rule(sa, s));

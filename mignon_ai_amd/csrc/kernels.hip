@@ -229,6 +229,7 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
 #pragma unroll
             for (int j = 0; j < RB; j++) {
                 const float inv_j = __shfl(inv, 16 * j, 64);
+                if (a.rinv && lane == 0 && rows[j] < a.M) a.rinv[rows[j]] = inv_j;
 #pragma unroll
                 for (int i = 0; i < NS4; i++) {
                     const int c = lane + 64 * i;
@@ -390,7 +391,11 @@ __device__ __forceinline__ float wave_max16(float (&v)[16], int lane) {
 //     whole 1 KiB fragments; the left neighbours n[t - dil] are loaded again (from cache) only then.
 // The output is byte-identical to scan_kernel followed by row_kernel in ROW_RULE mode, without writing
 // g and reading it back. g is stored only as a session's exported state.
+// RN: n is not read from a normalised copy but recomputed from the norm's source rows and the row
+// kernel's 1/rms per row, with the row kernel's operations, (x * rinv) * gamma: the same bits, and the
+// normalised rows never have to be written.
 // ------------------------------------------------------------------------------------------------
+template <bool RN>
 __global__ __launch_bounds__(512) void scan_rule_kernel(ScanArgs a) {
     extern __shared__ __align__(16) int8_t sr_smem[];
     const int b = blockIdx.x, j = threadIdx.x, lane = j & 63, w = j >> 6, nw = blockDim.x >> 6;
@@ -412,18 +417,28 @@ __global__ __launch_bounds__(512) void scan_rule_kernel(ScanArgs a) {
     const int o0 = (cc >> 4) * 3072 + 256 * ((cc >> 2) & 3) + 4 * (cc & 3) + 2 * (j & 1);
     const int p = 8 * ((lane >> 5) & 1) + 4 * ((lane >> 4) & 1) + 2 * ((lane >> 3) & 1) + ((lane >> 2) & 1);
     float g0 = 0.0f, g1 = 0.0f;
-    // n and lambda of the round, loaded while the previous round is packed and stored
+    const float* nsrc = RN ? a.xn : a.nf;
+    const float2 gm = RN ? *(const float2*)(a.gamma + 2 * jc) : make_float2(1.0f, 1.0f);
+    // n of a row from its loaded value (RN: the source value and the row's 1/rms)
+    auto nrm = [&](float2 v, float r) { return RN ? make_float2((v.x * r) * gm.x, (v.y * r) * gm.y) : v; };
+    // 1/rms of the round's row k: lane k of a vector load (each lane loads row lane & 15), read out with
+    // readlane (scalar loads would share the LDS traffic's completion counter)
+    auto lane_k = [](float v, int k) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), k)); };
+    // n (RN: its source and 1/rms) and lambda of the round, loaded while the previous round is packed
+    // and stored
     float2 nv[16], gv[16];
+    float rn = RN ? a.rinv[seq0 + (lane & 15)] : 1.0f;
 #pragma unroll
     for (int k = 0; k < 16; k++) {
-        nv[k] = *(const float2*)(a.nf + (seq0 + k) * Dp + 2 * jc);
+        nv[k] = *(const float2*)(nsrc + (seq0 + k) * Dp + 2 * jc);
         gv[k] = *(const float2*)(a.lam + (seq0 + k) * Dp + 2 * jc);
     }
     for (int t0 = 0; t0 < T; t0 += 16) {
         float mn[16], mg[16];
 #pragma unroll
         for (int k = 0; k < 16; k++) {
-            const float n0 = c0 ? nv[k].x : 0.0f, n1 = c1 ? nv[k].y : 0.0f;
+            const float2 nk = nrm(nv[k], lane_k(rn, k));
+            const float n0 = c0 ? nk.x : 0.0f, n1 = c1 ? nk.y : 0.0f;
             if (c0) {
                 const float p1 = gv[k].x * g0;
                 const float p2 = (1.0f - gv[k].x) * n0;
@@ -468,19 +483,22 @@ __global__ __launch_bounds__(512) void scan_rule_kernel(ScanArgs a) {
         __syncthreads();
         // the left neighbours (recently loaded rows: from cache), staged second
         float2 lv[16];
+        const float rl = RN ? a.rinv[seq0 + max(t0 + (lane & 15) - dil, 0)] : 1.0f;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             const int t = t0 + k;
-            const float2 v = *(const float2*)(a.nf + (seq0 + max(t - dil, 0)) * Dp + 2 * jc);
+            const long long ml = seq0 + max(t - dil, 0);
+            const float2 v = nrm(*(const float2*)(nsrc + ml * Dp + 2 * jc), lane_k(rl, k));
             const bool hl = t >= dil;
             lv[k] = make_float2((hl && c0) ? v.x : 0.0f, (hl && c1) ? v.y : 0.0f);
         }
         // the next round's n and lambda (this round's again after the last: in bounds, unused)
         const int tn = t0 + 16 < T ? t0 + 16 : t0;
         float2 nvn[16], gvn[16];
+        const float rnn = RN ? a.rinv[seq0 + tn + (lane & 15)] : 1.0f;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
-            nvn[k] = *(const float2*)(a.nf + (seq0 + tn + k) * Dp + 2 * jc);
+            nvn[k] = *(const float2*)(nsrc + (seq0 + tn + k) * Dp + 2 * jc);
             gvn[k] = *(const float2*)(a.lam + (seq0 + tn + k) * Dp + 2 * jc);
         }
         float inv[16];
@@ -514,6 +532,7 @@ __global__ __launch_bounds__(512) void scan_rule_kernel(ScanArgs a) {
             nv[k] = nvn[k];
             gv[k] = gvn[k];
         }
+        rn = rnn;
     }
 }
 
@@ -3052,7 +3071,10 @@ hipError_t launch_scan_rule(const ScanArgs& a, hipStream_t s) {
     if (a.B == 0 || a.T == 0) return hipSuccess;
     const int threads = ((a.Dp / 2 + 63) / 64) * 64;
     const size_t lds = (size_t)(a.Dp / 64) * 3 * 1088 + (2 * (threads / 64) * 16 + 64 + 16 + 16) * sizeof(float);
-    hipLaunchKernelGGL(scan_rule_kernel, dim3(a.B), dim3(threads), lds, s, a);
+    if ((a.xn != nullptr) != (a.rinv != nullptr) || (a.xn != nullptr) != (a.gamma != nullptr) || (!a.xn && !a.nf))
+        return hipErrorInvalidValue;
+    if (a.xn) hipLaunchKernelGGL(scan_rule_kernel<true>, dim3(a.B), dim3(threads), lds, s, a);
+    else hipLaunchKernelGGL(scan_rule_kernel<false>, dim3(a.B), dim3(threads), lds, s, a);
     return hipGetLastError();
 }
 

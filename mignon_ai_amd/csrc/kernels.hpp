@@ -25,6 +25,7 @@ struct RowArgs {
     const int32_t* row_map = nullptr;  // ROW_SRC: output row m reads source row row_map[m]
     const float* gamma = nullptr;      // RMSNorm scales, or null (copy)
     float* nout = nullptr;             // normalised rows [M][Dp], or null
+    float* rinv = nullptr;             // with gamma: each row's 1/rms [M], or null
     int8_t* limbs = nullptr;           // limb-expanded rows in the GEMM fragment layout (K = Dp)
     float* lscale = nullptr;           // [M]
     // ROW_RULE: the rule input [n | left | g] of each position, three segments of `seg` columns (Dp =
@@ -40,6 +41,11 @@ struct ScanArgs {
     int B = 0, T = 0, D = 0, Dp = 0;
     const float* lam = nullptr;  // [B*T][Dp]
     const float* nf = nullptr;   // [B*T][Dp]
+    // scan_rule only, in place of nf: n recomputed as (x * rinv) * gamma from the norm's source rows x
+    // [B*T][Dp] and the row kernel's 1/rms per row, the row kernel's own operations (bit-identical)
+    const float* xn = nullptr;
+    const float* rinv = nullptr;
+    const float* gamma = nullptr;
     float* g = nullptr;          // [B*T][Dp] latch state after each position (may be lam itself)
     const int32_t* lens = nullptr;  // per-sequence length (export position lens[b]-1) or null
     float* g_out = nullptr;         // exported latch state [B][Dp] or null

@@ -1,7 +1,9 @@
 """The fused latch scan + rule-input packing (one kernel, no latch state written) and the separate path
 (the scan writes the latch state of every position, then the row kernel packs [n | left | g]) build
 byte-identical GEMM operands, so every model output must be bit-identical between them; the fused path is
-also checked against the oracle. Covers dilations 1..32 (left neighbours up to two tiles back), padded
+also checked against the oracle. In a batched forward without a session export the fused kernel does not
+read the normalised rows n but recomputes them from the norm's source rows and the row kernel's 1/rms per
+row, so the bit equality also pins that recomputation. Covers dilations 1..32 (left neighbours up to two tiles back), padded
 widths (D not a multiple of 64), several blocks and steps, 16..256-token sequences, the session export of
 the latch state at each prompt's last position (ragged prefill lengths, then greedy steps), and lengths
 that are not a multiple of 16 (where the separate kernels run whatever the option says)."""
