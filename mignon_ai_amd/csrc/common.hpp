@@ -69,22 +69,28 @@ __device__ __forceinline__ Limbs split_limbs(float x, float inv) {
 // (ties to even, like rintf) and leaves that integer's two's-complement low byte as the sum's low
 // mantissa byte, so no clamp or float-to-int conversion is needed: |x*inv| <= 127 (up to rounding) by
 // the choice of scale, and every residual times 254 lies in [-127, 127].
+//
+// Each residual (y - q)*254 is formed as fma(y, 254, fma(t, -254, 254*C)) with t = y + C: the inner fma is
+// -254*q exactly (an integer of at most 32258), and the outer one rounds the exact 254*(y - q) once, which
+// is what the product of the exact difference y - q and 254 rounds to. Eight operations per element.
+__device__ __forceinline__ void digits3(float y, uint32_t& b0, uint32_t& b1, uint32_t& b2) {
+    const float C = 12582912.0f;        // 1.5 * 2^23
+    const float C254 = 254.0f * C;      // exact: 381 * 2^23
+    const float t0 = y + C;
+    const float y1 = fmaf(y, kLimbBase, fmaf(t0, -kLimbBase, C254));
+    const float t1 = y1 + C;
+    const float y2 = fmaf(y1, kLimbBase, fmaf(t1, -kLimbBase, C254));
+    const float t2 = y2 + C;
+    b0 = __float_as_uint(t0);
+    b1 = __float_as_uint(t1);
+    b2 = __float_as_uint(t2);
+}
+
 __device__ __forceinline__ void split4_pack(float4 x, float inv, uint32_t& w0, uint32_t& w1, uint32_t& w2) {
-    const float C = 12582912.0f;  // 1.5 * 2^23
     const float xs[4] = {x.x, x.y, x.z, x.w};
     uint32_t b0[4], b1[4], b2[4];
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const float y = xs[e] * inv;
-        const float t0 = y + C;
-        const float y1 = (y - (t0 - C)) * kLimbBase;
-        const float t1 = y1 + C;
-        const float y2 = (y1 - (t1 - C)) * kLimbBase;
-        const float t2 = y2 + C;
-        b0[e] = __float_as_uint(t0);
-        b1[e] = __float_as_uint(t1);
-        b2[e] = __float_as_uint(t2);
-    }
+    for (int e = 0; e < 4; e++) digits3(xs[e] * inv, b0[e], b1[e], b2[e]);
     // v_perm_b32: selector bytes 0-3 take the second operand's bytes, 4-7 the first's, 0x0c gives zero
     w0 = __builtin_amdgcn_perm(b0[1], b0[0], 0x0c0c0400u) | __builtin_amdgcn_perm(b0[3], b0[2], 0x04000c0cu);
     w1 = __builtin_amdgcn_perm(b1[1], b1[0], 0x0c0c0400u) | __builtin_amdgcn_perm(b1[3], b1[2], 0x04000c0cu);
@@ -93,21 +99,10 @@ __device__ __forceinline__ void split4_pack(float4 x, float inv, uint32_t& w0, u
 
 // split4_pack for two consecutive elements: their digits in bytes 0 and 1 of each word.
 __device__ __forceinline__ void split2_pack(float2 x, float inv, uint32_t& w0, uint32_t& w1, uint32_t& w2) {
-    const float C = 12582912.0f;  // 1.5 * 2^23
     const float xs[2] = {x.x, x.y};
     uint32_t b0[2], b1[2], b2[2];
 #pragma unroll
-    for (int e = 0; e < 2; e++) {
-        const float y = xs[e] * inv;
-        const float t0 = y + C;
-        const float y1 = (y - (t0 - C)) * kLimbBase;
-        const float t1 = y1 + C;
-        const float y2 = (y1 - (t1 - C)) * kLimbBase;
-        const float t2 = y2 + C;
-        b0[e] = __float_as_uint(t0);
-        b1[e] = __float_as_uint(t1);
-        b2[e] = __float_as_uint(t2);
-    }
+    for (int e = 0; e < 2; e++) digits3(xs[e] * inv, b0[e], b1[e], b2[e]);
     w0 = __builtin_amdgcn_perm(b0[1], b0[0], 0x0c0c0400u);
     w1 = __builtin_amdgcn_perm(b1[1], b1[0], 0x0c0c0400u);
     w2 = __builtin_amdgcn_perm(b2[1], b2[0], 0x0c0c0400u);

@@ -8,6 +8,11 @@
         every kernel are also given in bytes, scaled by the copy kernel's counter-to-bytes ratio, under
         the engine's kernel-class name (what bench.py reports and reads back as roofline traffic)
 
+    python -m mignon_ai_amd.profsum clock OUT.md CMD  COUNTERS.csv AGENT_INFO.csv
+        per kernel from one `rocprofv3 --pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES SQ_ACTIVE_INST_VALU`
+        run: the average shader clock over the dispatch (GPU-active cycles per XCD over the dispatch's
+        duration) and the fraction of SIMD cycles the matrix core and the VALU were busy
+
 CMD is the command line that produced the files, recorded in the summary.
 """
 from __future__ import annotations
@@ -126,17 +131,56 @@ def traffic_for(path: str, cls: str) -> float | None:
     return best
 
 
+def clock(out: str, cmd: str, path: str, agent_path: str) -> None:
+    gpu = [a for a in csv.DictReader(open(agent_path)) if a["Agent_Type"] == "GPU"][0]
+    nxcc, simds, cus = int(gpu["Num_Xcc"]), int(gpu["Simd_Count"]), int(gpu["Cu_Count"])
+    fmax = float(gpu["Max_Engine_Clk_Fcompute"]) / 1e3
+    per = defaultdict(dict)  # dispatch -> counter -> value (summed over dimensions), plus duration
+    names = {}
+    for r in csv.DictReader(open(path)):
+        d = r["Dispatch_Id"]
+        per[d][r["Counter_Name"]] = per[d].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        per[d]["ns"] = float(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        names[d] = _short(r["Kernel_Name"])
+    acc = defaultdict(lambda: defaultdict(float))
+    for d, v in per.items():
+        k = acc[names[d]]
+        k["n"] += 1
+        for c, x in v.items():
+            k[c] += x
+    lines = [f"Command (from the repository root, one MI355X):", "", "```", cmd, "```", "",
+             f"Shader clock: GRBM_GUI_ACTIVE per XCD ({nxcc} XCDs) over the dispatch duration (maximum "
+             f"{fmax:.2f} GHz). Matrix core busy: SQ_VALU_MFMA_BUSY_CYCLES over the {simds} SIMDs' cycles "
+             "(rocprofv3's MfmaUtil); VALU busy: SQ_ACTIVE_INST_VALU over the CUs' cycles (its VALUBusy).", "",
+             "| kernel | dispatches | avg ms | clock GHz | matrix core busy | VALU busy |",
+             "|---|---:|---:|---:|---:|---:|"]
+    for k, v in sorted(acc.items(), key=lambda kv: -kv[1]["ns"]):
+        n = v["n"]
+        cyc = v["GRBM_GUI_ACTIVE"] / n / nxcc
+        ms = v["ns"] / n / 1e6
+        if cyc <= 0 or ms < 0.05:
+            continue
+        mf = v.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / n / (cyc * simds)
+        va = v.get("SQ_ACTIVE_INST_VALU", 0.0) / n / (cyc * cus)
+        lines.append(f"| `{k}` | {int(n)} | {ms:.3f} | {cyc / (ms * 1e-3) / 1e9:.2f} | {100 * mf:.1f}% | "
+                     f"{100 * va:.1f}% |")
+    _write(out, lines)
+
+
 def _write(out: str, lines: list[str]) -> None:
     with open(out, "w") as f:
         f.write("\n".join(lines) + "\n")
 
 
 def main(argv: list[str]) -> None:
-    if len(argv) < 4 or argv[0] not in ("stats", "pmc"):
+    if len(argv) < 4 or argv[0] not in ("stats", "pmc", "clock"):
         raise SystemExit(__doc__)
     mode, out, cmd, rest = argv[0], argv[1], argv[2], argv[3:]
     if mode == "stats":
         stats(out, cmd, rest[0])
+        return
+    if mode == "clock":
+        clock(out, cmd, rest[0], rest[1])
         return
     calib = None
     if "--calib" in rest:

@@ -19,6 +19,10 @@ int finish(hipError_t launched) {
 
 extern "C" {
 
+// Digest of the engine headers this library was compiled against (the loader compares it with the
+// current headers': a stale library would pass misplaced argument fields to the engine's launchers).
+const char* mgt_headers_digest(void) { return MGT_HEADERS_DIGEST; }
+
 // The row kernel in ROW_SRC mode over M rows of D values (row stride Dp, a multiple of 64): RMSNorm with
 // gamma (null: a copy) into nout ([M][Dp], or null), and the limb expansion into the GEMM operand layout
 // (limbs: [ceil(M/16)][Dp/64][3][1 KiB], lscale: [M]; both null for none).

@@ -6,6 +6,7 @@ engine's kernels on torch device buffers, for the stage-level parity tests. Test
 from __future__ import annotations
 
 import ctypes
+import hashlib
 import os
 import subprocess
 import sys
@@ -20,6 +21,20 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 _lib = None
 
+# The hooks fill the engine's argument structs (kernels.hpp) and pass them to its launchers: a hooks
+# library compiled against other headers than the engine's would hand the launchers misplaced fields
+# (pointers read as sizes, buffers swapped), so the build records a digest of the headers it compiled
+# against and the loader refuses a library whose digest differs from the current headers'.
+HEADERS = [os.path.join(ROOT, "mignon_ai_amd", "csrc", h) for h in ("kernels.hpp", "common.hpp", "gemm.hpp")]
+
+
+def headers_digest() -> str:
+    h = hashlib.sha256()
+    for p in HEADERS:
+        with open(p, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
 
 def build() -> str:
     """Compile the hooks for gfx950 against the engine library (which must be built first)."""
@@ -29,7 +44,8 @@ def build() -> str:
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-           "-I", os.path.join(ROOT, "mignon_ai_amd", "csrc"), "-shared", SRC, "-o", tmp,
+           "-I", os.path.join(ROOT, "mignon_ai_amd", "csrc"), f'-DMGT_HEADERS_DIGEST="{headers_digest()}"',
+           "-shared", SRC, "-o", tmp,
            "-L", ENGINE_DIR, "-lmignon_hip", "-Wl,-rpath,$ORIGIN/../../mignon_ai_amd/_build"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -49,6 +65,11 @@ def lib():
         if not os.path.exists(LIB):
             raise RuntimeError(f"{LIB} is missing: run python tests/stage_hooks.py after building the engine")
         L = ctypes.CDLL(LIB)
+        L.mgt_headers_digest.restype = ctypes.c_char_p
+        built, now = L.mgt_headers_digest().decode(), headers_digest()
+        if built != now:
+            raise RuntimeError(f"{LIB} was compiled against other engine headers ({built}, now {now}): "
+                               "rebuild it (python tests/stage_hooks.py) after the engine")
         p, i = ctypes.c_void_p, ctypes.c_int
         sig = {
             "mgt_row": [p, i, i, i, p, p, p, p],
