@@ -13,7 +13,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 
 import numpy as np
 
@@ -40,14 +40,39 @@ class Piece:
     prob: float
 
 
-@dataclass
 class Result:
     """infer.Result: the reply, trimmed of surrounding whitespace, and its tokens (built on first use from
-    the token ids, their probabilities and the tokenizer's per-token texts)."""
-    text: str
-    ids: list[int] = field(default_factory=list)
-    probs: list[float] = field(default_factory=list)
-    _texts: list[str] | None = field(default=None, repr=False, compare=False)
+    the token ids, their probabilities and the tokenizer's per-token texts).
+
+    A batch of thousands of replies would otherwise leave several garbage-collected containers per reply
+    (a dict, two lists), whose count sets off Python's cyclic collector over the whole heap several times
+    per batch; the ids and probabilities are therefore kept as the call's own numpy rows and turned into
+    lists when read, and the fields live in slots."""
+    __slots__ = ("text", "_ids", "_probs", "_texts")
+
+    def __init__(self, text: str, ids=(), probs=(), texts: list[str] | None = None):
+        self.text = text
+        self._ids = ids      # token ids: a numpy row or a sequence
+        self._probs = probs  # their probabilities (empty when sampled)
+        self._texts = texts
+
+    @property
+    def ids(self) -> list[int]:
+        return np.asarray(self._ids, np.int64).tolist()
+
+    @property
+    def probs(self) -> list[float]:
+        return np.asarray(self._probs, np.float64).tolist()
+
+    def __eq__(self, other) -> bool:
+        if not isinstance(other, Result):
+            return NotImplemented
+        return (self.text, self.ids, self.probs) == (other.text, other.ids, other.probs)
+
+    __hash__ = None
+
+    def __repr__(self) -> str:
+        return f"Result(text={self.text!r}, ids={self.ids!r}, probs={self.probs!r})"
 
     @property
     def tokens(self) -> list[Piece]:
@@ -113,8 +138,8 @@ class Generator:
             out = []
             for i in range(n):
                 k = int(counts[i])
-                row = ids[i, :k].tolist()
-                out.append(Result(trim_space("".join([texts[t] for t in row])), row, probs[i, :k].tolist(), texts))
+                out.append(Result(trim_space("".join([texts[t] for t in ids[i, :k].tolist()])), ids[i, :k],
+                                  probs[i, :k], texts))
             return out
         sp = Sampling(temperature=temperature, rep_penalty=rep_penalty, top_p=top_p if top_p > 0 else 1.0,
                       top_k=top_k, penalize_prompt=0)
@@ -127,7 +152,7 @@ class Generator:
                                        max_tokens, int(chat), ctypes.byref(sp), ptr(sd), ptr(ids), ptr(counts)))
         out = []
         for i in range(n):
-            row = ids[i, :int(counts[i])].tolist()
-            text = "".join([texts[t] for t in row])
-            out.append(Result(trim_space(text) if chat else text, row, [], texts))  # Tokens stay empty
+            k = int(counts[i])
+            text = "".join([texts[t] for t in ids[i, :k].tolist()])
+            out.append(Result(trim_space(text) if chat else text, ids[i, :k], (), texts))  # Tokens stay empty
         return out
