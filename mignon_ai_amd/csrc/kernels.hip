@@ -38,8 +38,12 @@ __device__ __forceinline__ void nt_store4(float* dst, float4 v) {
 // the banks.
 __device__ __forceinline__ int stage_off(int o) { return (o >> 10) * 1088 + ((o >> 8) & 3) * 272 + (o & 255); }
 
+// Rows per wave pass: enough loads in flight for narrow rows, few enough registers for wide ones (the
+// 1024-column rows of the GLU output: one row per pass holds 162 registers, three waves per SIMD, against
+// 213 and two for two rows: c5 row kernels 28.0 -> 27.0 ms per step; 384-column rows lose 5 ms with two
+// per pass instead of four).
 template <int NS4>
-constexpr int row_batch() { return NS4 <= 2 ? 4 : (NS4 <= 4 ? 2 : 1); }
+constexpr int row_batch() { return NS4 <= 2 ? 4 : (NS4 <= 3 ? 2 : 1); }
 
 template <int NS4>
 __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
