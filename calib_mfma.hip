@@ -9,6 +9,9 @@
 //     hipcc --offload-arch=gfx950 -O3 -std=c++17 -Xclang -target-feature -Xclang -packed-fp32-ops \
 //         calib_mfma.hip -o gpurun_out/calib_mfma && gpurun_out/calib_mfma [iterations]
 //
+// A third run issues the same work as v_mfma_i32_32x32x32_i8 (each wave 32 tokens x 64 channels x 3
+// planes per K step: half the LDS weight bytes and register operand reads per operation), random operands.
+//
 // Prints the achieved TOP/s (2 ops per multiply-accumulate) of the best of three timed launches per
 // operand set.
 #include <hip/hip_runtime.h>
@@ -17,6 +20,7 @@
 #include <cstdlib>
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int KS = 18;  // K steps held in LDS: 144 KiB, one workgroup per CU as in the slab GEMM
 
@@ -66,6 +70,57 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     out[blockIdx.x * blockDim.x + threadIdx.x] = x;
 }
 
+// The same K steps on the 32x32x32 form: per K step of 64, two 32-deep halves, each two LDS fragment reads
+// (64 channels) against three activation fragments: 12 MFMAs of 65536 ops, the work of the 24 above.
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void mfma_steps32(int iters, int* out) {
+    extern __shared__ __align__(16) int8_t slab[];
+    const int t = (int)threadIdx.x, lane = t & 63;
+    for (int i = t; i < KS * 8192 / 4; i += 512) ((int*)slab)[i] = mix(i, 7u);
+    __syncthreads();
+    v4i a[2][3];
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int l = 0; l < 3; l++) {
+            const int k = 8 * t + 3 * h + l;
+            a[h][l] = v4i{mix(k, 11u), mix(k, 13u), mix(k, 17u), mix(k, 19u)};
+        }
+    v16i acc[3][2];
+#pragma unroll
+    for (int l = 0; l < 3; l++)
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[l][i][r] = 0;
+    for (int it = 0; it < iters; it++) {
+        for (int ks = 0; ks < KS; ks++) {
+            const int8_t* wp = slab + ks * 8192 + lane * 16;
+            v4i wf[2][2];
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int i = 0; i < 2; i++) wf[h][i] = *(const v4i*)(wp + (h * 2 + i) * 1024);
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int l = 0; l < 3; l++)
+                        acc[l][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[h][i], a[h][l], acc[l][i], 0, 0, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 12, 0);
+        }
+    }
+    int x = 0;
+#pragma unroll
+    for (int l = 0; l < 3; l++)
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) x ^= acc[l][i][r];
+    out[blockIdx.x * blockDim.x + threadIdx.x] = x;
+}
+
 static void check(hipError_t e, const char* what) {
     if (e != hipSuccess) {
         std::fprintf(stderr, "%s: %s\n", what, hipGetErrorString(e));
@@ -110,6 +165,24 @@ int main(int argc, char** argv) {
         std::printf("int8 MFMA (v_mfma_i32_16x16x64_i8), %d CUs, %s operands: %.3f ms, %.1f TOP/s\n", cus,
                     random ? "random" : "zero", best, ops / best / 1e9);
     }
+    check(hipFuncSetAttribute((const void*)mfma_steps32, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+          "hipFuncSetAttribute");
+    hipLaunchKernelGGL(mfma_steps32, dim3(blocks), dim3(threads), lds, 0, 4, out);
+    check(hipGetLastError(), "launch");
+    check(hipDeviceSynchronize(), "warm-up");
+    float best = 1e30f;
+    for (int rep = 0; rep < 3; rep++) {
+        check(hipEventRecord(e0), "hipEventRecord");
+        hipLaunchKernelGGL(mfma_steps32, dim3(blocks), dim3(threads), lds, 0, iters, out);
+        check(hipGetLastError(), "launch");
+        check(hipEventRecord(e1), "hipEventRecord");
+        check(hipEventSynchronize(e1), "hipEventSynchronize");
+        float ms = 0.0f;
+        check(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime");
+        if (ms < best) best = ms;
+    }
+    std::printf("int8 MFMA (v_mfma_i32_32x32x32_i8), %d CUs, random operands: %.3f ms, %.1f TOP/s\n", cus, best,
+                ops / best / 1e9);
     check(hipFree(out), "hipFree");
     return 0;
 }

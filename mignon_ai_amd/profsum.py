@@ -151,14 +151,18 @@ def clock(out: str, cmd: str, path: str, agent_path: str) -> None:
     lines = [f"Command (from the repository root, one MI355X):", "", "```", cmd, "```", "",
              f"Shader clock: GRBM_GUI_ACTIVE per XCD ({nxcc} XCDs) over the dispatch duration (maximum "
              f"{fmax:.2f} GHz). Matrix core busy: SQ_VALU_MFMA_BUSY_CYCLES over the {simds} SIMDs' cycles "
-             "(rocprofv3's MfmaUtil); VALU busy: SQ_ACTIVE_INST_VALU over the CUs' cycles (its VALUBusy).", "",
+             "(rocprofv3's MfmaUtil); VALU busy: SQ_ACTIVE_INST_VALU over the CUs' cycles (its VALUBusy). "
+             "Kernels with at least 0.5% of the run's kernel time; for dispatches of a few tens of "
+             "microseconds the clock figure is approximate (the counter's window is wider than the "
+             "dispatch).", "",
              "| kernel | dispatches | avg ms | clock GHz | matrix core busy | VALU busy |",
              "|---|---:|---:|---:|---:|---:|"]
+    total_ns = sum(v["ns"] for v in acc.values())
     for k, v in sorted(acc.items(), key=lambda kv: -kv[1]["ns"]):
         n = v["n"]
         cyc = v["GRBM_GUI_ACTIVE"] / n / nxcc
         ms = v["ns"] / n / 1e6
-        if cyc <= 0 or ms < 0.05:
+        if cyc <= 0 or v["ns"] < 0.005 * total_ns:
             continue
         mf = v.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / n / (cyc * simds)
         va = v.get("SQ_ACTIVE_INST_VALU", 0.0) / n / (cyc * cus)
