@@ -827,37 +827,44 @@ __device__ __forceinline__ int vswz(int r) { return 4 * ((r >> 3) & 3); }
 
 // S^T for key blocks SKIP..NKB-1 of one wave; the SKIP leading blocks hold only keys before the
 // sequence start (masked in the softmax), so their scores stay zero and no MFMA is spent on them.
+// Each block's sum runs over (g, e) in order; the blocks' chains are independent and interleaved, so
+// consecutive MFMAs never wait on each other's results.
 template <int ND, int NKB, int KS, int SKIP>
 __device__ __forceinline__ void attn_scores(v4f (&s)[NKB], const float* att_lds, int w, int qi, int kg,
                                             const v4f (&qv)[ND]) {
 #pragma unroll
-    for (int kb = 0; kb < NKB; kb++) {
-        s[kb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-        if (kb < SKIP) continue;
+    for (int kb = 0; kb < NKB; kb++) s[kb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int g = 0; g < ND; g++) {
-            const v4f kv = *(const v4f*)(att_lds + (16 * (w + kb) + qi) * KS + 16 * g + 4 * kg);
+    for (int g = 0; g < ND; g++) {
+        v4f kv[NKB];
 #pragma unroll
-            for (int e = 0; e < 4; e++) s[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[e], qv[g][e], s[kb], 0, 0, 0);
-        }
+        for (int kb = SKIP; kb < NKB; kb++) kv[kb] = *(const v4f*)(att_lds + (16 * (w + kb) + qi) * KS + 16 * g + 4 * kg);
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+#pragma unroll
+            for (int kb = SKIP; kb < NKB; kb++) s[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[kb][e], qv[g][e], s[kb], 0, 0, 0);
     }
 }
 
 // out = P V over key blocks SKIP..NKB-1 (the skipped blocks' probabilities are zero: leaving them out
 // adds nothing, bit for bit).
+// Each output group's sum runs over (kb, r) in order; the groups' chains are interleaved.
 template <int ND, int NKB, int VS, int SKIP>
 __device__ __forceinline__ void attn_pv(v4f (&o)[ND], const v4f (&s)[NKB], float inv, const float* att_lds, int w,
                                         int qi, int kg) {
 #pragma unroll
     for (int g = 0; g < ND; g++) o[g] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int kb = 0; kb < NKB; kb++) {
-        if (kb < SKIP) continue;
+    for (int kb = SKIP; kb < NKB; kb++) {
+        v4f vv[ND];
 #pragma unroll
-        for (int g = 0; g < ND; g++) {
-            const v4f vv = *(const v4f*)(att_lds + (16 * g + qi) * VS + ((16 * (w + kb) + 4 * kg) ^ vswz(16 * g + qi)));
+        for (int g = 0; g < ND; g++)
+            vv[g] = *(const v4f*)(att_lds + (16 * g + qi) * VS + ((16 * (w + kb) + 4 * kg) ^ vswz(16 * g + qi)));
 #pragma unroll
-            for (int r = 0; r < 4; r++) o[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(s[kb][r] * inv, vv[r], o[g], 0, 0, 0);
+        for (int r = 0; r < 4; r++) {
+            const float p = s[kb][r] * inv;
+#pragma unroll
+            for (int g = 0; g < ND; g++) o[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(p, vv[g][r], o[g], 0, 0, 0);
         }
     }
 }
