@@ -227,6 +227,14 @@ long long mg_tokenizer_encode(mg_tokenizer* t, const char* text, size_t n, int m
 /* Decode (internal/tokenizer/tokenizer.go:348-367): writes at most cap bytes (no terminator) and returns
  * the decoded length in bytes. */
 long long mg_tokenizer_decode(const mg_tokenizer* t, const int32_t* ids, long long n, char* out, long long cap);
+/* Decode of n rows at once, for a batch of replies (infer.Generate's Result.Text: strings.TrimSpace of
+ * the decoded reply, pkg/infer/infer.go:76-79): row i is counts[i] ids at ids + i*ld; with trim != 0 each
+ * row's text loses its leading and trailing white space (unicode.IsSpace). The texts are written one
+ * after another into out (at most cap bytes, no terminators) and row i's text is
+ * out[offsets[i], offsets[i+1]) (offsets: n + 1 entries, always written). Returns the total length in
+ * bytes; when it exceeds cap, out holds only the texts that fit whole. */
+long long mg_tokenizer_decode_rows(const mg_tokenizer* t, const int32_t* ids, const int32_t* counts, int n, int ld,
+                                   int trim, char* out, long long cap, long long* offsets);
 /* The vocabulary entry of id (Tokenizer.Vocab[id]): writes at most cap bytes (no terminator) and returns
  * its length, or MG_ERR_INVALID for an id outside the vocabulary. */
 long long mg_tokenizer_token(const mg_tokenizer* t, int id, char* out, long long cap);

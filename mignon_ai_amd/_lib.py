@@ -91,6 +91,7 @@ SIGNATURES = {
     "mg_tokenizer_special": (_int, [_vp, _int]),
     "mg_tokenizer_encode": (_ll, [_vp, ctypes.c_char_p, ctypes.c_size_t, _int, _vp, _ll]),
     "mg_tokenizer_decode": (_ll, [_vp, _vp, _ll, _vp, _ll]),
+    "mg_tokenizer_decode_rows": (_ll, [_vp, _vp, _vp, _int, _int, _int, _vp, _ll, _vp]),
     "mg_tokenizer_token": (_ll, [_vp, _int, _vp, _ll]),
     "mg_tokenizer_token_bytes": (_int, [_vp, _vp]),
     "mg_pretokenize": (_ll, [ctypes.c_char_p, ctypes.c_size_t, _vp, _ll]),

@@ -8,6 +8,7 @@
 #include <new>
 #include <stdexcept>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "../../include/mignon_hip.h"
@@ -162,6 +163,30 @@ long long mg_tokenizer_decode(const mg_tokenizer* t, const int32_t* ids, long lo
             if (k) std::memcpy(out, s.data(), (size_t)k);
             return (long long)s.size();
         });
+}
+
+long long mg_tokenizer_decode_rows(const mg_tokenizer* t, const int32_t* ids, const int32_t* counts, int n, int ld,
+                                   int trim, char* out, long long cap, long long* offsets) {
+    return guarded([&]() -> long long {
+        need(t != nullptr && n >= 0 && offsets != nullptr && (n == 0 || (ids && counts)),
+             "mg_tokenizer_decode_rows: null argument");
+        need(ld >= 0 && cap >= 0 && (out != nullptr || cap == 0), "mg_tokenizer_decode_rows: bad buffer");
+        std::string s;
+        long long pos = 0;
+        offsets[0] = 0;
+        for (int i = 0; i < n; i++) {
+            need(counts[i] >= 0 && counts[i] <= ld, "mg_tokenizer_decode_rows: row length outside 0..ld");
+            s.clear();
+            t->tok->decode(ids + (size_t)i * ld, (size_t)counts[i], s);
+            size_t b = 0, e = s.size();
+            if (trim) std::tie(b, e) = trim_space(s.data(), s.size());
+            const long long len = (long long)(e - b);
+            if (pos + len <= cap && len) std::memcpy(out + pos, s.data() + b, (size_t)len);
+            pos += len;
+            offsets[i + 1] = pos;
+        }
+        return pos;
+    });
 }
 
 long long mg_tokenizer_token(const mg_tokenizer* t, int id, char* out, long long cap) {

@@ -130,6 +130,9 @@ struct Tokenizer {
     std::unordered_map<std::string, int> rank;  // pair1 + '\0' + pair2 -> merge rank
     std::unordered_map<std::string, std::vector<int32_t>> cache;
     std::mutex cache_mu;
+    // what Decode writes for each id: 0 its vocabulary text, 1 nothing (<PAD>, <EOS>, <USER>, <BOT>),
+    // 2 U+FFFD (<UNK>); fixed at construction so that decoding compares no strings
+    std::vector<uint8_t> decode_kind;
 
     static constexpr const char* kPad = "<PAD>";
     static constexpr const char* kUnk = "<UNK>";
@@ -144,6 +147,12 @@ struct Tokenizer {
         for (size_t i = 0; i < vocab.size(); i++) id[vocab[i]] = (int)i;
         rank.reserve(merges.size() * 2);
         for (size_t r = 0; r < merges.size(); r++) rank[pair_key(merges[r].first, merges[r].second)] = (int)r;
+        decode_kind.resize(vocab.size(), 0);
+        for (size_t i = 0; i < vocab.size(); i++) {
+            const std::string& s = vocab[i];
+            if (s == kPad || s == kEos || s == kUser || s == kBot) decode_kind[i] = 1;
+            else if (s == kUnk) decode_kind[i] = 2;
+        }
     }
 
     // The tokenizer of a parsed model-file header, after tokenizer.CheckFormat on its metadata
@@ -305,10 +314,10 @@ struct Tokenizer {
         for (size_t i = 0; i < n; i++) {
             const int32_t t = ids[i];
             if (t < 0 || (size_t)t >= vocab.size()) continue;
-            const std::string& s = vocab[t];
-            if (s == kPad || s == kEos || s == kUser || s == kBot) continue;
-            if (s == kUnk) out += "\xEF\xBF\xBD";
-            else out += s;
+            const uint8_t k = decode_kind[t];
+            if (k == 1) continue;
+            if (k == 2) out += "\xEF\xBF\xBD";
+            else out += vocab[t];
         }
     }
 

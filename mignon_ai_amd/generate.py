@@ -135,12 +135,10 @@ class Generator:
             probs = np.empty((n, max_tokens), np.float64)
             check(lib().mg_generate_greedy(self.model.handle, self.tok.handle, arr, lens, n, self.context_size(),
                                            max_tokens, int(chat), ptr(ids), ptr(probs), ptr(counts)))
-            out = []
-            for i in range(n):
-                k = int(counts[i])
-                out.append(Result(trim_space("".join([texts[t] for t in ids[i, :k].tolist()])), ids[i, :k],
-                                  probs[i, :k], texts))
-            return out
+            # infer.Result.Text: strings.TrimSpace of the decoded reply (pkg/infer/infer.go:76-79)
+            replies = self.tok.decode_rows(ids, counts, trim=True)
+            cl = counts.tolist()
+            return [Result(replies[i], ids[i, :cl[i]], probs[i, :cl[i]], texts) for i in range(n)]
         sp = Sampling(temperature=temperature, rep_penalty=rep_penalty, top_p=top_p if top_p > 0 else 1.0,
                       top_k=top_k, penalize_prompt=0)
         if seeds is None:
@@ -150,9 +148,6 @@ class Generator:
             raise ValueError("one seed per prompt")
         check(lib().mg_generate_sample(self.model.handle, self.tok.handle, arr, lens, n, self.context_size(),
                                        max_tokens, int(chat), ctypes.byref(sp), ptr(sd), ptr(ids), ptr(counts)))
-        out = []
-        for i in range(n):
-            k = int(counts[i])
-            text = "".join([texts[t] for t in ids[i, :k].tolist()])
-            out.append(Result(trim_space(text) if chat else text, ids[i, :k], (), texts))  # Tokens stay empty
-        return out
+        replies = self.tok.decode_rows(ids, counts, trim=chat)
+        cl = counts.tolist()
+        return [Result(replies[i], ids[i, :cl[i]], (), texts) for i in range(n)]  # Tokens stay empty

@@ -129,6 +129,24 @@ class Tokenizer:
     def decode(self, ids) -> str:
         return self.decode_bytes(ids).decode("utf-8", errors="replace")
 
+    def decode_rows(self, ids, counts, trim: bool = False) -> list[str]:
+        """mg_tokenizer_decode_rows: Decode of every row of a [n][ld] id matrix (row i: its first counts[i]
+        ids), each text trimmed of surrounding white space (strings.TrimSpace) when trim is set, in one
+        call; invalid UTF-8 reads as U+FFFD."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        counts = np.ascontiguousarray(counts, np.int32)
+        n, ld = ids.shape
+        if getattr(self, "_max_token_bytes", None) is None:
+            self._max_token_bytes = max(self.token_bytes(), default=0)
+        cap = int(counts.sum()) * self._max_token_bytes
+        buf = ctypes.create_string_buffer(max(cap, 1))
+        off = np.empty(n + 1, np.int64)
+        total = check(lib().mg_tokenizer_decode_rows(self._h, ptr(ids), ptr(counts), n, ld, int(trim), buf, cap,
+                                                     ptr(off)))
+        raw = ctypes.string_at(buf, total)
+        o = off.tolist()
+        return [raw[o[i]:o[i + 1]].decode("utf-8", errors="replace") for i in range(n)]
+
     def piece_texts(self) -> list[str]:
         """Decode([id]) for every id (cached): the text each token contributes; Decode of a sequence is the
         concatenation of its tokens' texts."""

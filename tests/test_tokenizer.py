@@ -287,3 +287,39 @@ def test_encode_round_trips_orders_requests(toks):
             for i in ids:
                 start, pos = pos, pos + len(tok.vocab[i])
                 assert not any(start < b < pos for b in bounds), text
+
+
+# unicode.IsSpace (Go): the Latin-1 spaces and the White_Space property above Latin-1
+GO_WHITE_SPACE = "\t\n\v\f\r \x85\xa0\u1680" + "".join(chr(c) for c in range(0x2000, 0x200B)) + \
+    "\u2028\u2029\u202f\u205f\u3000"
+
+
+def test_decode_rows_equals_decode_of_each_row(toks):
+    """mg_tokenizer_decode_rows (one call for a batch of replies) gives every row what Decode gives it
+    (the restatement's), and with trimming strings.TrimSpace of that: rows of random ids and of encoded
+    text with white space at either end, markers, <UNK>, empty and full rows."""
+    import numpy as np
+
+    p, o = toks["product"], toks["oracle"]
+    rng = random.Random(12)
+    V = p.vocab_size()
+    rows = []
+    for i in range(300):
+        if i % 3 == 0:
+            rows.append([rng.randrange(V) for _ in range(rng.randrange(0, 40))])
+        else:
+            pre = "".join(rng.choice(GO_WHITE_SPACE) for _ in range(rng.randrange(0, 3)))
+            post = "".join(rng.choice(GO_WHITE_SPACE + "<EOS>") for _ in range(rng.randrange(0, 3)))
+            rows.append(p.encode(pre + _random_text(rng, rng.randrange(0, 30)).decode("utf-8") + post))
+    rows.append([])
+    rows.append(p.encode(" \t\n "))  # white space only
+    ld = max(len(r) for r in rows)
+    ids = np.zeros((len(rows), ld), np.int32)
+    counts = np.array([len(r) for r in rows], np.int32)
+    for i, r in enumerate(rows):
+        ids[i, :len(r)] = r
+        ids[i, len(r):] = rng.randrange(V)  # past the row's end: never read
+    want = [o.decode(r).decode("utf-8", errors="replace") for r in rows]
+    assert p.decode_rows(ids, counts) == want
+    assert p.decode_rows(ids, counts, trim=True) == [w.strip(GO_WHITE_SPACE) for w in want]
+    assert p.decode_rows(ids[:0], counts[:0]) == []
