@@ -43,7 +43,8 @@ def stats(out: str, cmd: str, path: str) -> None:
 # kernel name -> the engine's kernel class (mg_model_profile names; GEMM classes by epilogue number)
 _GEMM_EPI = {1: "gemm_qkv", 2: "gemm_latch", 3: "gemm_glu", 4: "gemm_highway", 5: "gemm_out", 6: "gemm_logits",
              7: "gemm_probs"}
-_CLASSES = [("gemm_c2_kernel", "gemm_i8"), ("row_kernel", "row_norm_pack"), ("scan_kernel", "latch_scan"),
+_CLASSES = [("gemm_c2_kernel", "gemm_i8"), ("row_kernel", "row_norm_pack"), ("scan_rule_kernel", "latch_scan"),
+            ("scan_kernel", "latch_scan"),
             ("latch_step_kernel", "latch_step"), ("attention_step", "attention_step"),
             ("qkv_attention_kernel", "qkv_attention"), ("attention", "attention"), ("head_combine_kernel", "head_combine"), ("bits_kernel", "bits"),
             ("export_", "state_export"), ("step1_kernel", "session_step"), ("tile_step_kernel", "tile_step")]
