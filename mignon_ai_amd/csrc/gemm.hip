@@ -834,8 +834,7 @@ hipError_t launch_any_t(const GemmArgs& a, hipStream_t stream) {
     // automatic: the weight-stationary kernel whenever its slab fits in LDS and the batch is large
     const int mode = option(OPT_GEMM_KERNEL);
     const bool fits = a.Kp >= 128 && (long long)(a.Kp / 64) * 8192 + LX_BN * 4 <= slab_lds_limit();
-    // (the residual epilogue's read-modify-write rows measured slower weight-stationary at 4096 rows)
-    const bool many = a.M >= kSlabMinRows || (a.M >= kSlabMinRowsWideK && a.Kp >= 256 && EPI != EPI_RESID);
+    const bool many = a.M >= kSlabMinRows || (a.M >= kSlabMinRowsWideK && a.Kp >= 256);
     if (fits && (mode == GEMM_SLAB || (mode == GEMM_AUTO && many))) return launch_slab_t<EPI>(a, stream);
     return launch_lx_t<EPI>(a, stream);
 }
