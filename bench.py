@@ -163,6 +163,13 @@ def roofline_for(work, config=None):
         r["traffic"], src = measured_traffic(config, dom)
         if src:
             r["traffic_source"] = src
+        # the kernel's shader clock and busy fractions from the committed counter summary: the limb GEMMs
+        # run at a power-limited clock, which is what separates the issued rate from the published peak
+        from mignon_ai_amd.profsum import clock_for
+        cpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"{config}_clock_busy.md")
+        c = clock_for(cpath, dom)
+        if c:
+            r["counters"] = dict(c, source=f"profiles/{config}_clock_busy.md")
     return dom, r
 
 

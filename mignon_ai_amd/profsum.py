@@ -172,6 +172,28 @@ def clock(out: str, cmd: str, path: str, agent_path: str) -> None:
     _write(out, lines)
 
 
+def clock_for(path: str, cls: str) -> dict | None:
+    """Shader clock and busy fractions recorded by `clock` for a kernel class (the kernel with the most
+    time when several implement the class), or None."""
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    best, best_ms = None, -1.0
+    for line in text.splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) != 6 or not cells[0].startswith("`") or kernel_class(cells[0]) != cls:
+            continue
+        try:
+            n, ms, ghz = int(cells[1]), float(cells[2]), float(cells[3])
+            mf, va = float(cells[4].rstrip("%")) / 100, float(cells[5].rstrip("%")) / 100
+        except ValueError:
+            continue
+        if n * ms > best_ms:
+            best, best_ms = {"clock_ghz": ghz, "matrix_core_busy": mf, "valu_busy": va}, n * ms
+    return best
+
+
 def _write(out: str, lines: list[str]) -> None:
     with open(out, "w") as f:
         f.write("\n".join(lines) + "\n")
