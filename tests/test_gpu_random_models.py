@@ -48,11 +48,25 @@ def test_random_model_forward_and_sessions(seed):
     rng = np.random.default_rng(seed)
     what = f"seed {seed}: {spec}"
 
-    # teacher-forced batch: every position of every sequence, against Call on each prefix
+    # teacher-forced batch: every position of every sequence, against Call on each prefix; with the
+    # automatic kernel choice, then with the weight-stationary GEMM, the fused scan and the fused attention
+    # forced (where the shapes take them), then the streaming GEMM, the separate scan and the
+    # reference-order attention
     B, T = 3, int(rng.choice([7, 16, 33, 128]))
     ids = rng.integers(0, spec.V, (B, T)).astype(np.int32)
-    got = gm.forward_batch(ids, logits=True)["logits"]
-    assert_close(got, om.forward_all(ids), what=f"forward, {what}")
+    ref = om.forward_all(ids)
+    combos = [None, dict(gemm="slab", scan="fused", attention="fused"),
+              dict(gemm="stream", scan="separate", attention="exact")]
+    for combo in combos:
+        prev = {k: engine_option(k) for k in ("gemm", "scan", "attention")}
+        try:
+            for k, v in (combo or {}).items():
+                engine_option(k, v)
+            got = gm.forward_batch(ids, logits=True)["logits"]
+        finally:
+            for k, v in prev.items():
+                engine_option(k, v)
+        assert_close(got, ref, what=f"forward {combo}, {what}")
 
     # sessions: ragged prefill, then steps
     S, ctx = 5, int(rng.choice([12, 40, spec.context]))
