@@ -888,7 +888,10 @@ int guarded(F&& f) {
     }
 }
 
-constexpr long long kMaxChunkTokens = 1 << 20;  // tokens per workspace pass of a teacher-forced batch
+// Tokens per workspace pass of a teacher-forced batch. c5's 2^21 tokens in one pass: 170.9 ms per step
+// against 172.1 in two passes of 2^20 (each kernel's ramp and tail once instead of twice), for ~44 GB of
+// workspace instead of ~22.
+constexpr long long kMaxChunkTokens = 1 << 21;
 
 // Stop tokens of a batched decode: after each column is written, scan() marks the sessions whose token is
 // a stop token and copies the stopped count into a pinned host slot behind an event; keep_going(k) holds

@@ -6,6 +6,8 @@
 // reproduced where a result depends on them (RMSNorm's sum of squares, attention dot products, softmax
 // sums, the P.V accumulation), so these stages are bit-identical to the reference given equal inputs.
 #include <algorithm>
+#include <cmath>
+#include <cstdlib>
 
 #include "common.hpp"
 #include "gemm.hpp"
@@ -2973,6 +2975,40 @@ hipError_t attn_mfma(const AttnArgs& a, int dh, hipStream_t s) {
     }
 }
 
+// Compute units of the current device (cached per device).
+int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev] && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus[dev] = 256;
+    return cus[dev];
+}
+
+// Sequences per workgroup of the fused attention (one workgroup per CU at a time: 139 KiB of LDS).
+// Around B*heads/2048 runs (long enough to amortise the slab copy, several workgroups per CU), chosen so
+// that the workgroups fill whole rounds of the CUs: a last round that occupies a few CUs keeps the rest
+// idle for a whole run (c5's 8192-sequence passes: 24 sequences per run made 8.02 rounds, 32 make 6;
+// 21.6 -> 18.0 ms per step). Ties go to the length nearest the target, then the longer one.
+int qkv_run_length(int B, int heads) {
+    const int cus = device_cus();
+    const int r0 = std::max(1, std::min(32, B * heads / 2048));
+    int best = r0;
+    double best_eff = -1.0;
+    for (int R = std::max(1, r0 / 2); R <= std::min(64, 2 * r0); R++) {
+        const double rounds = (double)heads * ((B + R - 1) / R) / cus;
+        const double eff = rounds / std::ceil(rounds);
+        const bool better = eff > best_eff + 1e-9 ||
+                            (eff > best_eff - 1e-9 && (std::abs(R - r0) < std::abs(best - r0) ||
+                                                       (std::abs(R - r0) == std::abs(best - r0) && R > best)));
+        if (better) {
+            best = R;
+            best_eff = std::max(best_eff, eff);
+        }
+    }
+    return best;
+}
+
 template <int ND, int NKB, int KC>
 hipError_t qkv_attn_t(const QkvAttnArgs& a, hipStream_t s) {
     constexpr int G = 8, DP = 16 * ND, KEYS = 16 * (NKB + G - 1), ZROWS = 16 * (NKB - 1);
@@ -2980,9 +3016,7 @@ hipError_t qkv_attn_t(const QkvAttnArgs& a, hipStream_t s) {
     static const hipError_t attr = hipFuncSetAttribute((const void*)qkv_attention_kernel<ND, NKB, KC>,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return attr;
-    // runs of sequences per workgroup: long enough to amortise the slab copy, short enough that every
-    // XCD's CUs get several workgroups
-    const int R = std::max(1, std::min(32, a.B * a.heads / 2048));
+    const int R = qkv_run_length(a.B, a.heads);
     const int n_runs = (a.B + R - 1) / R;
     const int grid = 8 * a.heads * ((n_runs + 7) / 8);
     hipLaunchKernelGGL((qkv_attention_kernel<ND, NKB, KC>), dim3(grid), dim3(512), lds, s, a, R, n_runs);

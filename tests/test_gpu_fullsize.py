@@ -1,11 +1,12 @@
 """The benchmark's own workloads at the sizes it times them, on device.
 
-c5 runs as two passes of 2^20 tokens (8192 sequences each), and inside a pass the probability rows sit up
-to 8.6e9 elements past the pass's base, so these tests reach the 64-bit offsets and the second pass that
-smaller batches never touch. Checks: every probability row sums to one; every sequence's bits per token
-equals -log2 of its gathered target probabilities (eval nll.score, internal/eval/eval.go:25-48); the
-log-probs equal the log of those probabilities; and four sequences at the pass boundaries (0, 8191, 8192,
-16383) against the oracle at 1e-4.
+c5 runs as one pass of 2^21 tokens, whose probability rows sit up to 1.7e10 elements past the base, so the
+test reaches the 64-bit offsets that smaller batches never touch. Checks: every probability row sums to
+one; every sequence's bits per token equals -log2 of its gathered target probabilities (eval nll.score,
+internal/eval/eval.go:25-48); the log-probs equal the log of those probabilities; and four sequences (0,
+8191, 8192, 16383) against the oracle at 1e-4. A batch of more tokens than one pass holds (the c1 model,
+17,000 x 128 tokens) checks the passes' boundary: log-probs and bits of sequences on both sides of it
+against the oracle.
 
 c2's timed call writes no int32 output, so its tiles leave through the LDS-staged row-segment stores; over
 all 262,144 rows it must equal, bit for bit, the call that also writes the int32 accumulators (whose rows
@@ -95,3 +96,33 @@ def test_c2_full_size_fp32_only_device():
     got = C1[torch.from_numpy(rows).cuda()].cpu().numpy()
     assert np.array_equal(got.view(np.uint32), Cr.view(np.uint32))
     assert np.array_equal(acc[torch.from_numpy(rows).cuda()].cpu().numpy(), accr)
+
+
+def test_batch_over_two_passes():
+    """17,000 sequences of 128 tokens: more than the 2^21 tokens of one workspace pass, so the batch runs
+    in two and the second starts at sequence 16384. Per-token log-probs and bits per token of sequences
+    around that boundary (and the first and last) against the oracle."""
+    import torch
+    data = model_bytes("c1")
+    spec = synth.CONFIGS["c1"]["spec"]
+    B, T = 17000, 128
+    assert B * T > (1 << 21)
+    ids_np = synth.token_ids(7, "two-pass", (B, T), spec.V)
+    m = Model(data)
+    ids = torch.from_numpy(ids_np).cuda()
+    logprob = torch.empty((B, T), dtype=torch.float32, device="cuda")
+    bits = torch.empty(B, dtype=torch.float32, device="cuda")
+    m.forward_batch_device(ids, logprob=logprob, bits=bits)
+    m.sync()
+    lp, bt = logprob.cpu().numpy(), bits.cpu().numpy()
+    om = oracle_model(data)
+    sub = [0, 16383, 16384, 16385, B - 1]
+    ref = om.forward_all(ids_np[sub])
+    for k, b in enumerate(sub):
+        r = ref[k].astype(np.float64)
+        mx = r.max(-1, keepdims=True)
+        lse = mx[:, 0] + np.log(np.exp(r - mx).sum(-1))
+        want = r[np.arange(T - 1), ids_np[b, 1:]] - lse[:-1]
+        assert np.abs(lp[b, :-1] - want).max() < 2e-5 * max(1.0, np.abs(want).max()), b
+        want_bits = -(want / np.log(2)).mean()
+        assert abs(bt[b] - want_bits) < 1e-5 * abs(want_bits), b
