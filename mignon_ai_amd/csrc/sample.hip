@@ -168,8 +168,8 @@ __device__ int seq_find(const double* x, int n, double r, int dflt) {
 
 constexpr int kExtract = 64;  // candidates taken one by one before falling back to a full sort
 
-// PHASE: 0 the whole draw; 1 up to the exponentials, stored to a.scratch; 2 from the exponentials in
-// a.scratch and their sums in a.sums (sample_sum_kernel) on, truncated sampling only.
+// PHASE: 0 the whole draw; 2 from the exponentials in a.scratch (sample_exp_kernel) and their sums in
+// a.sums (sample_sum_kernel) on, truncated sampling only.
 template <int PHASE>
 __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
     __shared__ double cand_v[kExtract];
@@ -180,6 +180,7 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
     __shared__ double red2_v[2][kThreads / 64];
     __shared__ int red2_i[2][kThreads / 64];
     __shared__ int chosen_sh;
+    __shared__ int32_t win_sh[kRepWindow];
     const int row = blockIdx.x;
     const int V = a.V, n2 = a.n2;
     double* key = smp_smem;           // [n2] logits, then probabilities
@@ -194,34 +195,40 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
     }
     __syncthreads();
 
-    if (PHASE != 2 && threadIdx.x == 0) {
+    if constexpr (PHASE != 2) {
         const int col = a.hist ? a.col : 0;
         const int32_t* g = a.hist ? a.hist + (long long)row * a.hist_ld : nullptr;
-        // trigram blocking over the generated tokens (sample.go:211-224)
+        // trigram blocking over the generated tokens (sample.go:211-224): every earlier occurrence of the
+        // last two tokens bans the token that followed it (one thread per position; a token banned twice
+        // is written the same value twice)
         if (a.trigram && col >= 2) {
             const int32_t w1 = g[col - 2], w2 = g[col - 1];
-            for (int i = 0; i + 2 < col; i++)
+            for (int i = threadIdx.x; i + 2 < col; i += blockDim.x)
                 if (g[i] == w1 && g[i + 1] == w2) {
                     const int32_t b = g[i + 2];
                     if (b >= 0 && b < V) key[b] = -DBL_MAX;
                 }
         }
-        // repetition penalty over the last kRepWindow tokens of prefix + generated, each distinct
-        // token once (sample.go:47-66, window sample.go:206-209)
-        if (a.p.rep_penalty > 1.0) {
-            int32_t w[kRepWindow];
-            int nwin = 0;
-            const int from_hist = min(col, kRepWindow);
-            const int plen = a.prefix_len ? a.prefix_len[row] : 0;
-            const int from_pre = min(plen, kRepWindow - from_hist);
-            const int32_t* pre = a.prefix ? a.prefix + (long long)row * a.prefix_ld : nullptr;
-            for (int k = plen - from_pre; k < plen; k++) w[nwin++] = pre[k];
-            for (int k = col - from_hist; k < col; k++) w[nwin++] = g[k];
+        // the repetition window: the last kRepWindow tokens of prefix + generated (sample.go:206-209),
+        // gathered by one thread each
+        const int from_hist = min(col, kRepWindow);
+        const int plen = a.prefix_len ? a.prefix_len[row] : 0;
+        const int from_pre = min(plen, kRepWindow - from_hist);
+        const int nwin = from_pre + from_hist;
+        if (a.p.rep_penalty > 1.0 && threadIdx.x < nwin) {
+            const int k = threadIdx.x;
+            win_sh[k] = k < from_pre ? a.prefix[(long long)row * a.prefix_ld + plen - from_pre + k]
+                                     : g[col - from_hist + (k - from_pre)];
+        }
+        __syncthreads();
+        // repetition penalty over the window, each distinct token once, after the bans
+        // (sample.go:47-66)
+        if (a.p.rep_penalty > 1.0 && threadIdx.x == 0) {
             for (int i = 0; i < nwin; i++) {
-                const int32_t t = w[i];
+                const int32_t t = win_sh[i];
                 if (t < 0 || t >= V) continue;
                 bool seen = false;
-                for (int j = 0; j < i; j++) seen |= w[j] == t;
+                for (int j = 0; j < i; j++) seen |= win_sh[j] == t;
                 if (!seen) key[t] = key[t] > 0 ? key[t] / a.p.rep_penalty : key[t] * a.p.rep_penalty;
             }
         }
@@ -248,12 +255,7 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
             double mx;
             int dummy;
             block_argmax(v, 0, red_v, red_i, mx, dummy);
-            for (int i = threadIdx.x; i < V; i += blockDim.x) {
-                const double e = exp(key[i] - mx);
-                if constexpr (PHASE == 1) a.scratch[(long long)row * V + i] = e;
-                else key[i] = e;
-            }
-            if constexpr (PHASE == 1) return;
+            for (int i = threadIdx.x; i < V; i += blockDim.x) key[i] = exp(key[i] - mx);
             __syncthreads();
         }
         const double u = a.u ? a.u[row] : uniform_draw(a.seeds[row], a.step);
@@ -418,76 +420,208 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
     }
 }
 
+// The penalised, tempered exponentials of one row per workgroup, the first launch of a sampled draw:
+// e[i] = exp(x[i] / T - max_j x[j] / T) into a.scratch, x the logits after the trigram bans and the
+// repetition penalty (sample.go:47-109 up to the exponentials, the same operations in float64 as
+// sample_rows_kernel). The row stays in registers, KP values per thread; the bans are a bit per token
+// in LDS and the window's penalised values a short list beside them, read by the threads that own those
+// tokens. Without a row in LDS many rows run per CU.
+template <int KP>
+__global__ __launch_bounds__(kThreads) void sample_exp_kernel(SampleArgs a) {
+    __shared__ uint32_t ban[kMaxSampleVocab / 32];
+    __shared__ int32_t win_sh[kRepWindow];
+    __shared__ int32_t ovr_t[kRepWindow];
+    __shared__ double ovr_v[kRepWindow];
+    __shared__ int novr_sh;
+    __shared__ double red_v[kThreads / 64];
+    __shared__ int red_i[kThreads / 64];
+    const int row = blockIdx.x, V = a.V, tid = threadIdx.x;
+    const long long base = (long long)row * a.ld;
+    auto logit = [&](int i) { return a.logits32 ? (double)a.logits32[base + i] : a.logits64[base + i]; };
+    // every load unconditional (columns clamped into the row), so that all KP are in flight at once
+    double x[KP];
+    if (a.logits32) {
+        float xf[KP];
+#pragma unroll
+        for (int k = 0; k < KP; k++) xf[k] = a.logits32[base + min(tid + k * kThreads, V - 1)];
+#pragma unroll
+        for (int k = 0; k < KP; k++) x[k] = xf[k];
+    } else {
+#pragma unroll
+        for (int k = 0; k < KP; k++) x[k] = a.logits64[base + min(tid + k * kThreads, V - 1)];
+    }
+    for (int w = tid; w < (V + 31) / 32; w += kThreads) ban[w] = 0;
+    const int col = a.hist ? a.col : 0;
+    const int32_t* g = a.hist ? a.hist + (long long)row * a.hist_ld : nullptr;
+    const int from_hist = min(col, kRepWindow);
+    const int plen = a.prefix_len ? a.prefix_len[row] : 0;
+    const int from_pre = min(plen, kRepWindow - from_hist);
+    const int nwin = from_pre + from_hist;
+    const bool rep = a.p.rep_penalty > 1.0;
+    if (rep && tid < nwin)  // the window: the last kRepWindow tokens of prefix + generated (sample.go:206-209)
+        win_sh[tid] = tid < from_pre ? a.prefix[(long long)row * a.prefix_ld + plen - from_pre + tid]
+                                     : g[col - from_hist + (tid - from_pre)];
+    __syncthreads();
+    // trigram blocking over the generated tokens (sample.go:211-224): every earlier occurrence of the
+    // last two tokens bans the token that followed it
+    if (a.trigram && col >= 2) {
+        const int32_t w1 = g[col - 2], w2 = g[col - 1];
+        for (int i = tid; i + 2 < col; i += kThreads)
+            if (g[i] == w1 && g[i + 1] == w2) {
+                const int32_t b = g[i + 2];
+                if (b >= 0 && b < V) atomicOr(&ban[b >> 5], 1u << (b & 31));
+            }
+    }
+    __syncthreads();
+    // repetition penalty, each distinct window token once, on its value after the bans (sample.go:47-66)
+    if (tid == 0) {
+        int no = 0;
+        if (rep)
+            for (int i = 0; i < nwin; i++) {
+                const int32_t t = win_sh[i];
+                if (t < 0 || t >= V) continue;
+                bool seen = false;
+                for (int j = 0; j < i; j++) seen |= win_sh[j] == t;
+                if (seen) continue;
+                const double k0 = (ban[t >> 5] >> (t & 31)) & 1 ? -DBL_MAX : logit(t);
+                ovr_t[no] = t;
+                ovr_v[no] = k0 > 0 ? k0 / a.p.rep_penalty : k0 * a.p.rep_penalty;
+                no++;
+            }
+        novr_sh = no;
+    }
+    __syncthreads();
+    const int novr = novr_sh;
+    const double invT = 1.0 / a.p.temperature;
+    double v = -DBL_MAX;
+#pragma unroll
+    for (int k = 0; k < KP; k++) {
+        const int i = tid + k * kThreads;
+        if (i >= V) continue;
+        double key = (ban[i >> 5] >> (i & 31)) & 1 ? -DBL_MAX : x[k];
+        for (int j = 0; j < novr; j++)
+            if (ovr_t[j] == i) key = ovr_v[j];
+        x[k] = key * invT;
+        v = fmax(v, x[k]);
+    }
+    double mx;
+    int dummy;
+    block_argmax(v, 0, red_v, red_i, mx, dummy);
+    double* e = a.scratch + (long long)row * V;
+#pragma unroll
+    for (int k = 0; k < KP; k++) {
+        const int i = tid + k * kThreads;
+        if (i < V) e[i] = exp(x[k] - mx);
+    }
+}
+
 // Truncated draw of one row by one wave, from the exponentials in a.scratch and the row sums in
-// a.sums (top-k of at most kExtract, or top-p): p = e * (1 / sum), then the candidates one at a time,
-// most probable first (equal probabilities by token id), until top-k or top-p is met, and the draw over
-// them (sample.go:111-190). Lane L owns tokens L, L + 64, ... and keeps the four best of them sorted in
-// registers; a round is one wave argmax over the lanes' heads, then the winning lane pops its head. The
-// candidates come out in descending order, so the ones taken so far are exactly those at or before the
-// last one taken: a lane whose four are all taken rescans its tokens past that point. The row stays in
-// global memory (no LDS staging), so many rows run per CU. A row whose top-p mass is not reached within
-// kExtract candidates is flagged for sample_rows_kernel<2>, which sorts it.
+// a.sums (top-k of at most kExtract, or top-p): p = e * (1 / sum), then the candidates in descending
+// order (equal probabilities by token id) until top-k or top-p is met, and the draw over them
+// (sample.go:111-190). The wave reads its row once, in batches of 8 values per lane. Every candidate
+// lies at or above t, the rounds-th largest of the lanes' largest probabilities (at least rounds values
+// do), and t only grows as the batches come in, so a batch's values at or above the current t are kept
+// (compacted into LDS) and the rest can never be candidates. The kept values are then sorted in LDS. A row
+// whose top-p mass is not reached within kExtract candidates, or whose kept values outgrow kPickCap, is
+// flagged for sample_rows_kernel<2>, which sorts the whole row.
+constexpr int kPickCap = 512;
+
+// The k-th largest (1 <= k <= 64) of the wave's 64 values, in every lane: a bitonic sort across the
+// lanes into descending order, then lane k - 1's value.
+__device__ __forceinline__ double wave_kth_largest(double x, int k, int lane) {
+#pragma unroll
+    for (int s = 2; s <= 64; s <<= 1) {
+#pragma unroll
+        for (int j = s >> 1; j > 0; j >>= 1) {
+            const double y = __shfl_xor(x, j);
+            const bool keep_max = ((lane & j) == 0) == ((lane & s) == 0);
+            x = keep_max ? fmax(x, y) : fmin(x, y);
+        }
+    }
+    return __shfl(x, k - 1);
+}
+
+// Drops the kept values below t, keeping the others' order; returns how many remain.
+__device__ __forceinline__ int pick_refilter(double* cv, int* ci, int count, double t, int lane) {
+    int kept = 0;
+    for (int q = 0; q < count; q += 64) {
+        const int i = q + lane;
+        const double v = i < count ? cv[i] : -1.0;
+        const int id = i < count ? ci[i] : 0;
+        const bool keep = i < count && v >= t;
+        const uint64_t bal = __builtin_amdgcn_ballot_w64(keep);
+        // every slot written lies below every slot still to be read
+        if (keep) {
+            const int pos = kept + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
+            cv[pos] = v;
+            ci[pos] = id;
+        }
+        kept += __popcll(bal);
+    }
+    return kept;
+}
+
 __global__ __launch_bounds__(64) void sample_pick_kernel(SampleArgs a) {
-    __shared__ double cand_v[kExtract];
-    __shared__ int cand_i[kExtract];
+    __shared__ double cand_v[kPickCap];
+    __shared__ int cand_i[kPickCap];
     const int row = blockIdx.x, lane = threadIdx.x, V = a.V;
     const double* e = a.scratch + (long long)row * V;
     const double inv = 1.0 / a.sums[row];
     const int kcap = (a.p.top_k > 0 && a.p.top_k < V) ? a.p.top_k : V;
     const bool use_p = a.p.top_p > 0.0 && a.p.top_p < 1.0;
     const int rounds = min(kcap, kExtract);
-    double cv4[4];
-    int ci4[4];
-    double lv = INFINITY;  // the last candidate taken: every token at or before it is taken
-    int li = -1;
-    auto refill = [&]() {
+    double m = -1.0;  // this lane's largest probability so far (probabilities are >= 0)
+    double t = -1.0;
+    int count = 0;
+    bool over = false;
+    for (int b = 0; b < V; b += 8 * 64) {
+        double kv[8];
 #pragma unroll
-        for (int q = 0; q < 4; q++) { cv4[q] = -INFINITY; ci4[q] = 0x7fffffff; }
-        for (int i0 = lane; i0 < V; i0 += 8 * 64) {
-            double kv[8];
+        for (int k = 0; k < 8; k++) kv[k] = e[min(b + 64 * k + lane, V - 1)] * inv;
 #pragma unroll
-            for (int k = 0; k < 8; k++) kv[k] = e[min(i0 + 64 * k, V - 1)] * inv;
+        for (int k = 0; k < 8; k++)
+            if (b + 64 * k + lane < V) m = fmax(m, kv[k]);
+        t = wave_kth_largest(m, rounds, lane);
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const int i = i0 + 64 * k;
-                double v = kv[k];
-                int vi = i;
-                if (i >= V || !before(lv, li, v, vi) || !before(v, vi, cv4[3], ci4[3])) continue;
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    if (before(v, vi, cv4[q], ci4[q])) {
-                        const double tv = cv4[q];
-                        const int ti = ci4[q];
-                        cv4[q] = v; ci4[q] = vi;
-                        v = tv; vi = ti;
-                    }
+        for (int k = 0; k < 8; k++) {
+            if (count + 64 > kPickCap) {
+                count = pick_refilter(cand_v, cand_i, count, t, lane);
+                if (count + 64 > kPickCap) {
+                    over = true;
+                    break;
                 }
             }
+            const int i = b + 64 * k + lane;
+            const bool keep = i < V && kv[k] >= t;
+            const uint64_t bal = __builtin_amdgcn_ballot_w64(keep);
+            if (keep) {
+                const int pos = count + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
+                cand_v[pos] = kv[k];
+                cand_i[pos] = i;
+            }
+            count += __popcll(bal);
         }
-    };
-    refill();
-    int taken = 0;  // this lane's tokens taken since its last refill
-    double cp = 0.0;
+        if (over) break;
+    }
     int act = 0;
-    for (int r = 0; r < rounds; r++) {
-        double bv = cv4[0];
-        int bi = ci4[0];
-        wave_argmax(bv, bi);
-        if (lane == 0) { cand_v[r] = bv; cand_i[r] = bi; }
-        cp += bv;
-        if ((use_p && cp >= a.p.top_p) || r + 1 == kcap) {
-            act = r + 1;
-            break;
+    if (!over) {
+        count = pick_refilter(cand_v, cand_i, count, t, lane);
+        int n2 = 64;
+        while (n2 < count) n2 <<= 1;
+        for (int i = count + lane; i < n2; i += 64) {
+            cand_v[i] = -1.0;  // padding sorts last
+            cand_i[i] = 0x7fffffff;
         }
-        if ((bi & 63) == lane) {
-            cv4[0] = cv4[1]; ci4[0] = ci4[1];
-            cv4[1] = cv4[2]; ci4[1] = ci4[2];
-            cv4[2] = cv4[3]; ci4[2] = ci4[3];
-            cv4[3] = -INFINITY; ci4[3] = 0x7fffffff;
-            if (++taken == 4) {
-                lv = bv; li = bi;
-                refill();
-                taken = 0;
+        __syncthreads();
+        bitonic_desc(cand_v, cand_i, n2);
+        if (lane == 0) {
+            double cp = 0.0;
+            for (int r = 0; r < rounds; r++) {
+                cp += cand_v[r];
+                if ((use_p && cp >= a.p.top_p) || r + 1 == kcap) {
+                    act = r + 1;
+                    break;
+                }
             }
         }
     }
@@ -508,103 +642,144 @@ __global__ __launch_bounds__(64) void sample_pick_kernel(SampleArgs a) {
     if (a.next_ids) a.next_ids[row] = c;
 }
 
-// The rows' sequential float64 sums, one lane per row (each lane's chain of dependent additions runs
-// beside 63 others instead of alone in a workgroup): sums[row] = e[0] + e[1] + ... in index order. For
-// pure temperature sampling (pure != 0) the lane also draws: the first index whose running sum reaches
-// u * sum (the same sums again), or 0 when none does.
+// The rows' sequential float64 sums, one lane per row: sums[row] = e[0] + e[1] + ... in index order (the
+// reference's loop). Each row is one chain of V dependent additions, so the kernel is bound by how fast a
+// lane can be fed: kSumRows rows per wave (the remaining lanes idle), one wave per CU, and the rows stream
+// through an LDS ring of kSumRing blocks of kSumCols columns, filled by direct global-to-LDS loads (no
+// registers held), so that about kSumRing blocks are in flight while the lanes add. For pure temperature
+// sampling (pure != 0) the lane also draws: the first index whose running sum reaches u * sum (the same
+// sums again), or 0 when none does.
 //
-// The wave's 64 rows pass through LDS in blocks of kSumCols columns: the block is loaded with
-// coalesced 16-byte loads (row by row), the next block's loads are in flight while each lane adds its
-// own row's values from LDS in index order. Rows are padded by one double, so the lanes' reads of one
-// column fall in different banks.
+// A block holds row j's 16-byte column pair p at slot j * kSumPairs + (p ^ j): the lanes reading one pair
+// of their rows at once touch 16 different slots, so the reads do not conflict in the LDS banks.
+constexpr int kSumRows = 16;
 constexpr int kSumCols = 32;
-constexpr int kSumLd = kSumCols + 1;
-constexpr int kSumLoads = 64 * kSumCols / 2 / 64;  // 16-byte loads per lane and block
+constexpr int kSumPairs = kSumCols / 2;
+constexpr int kSumBlockLoads = kSumRows * kSumPairs / 64;  // 1 KiB direct-to-LDS loads per block
+constexpr int kSumBlock = kSumRows * kSumCols;             // doubles per ring slot
+constexpr int kSumRing = 16;
+static_assert(kSumPairs == kSumRows, "the slot swizzle pairs every row with every column pair");
+static_assert(kSumBlockLoads * (kSumRing - 2) == 56, "the ring's waits below count 56 loads in flight");
 
-// Block cb of the wave's rows r0.. into registers: load u of lane L covers the double pair
-// (row (u*64 + L) / (kSumCols/2), columns 2*((u*64 + L) % (kSumCols/2)) + {0, 1}), clamped into the
-// arrays (clamped lanes load valid memory that nobody reads).
-__device__ __forceinline__ void sum_block_load(const double* e, int n, int V, int r0, int cb, int lane,
-                                               double2 (&buf)[kSumLoads]) {
+// One 16-byte load per lane from global memory straight into LDS: lane L's bytes land at LDS offset
+// lds + 16 L. Issued through inline assembly, with the waits for it written out below, because the
+// compiler, which cannot tell which LDS bytes such a load writes, waits for every one of them before any
+// LDS read, and the ring would then hold one block in flight instead of kSumRing.
+__device__ __forceinline__ void lds_load16(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Loads block cb of rows r0.. into ring slot dst: load u of lane L fills slot u * 64 + L, i.e. row
+// (u * 64 + L) / kSumPairs and pair ((u * 64 + L) % kSumPairs) ^ row; rows and columns clamped into the
+// array (clamped loads fetch valid memory that nobody reads).
+__device__ __forceinline__ void sum_block_issue(const double* e, int n, int V, int r0, int cb, int lane,
+                                                uint32_t dst) {
 #pragma unroll
-    for (int u = 0; u < kSumLoads; u++) {
-        const int q = u * 64 + lane;
-        const int r = min(r0 + q / (kSumCols / 2), n - 1);
-        const int c = min(cb * kSumCols + 2 * (q % (kSumCols / 2)), V - 2);
-        buf[u] = *(const double2*)(e + (long long)r * V + c);
+    for (int u = 0; u < kSumBlockLoads; u++) {
+        const int s = u * 64 + lane, j = s / kSumPairs, p = (s % kSumPairs) ^ j;
+        const int r = min(r0 + j, n - 1);
+        const int c = min(cb * kSumCols + 2 * p, V - 2);
+        lds_load16(e + (long long)r * V + c, dst + u * 1024);
     }
 }
 
-__device__ __forceinline__ void sum_block_store(double* blk, int lane, const double2 (&buf)[kSumLoads]) {
-#pragma unroll
-    for (int u = 0; u < kSumLoads; u++) {
-        const int q = u * 64 + lane;
-        double* d = blk + (q / (kSumCols / 2)) * kSumLd + 2 * (q % (kSumCols / 2));
-        d[0] = buf[u].x;
-        d[1] = buf[u].y;
-    }
-}
-
-// Visits e[row][0], e[row][1], ... in order for the wave's rows (lane L: row r0 + L), f(index, value)
-// per element; stops after the block in which every lane's f has returned true.
+// Visits e[row][0], e[row][1], ... in order for the wave's rows (lane L < kSumRows: row r0 + L), f(index,
+// value) per element; stops after the block in which every lane's f has returned true.
 template <class F>
-__device__ __forceinline__ void sum_rows_scan(const double* e, int n, int V, int r0, int lane, double* blk, F&& f) {
+__device__ __forceinline__ void sum_rows_scan(const double* e, int n, int V, int r0, int lane, double* ring, F&& f) {
+    const bool mine_row = lane < kSumRows;
     if (V & 1) {  // rows not 16-byte aligned: each lane reads its own row
+        if (!mine_row) return;
         const double* rowp = e + (long long)min(r0 + lane, n - 1) * V;
         for (int c = 0; c < V; c++)
             if (f(c, rowp[c])) break;
         return;
     }
     const int nb = (V + kSumCols - 1) / kSumCols;
-    double2 buf[kSumLoads];
-    sum_block_load(e, n, V, r0, 0, lane, buf);
-    bool done = false;
-    for (int cb = 0; cb < nb; cb++) {
-        sum_block_store(blk, lane, buf);
-        if (cb + 1 < nb) sum_block_load(e, n, V, r0, cb + 1, lane, buf);
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the block is in LDS
-        __builtin_amdgcn_wave_barrier();
-        const double* mine = blk + lane * kSumLd;
+    const uint32_t ring0 = lds_offset(ring);
+    constexpr uint32_t kSlotBytes = kSumBlock * sizeof(double);
+    // only vector memory operations of this scan may be outstanding when its waits count them
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const int pre = min(nb, kSumRing - 1);
+    for (int b = 0; b < pre; b++) sum_block_issue(e, n, V, r0, b, lane, ring0 + b * kSlotBytes);
+    bool done = !mine_row;
+    const int jl = lane & (kSumRows - 1);
+    auto full = [&](int cb) { return (cb + 1) * kSumCols <= V; };
+    // a block's values into registers; read by every lane whatever it needs (a ring slot is always valid
+    // LDS), so that no branch hides from the compiler how many LDS reads are outstanding, and the wait for
+    // one block's values does not also wait for the next block's
+    auto rd = [&](double2(&v)[kSumPairs], int cb) {
+        const double2* m = (const double2*)(ring + (cb % kSumRing) * kSumBlock) + jl * kSumPairs;
+#pragma unroll
+        for (int p = 0; p < kSumPairs; p++) v[p] = m[p ^ jl];
+    };
+    // Block cb from registers cur, while block cb + 1 is read into nxt: the LDS reads of the next block
+    // overlap the chain of additions. True once every lane is done.
+    auto step = [&](int cb, double2(&cur)[kSumPairs], double2(&nxt)[kSumPairs]) {
+        // cur has arrived, and the slot refilled now (block cb - 1's) was read before it (the builtin, not
+        // inline assembly: the compiler counts this wait, so it adds no wait of its own for cur below)
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        asm volatile("" ::: "memory");
+        if (cb + kSumRing - 1 < nb) {
+            sum_block_issue(e, n, V, r0, cb + kSumRing - 1, lane, ring0 + ((cb + kSumRing - 1) % kSumRing) * kSlotBytes);
+            asm volatile("s_waitcnt vmcnt(56)" ::: "memory");  // block cb + 1 is in LDS
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        rd(nxt, cb + 1);
         const int c0 = cb * kSumCols;
         if (!done) {
-            // the last block of a vocabulary that is not a multiple of kSumCols was loaded from clamped
-            // columns: its values are read from their true columns
-            if (c0 + kSumCols <= V) {
-#pragma unroll 8
-                for (int c = 0; c < kSumCols; c++)
-                    if (!done && f(c0 + c, mine[c])) done = true;
+            if (full(cb)) {
+#pragma unroll
+                for (int p = 0; p < kSumPairs; p++) {
+                    if (!done && f(c0 + 2 * p, cur[p].x)) done = true;
+                    if (!done && f(c0 + 2 * p + 1, cur[p].y)) done = true;
+                }
             } else {
+                // the last block of a vocabulary that is not a multiple of kSumCols was loaded from
+                // clamped columns: its values are read from their true columns
                 const double* rowp = e + (long long)min(r0 + lane, n - 1) * V;
                 for (int c = c0; c < V; c++)
                     if (!done && f(c, rowp[c])) done = true;
             }
         }
-        if (__builtin_amdgcn_ballot_w64(!done) == 0) break;
-        __builtin_amdgcn_wave_barrier();  // every lane's reads of this block come before the next store
-        __builtin_amdgcn_s_waitcnt(0xc07f);
+        return __builtin_amdgcn_ballot_w64(!done) == 0;
+    };
+    double2 va[kSumPairs], vb[kSumPairs];
+    if (pre == kSumRing - 1) asm volatile("s_waitcnt vmcnt(56)" ::: "memory");  // block 0 is in LDS
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    rd(va, 0);
+    for (int cb = 0; cb < nb; cb += 2) {
+        if (step(cb, va, vb)) break;
+        if (cb + 1 < nb && step(cb + 1, vb, va)) break;
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load into LDS outlives the scan
 }
 
 __global__ __launch_bounds__(64) void sample_sum_kernel(SampleArgs a, int pure) {
-    __shared__ double blk[64 * kSumLd];
-    const int lane = threadIdx.x, r0 = blockIdx.x * 64, row = r0 + lane;
+    __shared__ __align__(16) double ring[kSumRing * kSumBlock];
+    const int lane = threadIdx.x, r0 = blockIdx.x * kSumRows, row = r0 + lane;
     const int V = a.V, n = a.n;
     double s = 0.0;
-    sum_rows_scan(a.scratch, n, V, r0, lane, blk, [&](int, double v) {
+    sum_rows_scan(a.scratch, n, V, r0, lane, ring, [&](int, double v) {
         s += v;
         return false;
     });
     if (!pure) {
-        if (row < n) a.sums[row] = s;
+        if (lane < kSumRows && row < n) a.sums[row] = s;
         return;
     }
-    // every lane stays for the second pass: the blocks are stored into LDS by all 64 lanes together
+    // every lane stays for the second pass: each lane loads its share of every block
     const int rc = min(row, n - 1);
     const double u = a.u ? a.u[rc] : uniform_draw(a.seeds[rc], a.step);
     const double r = u * s;
     double c = 0.0;
     int t = V;
-    sum_rows_scan(a.scratch, n, V, r0, lane, blk, [&](int i, double v) {
+    sum_rows_scan(a.scratch, n, V, r0, lane, ring, [&](int i, double v) {
         c += v;
         if (c >= r) {
             t = i;
@@ -612,7 +787,7 @@ __global__ __launch_bounds__(64) void sample_sum_kernel(SampleArgs a, int pure) 
         }
         return false;
     });
-    if (row >= n) return;
+    if (lane >= kSumRows || row >= n) return;
     const int chosen = t < V ? t : 0;
     a.out[(long long)row * a.out_ld + a.out_col] = chosen;
     if (a.next_ids) a.next_ids[row] = chosen;
@@ -647,11 +822,7 @@ hipError_t launch_sample(const SampleArgs& a, hipStream_t s) {
     static const hipError_t attr2 = hipFuncSetAttribute((const void*)sample_rows_kernel<2>,
                                                         hipFuncAttributeMaxDynamicSharedMemorySize,
                                                         (int)sample_lds_bytes(kMaxSampleVocab));
-    static const hipError_t attr1 = hipFuncSetAttribute((const void*)sample_rows_kernel<1>,
-                                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                        (int)(kMaxSampleVocab * sizeof(double)));
     if (attr0 != hipSuccess) return attr0;
-    if (attr1 != hipSuccess) return attr1;
     if (attr2 != hipSuccess) return attr2;
     const bool sampled = a.p.temperature > 0.001;
     if (!sampled || !a.scratch || !a.sums) {
@@ -660,8 +831,11 @@ hipError_t launch_sample(const SampleArgs& a, hipStream_t s) {
     }
     // three passes: exponentials per row, the rows' sums one lane per row, then the truncated draw (one
     // wave per row; the rows it flags, and every row when top-k exceeds kExtract without top-p, sorted)
-    hipLaunchKernelGGL(sample_rows_kernel<1>, dim3(a.n), dim3(kThreads), (size_t)a.V * sizeof(double), s, a);
-    hipLaunchKernelGGL(sample_sum_kernel, dim3((a.n + 63) / 64), dim3(64), 0, s, a, truncated ? 0 : 1);
+    if (a.V <= 4 * kThreads) hipLaunchKernelGGL(sample_exp_kernel<4>, dim3(a.n), dim3(kThreads), 0, s, a);
+    else if (a.V <= 8 * kThreads) hipLaunchKernelGGL(sample_exp_kernel<8>, dim3(a.n), dim3(kThreads), 0, s, a);
+    else if (a.V <= 16 * kThreads) hipLaunchKernelGGL(sample_exp_kernel<16>, dim3(a.n), dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL(sample_exp_kernel<kMaxSampleVocab / kThreads>, dim3(a.n), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(sample_sum_kernel, dim3((a.n + kSumRows - 1) / kSumRows), dim3(64), 0, s, a, truncated ? 0 : 1);
     if (truncated) {
         SampleArgs b = a;
         b.flags = nullptr;
