@@ -177,8 +177,6 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(SampleArgs a) {
     extern __shared__ __align__(16) double smp_smem[];
     __shared__ double red_v[kThreads / 64];
     __shared__ int red_i[kThreads / 64];
-    __shared__ double red2_v[2][kThreads / 64];
-    __shared__ int red2_i[2][kThreads / 64];
     __shared__ int chosen_sh;
     __shared__ int32_t win_sh[kRepWindow];
     const int row = blockIdx.x;
@@ -664,9 +662,11 @@ static_assert(kSumBlockLoads * (kSumRing - 2) == 56, "the ring's waits below cou
 // One 16-byte load per lane from global memory straight into LDS: lane L's bytes land at LDS offset
 // lds + 16 L. Issued through inline assembly, with the waits for it written out below, because the
 // compiler, which cannot tell which LDS bytes such a load writes, waits for every one of them before any
-// LDS read, and the ring would then hold one block in flight instead of kSumRing.
+// LDS read, and the ring would then hold one block in flight instead of kSumRing. The load takes its LDS
+// address from M0, which the compiler reserves (it cannot be listed as clobbered): nothing else in this
+// file's device code uses M0, so no value of the compiler's lives there.
 __device__ __forceinline__ void lds_load16(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory");
 }
 
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
@@ -705,7 +705,23 @@ __device__ __forceinline__ void sum_rows_scan(const double* e, int n, int V, int
     // only vector memory operations of this scan may be outstanding when its waits count them
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     const int pre = min(nb, kSumRing - 1);
-    for (int b = 0; b < pre; b++) sum_block_issue(e, n, V, r0, b, lane, ring0 + b * kSlotBytes);
+    // each lane's source of load u of a whole block, column 0: block cb adds cb * kSumCols (the clamped
+    // addresses of sum_block_issue are needed only for the last, partial block)
+    const double* src[kSumBlockLoads];
+#pragma unroll
+    for (int u = 0; u < kSumBlockLoads; u++) {
+        const int s = u * 64 + lane, j = s / kSumPairs, p = (s % kSumPairs) ^ j;
+        src[u] = e + (long long)min(r0 + j, n - 1) * V + 2 * p;
+    }
+    auto issue = [&](int cb, uint32_t dst) {
+        if ((cb + 1) * kSumCols <= V) {
+#pragma unroll
+            for (int u = 0; u < kSumBlockLoads; u++) lds_load16(src[u] + cb * kSumCols, dst + u * 1024);
+        } else {
+            sum_block_issue(e, n, V, r0, cb, lane, dst);
+        }
+    };
+    for (int b = 0; b < pre; b++) issue(b, ring0 + b * kSlotBytes);
     bool done = !mine_row;
     const int jl = lane & (kSumRows - 1);
     auto full = [&](int cb) { return (cb + 1) * kSumCols <= V; };
@@ -725,7 +741,7 @@ __device__ __forceinline__ void sum_rows_scan(const double* e, int n, int V, int
         __builtin_amdgcn_s_waitcnt(0xc07f);
         asm volatile("" ::: "memory");
         if (cb + kSumRing - 1 < nb) {
-            sum_block_issue(e, n, V, r0, cb + kSumRing - 1, lane, ring0 + ((cb + kSumRing - 1) % kSumRing) * kSlotBytes);
+            issue(cb + kSumRing - 1, ring0 + ((cb + kSumRing - 1) % kSumRing) * kSlotBytes);
             asm volatile("s_waitcnt vmcnt(56)" ::: "memory");  // block cb + 1 is in LDS
         } else {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
