@@ -249,7 +249,9 @@ long long mg_pretokenize(const char* text, size_t n, long long* ends, long long 
  * each prompt (UTF-8, prompt_lens[i] bytes) goes through the chat template when chat != 0; the reply
  * stops before <EOS>, <USER> or <BOT> or after max_tokens (> 0) tokens. out_ids / out_probs are
  * [n][max_tokens]; out_counts[i] is the reply length. Decode the ids with mg_tokenizer_decode and trim
- * surrounding whitespace for infer.Result.Text. */
+ * surrounding whitespace for infer.Result.Text. The session set a call decodes on stays allocated in m
+ * afterwards (cleared and reused by the next mg_generate_* call with as many non-empty prompts and the same
+ * window, replaced otherwise, freed by mg_model_free); calls running at once on m use sets of their own. */
 int mg_generate_greedy(mg_model* m, mg_tokenizer* t, const char* const* prompts, const size_t* prompt_lens, int n,
                        int context, int max_tokens, int chat, int32_t* out_ids, double* out_probs,
                        int32_t* out_counts);
@@ -259,7 +261,8 @@ int mg_generate_greedy(mg_model* m, mg_tokenizer* t, const char* const* prompts,
  * the repetition window over the reply; internal/generate/chat.go:104-140), generate.Text otherwise (the
  * prompt as is, the window starting in the prompt; chat.go:62-70). sp->penalize_prompt is ignored. Replies
  * stop before <EOS>, <USER> or <BOT> or after max_tokens (> 0) tokens; seeds[i] seeds prompt i's draws
- * (mg_sessions_decode_sample). out_ids [n][max_tokens], out_counts[n]. */
+ * (mg_sessions_decode_sample). out_ids [n][max_tokens], out_counts[n]. Its session set is kept in m as
+ * mg_generate_greedy's is (one set for both). */
 int mg_generate_sample(mg_model* m, mg_tokenizer* t, const char* const* prompts, const size_t* prompt_lens, int n,
                        int context, int max_tokens, int chat, const mg_sampling_t* sp, const uint64_t* seeds,
                        int32_t* out_ids, int32_t* out_counts);

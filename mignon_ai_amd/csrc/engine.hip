@@ -215,6 +215,9 @@ struct mg_model {
     mg::Workspace* wsp = nullptr;  // while set (an allocation-free call), the workspace in use instead of ws
     mg::Profile prof;
     std::mutex mu;
+    // the session set of the last mg_generate_* call, kept for the next call of the same size and window
+    // (taken out while a call uses it, so concurrent calls never share it)
+    std::atomic<mg_sessions*> gen_cache{nullptr};
 };
 
 struct mg_sessions {
@@ -1143,6 +1146,7 @@ int mg_model_sync(mg_model* m) {
 void mg_model_free(mg_model* m) {
     if (!m) return;
     (void)hipSetDevice(m->device);
+    if (mg_sessions* s = m->gen_cache.exchange(nullptr)) mg_sessions_free(s);
     if (m->stream) (void)hipStreamSynchronize(m->stream);
     if (m->own_stream) (void)hipStreamDestroy(m->own_stream);
     delete m;
@@ -1324,6 +1328,20 @@ int mg_model_call(mg_model* m, const int32_t* ids, int n, double* logits) {
     });
 }
 
+namespace {
+
+// A new set's state: empty norm rings, latches and K/V rings, every position 0 (on the model's stream).
+void clear_sessions(mg_sessions* s) {
+    mg_model* m = s->m;
+    HIPCHECK(launch_fill_f32(s->norm_ring.as<float>(), (long long)(s->norm_ring.n / 4), 0.0f, m->stream));
+    HIPCHECK(launch_fill_f32(s->g.as<float>(), (long long)(s->g.n / 4), 0.0f, m->stream));
+    HIPCHECK(launch_fill_f32(s->kring.as<float>(), (long long)(s->kring.n / 4), 0.0f, m->stream));
+    HIPCHECK(launch_fill_f32(s->vring.as<float>(), (long long)(s->vring.n / 4), 0.0f, m->stream));
+    HIPCHECK(launch_fill_i32(s->pos.as<int32_t>(), s->n, 0, m->stream));
+}
+
+}  // namespace
+
 int mg_sessions_create(mg_model* m, int n, int context, mg_sessions** out) {
     return guarded([&] {
         require(m && out, "mg_sessions_create: null argument");
@@ -1341,16 +1359,39 @@ int mg_sessions_create(mg_model* m, int n, int context, mg_sessions** out) {
         s->vring.ensure(std::max<size_t>(16, (size_t)m->nattn * n * m->cap * D * 4));
         s->pos.ensure((size_t)n * 4);
         s->next_ids.ensure((size_t)n * 4);
-        HIPCHECK(launch_fill_f32(s->norm_ring.as<float>(), (long long)(s->norm_ring.n / 4), 0.0f, m->stream));
-        HIPCHECK(launch_fill_f32(s->g.as<float>(), (long long)(s->g.n / 4), 0.0f, m->stream));
-        HIPCHECK(launch_fill_f32(s->kring.as<float>(), (long long)(s->kring.n / 4), 0.0f, m->stream));
-        HIPCHECK(launch_fill_f32(s->vring.as<float>(), (long long)(s->vring.n / 4), 0.0f, m->stream));
-        HIPCHECK(launch_fill_i32(s->pos.as<int32_t>(), n, 0, m->stream));
+        clear_sessions(s.get());
         HIPCHECK(hipStreamSynchronize(m->stream));
         *out = s.release();
         return MG_OK;
     });
 }
+
+extern "C++" {
+namespace mg {
+
+int generate_sessions_acquire(mg_model* m, int n, int context, mg_sessions** out) {
+    mg_sessions* s = m->gen_cache.exchange(nullptr);
+    const int window = (context > 0 && context < m->max_context) ? context : m->max_context;
+    if (s && (s->n != n || s->window != window)) {
+        mg_sessions_free(s);
+        s = nullptr;
+    }
+    if (!s) return mg_sessions_create(m, n, context, out);
+    std::unique_ptr<mg_sessions, void (*)(mg_sessions*)> hold(s, mg_sessions_free);
+    return guarded([&] {
+        Guard gd(m);
+        clear_sessions(hold.get());  // on the model's stream, ahead of the call's prefill
+        *out = hold.release();
+        return MG_OK;
+    });
+}
+
+void generate_sessions_release(mg_model* m, mg_sessions* s) {
+    if (mg_sessions* old = m->gen_cache.exchange(s)) mg_sessions_free(old);
+}
+
+}  // namespace mg
+}  // extern "C++"
 
 namespace {
 

@@ -259,10 +259,10 @@ int mg_generate_greedy(mg_model* m, mg_tokenizer* t, const char* const* prompts,
         for (int id : {t->tok->eos_id(), t->tok->user_id(), t->tok->bot_id()})
             if (id >= 0) stops.push_back(id);
         mg_sessions* ss = nullptr;
-        engine(mg_sessions_create(m, S, context, &ss));
+        engine(mg::generate_sessions_acquire(m, S, context, &ss));
         const int rc = mg_sessions_decode_greedy_until(ss, arr.data(), lens.data(), L, max_tokens, stops.data(),
                                                        (int)stops.size(), ids.data(), probs.data(), counts.data(), 0);
-        mg_sessions_free(ss);
+        mg::generate_sessions_release(m, ss);
         engine(rc);
         for (int r = 0; r < S; r++) {
             const int i = live[r], k = counts[r];
@@ -317,10 +317,10 @@ int mg_generate_sample(mg_model* m, mg_tokenizer* t, const char* const* prompts,
         for (int id : {t->tok->eos_id(), t->tok->user_id(), t->tok->bot_id()})
             if (id >= 0) stops.push_back(id);
         mg_sessions* ss = nullptr;
-        engine(mg_sessions_create(m, S, context, &ss));
+        engine(mg::generate_sessions_acquire(m, S, context, &ss));
         const int rc = mg_sessions_decode_sample(ss, arr.data(), lens.data(), L, max_tokens, &p, sd.data(), stops.data(),
                                                  (int)stops.size(), ids.data(), counts.data(), 0);
-        mg_sessions_free(ss);
+        mg::generate_sessions_release(m, ss);
         engine(rc);
         for (int r = 0; r < S; r++) {
             const int i = live[r], k = counts[r];

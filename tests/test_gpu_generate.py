@@ -73,6 +73,15 @@ def test_batched_replies_match_oracle(gpu, ref, requests_):
         _check(g, ref, q)
 
 
+def test_batches_of_one_size_in_a_row(gpu, ref, requests_):
+    """The model keeps mg_generate_*'s session set for the next call of the same size: the second batch
+    starts from cleared state, not from the first batch's."""
+    a, b = requests_[:8], requests_[8:16][::-1]
+    gpu.generate_batch(a, MAX_REPLY_TOKENS)
+    for q, g in zip(b, gpu.generate_batch(b, MAX_REPLY_TOKENS)):
+        _check(g, ref, q)
+
+
 def test_max_tokens_and_empty_batch(gpu, ref):
     got = gpu.generate_batch(["unpaid orders", REQUEST], 2)
     assert all(len(r.tokens) <= 2 for r in got)
