@@ -46,23 +46,32 @@ class Result:
 
     A batch of thousands of replies would otherwise leave several garbage-collected containers per reply
     (a dict, two lists), whose count sets off Python's cyclic collector over the whole heap several times
-    per batch; the ids and probabilities are therefore kept as the call's own numpy rows and turned into
+    per batch; the ids and probabilities are therefore kept as the call's own numpy arrays (with row
+    set: the batch's matrices, of which this reply is the first n entries of that row) and turned into
     lists when read, and the fields live in slots."""
-    __slots__ = ("text", "_ids", "_probs", "_texts")
+    __slots__ = ("text", "_ids", "_probs", "_texts", "_row", "_n")
 
-    def __init__(self, text: str, ids=(), probs=(), texts: list[str] | None = None):
+    def __init__(self, text: str, ids=(), probs=(), texts: list[str] | None = None, row: int | None = None,
+                 n: int = 0):
         self.text = text
-        self._ids = ids      # token ids: a numpy row or a sequence
-        self._probs = probs  # their probabilities (empty when sampled)
+        self._ids = ids      # token ids: a sequence, or the batch's id matrix
+        self._probs = probs  # their probabilities (empty when sampled), or the batch's matrix
         self._texts = texts
+        self._row = row
+        self._n = n
+
+    def _mine(self, a):
+        if self._row is None or not isinstance(a, np.ndarray) or a.ndim != 2:
+            return a
+        return a[self._row, :self._n]
 
     @property
     def ids(self) -> list[int]:
-        return np.asarray(self._ids, np.int64).tolist()
+        return np.asarray(self._mine(self._ids), np.int64).tolist()
 
     @property
     def probs(self) -> list[float]:
-        return np.asarray(self._probs, np.float64).tolist()
+        return np.asarray(self._mine(self._probs), np.float64).tolist()
 
     def __eq__(self, other) -> bool:
         if not isinstance(other, Result):
@@ -138,7 +147,7 @@ class Generator:
             # infer.Result.Text: strings.TrimSpace of the decoded reply (pkg/infer/infer.go:76-79)
             replies = self.tok.decode_rows(ids, counts, trim=True)
             cl = counts.tolist()
-            return [Result(replies[i], ids[i, :cl[i]], probs[i, :cl[i]], texts) for i in range(n)]
+            return [Result(replies[i], ids, probs, texts, i, cl[i]) for i in range(n)]
         sp = Sampling(temperature=temperature, rep_penalty=rep_penalty, top_p=top_p if top_p > 0 else 1.0,
                       top_k=top_k, penalize_prompt=0)
         if seeds is None:
@@ -150,4 +159,4 @@ class Generator:
                                        max_tokens, int(chat), ctypes.byref(sp), ptr(sd), ptr(ids), ptr(counts)))
         replies = self.tok.decode_rows(ids, counts, trim=chat)
         cl = counts.tolist()
-        return [Result(replies[i], ids[i, :cl[i]], (), texts) for i in range(n)]  # Tokens stay empty
+        return [Result(replies[i], ids, (), texts, i, cl[i]) for i in range(n)]  # Tokens stay empty
