@@ -33,6 +33,10 @@ cpu_baseline: the CPU restatement of the reference engine (oracle/, AVX2 dot ker
 on a bounded sample of the same workload.
 single_session_append (c5 line) and --config append: one session's Append latency beside the reference's
 published figure for that shape.
+The c5 line (the default) also carries compact objects of the other workloads measured in the same run
+(decode = c4, c1, c2, c3, score, sample, chat; --no-extras leaves them out).
+  copy          a device-to-device copy of --copy-mib MiB: the HBM counters' calibration (FETCH_SIZE and
+                WRITE_SIZE of this copy against its known size) and the practical bandwidth ceiling
 """
 from __future__ import annotations
 
@@ -50,9 +54,9 @@ sys.path.insert(0, ROOT)
 METRIC = "INT8 tokens/sec (batched forward + decode); % of int8-MFMA / HBM roofline"
 PEAK_MFMA_TOPS = 5000.0   # MI355X dense int8 MFMA, TOP/s
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, GB/s
-# What the slab GEMM's K step sustains on this part with random int8 operands (calib_mfma.hip, the runs
-# recorded in profiles/mfma_ceiling.md): the clock the part holds while every MAC switches stays below the
-# one the published peak assumes (zero operands reach 4728).
+# What the slab GEMM's K step sustains on this part with random int8 operands (a matrix-core probe whose
+# recorded runs profiles/mfma_ceiling.md holds): the clock the part holds while every MAC switches stays
+# below the one the published peak assumes (zero operands reach 4728).
 SUSTAINED_MFMA_TOPS = 3664.0
 LIMB_PLANES = 3
 # kernel classes whose int8 work runs on limb-expanded activations (the fused attention class counts its
@@ -80,8 +84,40 @@ def per_token_macs(spec):
     }
 
 
+def host_cores():
+    """Cores this process may run on (its affinity set), which on a shared box can be fewer than the
+    machine's count."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
+# Worker threads of the CPU baselines: every core this process may use, up to the 16 cores a one-GPU
+# share of the GPU box holds (its MAX_JOBS / OMP_NUM_THREADS setting).
+CPU_SHARE = 16
+
+
 def cpu_threads():
-    return max(1, min(16, os.cpu_count() or 1))
+    return max(1, min(CPU_SHARE, host_cores()))
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_fields(thr):
+    """What a CPU baseline states about the host beside its thread count."""
+    return {"cpu_model": cpu_model(), "host_cores": host_cores(), "machine_cores": os.cpu_count(),
+            "threads_note": f"{thr} worker threads: every core of this process's affinity set, capped at the "
+                            f"{CPU_SHARE}-core share of one GPU on the box"}
 
 
 def measured_traffic(config, cls):
@@ -229,7 +265,7 @@ def cpu_baseline_forward(data, spec, B, T, seconds, seed):
     nseq = int(max(min(thr, B), min(B, rate * seconds / T)))
     ids = synth_ids(seed, "cpu-sample", (nseq, T), spec.V)
     passes, dt = _repeat(lambda: om.forward_all(ids, nthreads=thr), seconds / 2)
-    return {"value": round(passes * ids.size / dt, 1), "unit": "tokens/s", "cores": thr, "kind": "port",
+    return {"value": round(passes * ids.size / dt, 1), "unit": "tokens/s", "cores": thr, **cpu_fields(thr), "kind": "port",
             "sample": f"{nseq} of {B} sequences x {T} tokens, {passes} pass(es), teacher-forced (session route: "
                       f"every position's logits), {dt:.1f} s; C++ restatement of the reference Go engine with AVX2 "
                       f"dot kernels"}
@@ -246,7 +282,8 @@ def cpu_baseline_decode(data, spec, S, P, G, seconds, seed):
     nses = int(max(min(thr, S), min(S, rate * seconds / (P + G))))
     prompts = synth_ids(seed, "cpu-sample", (nses, P), spec.V)
     passes, dt = _repeat(lambda: om.greedy(prompts, G, nthreads=thr), seconds / 2)
-    return {"value": round(passes * nses * G / dt, 1), "unit": "generated tokens/s", "cores": thr, "kind": "port",
+    return {"value": round(passes * nses * G / dt, 1), "unit": "generated tokens/s", "cores": thr, **cpu_fields(thr),
+            "kind": "port",
             "sample": f"{nses} of {S} sessions x ({P}-token prefill + {G} greedy tokens), {passes} pass(es), "
                       f"{dt:.1f} s; C++ restatement of the reference Go engine with AVX2 dot kernels"}
 
@@ -260,7 +297,7 @@ def cpu_baseline_gemm(A, W, s, seconds):
     rate = rows / max(time.perf_counter() - t0, 1e-6)
     n = int(min(len(A), max(rows, rate * seconds)))
     passes, dt = _repeat(lambda: O.gemm_i8_ref(A[:n], W, s, nthreads=thr), seconds / 2)
-    return {"value": round(passes * n / dt, 1), "unit": "rows/s", "cores": thr, "kind": "port",
+    return {"value": round(passes * n / dt, 1), "unit": "rows/s", "cores": thr, **cpu_fields(thr), "kind": "port",
             "sample": f"{n} of {len(A)} rows, {passes} pass(es), {dt:.1f} s; MatVecInt8 per row (DotInt8F32, AVX2) "
                       f"as the reference"}
 
@@ -282,7 +319,7 @@ def cpu_baseline_score(data, tokens, context, seconds):
         for _ in range(8):
             one()
     dt = time.perf_counter() - t0
-    return {"value": round(done[0] / dt, 1), "unit": "targets/s", "cores": 1, "kind": "port",
+    return {"value": round(done[0] / dt, 1), "unit": "targets/s", "cores": 1, **cpu_fields(1), "kind": "port",
             "sample": f"the first {done[0]} targets of the stream, one {context}-token window Call each (the "
                       f"reference's sequential nll.score loop), {dt:.1f} s; C++ restatement of the reference Go "
                       f"engine with AVX2 dot kernels"}
@@ -302,7 +339,7 @@ def cpu_baseline_chat(data, requests, max_tokens, seconds):
         n += 1
         gen += len(ids)
     dt = time.perf_counter() - t0
-    return {"value": round(n / dt, 1), "unit": "requests/s", "cores": 1, "kind": "port",
+    return {"value": round(n / dt, 1), "unit": "requests/s", "cores": 1, **cpu_fields(1), "kind": "port",
             "sample": f"{n} requests ({gen} generated tokens) one after another, {dt:.1f} s; the restated "
                       f"tokenizer and greedy loop over the C++ restatement of the reference Go engine"}
 
@@ -382,6 +419,28 @@ def run(args):
            "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic"}
     cpu = None
 
+    if name == "copy":
+        # The HBM counters' calibration: a device-to-device copy of a known size (rocprofv3 --pmc FETCH_SIZE,
+        # then WRITE_SIZE, over this mode gives the factor by which those counters are scaled to bytes for
+        # the engine's kernels), and the copy's own rate as the practical bandwidth ceiling.
+        n = args.copy_mib << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda")
+        src.fill_(1)
+        dst = torch.empty_like(src)
+
+        def step():
+            dst.copy_(src)
+
+        ms, wall, _ = timed(step, args.warmup, args.steps, torch)
+        gbs = 2 * n / (ms / 1e3) / 1e9
+        out.update(metric="HBM device-to-device copy (counter calibration)", value=round(gbs, 1), unit="GB/s",
+                   ms_per_step=round(ms, 4), dtype="u8",
+                   config={"workload": f"copy of {args.copy_mib} MiB, read + write bytes per second",
+                           "bytes_each_way": n})
+        out["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                           "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": 2 * n, "kernel": "copy"}
+        out["cpu_baseline"] = None
+        return out
     if name == "append":
         a = append_latency(args.seed, cpu_seconds=0 if args.no_cpu_baseline else min(args.cpu_seconds, 10.0))
         us = a["us_per_token"]
@@ -585,15 +644,50 @@ def run(args):
     return out
 
 
+# Compact objects added to the c5 line: (key, configuration)
+EXTRAS = [("decode", "c4"), ("c1", "c1"), ("c2", "c2"), ("c3", "c3"), ("score", "score"), ("sample", "sample"),
+          ("chat", "chat")]
+
+
+def compact(r):
+    """The figures of one configuration's line that the headline carries: its throughput and step time,
+    the roofline of its dominant kernel class (for a decode, also decode attention's fraction of HBM) and
+    its CPU baseline."""
+    c = {"workload": r["config"]["workload"], "value": r["value"], "unit": r["unit"], "ms_per_step": r["ms_per_step"],
+         "steps": r["steps"]}
+    roof = r.get("roofline")
+    if roof:
+        c["roofline"] = {k: roof[k] for k in ("kernel", "bound", "achieved", "unit", "frac") if k in roof}
+    path = r.get("path_roofline")
+    if path:
+        c["path_roofline_frac"] = path["frac"]
+    att = r.get("kernel_classes", {}).get("attention_step")
+    if att and "frac" in att:
+        c["decode_attention"] = {"ms_per_step": att["ms_per_step"], "bound": att["bound"], "achieved": att["achieved"],
+                                 "unit": att["unit"], "frac": att["frac"]}
+    for k in ("generated_tokens", "generated_tokens_per_s"):
+        if k in r["config"]:
+            c[k] = r["config"][k]
+    cpu = r.get("cpu_baseline")
+    if cpu:
+        c["cpu_baseline"] = {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample") if k in cpu}
+        if cpu.get("value"):
+            c["gpu_over_cpu"] = round(r["value"] / cpu["value"], 1) if not r.get("higher_is_better") is False else None
+    return c
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", default="c5", choices=["c1", "c2", "c3", "c4", "c5", "score", "chat", "sample",
-                                                       "append"])
+                                                       "append", "copy"])
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="c5 only: leave out the compact objects of the other configurations")
+    ap.add_argument("--copy-mib", type=int, default=1024, help="--config copy: bytes copied each way (MiB)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--gemm", default="auto", choices=["auto", "stream", "slab"],
                     help="limb-expanded GEMM kernel (mg_engine_option); both give identical results")
@@ -611,6 +705,15 @@ def main():
                           "n_gpus": args.gpus}))
         sys.exit(2)
     out = run(args)
+    if args.config == "c5" and not args.no_extras:
+        # every other configuration and workload from the same run, each as a compact object: c4's decode
+        # first (the metric's "+ decode"), then c1-c3, scoring, sampled decode and chat
+        for key, cfg in EXTRAS:
+            sub = argparse.Namespace(**vars(args))
+            sub.config = cfg
+            sub.cpu_seconds = args.cpu_seconds / 4
+            out[key] = compact(run(sub))
+            print(f"[bench] {key} done", file=sys.stderr, flush=True)
     print(json.dumps(out), flush=True)
 
 
