@@ -409,6 +409,7 @@ def run(args):
     engine_option("gemm", args.gemm)
     engine_option("attention", args.attention)
     engine_option("scan", args.scan)
+    engine_option("operands", args.operands)
     torch.cuda.set_device(0)
     # Everything runs on one non-default stream: the engine's launches, its HIP-event kernel timing and
     # the torch events bracketing the timed region.
@@ -640,7 +641,7 @@ def run(args):
             # the one latency figure the reference publishes for this path, measured beside the headline
             out["single_session_append"] = append_latency(args.seed, repeats=10)
     out["cpu_baseline"] = cpu
-    out["kernels"] = {"gemm": args.gemm, "attention": args.attention, "scan": args.scan}
+    out["kernels"] = {"gemm": args.gemm, "attention": args.attention, "scan": args.scan, "operands": args.operands}
     return out
 
 
@@ -693,6 +694,9 @@ def main():
                     help="limb-expanded GEMM kernel (mg_engine_option); both give identical results")
     ap.add_argument("--attention", default="auto", choices=["auto", "exact", "mfma"],
                     help="attention kernel (mg_engine_option): reference order or matrix cores")
+    ap.add_argument("--operands", default="auto", choices=["auto", "limbs", "fp32"],
+                    help="batched forward: GLU and attention outputs as limb planes written by a row pass, or read "
+                         "as fp32 by the GEMMs that take them (mg_engine_option)")
     ap.add_argument("--scan", default="auto", choices=["auto", "separate", "fused"],
                     help="latch scan and rule-input packing as two kernels or one (mg_engine_option); both "
                          "give identical results")

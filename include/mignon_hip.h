@@ -320,6 +320,12 @@ int mg_quantize_f32(const float* w, long long n, int8_t* q, float* scale, int fl
  *     256 sessions and tiles larger ones, where the model fits. The fused step's one
  *     kernel reads the ids of an mg_sessions_step call with host pointers from, and writes its outputs
  *     to, the set's pinned host buffers directly (no copies between host and device buffers).
+ *   MG_OPT_OPERANDS: MG_OPERANDS_LIMBS writes the limb planes of every GEMM operand of a batched forward
+ *     in a pass of their own; MG_OPERANDS_FP32 lets the highway GEMM read the GLU output, and the
+ *     attention's output projection the attention output, as fp32 rows (each expanded to base-256 digit
+ *     planes as it is loaded, with the row's scale from maxima its producer writes), where the weight-
+ *     stationary kernel runs them; results agree within 2e-7 of the row's largest value per operand
+ *     element. Automatic is MG_OPERANDS_FP32.
  * value < 0 only reads the option. Returns the previous value, or MG_ERR_INVALID. */
 #define MG_OPT_GEMM_KERNEL 0
 #define MG_OPT_ATTENTION_KERNEL 1
@@ -338,6 +344,9 @@ int mg_quantize_f32(const float* w, long long n, int8_t* q, float* scale, int fl
 #define MG_ATTN_EXACT 1
 #define MG_ATTN_MFMA 2
 #define MG_ATTN_FUSED 3
+#define MG_OPT_OPERANDS 5
+#define MG_OPERANDS_LIMBS 1
+#define MG_OPERANDS_FP32 2
 int mg_engine_option(int option, int value);
 
 #ifdef __cplusplus

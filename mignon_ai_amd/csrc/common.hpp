@@ -108,6 +108,40 @@ __device__ __forceinline__ void split2_pack(float2 x, float inv, uint32_t& w0, u
     w2 = __builtin_amdgcn_perm(b2[1], b2[0], 0x0c0c0400u);
 }
 
+// Base-256 digits of four consecutive elements for the GEMMs that read an fp32 operand (launch_gemm_fa).
+// With inv about 2^22/amax (limb256_scale), fma(x, inv, 1.5*2^23) rounds x*inv to the nearest integer q
+// (ties to even; |q| < 2^22) and its bit pattern is 0x4B400000 + q. The signed-byte digits of
+// q = 65536*q0 + 256*q1 + q2 are q2 = the low byte of q, q1 = byte 1 of q + 0x80 and q0 = byte 2 of
+// q + 0x8080 (so |q0| <= 64). With z = that pattern + 0x8080 - 0x400000 (byte 3 aside, q + 0x8080), q0 is
+// byte 2 of z, and bytes 1 and 0 of z are q1 and q2 with bit 7 flipped (adding 0x8000 flips bit 15 and
+// leaves bits 0-14; adding 0x80 to a byte flips its bit 7). w0 holds q0 of the four elements (element e in
+// byte e), w1 q1, w2 q2. Seventeen operations for the four elements.
+__device__ __forceinline__ void digits256_4(float4 x, float inv, uint32_t& w0, uint32_t& w1, uint32_t& w2) {
+    const float C = 12582912.0f;  // 1.5 * 2^23
+    const uint32_t z0 = __float_as_uint(fmaf(x.x, inv, C)) - 0x3F7F80u, z1 = __float_as_uint(fmaf(x.y, inv, C)) - 0x3F7F80u,
+                   z2 = __float_as_uint(fmaf(x.z, inv, C)) - 0x3F7F80u, z3 = __float_as_uint(fmaf(x.w, inv, C)) - 0x3F7F80u;
+    // v_perm_b32: selector bytes 0-3 take the second operand's bytes, 4-7 the first's, 0x0c gives zero
+    const uint32_t a01 = __builtin_amdgcn_perm(z1, z0, 0x05010400u);  // bytes 0 of z0, z1, bytes 1 of z0, z1
+    const uint32_t a23 = __builtin_amdgcn_perm(z3, z2, 0x05010400u);
+    w2 = __builtin_amdgcn_perm(a23, a01, 0x05040100u) ^ 0x80808080u;
+    w1 = __builtin_amdgcn_perm(a23, a01, 0x07060302u) ^ 0x80808080u;
+    w0 = __builtin_amdgcn_perm(z1, z0, 0x0c0c0602u) | __builtin_amdgcn_perm(z3, z2, 0x06020c0cu);
+}
+// inv of digits256_4 for a row whose largest magnitude is amax (0 for a zero row): (2^22 - 256)/amax, so
+// that |x*inv| stays below 2^22 whatever the roundings; and the row's scale 65536/inv (about amax/64) by
+// which the combined digit sums q0 + q1/256 + q2/65536 are multiplied.
+__device__ __forceinline__ void limb256_scale(float amax, float& scale, float& inv) {
+    if (amax < kTinyAmax) {
+        scale = 0.0f;
+        inv = 0.0f;
+    } else {
+        inv = 4194048.0f / amax;
+        scale = 65536.0f / inv;
+    }
+}
+constexpr float kInvLimb256_1 = 1.0f / 256.0f;
+constexpr float kInvLimb256_2 = 1.0f / 65536.0f;
+
 __device__ __forceinline__ void limb_scale(float amax, float& scale, float& inv) {
     if (amax < kTinyAmax) {
         scale = 0.0f;

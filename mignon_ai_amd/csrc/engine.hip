@@ -186,7 +186,15 @@ struct Workspace {
     long long gen = 0;  // bumped whenever the buffers below are reallocated (captured graphs hold their addresses)
     DevBuf cur, bin, nf, rinv, lam, nl, ns, xl, xs, h, hl, hs, qkv, att, stats, lse, tlog, logprob, argmax, prob, ids,
         tgt, rowmap, lens, tmp;
+    // partial row maxima of the GEMM operands read as fp32: the GLU output's per channel tile, the attention
+    // output's per head
+    DevBuf hmx, amx;
 };
+
+// Row strides (floats) of the partial-maxima buffers: at least 4 and a multiple of 4 (the fp32-operand
+// GEMM reads them as float4s).
+int hmx_ld(int Hp) { return round_up(std::max(Hp / 64, 4), 4); }
+int amx_ld(int heads) { return round_up(std::max(heads, 4), 4); }
 
 }  // namespace
 }  // namespace mg
@@ -444,12 +452,14 @@ void ws_sizes(const mg_model* m, Workspace& w, int tokens, F&& f) {
     f(w.ns, Mp * 4);
     f(w.xl, Mp * 9 * Dp);
     f(w.xs, Mp * 4);
-    f(w.h, M * Hp * 4);
+    f(w.h, Mp * Hp * 4);  // rows, or whole 16-row tiles in the fp32-operand fragment order
     f(w.hl, Mp * 3 * Hp);
     f(w.hs, Mp * 4);
+    f(w.hmx, M * hmx_ld(m->Hp) * 4);
     if (m->nattn) {
         f(w.qkv, M * 3 * D * 4);
-        f(w.att, M * Dp * 4);
+        f(w.att, Mp * Dp * 4);
+        f(w.amx, M * amx_ld(m->heads) * 4);
     }
     f(w.stats, M * (m->Vp / LX_BN) * 12);
     f(w.lse, M * 4);
@@ -540,6 +550,18 @@ void gemm(mg_model* m, int epi, const GemmArgs& g, hipStream_t s) {
     if (m->prof.on) gemm_work(m, epi, g, bytes, ops);
     ProfScope ps(m->prof, gemm_class(epi), s, bytes, ops);
     HIPCHECK(launch_gemm_lx(epi, g, s));
+}
+
+// The GEMM on an fp32 operand (launch_gemm_fa): its algorithmic bytes count the fp32 rows and their
+// partial maxima instead of limb planes.
+void gemm_fa(mg_model* m, int epi, const GemmArgs& g, hipStream_t s) {
+    double bytes = 0, ops = 0;
+    if (m->prof.on) {
+        gemm_work(m, epi, g, bytes, ops);
+        bytes += (double)g.M * (4.0 * g.Kp + 4.0 * g.amax_n - (3.0 * g.Kp + 4));
+    }
+    ProfScope ps(m->prof, gemm_class(epi), s, bytes, ops);
+    HIPCHECK(launch_gemm_fa(epi, g, s));
 }
 
 // Bytes a row-kernel launch must move: its source rows (the embedding's int8 rows and ids; cur and
@@ -666,6 +688,9 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
     // cur. The next block then reads its input from blockIn (norm and first highway), and cur is only
     // written again by that highway.
     bool in_bin = false;  // this block's input is in blockIn, and cur is stale
+    // GEMMs that read the GLU output or the attention output as fp32 rows (batched passes; decode steps
+    // keep one operand path, so that their kernels stay bit-identical to each other)
+    const bool fp32_ops = !c.step && option(OPT_OPERANDS) != 1;
     for (size_t b = 0; b < m->blocks.size(); b++) {
         const DevBlock& blk = m->blocks[b];
         const int mode = b == 0 ? ROW_EMBED : ROW_RESID;
@@ -741,23 +766,35 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                     HIPCHECK(launch_row(r, s));
                 }
             }
-            // h = GLU(x) (stream.go:214-220) in fp32, then limb-expanded with one scale per row
+            // cur = highway(cur, W2 h) (stream.go:222-229): on h as fp32 rows where the fp32-operand GEMM
+            // takes it (the GLU then also writes each row's partial maxima), else on h's limb planes
+            GemmArgs gh = lx_args(w.hl.as<int8_t>(), w.hs.as<float>(), blk.w2, 2 * Dp, Hp, M, D, blk.s2);
+            gh.bias = blk.b2; gh.cur = w.cur.as<float>(); gh.ldcur = Dp;
+            if (st == 0 && in_bin) gh.cur_in = w.bin.as<float>();
+            if (st + 1 == blk.steps && !blk.attn && fuse_next) gh.resid = w.bin.as<float>();
+            gh.Af = w.h.as<float>();
+            gh.amax = w.hmx.as<float>(); gh.amax_ld = hmx_ld(Hp); gh.amax_n = Hp / 64;
+            const bool h_fp32 = fp32_ops && gemm_fa_fits(EPI_HIGHWAY, gh);
+            // h = GLU(x) (stream.go:214-220) in fp32
             g = lx_args(w.xl.as<int8_t>(), w.xs.as<float>(), blk.w1, 2 * Hp, 3 * Dp, M, m->H, blk.s1);
             g.bias = blk.b1; g.out = w.h.as<float>(); g.ldo = Hp;
+            if (h_fp32) {
+                g.amax_out = w.hmx.as<float>(); g.amax_out_ld = hmx_ld(Hp);
+            }
             gemm(m, EPI_GLU, g, s);
-            {
+            if (h_fp32) {
+                gemm_fa(m, EPI_HIGHWAY, gh, s);
+            } else {
+                // h limb-expanded with one scale per row
                 RowArgs r;
                 r.M = M; r.D = m->H; r.Dp = Hp; r.mode = ROW_SRC; r.src = w.h.as<float>(); r.lds = Hp;
                 r.limbs = w.hl.as<int8_t>(); r.lscale = w.hs.as<float>();
-                ProfScope ps(m->prof, K_ROW, s, row_bytes(r));
-                HIPCHECK(launch_row(r, s));
+                {
+                    ProfScope ps(m->prof, K_ROW, s, row_bytes(r));
+                    HIPCHECK(launch_row(r, s));
+                }
+                gemm(m, EPI_HIGHWAY, gh, s);
             }
-            // cur = highway(cur, W2 h) (stream.go:222-229)
-            g = lx_args(w.hl.as<int8_t>(), w.hs.as<float>(), blk.w2, 2 * Dp, Hp, M, D, blk.s2);
-            g.bias = blk.b2; g.cur = w.cur.as<float>(); g.ldcur = Dp;
-            if (st == 0 && in_bin) g.cur_in = w.bin.as<float>();
-            if (st + 1 == blk.steps && !blk.attn && fuse_next) g.resid = w.bin.as<float>();
-            gemm(m, EPI_HIGHWAY, g, s);
         }
         if (blk.attn) {
             // attendPosition (internal/quant/attention.go:69-104)
@@ -771,6 +808,17 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
             qa.att = w.att.as<float>();
             const int am = option(OPT_ATTENTION_KERNEL);
             const bool fused = !c.step && !c.sess && (am == ATTN_AUTO || am == ATTN_FUSED) && qkv_attention_fits(qa);
+            // cur += W_o att (attention.go:100-103): on att as fp32 rows where the fp32-operand GEMM takes it
+            // (the fused attention then also writes each row's per-head maxima)
+            GemmArgs go = lx_args(w.nl.as<int8_t>(), w.ns.as<float>(), blk.wo, m->NpD, Dp, M, D, blk.so);
+            go.cur = w.cur.as<float>(); go.ldcur = Dp;
+            if (fuse_next) go.resid = w.bin.as<float>();
+            go.Af = w.att.as<float>();
+            go.amax = w.amx.as<float>(); go.amax_ld = amx_ld(m->heads); go.amax_n = m->heads;
+            const bool att_fp32 = fused && fp32_ops && gemm_fa_fits(EPI_RESID, go);
+            if (att_fp32) {
+                qa.amax = w.amx.as<float>(); qa.amax_ld = amx_ld(m->heads);
+            }
             GemmArgs g = lx_args(w.nl.as<int8_t>(), w.ns.as<float>(), blk.qkv, m->Np3, Dp, M, 3 * D, blk.sqkv);
             g.out = w.qkv.as<float>(); g.ldo = 3 * D;
             if (fused) {
@@ -814,11 +862,12 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                 ProfScope ps(m->prof, K_ATTN, s, (double)M * 16.0 * D);
                 HIPCHECK(launch_attention(aa, s));
             }
-            if (!att_limbs) row_call(m, M, ROW_SRC, nullptr, w.att.as<float>(), Dp, nullptr, nullptr, nullptr, true, s);
-            g = lx_args(w.nl.as<int8_t>(), w.ns.as<float>(), blk.wo, m->NpD, Dp, M, D, blk.so);
-            g.cur = w.cur.as<float>(); g.ldcur = Dp;
-            if (fuse_next) g.resid = w.bin.as<float>();
-            gemm(m, EPI_RESID, g, s);
+            if (att_fp32) {
+                gemm_fa(m, EPI_RESID, go, s);
+            } else {
+                if (!att_limbs) row_call(m, M, ROW_SRC, nullptr, w.att.as<float>(), Dp, nullptr, nullptr, nullptr, true, s);
+                gemm(m, EPI_RESID, go, s);
+            }
             ab++;
         }
         in_bin = fuse_next;

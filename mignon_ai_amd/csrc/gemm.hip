@@ -44,7 +44,11 @@ __device__ __forceinline__ void store4(float* dst, const float v[4], int nvalid_
 // bias is added with the same FMA. Token of this lane: mt0 + (L & 15); channel of (ti, r):
 // n0 + 16ti + 4*(L >> 4) + r. Kept lean: for K = 384 the epilogue's VALU work is comparable to the
 // MFMA work of the whole tile.
+// B256: the digits are base 256 (an fp32 operand expanded as it is loaded, digits256_4).
+template <bool B256 = false>
 __device__ __forceinline__ float limb_dot(const v4i (&acc)[3][8], int ti, int r) {
+    if constexpr (B256)
+        return fmaf((float)acc[2][ti][r], kInvLimb256_2, fmaf((float)acc[1][ti][r], kInvLimb256_1, (float)acc[0][ti][r]));
     return fmaf((float)acc[2][ti][r], kInvLimb2, fmaf((float)acc[1][ti][r], kInvLimb1, (float)acc[0][ti][r]));
 }
 
@@ -128,7 +132,7 @@ __device__ __forceinline__ void stg_flush(const GemmArgs& g, const float* stg, i
 
 // bias_t: the bias of this tile's 128 channels (global memory, or the workgroup's LDS copy).
 // STG: outputs of EPI_F32, EPI_LATCH, EPI_PROBS and EPI_LOGITS go through the wave's LDS region `stg`.
-template <int EPI, bool STG = false>
+template <int EPI, bool STG = false, bool B256 = false>
 __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[3][8], int mt0, int n0, int n_tile,
                                             int lane, const EpiRow& row, const float* bias_t, float* stg = nullptr) {
     const int g4 = lane >> 4;
@@ -151,10 +155,10 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
                 const float4 b = *(const float4*)(bias_t + 4 * g4 + ti * 16);
                 const float bb[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
-                for (int r = 0; r < 4; r++) v[r] = sigmoid_epi(fmaf(limb_dot(acc, ti, r), sw, bb[r]));
+                for (int r = 0; r < 4; r++) v[r] = sigmoid_epi(fmaf(limb_dot<B256>(acc, ti, r), sw, bb[r]));
             } else {
 #pragma unroll
-                for (int r = 0; r < 4; r++) v[r] = limb_dot(acc, ti, r) * sw;
+                for (int r = 0; r < 4; r++) v[r] = limb_dot<B256>(acc, ti, r) * sw;
             }
             if constexpr (STG) stg_put(stg, lane, ti, v);
             else store4(orow + n, v, nv, vec);
@@ -195,7 +199,7 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
             if (nv <= 0) continue;
             float v[4];
 #pragma unroll
-            for (int r = 0; r < 4; r++) v[r] = c[ti][r] + limb_dot(acc, ti, r) * sw;
+            for (int r = 0; r < 4; r++) v[r] = c[ti][r] + limb_dot<B256>(acc, ti, r) * sw;
             if (g.resid) {
 #pragma unroll
                 for (int r = 0; r < 4; r++) v[r] = rs[ti][r] + v[r];  // blockIn += cur (stream.go:157-163)
@@ -217,7 +221,7 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
             const float bb[4] = {b.x, b.y, b.z, b.w};
             float v[4];
 #pragma unroll
-            for (int r = 0; r < 4; r++) v[r] = __builtin_amdgcn_exp2f(fmaf(limb_dot(acc, ti, r), swl, fmaf(bb[r], l2e, -lsel)));
+            for (int r = 0; r < 4; r++) v[r] = __builtin_amdgcn_exp2f(fmaf(limb_dot<B256>(acc, ti, r), swl, fmaf(bb[r], l2e, -lsel)));
             if constexpr (STG) stg_put(stg, lane, ti, v);
             else store4(orow + n, v, nv, vec);
         }
@@ -257,6 +261,7 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
             }
         }
         float* orow = g.out + (long long)m * g.ldo;
+        float hm = 0.0f;  // EPI_GLU: the largest |h| of this lane's outputs
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             const int ch = n0 / 2 + p * 16 + 4 * g4;
@@ -268,14 +273,23 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
             float ov[4], gt[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                ov[r] = fmaf(limb_dot(acc, 2 * p, r), sw, bvv[r]);
-                gt[r] = sigmoid_epi(fmaf(limb_dot(acc, 2 * p + 1, r), sw, bgg[r]));
+                ov[r] = fmaf(limb_dot<B256>(acc, 2 * p, r), sw, bvv[r]);
+                gt[r] = sigmoid_epi(fmaf(limb_dot<B256>(acc, 2 * p + 1, r), sw, bgg[r]));
             }
             float v[4];
             if constexpr (EPI == EPI_GLU) {
 #pragma unroll
                 for (int r = 0; r < 4; r++) v[r] = ov[r] * gt[r];  // mlpHidden *= sigmoid(gate) (stream.go:218-220)
-                store4(orow + ch, v, nv, vec);
+                if (g.amax_out) {
+                    // fragment order: the four channels are consecutive there too (one 16-byte store;
+                    // padding channels hold the zeros their zero weights and bias give)
+                    *(float4*)(g.out + frag_off_f32(m, ch, g.Np >> 7)) = make_float4(v[0], v[1], v[2], v[3]);
+                } else {
+                    store4(orow + ch, v, nv, vec);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (r < nv) hm = fmaxf(hm, fabsf(v[r]));
             } else {
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
@@ -288,6 +302,14 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
                     for (int r = 0; r < 4; r++) v[r] = rs[p][r] + v[r];  // blockIn += cur (stream.go:157-163)
                 }
                 store4(wrow + ch, v, nv, cvec);
+            }
+        }
+        if constexpr (EPI == EPI_GLU) {
+            // the row's partial maximum over this tile's 64 outputs: the four lane groups of a token combine
+            if (g.amax_out) {
+                hm = fmaxf(hm, __shfl_xor(hm, 16, 64));
+                hm = fmaxf(hm, __shfl_xor(hm, 32, 64));
+                if (g4 == 0) g.amax_out[(long long)m * g.amax_out_ld + n_tile] = hm;
             }
         }
     } else if constexpr (EPI == EPI_LOGITS) {
@@ -303,7 +325,7 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
             const float4 b = *(const float4*)(bias_t + 4 * g4 + ti * 16);
             const float bb[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
-            for (int r = 0; r < 4; r++) y[ti][r] = fmaf(limb_dot(acc, ti, r), sw, bb[r]);
+            for (int r = 0; r < 4; r++) y[ti][r] = fmaf(limb_dot<B256>(acc, ti, r), sw, bb[r]);
             if constexpr (STG) {
                 if (orow || g.tgt) stg_put(stg, lane, ti, y[ti]);
             } else if (orow && mok) {
@@ -633,6 +655,183 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 // ------------------------------------------------------------------------------------------------
+// Weight-stationary GEMM on an fp32 operand
+// ------------------------------------------------------------------------------------------------
+// gemm_slab_kernel's structure (the channel slab in LDS, runs of tiles per workgroup, 8 waves, two per
+// SIMD, the same block-to-XCD mapping) with the activations read as fp32 rows, so that no separate pass
+// writes their limb planes. Lane L loads the 16 consecutive values of its token (L & 15) that make up its
+// part of a K step's fragment (columns 64k + 16(L >> 4) .. +15: four 16-byte loads, each 1 KiB contiguous
+// over the wave in the operand's fragment order) and expands them to the three base-256 digit planes (digits256_4) with the row's scale, taken from its producer's partial
+// maxima (GemmArgs::amax; lane group g loads four of them, the next tile's while the current one runs).
+//
+// Software pipeline over the K steps k of a tile: step k issues the loads of step k+2 (of this tile, or
+// the next tile's first two), expands step k+1's values, loaded one step earlier, and runs step k's MFMAs
+// on the digits expanded during step k-1; the expansion's VALU instructions are interleaved with those
+// MFMAs (they do not feed them), so one wave keeps the matrix core busy while it expands. The last step of
+// a tile expands the next tile's first step with that tile's scale. Two buffers each of values (raw) and
+// digits (dg) alternate with the parity of k: the K loop is unrolled by two.
+template <int EPI, bool ODD>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_slab_fa_kernel(GemmArgs g,
+                                                                                                      int run_tiles,
+                                                                                                      int n_runs) {
+    extern __shared__ __align__(16) int8_t slab[];
+    const int nt = g.Np / LX_BN;
+    const int slot = blockIdx.x >> 3;
+    const int n_tile = slot % nt;
+    const int run = (slot / nt) * 8 + (blockIdx.x & 7);
+    if (run >= n_runs) return;
+    const int n0 = n_tile * LX_BN;
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kc = g.Kp >> 6;  // >= 2; odd exactly when ODD
+    float* bias_s = (float*)(slab + kc * 8192);
+    {
+        const int8_t* src = g.W + (long long)(n0 >> 4) * 1024;
+        const long long wstep = (long long)(g.Np >> 4) * 1024;
+#pragma unroll 4
+        for (int c = tid; c < kc * 512; c += 512)
+            *(v4i*)(slab + ((long long)c << 4)) = *(const v4i*)(src + (c >> 9) * wstep + ((c & 511) << 4));
+        if (tid < LX_BN) bias_s[tid] = g.bias ? g.bias[n0 + tid] : 0.0f;
+    }
+    __syncthreads();
+
+    const int mtiles = (g.M + 15) >> 4;
+    const int t_begin = run * run_tiles;
+    const int t_end = min(t_begin + run_tiles, mtiles);
+    int tile = t_begin + w;
+    if (tile >= t_end) return;
+    const int8_t* wlane = slab + lane * 16;
+    const int lg = lane >> 4;
+    // this lane's part of a tile's K step 0 in the fragment-ordered operand (rows of the last tile past M
+    // hold whatever the buffer held: loaded, never stored); K step k is 1024 floats further
+    auto arow = [&](int t) -> const float* { return g.Af + ((long long)t * kc * 4 << 8) + lane * 4; };
+    // partial maxima j = 4*lg .. 4*lg + 3 of a tile's row (clamped into the row's amax_ld >= 4 entries;
+    // entries from amax_n on are masked when reduced)
+    auto amax4 = [&](int t) -> float4 {
+        const float* p = g.amax + (long long)min(t * 16 + (lane & 15), g.M - 1) * g.amax_ld + min(4 * lg, g.amax_ld - 4);
+        return *(const float4*)p;
+    };
+    auto row_scale = [&](float4 v, float& s, float& inv) {
+        const int j = 4 * lg;
+        float m = fmaxf(fmaxf(j < g.amax_n ? v.x : 0.0f, j + 1 < g.amax_n ? v.y : 0.0f),
+                        fmaxf(j + 2 < g.amax_n ? v.z : 0.0f, j + 3 < g.amax_n ? v.w : 0.0f));
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        limb256_scale(m, s, inv);
+    };
+    auto load_step = [&](f4v (&r)[4], const float* p) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) r[i] = *(const f4v*)(p + 256 * i);
+    };
+    auto expand = [&](const f4v (&r)[4], float inv, v4i (&d)[3]) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            uint32_t w0, w1, w2;
+            digits256_4(float4{r[i].x, r[i].y, r[i].z, r[i].w}, inv, w0, w1, w2);
+            d[0][i] = (int)w0;
+            d[1][i] = (int)w1;
+            d[2][i] = (int)w2;
+        }
+    };
+
+    // Entering a tile: step 0's digits in dg[0], step 1's values in raw[1].
+    f4v raw[2][4];
+    v4i dg[2][3];
+    const float* ap = arow(tile);
+    float s_cur, inv_cur;
+    row_scale(amax4(tile), s_cur, inv_cur);
+    load_step(raw[0], ap);
+    load_step(raw[1], ap + 1024);
+    expand(raw[0], inv_cur, dg[0]);
+
+    for (;;) {
+        const int next = tile + 8;
+        const bool more = next < t_end;
+        const float* np = more ? arow(next) : ap;
+        const float4 am_next = amax4(more ? next : tile);
+        float s_next = s_cur, inv_next = inv_cur;
+        v4i acc[3][8];
+        // Step k: raw[P] held step k's values (expanded at step k-1) and takes step k+2's; raw[P^1] holds
+        // step k+1's, expanded into dg[P^1] (the next tile's step 0 at the last step); MFMAs on dg[P].
+        auto step = [&](int k, auto par, auto first, auto last) {
+            constexpr int P = decltype(par)::value, Q = P ^ 1;
+            // loads of step k + 2: this tile's, or the next tile's step 0 or 1 (this tile's own again when
+            // there is no next tile: harmless, in bounds)
+            load_step(raw[P], k + 2 < kc ? ap + (k + 2) * 1024 : np + (k + 2 - kc) * 1024);
+            float iv = inv_cur;
+            if constexpr (decltype(last)::value) {
+                row_scale(am_next, s_next, inv_next);
+                iv = inv_next;
+            }
+            v4i wf[4];
+            const int8_t* wp = wlane + k * 8192;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+#pragma unroll
+                for (int ti = 0; ti < 4; ti++) wf[ti] = *(const v4i*)(wp + (4 * h + ti) * 1024);
+                // half of the expansion of step k + 1 (two of its four 16-byte groups)
+#pragma unroll
+                for (int i = 2 * h; i < 2 * h + 2; i++) {
+                    uint32_t w0, w1, w2;
+                    digits256_4(float4{raw[Q][i].x, raw[Q][i].y, raw[Q][i].z, raw[Q][i].w}, iv, w0, w1, w2);
+                    dg[Q][0][i] = (int)w0;
+                    dg[Q][1][i] = (int)w1;
+                    dg[Q][2][i] = (int)w2;
+                }
+#pragma unroll
+                for (int ti = 0; ti < 4; ti++)
+#pragma unroll
+                    for (int l = 0; l < 3; l++)
+                        acc[l][4 * h + ti] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            wf[ti], dg[P][l], decltype(first)::value ? v4i{0, 0, 0, 0} : acc[l][4 * h + ti], 0, 0, 0);
+                if (h == 0) __builtin_amdgcn_sched_group_barrier(0x020, 4, 0);  // the step's four global loads
+                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);              // four LDS weight reads
+#pragma unroll
+                for (int i = 0; i < 12; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // up to three VALU instructions
+                }
+            }
+        };
+        constexpr std::integral_constant<int, 0> P0{};
+        constexpr std::integral_constant<int, 1> P1{};
+        constexpr std::true_type YES{};
+        constexpr std::false_type NO{};
+        step(0, P0, YES, NO);
+        if constexpr (ODD) {
+            // kc = 2j + 1 >= 3: the last step is even
+            for (int k = 1; k < kc - 2; k += 2) {
+                step(k, P1, NO, NO);
+                step(k + 1, P0, NO, NO);
+            }
+            step(kc - 2, P1, NO, NO);
+            step(kc - 1, P0, NO, YES);
+        } else {
+            // kc = 2j >= 2: the last step is odd
+            for (int k = 1; k < kc - 1; k += 2) {
+                step(k, P1, NO, NO);
+                step(k + 1, P0, NO, NO);
+            }
+            step(kc - 1, P1, NO, YES);
+        }
+        EpiRow row;
+        row.s = s_cur;
+        lx_epilogue<EPI, false, true>(g, acc, tile * 16, n0, n_tile, lane, row, bias_s);
+        if (!more) break;
+        tile = next;
+        ap = np;
+        s_cur = s_next;
+        inv_cur = inv_next;
+        if constexpr (ODD) {
+            // the last (even) step expanded the next tile's step 0 into dg[1] and loaded its step 1 into raw[0]
+#pragma unroll
+            for (int l = 0; l < 3; l++) dg[0][l] = dg[1][l];
+#pragma unroll
+            for (int i = 0; i < 4; i++) raw[1][i] = raw[0][i];
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
 // Plain int8 GEMM (config 2)
 // ------------------------------------------------------------------------------------------------
 constexpr int LDSR = 80;  // LDS row stride in bytes (64 data + 16 pad)
@@ -839,6 +1038,32 @@ hipError_t launch_any_t(const GemmArgs& a, hipStream_t stream) {
     return launch_lx_t<EPI>(a, stream);
 }
 
+template <int EPI, bool ODD>
+hipError_t fa_launch(const GemmArgs& a, int grid, int lds, int run_tiles, int n_runs, hipStream_t stream) {
+    static const hipError_t attr = hipFuncSetAttribute((const void*)gemm_slab_fa_kernel<EPI, ODD>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, slab_lds_limit());
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL((gemm_slab_fa_kernel<EPI, ODD>), dim3(grid), dim3(512), lds, stream, a, run_tiles, n_runs);
+    return hipGetLastError();
+}
+
+template <int EPI>
+hipError_t launch_fa_t(const GemmArgs& a, hipStream_t stream) {
+    const int nt = a.Np / LX_BN;
+    const int mtiles = (a.M + 15) / 16;
+    if (mtiles == 0) return hipSuccess;
+    const int kc = a.Kp / 64;
+    const int lds = kc * 8192 + LX_BN * 4;
+    // the runs of launch_slab_t
+    const int groups = (mtiles + 7) / 8;
+    const int R = std::max(1, std::min(nt >= 8 ? 32 : 16, groups * nt / 512));
+    const int run_tiles = 8 * R;
+    const int n_runs = (mtiles + run_tiles - 1) / run_tiles;
+    const int grid = 8 * nt * ((n_runs + 7) / 8);
+    if (kc & 1) return fa_launch<EPI, true>(a, grid, lds, run_tiles, n_runs, stream);
+    return fa_launch<EPI, false>(a, grid, lds, run_tiles, n_runs, stream);
+}
+
 }  // namespace
 
 int slab_lds_limit() {
@@ -863,6 +1088,24 @@ hipError_t launch_gemm_lx(int epi, const GemmArgs& a, hipStream_t stream) {
         case EPI_PROBS: return launch_any_t<EPI_PROBS>(a, stream);
         default: return hipErrorInvalidValue;
     }
+}
+
+bool gemm_fa_fits(int epi, const GemmArgs& a) {
+    if (epi != EPI_HIGHWAY && epi != EPI_RESID) return false;
+    if (a.Np % LX_BN || a.Kp % 64 || a.Kp < 128 || a.M <= 0) return false;
+    if (!a.Af || !a.amax || a.amax_n < 1 || a.amax_n > 16 || a.amax_ld < 4 || a.amax_ld < a.amax_n || (a.amax_ld & 3))
+        return false;
+    if ((uintptr_t)a.Af & 15) return false;
+    if ((long long)(a.Kp / 64) * 8192 + LX_BN * 4 > slab_lds_limit()) return false;
+    const int mode = option(OPT_GEMM_KERNEL);
+    const bool many = a.M >= kSlabMinRows || (a.M >= kSlabMinRowsWideK && a.Kp >= 256);
+    return mode == GEMM_SLAB || (mode == GEMM_AUTO && many);
+}
+
+hipError_t launch_gemm_fa(int epi, const GemmArgs& a, hipStream_t stream) {
+    if (!gemm_fa_fits(epi, a)) return hipErrorInvalidValue;
+    if (epi == EPI_HIGHWAY) return launch_fa_t<EPI_HIGHWAY>(a, stream);
+    return launch_fa_t<EPI_RESID>(a, stream);
 }
 
 hipError_t launch_gemm_c2(const GemmArgs& a, hipStream_t stream) {

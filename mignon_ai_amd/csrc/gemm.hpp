@@ -31,6 +31,12 @@ __host__ __device__ inline long long frag_off_a(int m, int k, int limb, int kc) 
 __host__ __device__ inline long long frag_off_w(int n, int k, int np) {
     return ((((long long)(k >> 6) * (np >> 4)) + (n >> 4)) << 10) + (((n & 15) + 16 * ((k >> 4) & 3)) << 4) + (k & 15);
 }
+// fp32 operand in fragment order (launch_gemm_fa), [Mp/16][K/64][4][64 lanes][4 floats]: element (m, k) sits
+// where lane (m & 15) + 16*((k >> 4) & 3) reads it with its (k >> 2) & 3'th 16-byte load of K step k >> 6,
+// so each of a K step's four loads is 1 KiB contiguous over the wave. Offset in floats.
+__host__ __device__ inline long long frag_off_f32(long long m, int k, int kc) {
+    return ((((m >> 4) * kc + (k >> 6)) * 4 + ((k >> 2) & 3)) << 8) + (((m & 15) + 16 * ((k >> 4) & 3)) << 2) + (k & 3);
+}
 
 // Tile of the limb-expanded GEMM: 128 channels x 64 tokens per workgroup (4 waves x 16 tokens).
 constexpr int LX_BN = 128;
@@ -69,6 +75,18 @@ struct GemmArgs {
     const int32_t* tgt = nullptr;     // EPI_LOGITS: target id per row (or null)
     float* tlog = nullptr;            // EPI_LOGITS: target logit per row
     const float* lse = nullptr;       // EPI_PROBS: log-sum-exp per row
+    // fp32 operand (launch_gemm_fa): A is given as fp32 values Af in fragment order (frag_off_f32 with
+    // kc = Kp/64, whole 16-row tiles; padding columns meet zero weights) and expanded to digits as it is
+    // loaded, with one scale per row from the largest of the row's partial maxima amax[m * amax_ld + j],
+    // j < amax_n (each the largest |x| over a part of the row, written by the kernel that produced the row).
+    const float* Af = nullptr;
+    const float* amax = nullptr;
+    int amax_ld = 0, amax_n = 0;
+    // EPI_GLU: when set, h goes to `out` in fragment order (frag_off_f32, kc = Np/128) instead of rows, and the
+    // largest |h| of each row's 64 outputs of every channel tile to amax_out[m * amax_out_ld + tile] (the
+    // operand of a GEMM reading h as fp32)
+    float* amax_out = nullptr;
+    int amax_out_ld = 0;
 };
 
 // Values of OPT_GEMM_KERNEL.
@@ -85,5 +103,14 @@ int slab_lds_limit();
 hipError_t launch_gemm_lx(int epi, const GemmArgs& a, hipStream_t stream);
 // Plain int8 GEMM of config 2 (EPI_C2).
 hipError_t launch_gemm_c2(const GemmArgs& a, hipStream_t stream);
+
+// The weight-stationary GEMM on an fp32 operand (Af, amax: see GemmArgs) for epilogues EPI_HIGHWAY and
+// EPI_RESID: each row is expanded to three base-256 digit planes as it is loaded,
+// x ~= (amax/64)*(q0 + q1/256 + q2/65536) with x*2^22/amax rounded to an integer q below 2^22 in
+// magnitude (representation error below 1.8e-7*amax), so no separate pass writes the limb planes.
+// gemm_fa_fits: whether the shapes and the batch take it (the same batch sizes as the weight-stationary
+// kernel of launch_gemm_lx).
+bool gemm_fa_fits(int epi, const GemmArgs& a);
+hipError_t launch_gemm_fa(int epi, const GemmArgs& a, hipStream_t stream);
 
 }  // namespace mg

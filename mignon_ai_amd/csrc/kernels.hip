@@ -1176,12 +1176,35 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             case 3: attn_pv<ND, NKB, VS, 3>(o, s, inv, vlds, w, qi, kg); break;
             default: attn_pv<ND, NKB, VS, 4>(o, s, inv, vlds, w, qi, kg); break;
         }
-        // o[g][r] = out[query 16w + 4kg + r][dim 16g + qi]
+        // o[g][r] = out[query 16w + 4kg + r][dim 16g + qi]: in rows, or in the fp32-operand GEMM's fragment
+        // order when that GEMM reads it (with the per-head maxima below)
+        if (a.amax) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            float* dst = a.att + (m0 + 4 * kg + r) * a.Dp + h * DP;
+            for (int r = 0; r < 4; r++)
 #pragma unroll
-            for (int g = 0; g < ND; g++) dst[16 * g + qi] = o[g][r];
+                for (int g = 0; g < ND; g++) a.att[frag_off_f32(m0 + 4 * kg + r, h * DP + 16 * g + qi, a.Dp >> 6)] = o[g][r];
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                float* dst = a.att + (m0 + 4 * kg + r) * a.Dp + h * DP;
+#pragma unroll
+                for (int g = 0; g < ND; g++) dst[16 * g + qi] = o[g][r];
+            }
+        }
+        if (a.amax) {
+            // the head's largest |value| of each query row, for the output projection's operand scale:
+            // query 16w + 4kg + r is held by the 16 lanes qi of row kg (a DPP row), ND values each
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                float v = fabsf(o[0][r]);
+#pragma unroll
+                for (int g = 1; g < ND; g++) v = fmaxf(v, fabsf(o[g][r]));
+                v = fmaxf(v, dpp_move<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+                v = fmaxf(v, dpp_move<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+                v = fmaxf(v, dpp_move<0x141>(v));  // row_half_mirror
+                v = fmaxf(v, dpp_move<0x140>(v));  // row_mirror
+                if (qi == r) a.amax[(m0 + 4 * kg + r) * a.amax_ld + h] = v;
+            }
         }
         __syncthreads();  // every wave's keys and values are read before the next sequence's are written
     }

@@ -92,7 +92,9 @@ struct QkvAttnArgs {
     const int8_t* W = nullptr;   // QKV weights, fragment layout [Dp/64][Np3/16][1 KiB], rows q | k | v
     int Np3 = 0;
     float wscale = 1.0f;
-    float* att = nullptr;        // [B*T][Dp]
+    float* att = nullptr;        // [B*T][Dp], or with amax in the fp32-operand fragment order (frag_off_f32)
+    float* amax = nullptr;       // when set: [B*T][amax_ld], entry h = the largest |att| of the row's head h
+    int amax_ld = 0;
 };
 // Whether the fused kernel takes these shapes: 128-token sequences, head width 32 or 64, Dp of 128, 256
 // or 384, and attended spans the matrix-core attention kernel covers.

@@ -12,6 +12,9 @@ enum Option : int {
     OPT_STEP_KERNEL = 4,       // decode steps: 0 automatic, 1 layer by layer, 2 one workgroup per session
                                // (step1_kernel), 3 one workgroup per 16 sessions (tile_step_kernel),
                                // wherever the model fits them
+    OPT_OPERANDS = 5,          // batched forward: 0 automatic, 1 limb planes written by a row pass before every
+                               // GEMM, 2 the GLU output and the attention output read as fp32 by the GEMMs
+                               // that take them (expanded to digits as they are loaded), where they fit
     OPT_COUNT
 };
 

@@ -298,7 +298,7 @@ def quantize_f32(w):
 
 _OPTIONS = {"gemm": (0, ["auto", "stream", "slab"]), "attention": (1, ["auto", "exact", "mfma", "fused"]),
             "scan": (2, ["auto", "separate", "fused"]), "step_graph": (3, ["auto", "off", "on"]),
-            "step_kernel": (4, ["auto", "layered", "fused", "tiled"])}
+            "step_kernel": (4, ["auto", "layered", "fused", "tiled"]), "operands": (5, ["auto", "limbs", "fp32"])}
 
 
 def sample_logits(logits, recent=None, temperature=1.0, top_k=0, top_p=1.0, rep_penalty=1.0, u=None):
@@ -327,8 +327,10 @@ def engine_option(name: str, value: str | None = None) -> str:
     """mg_engine_option: which implementation runs for "gemm" ("auto", "stream", "slab"), "attention"
     ("auto", "exact", "mfma", "fused": the projection fused with matrix-core attention), "scan" ("auto",
     "separate", "fused"), "step_graph" (decode steps replayed from a captured HIP graph: "auto", "off",
-    "on") or "step_kernel" (decode steps: "auto", "layered", "fused": one workgroup per session, "tiled":
-    one per 16 sessions), for the whole process. Returns the previous value (value None only reads it)."""
+    "on"), "step_kernel" (decode steps: "auto", "layered", "fused": one workgroup per session, "tiled":
+    one per 16 sessions) or "operands" (batched forward: "auto", "limbs": every GEMM operand's limb planes
+    written by a pass of their own, "fp32": the GLU and attention outputs read as fp32 by the GEMMs that
+    take them), for the whole process. Returns the previous value (value None only reads it)."""
     opt, names = _OPTIONS[name]
     prev = lib().mg_engine_option(opt, -1 if value is None else names.index(value))
     check(prev if prev < 0 else 0)

@@ -67,9 +67,11 @@ def test_engine_option_validates():
     assert b"mg_engine_option" in L.mg_last_error()
     assert L.mg_engine_option(_lib.MG_OPT_GEMM_KERNEL, 3) == _lib.MG_ERR_INVALID
     assert L.mg_engine_option(_lib.MG_OPT_STEP_KERNEL, 4) == _lib.MG_ERR_INVALID
+    assert L.mg_engine_option(_lib.MG_OPT_OPERANDS, 3) == _lib.MG_ERR_INVALID
     for opt, val in ((_lib.MG_OPT_GEMM_KERNEL, _lib.MG_GEMM_SLAB), (_lib.MG_OPT_ATTENTION_KERNEL, _lib.MG_ATTN_EXACT),
                      (_lib.MG_OPT_SCAN_KERNEL, _lib.MG_SCAN_FUSED), (_lib.MG_OPT_STEP_GRAPH, _lib.MG_STEP_EAGER),
-                     (_lib.MG_OPT_STEP_KERNEL, _lib.MG_STEP_LAYERED), (_lib.MG_OPT_STEP_KERNEL, _lib.MG_STEP_TILED)):
+                     (_lib.MG_OPT_STEP_KERNEL, _lib.MG_STEP_LAYERED), (_lib.MG_OPT_STEP_KERNEL, _lib.MG_STEP_TILED),
+                     (_lib.MG_OPT_OPERANDS, _lib.MG_OPERANDS_LIMBS), (_lib.MG_OPT_OPERANDS, _lib.MG_OPERANDS_FP32)):
         prev = L.mg_engine_option(opt, val)
         assert prev in (0, 1, 2)
         assert L.mg_engine_option(opt, -1) == val

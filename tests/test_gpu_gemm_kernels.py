@@ -1,6 +1,6 @@
 """The two limb-expanded GEMM kernels (streaming and weight-stationary) accumulate the same exact int32
-sums and share one epilogue, so every model output must be bit-identical between them; both are also
-checked against the oracle. Covers ragged token counts (not multiples of 16 or 128), a single token,
+sums and share one epilogue, so every model output must be bit-identical between them (with every operand
+as limb planes); both are also checked against the oracle. Covers ragged token counts (not multiples of 16 or 128), a single token,
 K of 2..18 K steps, every epilogue (latch, GLU, highway, QKV, residual, logits, probabilities) and an
 odd vocabulary."""
 import numpy as np
@@ -14,9 +14,12 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture
 def restore_selection():
+    # both kernels on limb-plane operands: the fp32-operand GEMM (weight-stationary only) has tests of its own
     prev = engine_option("gemm", "auto")
+    prev_ops = engine_option("operands", "limbs")
     yield
     engine_option("gemm", prev)
+    engine_option("operands", prev_ops)
 
 
 def _both(m, ids, **kw):

@@ -16,9 +16,13 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture
 def restore_attention():
+    # the output projection on the attention output's limb planes in both modes (the separate kernels
+    # write no per-head maxima, so only the fused mode could take the fp32 operand)
     prev = engine_option("attention", "auto")
+    prev_ops = engine_option("operands", "limbs")
     yield
     engine_option("attention", prev)
+    engine_option("operands", prev_ops)
 
 
 def _both(data, ids, logits):

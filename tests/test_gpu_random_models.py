@@ -49,16 +49,16 @@ def test_random_model_forward_and_sessions(seed):
     what = f"seed {seed}: {spec}"
 
     # teacher-forced batch: every position of every sequence, against Call on each prefix; with the
-    # automatic kernel choice, then with the weight-stationary GEMM, the fused scan and the fused attention
-    # forced (where the shapes take them), then the streaming GEMM, the separate scan and the
-    # reference-order attention
+    # automatic kernel choice, then with the weight-stationary GEMM, the fused scan, the fused attention and
+    # the fp32 operands forced (where the shapes take them), then the streaming GEMM, the separate scan, the
+    # reference-order attention and limb-plane operands
     B, T = 3, int(rng.choice([7, 16, 33, 128]))
     ids = rng.integers(0, spec.V, (B, T)).astype(np.int32)
     ref = om.forward_all(ids)
-    combos = [None, dict(gemm="slab", scan="fused", attention="fused"),
-              dict(gemm="stream", scan="separate", attention="exact")]
+    combos = [None, dict(gemm="slab", scan="fused", attention="fused", operands="fp32"),
+              dict(gemm="stream", scan="separate", attention="exact", operands="limbs")]
     for combo in combos:
-        prev = {k: engine_option(k) for k in ("gemm", "scan", "attention")}
+        prev = {k: engine_option(k) for k in ("gemm", "scan", "attention", "operands")}
         try:
             for k, v in (combo or {}).items():
                 engine_option(k, v)
