@@ -135,8 +135,11 @@ int mg_sessions_step(mg_sessions* s, const int32_t* ids, float* logits, int32_t*
  * per GPU (held until the process ends) instead of the model's workspace. All pointers are device
  * pointers; logits, argmax and prob may be NULL. A set whose sessions need more than 64 MiB of workspace
  * (about 4300 sessions of c4's D256/H512/V4096 model, fewer for wider models) is MG_ERR_INVALID. Calls on
- * one GPU share the array: calls that overlap in time on one GPU (other streams, other models) race;
- * calls on one model's stream are ordered. The step is enqueued on the model's stream and not waited for. */
+ * one GPU share the array, so each call is ordered after the previous one on that GPU: a call enqueued on
+ * another stream (another model's) first waits on the device for the previous call's work. Under stream
+ * capture that wait is not recorded: callers capturing these calls from several streams order them
+ * themselves, or calls that overlap in time race. The step is enqueued on the model's stream and not
+ * waited for. */
 int mg_sessions_step_noalloc(mg_sessions* s, const int32_t* ids, float* logits, int32_t* argmax, double* prob);
 
 /* generate.greedyLoop for every session without stop tokens (internal/generate/greedy.go:63-87):

@@ -940,10 +940,31 @@ int guarded(F&& f) {
     }
 }
 
-// Tokens per workspace pass of a teacher-forced batch. c5's 2^21 tokens in one pass: 170.9 ms per step
-// against 172.1 in two passes of 2^20 (each kernel's ramp and tail once instead of twice), for ~44 GB of
-// workspace instead of ~22.
+// Tokens per workspace pass of a teacher-forced batch, at most. c5's 2^21 tokens in one pass: 170.9 ms per
+// step against 172.1 in two passes of 2^20 (each kernel's ramp and tail once instead of twice), for ~44 GB
+// of workspace instead of ~22.
 constexpr long long kMaxChunkTokens = 1 << 21;
+
+// Tokens per pass for this model: kMaxChunkTokens, or fewer where the device's free memory (plus what the
+// workspace already holds, which a larger one replaces) would not hold that workspace with a quarter of
+// the free memory to spare. At least 1 (a pass that cannot be allocated then fails with MG_ERR_NOMEM).
+long long pass_tokens(mg_model* m) {
+    Workspace& w = ws_of(m);
+    if (w.cap_tokens >= kMaxChunkTokens) return kMaxChunkTokens;
+    if (m->wsp) return std::max(1, w.cap_tokens);  // a borrowed workspace cannot grow
+    Workspace probe;
+    const int sample = 1 << 16;
+    const double per_token = (double)carve_ws(m, probe, sample, nullptr) / sample;
+    size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) {
+        (void)hipGetLastError();
+        return kMaxChunkTokens;
+    }
+    double held = 0;
+    ws_sizes(m, w, std::max(w.cap_tokens, 1), [&](DevBuf& b, size_t) { held += (double)b.n; });
+    const double budget = 0.75 * (double)free_b + held;
+    return std::max<long long>(1, std::min<long long>(kMaxChunkTokens, (long long)(budget / per_token)));
+}
 
 // Stop tokens of a batched decode: after each column is written, scan() marks the sessions whose token is
 // a stop token and copies the stopped count into a pinned host slot behind an event; keep_going(k) holds
@@ -1039,6 +1060,17 @@ constexpr int kMaxScratchDevices = 64;
 std::mutex g_scratch_mu;
 uint8_t* g_scratch_ptr[kMaxScratchDevices] = {};
 
+// Ordering of the allocation-free calls of one device: each model enqueues on its own stream, so a call
+// from another stream than the previous call's first waits on the device for the event that call
+// recorded (set up with the array; the mutex orders the host side).
+struct ScratchOrder {
+    std::mutex mu;
+    hipEvent_t ev = nullptr;
+    hipStream_t last = nullptr;
+    bool used = false;
+};
+ScratchOrder g_scratch_order[kMaxScratchDevices];
+
 // Resolves this device's copy of `scratch`, once per device, with that device current (mg_model_load).
 void scratch_setup(int device) {
     require(device >= 0 && device < kMaxScratchDevices, "device index beyond the scratch table");
@@ -1047,6 +1079,7 @@ void scratch_setup(int device) {
     void* p = nullptr;
     HIPCHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
     require(p != nullptr, "hipGetSymbolAddress returned no address for the scratch array");
+    HIPCHECK(hipEventCreateWithFlags(&g_scratch_order[device].ev, hipEventDisableTiming));
     g_scratch_ptr[device] = (uint8_t*)p;
 }
 
@@ -1211,7 +1244,7 @@ int mg_forward_batch(mg_model* m, const int32_t* ids, int B, int T, float* logit
         hipStream_t s = m->stream;
         const bool dev = flags & MG_PTR_DEVICE;
         const int V = m->V;
-        int chunk = (int)std::max<long long>(1, std::min<long long>(B, kMaxChunkTokens / std::max(T, 1)));
+        int chunk = (int)std::max<long long>(1, std::min<long long>(B, pass_tokens(m) / std::max(T, 1)));
         ensure_ws(m, chunk * T);
         Workspace& w = ws_of(m);
         Staging st;
@@ -1305,10 +1338,11 @@ int mg_score_sequences(mg_model* m, const int32_t* tokens, const long long* offs
         long long row_tokens = 0;
         for (const Row& r : rows) row_tokens += r.len;
         // every chunk holds at most `cap` row tokens (cap >= the longest row, so a chunk is never empty)
-        const long long cap = std::min<long long>(kMaxChunkTokens, row_tokens);
+        Guard gd(m);
+        const long long cap =
+            std::max<long long>(rows.empty() ? 1 : rows[0].len, std::min<long long>(pass_tokens(m), row_tokens));
         const size_t max_rows = std::min<size_t>(rows.size(), (size_t)cap);
 
-        Guard gd(m);
         hipStream_t s = m->stream;
         ensure_ws(m, (int)cap);
         Workspace& w = ws_of(m);
@@ -1775,7 +1809,21 @@ int mg_sessions_step_noalloc(mg_sessions* s, const int32_t* ids, float* logits, 
         HeadCombineArgs hc;
         hc.argmax = argmax;
         hc.prob = prob;
+        // after the previous allocation-free call of this device, whichever stream it was on (not under
+        // stream capture, where a wait on an event recorded outside the capture is not allowed: a caller
+        // capturing these calls orders them itself)
+        ScratchOrder& o = g_scratch_order[m->device];
+        std::lock_guard<std::mutex> lk(o.mu);
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        HIPCHECK(hipStreamIsCapturing(m->stream, &cs));
+        const bool capturing = cs != hipStreamCaptureStatusNone;
+        if (!capturing && o.used && o.last != m->stream) HIPCHECK(hipStreamWaitEvent(m->stream, o.ev, 0));
         step_device(s, ids, logits, hc, m->stream);
+        if (!capturing) {
+            HIPCHECK(hipEventRecord(o.ev, m->stream));
+            o.last = m->stream;
+            o.used = true;
+        }
         return MG_OK;
     });
 }

@@ -48,7 +48,9 @@ class Result:
     (a dict, two lists), whose count sets off Python's cyclic collector over the whole heap several times
     per batch; the ids and probabilities are therefore kept as the call's own numpy arrays (with row
     set: the batch's matrices, of which this reply is the first n entries of that row) and turned into
-    lists when read, and the fields live in slots."""
+    lists when first read, and the fields live in slots. The lists are kept once built (so edits to them
+    stay) and may be replaced by assignment; once both have been read the reply holds no reference to the
+    batch's matrices."""
     __slots__ = ("text", "_ids", "_probs", "_texts", "_row", "_n")
 
     def __init__(self, text: str, ids=(), probs=(), texts: list[str] | None = None, row: int | None = None,
@@ -67,11 +69,23 @@ class Result:
 
     @property
     def ids(self) -> list[int]:
-        return np.asarray(self._mine(self._ids), np.int64).tolist()
+        if not isinstance(self._ids, list):
+            self._ids = np.asarray(self._mine(self._ids), np.int64).tolist()
+        return self._ids
+
+    @ids.setter
+    def ids(self, v):
+        self._ids = list(v)
 
     @property
     def probs(self) -> list[float]:
-        return np.asarray(self._mine(self._probs), np.float64).tolist()
+        if not isinstance(self._probs, list):
+            self._probs = np.asarray(self._mine(self._probs), np.float64).tolist()
+        return self._probs
+
+    @probs.setter
+    def probs(self, v):
+        self._probs = list(v)
 
     def __eq__(self, other) -> bool:
         if not isinstance(other, Result):

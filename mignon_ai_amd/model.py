@@ -37,6 +37,7 @@ def read_metadata(data: bytes) -> dict:
 
 class Model:
     def __init__(self, data: bytes, max_context: int = 0):
+        self._cancel_flags = []  # every cancellation flag this model was given (set_cancel)
         buf = (ctypes.c_uint8 * len(data)).from_buffer_copy(data)
         h = ctypes.c_void_p()
         check(lib().mg_model_load(buf, len(data), int(max_context), ctypes.byref(h)))
@@ -89,9 +90,11 @@ class Model:
 
     def set_cancel(self, flag: "ctypes.c_int32 | None"):
         """mg_model_set_cancel: while flag.value is nonzero (any thread may set it), a batched decode on this
-        model stops before its next token and returns the replies produced so far. The model keeps the
-        flag alive; None removes it."""
-        self._cancel = flag
+        model stops before its next token and returns the replies produced so far. None removes it. The
+        model keeps every flag it was given alive for its own lifetime: a decode running on another thread
+        may still read the one this call replaces."""
+        if flag is not None:
+            self._cancel_flags.append(flag)
         check(lib().mg_model_set_cancel(self._h, ctypes.addressof(flag) if flag is not None else None))
 
     def profile(self, on: bool):

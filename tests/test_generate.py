@@ -152,3 +152,21 @@ def test_score_windows(orders):
     for t in (1, 3, len(ids) - 1):
         want = T.log_prob(m.call(ids[max(0, t - 4):t]), ids[t])
         assert terms[t - 1] == want
+
+
+def test_result_fields_from_batch_matrices():
+    """generate.Result over a batch's id and probability matrices (the library's batched replies): its
+    ids and probs are the row's first n entries, built once and kept, so edits persist and assignment
+    replaces them; once both are read the reply no longer refers to the matrices."""
+    import numpy as np
+    from mignon_ai_amd.generate import Result
+    ids = np.arange(12, dtype=np.int32).reshape(3, 4)
+    probs = np.linspace(0.1, 0.9, 12).reshape(3, 4)
+    r = Result("x", ids, probs, ["t%d" % i for i in range(12)], row=1, n=3)
+    assert r.ids == [4, 5, 6] and r.probs == pytest.approx(list(probs[1, :3]))
+    r.ids.append(7)
+    assert r.ids == [4, 5, 6, 7]
+    r.probs = [0.5]
+    assert r.probs == [0.5] and r.min_prob == 0.5
+    assert not isinstance(r._ids, np.ndarray) and not isinstance(r._probs, np.ndarray)
+    assert [p.text for p in Result("y", ids, probs, ["t%d" % i for i in range(12)], row=0, n=2).tokens] == ["t0", "t1"]

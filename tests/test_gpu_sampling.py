@@ -22,7 +22,9 @@ PARAMS = [  # temperature, top_k, top_p, rep_penalty
 ]
 
 
-@pytest.mark.parametrize("V", [4, 300, 301, 2048, 8192])
+# vocabulary sizes across every exponentials-kernel instantiation (4 values per thread up to 1024, 8 up to
+# 2048, 16 up to 4096, 32 above), uneven sizes inside each
+@pytest.mark.parametrize("V", [4, 300, 301, 1500, 2048, 3000, 4096, 8192])
 def test_sampler_matches_oracle(V):
     rng = np.random.default_rng(V)
     n = 24
@@ -77,11 +79,13 @@ def _replay(gm, prompts, lens, G, seeds, temp, k, p, rp, penalize, stops):
     return gen
 
 
-@pytest.mark.parametrize("params", [(1.0, 0, 1.0, 1.2, False), (0.8, 40, 0.9, 1.3, True), (0.0, 0, 1.0, 1.5, True)])
-def test_decode_sample_matches_replay(params):
+@pytest.mark.parametrize("cfg,params", [("c3", (1.0, 0, 1.0, 1.2, False)), ("c3", (0.8, 40, 0.9, 1.3, True)),
+                                        ("c3", (0.0, 0, 1.0, 1.5, True)), ("c4", (0.7, 40, 0.9, 1.2, False))])
+def test_decode_sample_matches_replay(cfg, params):
+    """c4: the benchmarked sampled workload's shape (V 4096) and parameters."""
     temp, k, p, rp, penalize = params
-    data = model_bytes("c3")
-    spec = synth.CONFIGS["c3"]["spec"]
+    data = model_bytes(cfg)
+    spec = synth.CONFIGS[cfg]["spec"]
     gm = Model(data)
     S, P, G = 12, 10, 24
     prompts = synth.token_ids(5, "sample:prompts", (S, P), spec.V)
