@@ -189,12 +189,17 @@ struct Workspace {
     // partial row maxima of the GEMM operands read as fp32: the GLU output's per channel tile, the attention
     // output's per head
     DevBuf hmx, amx;
+    // the next block's RMSNorm statistics per row and channel tile of the GEMM that wrote blockIn
+    DevBuf ssq, mxg;
 };
 
 // Row strides (floats) of the partial-maxima buffers: at least 4 and a multiple of 4 (the fp32-operand
 // GEMM reads them as float4s).
 int hmx_ld(int Hp) { return round_up(std::max(Hp / 64, 4), 4); }
 int amx_ld(int heads) { return round_up(std::max(heads, 4), 4); }
+// ... and of the RMSNorm statistics: one entry per channel tile of the highway (2*Dp/128) or out
+// projection (NpD/128) GEMM
+int stat_ld(const mg_model* m);
 
 }  // namespace
 }  // namespace mg
@@ -437,6 +442,8 @@ void build_device_model(mg_model* m, const HostModel& hm, int max_context) {
 // installs for its duration.
 Workspace& ws_of(mg_model* m) { return m->wsp ? *m->wsp : m->ws; }
 
+int stat_ld(const mg_model* m) { return round_up(std::max(std::max(2 * m->Dp, m->NpD) / LX_BN, 4), 4); }
+
 // Calls f(buffer, bytes) for every workspace buffer that `tokens` rows need.
 template <class F>
 void ws_sizes(const mg_model* m, Workspace& w, int tokens, F&& f) {
@@ -456,6 +463,8 @@ void ws_sizes(const mg_model* m, Workspace& w, int tokens, F&& f) {
     f(w.hl, Mp * 3 * Hp);
     f(w.hs, Mp * 4);
     f(w.hmx, M * hmx_ld(m->Hp) * 4);
+    f(w.ssq, M * stat_ld(m) * 4);
+    f(w.mxg, M * stat_ld(m) * 4);
     if (m->nattn) {
         f(w.qkv, M * 3 * D * 4);
         f(w.att, Mp * Dp * 4);
@@ -553,12 +562,13 @@ void gemm(mg_model* m, int epi, const GemmArgs& g, hipStream_t s) {
 }
 
 // The GEMM on an fp32 operand (launch_gemm_fa): its algorithmic bytes count the fp32 rows and their
-// partial maxima instead of limb planes.
+// partial maxima (or RMSNorm statistics, and the 1/rms written) instead of limb planes.
 void gemm_fa(mg_model* m, int epi, const GemmArgs& g, hipStream_t s) {
     double bytes = 0, ops = 0;
     if (m->prof.on) {
         gemm_work(m, epi, g, bytes, ops);
-        bytes += (double)g.M * (4.0 * g.Kp + 4.0 * g.amax_n - (3.0 * g.Kp + 4));
+        const double per_row = epi == EPI_LATCH ? 8.0 * g.stat_n + 4.0 : 4.0 * g.amax_n;
+        bytes += (double)g.M * (4.0 * g.Kp + per_row - (3.0 * g.Kp + 4));
     }
     ProfScope ps(m->prof, gemm_class(epi), s, bytes, ops);
     HIPCHECK(launch_gemm_fa(epi, g, s));
@@ -691,6 +701,35 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
     // GEMMs that read the GLU output or the attention output as fp32 rows (batched passes; decode steps
     // keep one operand path, so that their kernels stay bit-identical to each other)
     const bool fp32_ops = !c.step && option(OPT_OPERANDS) != 1;
+    const int sk = option(OPT_SCAN_KERNEL);
+    const bool many = (long long)c.B * ((Dp / 2 + 63) / 64) >= 1024;
+    auto fused_scan_at = [&](const DevBlock& blk, int st) {
+        return !c.step && scan_rule_fits(c.T, Dp, blk.dilation(st)) && (sk == 2 || (sk == 0 && many));
+    };
+    // The latch GEMM of a block whose input is in blockIn (added there by the previous block's last GEMM)
+    // reads those rows itself and normalises them as it loads them, from RMSNorm statistics that last GEMM
+    // writes, where the fp32 operands are on, the fused scan recomputes n (so n itself is never needed) and
+    // the kernel takes the shapes. Decided for every block first: the previous block's GEMM must know.
+    std::vector<char> norm_fused(m->blocks.size(), 0);
+    for (size_t b = 1; b < m->blocks.size(); b++) {
+        const DevBlock& pb = m->blocks[b - 1];
+        const DevBlock& blk = m->blocks[b];
+        const bool prev_into_bin = blk.steps > 0 && (pb.attn || pb.steps > 0);
+        if (!fp32_ops || c.sess || !prev_into_bin || !blk.gamma || !fused_scan_at(blk, 0)) continue;
+        GemmArgs t;
+        t.W = blk.wsel; t.Np = m->NpD; t.Kp = Dp; t.M = M;
+        t.Af = w.bin.as<float>(); t.lda = Dp; t.ssq = w.ssq.as<float>(); t.mxg = w.mxg.as<float>();
+        t.gamma = blk.gamma; t.rinv = w.rinv.as<float>(); t.D = D; t.stat_ld = stat_ld(m);
+        t.stat_n = (pb.attn ? m->NpD : 2 * Dp) / LX_BN;
+        norm_fused[b] = gemm_fa_fits(EPI_LATCH, t);
+    }
+    // the RMSNorm statistics a GEMM writing block b's new blockIn adds, where block b + 1 takes them
+    auto stats_for_next = [&](size_t b, GemmArgs& g) {
+        if (b + 1 < m->blocks.size() && norm_fused[b + 1]) {
+            g.ssq_out = w.ssq.as<float>(); g.mxg_out = w.mxg.as<float>();
+            g.gamma_next = m->blocks[b + 1].gamma; g.stat_ld = stat_ld(m);
+        }
+    };
     for (size_t b = 0; b < m->blocks.size(); b++) {
         const DevBlock& blk = m->blocks[b];
         const int mode = b == 0 ? ROW_EMBED : ROW_RESID;
@@ -703,24 +742,31 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
             // fused, c1's 64 separate) to cover the latency of its sequential rounds. Without a session
             // export (and with a norm) it recomputes n from the norm's source rows and 1/rms, so n is
             // never stored.
-            const int sk = option(OPT_SCAN_KERNEL);
-            const bool many = (long long)c.B * ((Dp / 2 + 63) / 64) >= 1024;
-            const bool fused_scan = !c.step && scan_rule_fits(c.T, Dp, dil) && (sk == 2 || (sk == 0 && many));
+            const bool fused_scan = fused_scan_at(blk, st);
             const bool keep_n = c.step || c.sess || !fused_scan || !blk.gamma;
             float* nout = keep_n ? w.nf.as<float>() : nullptr;
             float* rinv = keep_n ? nullptr : w.rinv.as<float>();
             // the rows the norm reads: blockIn when the previous block added its state there, else cur
             // (the embedding and the residual write both)
             const float* nsrc = (st == 0 && in_bin) ? w.bin.as<float>() : w.cur.as<float>();
-            // n = RMSNorm(cur; gamma) (stream.go:166-171), fused with the embedding / residual at step 0
-            if (st == 0 && in_bin)
-                row_call(m, M, ROW_SRC, nullptr, w.bin.as<float>(), Dp, nullptr, blk.gamma, nout, true, s, rinv);
-            else
-                row_call(m, M, st == 0 ? mode : ROW_SRC, c.ids, nullptr, 0, nullptr, blk.gamma, nout, true, s, rinv);
-            // lambda = sigmoid_clamped(n.W_sel*s + base) (stream.go:195-205)
+            // lambda = sigmoid_clamped(n.W_sel*s + base) (stream.go:195-205) on n = RMSNorm(cur; gamma)
+            // (stream.go:166-171): the norm in a row pass (fused with the embedding / residual at step 0) that
+            // writes n's limb planes, or, at a block's first step, inside the latch GEMM
             GemmArgs g = lx_args(w.nl.as<int8_t>(), w.ns.as<float>(), blk.wsel, m->NpD, Dp, M, D, blk.ssel);
             g.bias = m->latch_base; g.out = w.lam.as<float>(); g.ldo = Dp;
-            gemm(m, EPI_LATCH, g, s);
+            if (st == 0 && norm_fused[b]) {
+                const DevBlock& pb = m->blocks[b - 1];
+                g.Af = w.bin.as<float>(); g.lda = Dp; g.ssq = w.ssq.as<float>(); g.mxg = w.mxg.as<float>();
+                g.gamma = blk.gamma; g.rinv = w.rinv.as<float>(); g.D = D; g.stat_ld = stat_ld(m);
+                g.stat_n = (pb.attn ? m->NpD : 2 * Dp) / LX_BN;
+                gemm_fa(m, EPI_LATCH, g, s);
+            } else {
+                if (st == 0 && in_bin)
+                    row_call(m, M, ROW_SRC, nullptr, w.bin.as<float>(), Dp, nullptr, blk.gamma, nout, true, s, rinv);
+                else
+                    row_call(m, M, st == 0 ? mode : ROW_SRC, c.ids, nullptr, 0, nullptr, blk.gamma, nout, true, s, rinv);
+                gemm(m, EPI_LATCH, g, s);
+            }
             if (c.step) {
                 LatchStepArgs la;
                 la.S = M; la.D = D; la.Dp = Dp; la.dil = dil; la.ring = m->ring;
@@ -771,7 +817,10 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
             GemmArgs gh = lx_args(w.hl.as<int8_t>(), w.hs.as<float>(), blk.w2, 2 * Dp, Hp, M, D, blk.s2);
             gh.bias = blk.b2; gh.cur = w.cur.as<float>(); gh.ldcur = Dp;
             if (st == 0 && in_bin) gh.cur_in = w.bin.as<float>();
-            if (st + 1 == blk.steps && !blk.attn && fuse_next) gh.resid = w.bin.as<float>();
+            if (st + 1 == blk.steps && !blk.attn && fuse_next) {
+                gh.resid = w.bin.as<float>();
+                stats_for_next(b, gh);
+            }
             gh.Af = w.h.as<float>();
             gh.amax = w.hmx.as<float>(); gh.amax_ld = hmx_ld(Hp); gh.amax_n = Hp / 64;
             const bool h_fp32 = fp32_ops && gemm_fa_fits(EPI_HIGHWAY, gh);
@@ -812,7 +861,10 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
             // (the fused attention then also writes each row's per-head maxima)
             GemmArgs go = lx_args(w.nl.as<int8_t>(), w.ns.as<float>(), blk.wo, m->NpD, Dp, M, D, blk.so);
             go.cur = w.cur.as<float>(); go.ldcur = Dp;
-            if (fuse_next) go.resid = w.bin.as<float>();
+            if (fuse_next) {
+                go.resid = w.bin.as<float>();
+                stats_for_next(b, go);
+            }
             go.Af = w.att.as<float>();
             go.amax = w.amx.as<float>(); go.amax_ld = amx_ld(m->heads); go.amax_n = m->heads;
             const bool att_fp32 = fused && fp32_ops && gemm_fa_fits(EPI_RESID, go);

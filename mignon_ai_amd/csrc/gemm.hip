@@ -130,6 +130,32 @@ __device__ __forceinline__ void stg_flush(const GemmArgs& g, const float* stg, i
     __builtin_amdgcn_wave_barrier();
 }
 
+// The next block's RMSNorm statistics of four new blockIn values at channels ch.. (nv of them valid): their
+// sum of squares and their largest |v * gamma_next|, accumulated per lane.
+__device__ __forceinline__ void block_stats(const GemmArgs& g, int ch, const float v[4], int nv, float& ssq,
+                                            float& mxg) {
+    const float4 gm = *(const float4*)(g.gamma_next + ch);  // gamma is padded to a multiple of 64 columns
+    const float gg[4] = {gm.x, gm.y, gm.z, gm.w};
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        if (r < nv) {
+            ssq = fmaf(v[r], v[r], ssq);
+            mxg = fmaxf(mxg, fabsf(v[r] * gg[r]));
+        }
+    }
+}
+// A row's statistics over the tile: the four lane groups of a token combine, the first writes.
+__device__ __forceinline__ void stats_out(const GemmArgs& g, int m, int n_tile, int lane, float ssq, float mxg) {
+    ssq += __shfl_xor(ssq, 16, 64);
+    ssq += __shfl_xor(ssq, 32, 64);
+    mxg = fmaxf(mxg, __shfl_xor(mxg, 16, 64));
+    mxg = fmaxf(mxg, __shfl_xor(mxg, 32, 64));
+    if (lane < 16) {
+        g.ssq_out[(long long)m * g.stat_ld + n_tile] = ssq;
+        g.mxg_out[(long long)m * g.stat_ld + n_tile] = mxg;
+    }
+}
+
 // bias_t: the bias of this tile's 128 channels (global memory, or the workgroup's LDS copy).
 // STG: outputs of EPI_F32, EPI_LATCH, EPI_PROBS and EPI_LOGITS go through the wave's LDS region `stg`.
 template <int EPI, bool STG = false, bool B256 = false>
@@ -192,6 +218,7 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
                 }
             }
         }
+        float ssq = 0.0f, mxg = 0.0f;  // the next block's RMSNorm statistics of the new blockIn values
 #pragma unroll
         for (int ti = 0; ti < 8; ti++) {
             const int n = nb + ti * 16;
@@ -205,7 +232,9 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
                 for (int r = 0; r < 4; r++) v[r] = rs[ti][r] + v[r];  // blockIn += cur (stream.go:157-163)
             }
             store4(orow + n, v, nv, cvec);
+            if (g.ssq_out) block_stats(g, n, v, nv, ssq, mxg);
         }
+        if (g.ssq_out) stats_out(g, m, n_tile, lane, ssq, mxg);
     } else if constexpr (EPI == EPI_PROBS) {
         // p = exp(l - lse) = 2^(x.w*log2e + (b - lse)*log2e)
         if (!STG && !mok) return;
@@ -262,6 +291,7 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
         }
         float* orow = g.out + (long long)m * g.ldo;
         float hm = 0.0f;  // EPI_GLU: the largest |h| of this lane's outputs
+        float ssq = 0.0f, mxg = 0.0f;  // EPI_HIGHWAY into blockIn: the next block's RMSNorm statistics
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             const int ch = n0 / 2 + p * 16 + 4 * g4;
@@ -302,7 +332,11 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
                     for (int r = 0; r < 4; r++) v[r] = rs[p][r] + v[r];  // blockIn += cur (stream.go:157-163)
                 }
                 store4(wrow + ch, v, nv, cvec);
+                if (g.ssq_out) block_stats(g, ch, v, nv, ssq, mxg);
             }
+        }
+        if constexpr (EPI == EPI_HIGHWAY) {
+            if (g.ssq_out) stats_out(g, m, n_tile, lane, ssq, mxg);
         }
         if constexpr (EPI == EPI_GLU) {
             // the row's partial maximum over this tile's 64 outputs: the four lane groups of a token combine
@@ -654,26 +688,35 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
+// Epilogues whose outputs go through the wave's LDS staging region
+template <int EPI>
+constexpr bool can_stage() { return EPI == EPI_F32 || EPI == EPI_LATCH || EPI == EPI_PROBS || EPI == EPI_LOGITS; }
+
 // ------------------------------------------------------------------------------------------------
 // Weight-stationary GEMM on an fp32 operand
 // ------------------------------------------------------------------------------------------------
 // gemm_slab_kernel's structure (the channel slab in LDS, runs of tiles per workgroup, 8 waves, two per
-// SIMD, the same block-to-XCD mapping) with the activations read as fp32 rows, so that no separate pass
-// writes their limb planes. Lane L loads the 16 consecutive values of its token (L & 15) that make up its
-// part of a K step's fragment (columns 64k + 16(L >> 4) .. +15: four 16-byte loads, each 1 KiB contiguous
-// over the wave in the operand's fragment order) and expands them to the three base-256 digit planes (digits256_4) with the row's scale, taken from its producer's partial
-// maxima (GemmArgs::amax; lane group g loads four of them, the next tile's while the current one runs).
+// SIMD, the same block-to-XCD mapping) with the activations read as fp32, so that no separate pass writes
+// their limb planes. Lane L loads the 16 consecutive values of its token (L & 15) that make up its part of
+// a K step's fragment (columns 64k + 16(L >> 4) .. +15: four 16-byte loads, each 1 KiB contiguous over the
+// wave in the operand's fragment order; or, for ROWS, from the row itself) and expands them to the three
+// base-256 digit planes (digits256_4) with the row's scale:
+//   fragment order (EPI_HIGHWAY, EPI_RESID): the scale from the producer's partial maxima (GemmArgs::amax);
+//   ROWS (EPI_LATCH): the values are first normalised as RMSNorm does, (x * (1/rms)) * gamma, 1/rms and the
+//     scale from the previous block's partial statistics (GemmArgs::ssq, mxg), gamma from LDS.
+// Lane group g loads four of the partials, the next tile's while the current one runs.
 //
 // Software pipeline over the K steps k of a tile: step k issues the loads of step k+2 (of this tile, or
 // the next tile's first two), expands step k+1's values, loaded one step earlier, and runs step k's MFMAs
 // on the digits expanded during step k-1; the expansion's VALU instructions are interleaved with those
-// MFMAs (they do not feed them), so one wave keeps the matrix core busy while it expands. The last step of
-// a tile expands the next tile's first step with that tile's scale. Two buffers each of values (raw) and
-// digits (dg) alternate with the parity of k: the K loop is unrolled by two.
-template <int EPI, bool ODD>
+// MFMAs (they do not feed them). The last step of a tile expands the next tile's first step with that
+// tile's scale. Two buffers each of values (raw) and digits (dg) alternate with the parity of k: the K loop
+// is unrolled by two.
+template <int EPI, bool ODD, bool ROWS>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_slab_fa_kernel(GemmArgs g,
                                                                                                       int run_tiles,
                                                                                                       int n_runs) {
+    constexpr bool STG = can_stage<EPI>();
     extern __shared__ __align__(16) int8_t slab[];
     const int nt = g.Np / LX_BN;
     const int slot = blockIdx.x >> 3;
@@ -684,6 +727,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kc = g.Kp >> 6;  // >= 2; odd exactly when ODD
     float* bias_s = (float*)(slab + kc * 8192);
+    float* stg = STG ? (float*)(slab + kc * 8192 + LX_BN * 4) + w * 16 * STG_LD : nullptr;
+    float* gam_s = (float*)(slab + kc * 8192 + LX_BN * 4 + (STG ? STG_BYTES : 0));  // ROWS: gamma, Kp floats
     {
         const int8_t* src = g.W + (long long)(n0 >> 4) * 1024;
         const long long wstep = (long long)(g.Np >> 4) * 1024;
@@ -691,6 +736,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int c = tid; c < kc * 512; c += 512)
             *(v4i*)(slab + ((long long)c << 4)) = *(const v4i*)(src + (c >> 9) * wstep + ((c & 511) << 4));
         if (tid < LX_BN) bias_s[tid] = g.bias ? g.bias[n0 + tid] : 0.0f;
+        if constexpr (ROWS)
+            for (int c = tid; c < g.Kp; c += 512) gam_s[c] = g.gamma[c];
     }
     __syncthreads();
 
@@ -701,35 +748,82 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (tile >= t_end) return;
     const int8_t* wlane = slab + lane * 16;
     const int lg = lane >> 4;
-    // this lane's part of a tile's K step 0 in the fragment-ordered operand (rows of the last tile past M
-    // hold whatever the buffer held: loaded, never stored); K step k is 1024 floats further
-    auto arow = [&](int t) -> const float* { return g.Af + ((long long)t * kc * 4 << 8) + lane * 4; };
-    // partial maxima j = 4*lg .. 4*lg + 3 of a tile's row (clamped into the row's amax_ld >= 4 entries;
-    // entries from amax_n on are masked when reduced)
-    auto amax4 = [&](int t) -> float4 {
-        const float* p = g.amax + (long long)min(t * 16 + (lane & 15), g.M - 1) * g.amax_ld + min(4 * lg, g.amax_ld - 4);
-        return *(const float4*)p;
+    // ROWS: rows past M read row M - 1 (loaded, never stored). Fragment order: rows of the last tile past M
+    // hold whatever the buffer held (loaded, never stored).
+    constexpr int KSTEP = ROWS ? 64 : 1024;  // floats from one K step of this lane's values to the next
+    constexpr int ISTEP = ROWS ? 4 : 256;    // and from one of its four loads to the next
+    auto arow = [&](int t) -> const float* {
+        if constexpr (ROWS) return g.Af + (long long)min(t * 16 + (lane & 15), g.M - 1) * g.lda + 16 * lg;
+        return g.Af + ((long long)t * kc * 4 << 8) + lane * 4;
     };
-    auto row_scale = [&](float4 v, float& s, float& inv) {
-        const int j = 4 * lg;
-        float m = fmaxf(fmaxf(j < g.amax_n ? v.x : 0.0f, j + 1 < g.amax_n ? v.y : 0.0f),
-                        fmaxf(j + 2 < g.amax_n ? v.z : 0.0f, j + 3 < g.amax_n ? v.w : 0.0f));
-        m = fmaxf(m, __shfl_xor(m, 16, 64));
-        m = fmaxf(m, __shfl_xor(m, 32, 64));
-        limb256_scale(m, s, inv);
+    // four partial values j = 4*lg .. 4*lg + 3 of a tile's row from p (clamped into the row's ld >= 4
+    // entries; entries from n on are masked when reduced)
+    auto part4 = [&](const float* p, int ld, int t) -> float4 {
+        return *(const float4*)(p + (long long)min(t * 16 + (lane & 15), g.M - 1) * ld + min(4 * lg, ld - 4));
+    };
+    struct Parts {
+        float4 a, b;
+    };
+    auto parts = [&](int t) -> Parts {
+        if constexpr (ROWS) return Parts{part4(g.ssq, g.stat_ld, t), part4(g.mxg, g.stat_ld, t)};
+        return Parts{part4(g.amax, g.amax_ld, t), float4{}};
+    };
+    struct Scale {
+        float s, inv, rinv;
+    };
+    // the row's scale (and 1/rms for ROWS) from its partials; every lane of the token gets the same values
+    auto row_scale = [&](const Parts& pv) -> Scale {
+        const int j = 4 * lg, n = ROWS ? g.stat_n : g.amax_n;
+        const float4 a = pv.a;
+        float m = fmaxf(fmaxf(j < n ? a.x : 0.0f, j + 1 < n ? a.y : 0.0f), fmaxf(j + 2 < n ? a.z : 0.0f, j + 3 < n ? a.w : 0.0f));
+        Scale r;
+        r.rinv = 1.0f;
+        if constexpr (ROWS) {
+            // sum of squares: the partials in a fixed order (each lane group's four, then the groups)
+            float ss = ((j < n ? a.x : 0.0f) + (j + 1 < n ? a.y : 0.0f)) + ((j + 2 < n ? a.z : 0.0f) + (j + 3 < n ? a.w : 0.0f));
+            ss += __shfl_xor(ss, 16, 64);
+            ss += __shfl_xor(ss, 32, 64);
+            const float4 b = pv.b;
+            m = fmaxf(fmaxf(j < n ? b.x : 0.0f, j + 1 < n ? b.y : 0.0f), fmaxf(j + 2 < n ? b.z : 0.0f, j + 3 < n ? b.w : 0.0f));
+            m = fmaxf(m, __shfl_xor(m, 16, 64));
+            m = fmaxf(m, __shfl_xor(m, 32, 64));
+            // nn.RMSNormForwardF32 (internal/nn/rmsnorm.go:14-32), as the row kernel computes it
+            const float rms = (float)sqrt((double)(ss / (float)g.D + 1e-5f));
+            r.rinv = 1.0f / rms;
+            // |(x * rinv) * gamma| <= rinv * |x * gamma| up to three roundings: a bound of the largest digit
+            m = r.rinv * m * 1.000001f;
+        } else {
+            m = fmaxf(m, __shfl_xor(m, 16, 64));
+            m = fmaxf(m, __shfl_xor(m, 32, 64));
+        }
+        limb256_scale(m, r.s, r.inv);
+        return r;
     };
     auto load_step = [&](f4v (&r)[4], const float* p) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) r[i] = *(const f4v*)(p + 256 * i);
+        for (int i = 0; i < 4; i++) r[i] = *(const f4v*)(p + ISTEP * i);
     };
-    auto expand = [&](const f4v (&r)[4], float inv, v4i (&d)[3]) {
+    // digits of one K step's values (k: the step, for gamma)
+    auto expand = [&](const f4v (&r)[4], int k, const Scale& sc, v4i (&d)[3]) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
+            float4 x = float4{r[i].x, r[i].y, r[i].z, r[i].w};
+            if constexpr (ROWS) {
+                const float4 gm = *(const float4*)(gam_s + 64 * k + 16 * lg + 4 * i);
+                x = float4{(x.x * sc.rinv) * gm.x, (x.y * sc.rinv) * gm.y, (x.z * sc.rinv) * gm.z, (x.w * sc.rinv) * gm.w};
+            }
             uint32_t w0, w1, w2;
-            digits256_4(float4{r[i].x, r[i].y, r[i].z, r[i].w}, inv, w0, w1, w2);
+            digits256_4(x, sc.inv, w0, w1, w2);
             d[0][i] = (int)w0;
             d[1][i] = (int)w1;
             d[2][i] = (int)w2;
+        }
+    };
+    // ROWS: 1/rms of each row of a tile, from the first channel tile's workgroups
+    auto put_rinv = [&](int t, const Scale& sc) {
+        if constexpr (ROWS) {
+            const int m = t * 16 + (lane & 15);
+            if (n_tile == 0 && lane < 16 && m < g.M) g.rinv[m] = sc.rinv;
         }
     };
 
@@ -737,18 +831,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     f4v raw[2][4];
     v4i dg[2][3];
     const float* ap = arow(tile);
-    float s_cur, inv_cur;
-    row_scale(amax4(tile), s_cur, inv_cur);
+    Scale cur = row_scale(parts(tile));
+    put_rinv(tile, cur);
     load_step(raw[0], ap);
-    load_step(raw[1], ap + 1024);
-    expand(raw[0], inv_cur, dg[0]);
+    load_step(raw[1], ap + KSTEP);
+    expand(raw[0], 0, cur, dg[0]);
 
     for (;;) {
         const int next = tile + 8;
         const bool more = next < t_end;
         const float* np = more ? arow(next) : ap;
-        const float4 am_next = amax4(more ? next : tile);
-        float s_next = s_cur, inv_next = inv_cur;
+        const Parts pn = parts(more ? next : tile);
+        Scale nxt = cur;
         v4i acc[3][8];
         // Step k: raw[P] held step k's values (expanded at step k-1) and takes step k+2's; raw[P^1] holds
         // step k+1's, expanded into dg[P^1] (the next tile's step 0 at the last step); MFMAs on dg[P].
@@ -756,11 +850,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             constexpr int P = decltype(par)::value, Q = P ^ 1;
             // loads of step k + 2: this tile's, or the next tile's step 0 or 1 (this tile's own again when
             // there is no next tile: harmless, in bounds)
-            load_step(raw[P], k + 2 < kc ? ap + (k + 2) * 1024 : np + (k + 2 - kc) * 1024);
-            float iv = inv_cur;
+            load_step(raw[P], k + 2 < kc ? ap + (k + 2) * KSTEP : np + (k + 2 - kc) * KSTEP);
+            Scale sc = cur;
+            int kx = k + 1;
             if constexpr (decltype(last)::value) {
-                row_scale(am_next, s_next, inv_next);
-                iv = inv_next;
+                nxt = row_scale(pn);
+                sc = nxt;
+                kx = 0;
             }
             v4i wf[4];
             const int8_t* wp = wlane + k * 8192;
@@ -771,8 +867,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 // half of the expansion of step k + 1 (two of its four 16-byte groups)
 #pragma unroll
                 for (int i = 2 * h; i < 2 * h + 2; i++) {
+                    float4 x = float4{raw[Q][i].x, raw[Q][i].y, raw[Q][i].z, raw[Q][i].w};
+                    if constexpr (ROWS) {
+                        const float4 gm = *(const float4*)(gam_s + 64 * kx + 16 * lg + 4 * i);
+                        x = float4{(x.x * sc.rinv) * gm.x, (x.y * sc.rinv) * gm.y, (x.z * sc.rinv) * gm.z,
+                                   (x.w * sc.rinv) * gm.w};
+                    }
                     uint32_t w0, w1, w2;
-                    digits256_4(float4{raw[Q][i].x, raw[Q][i].y, raw[Q][i].z, raw[Q][i].w}, iv, w0, w1, w2);
+                    digits256_4(x, sc.inv, w0, w1, w2);
                     dg[Q][0][i] = (int)w0;
                     dg[Q][1][i] = (int)w1;
                     dg[Q][2][i] = (int)w2;
@@ -784,7 +886,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                         acc[l][4 * h + ti] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
                             wf[ti], dg[P][l], decltype(first)::value ? v4i{0, 0, 0, 0} : acc[l][4 * h + ti], 0, 0, 0);
                 if (h == 0) __builtin_amdgcn_sched_group_barrier(0x020, 4, 0);  // the step's four global loads
-                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);              // four LDS weight reads
+                __builtin_amdgcn_sched_group_barrier(0x100, ROWS ? 6 : 4, 0);   // LDS weight (and gamma) reads
 #pragma unroll
                 for (int i = 0; i < 12; i++) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
@@ -814,13 +916,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             step(kc - 1, P1, NO, YES);
         }
         EpiRow row;
-        row.s = s_cur;
-        lx_epilogue<EPI, false, true>(g, acc, tile * 16, n0, n_tile, lane, row, bias_s);
+        row.s = cur.s;
+        lx_epilogue<EPI, STG, true>(g, acc, tile * 16, n0, n_tile, lane, row, bias_s, stg);
         if (!more) break;
         tile = next;
         ap = np;
-        s_cur = s_next;
-        inv_cur = inv_next;
+        cur = nxt;
+        put_rinv(tile, cur);
         if constexpr (ODD) {
             // the last (even) step expanded the next tile's step 0 into dg[1] and loaded its step 1 into raw[0]
 #pragma unroll
@@ -984,8 +1086,6 @@ hipError_t slab_launch_full(int kc, const GemmArgs& a, int grid, int lds, int ru
     return slab_launch<EPI, 0, STG, 6>(a, grid, lds, run_tiles, n_runs, stream);
 }
 
-template <int EPI>
-constexpr bool can_stage() { return EPI == EPI_F32 || EPI == EPI_LATCH || EPI == EPI_PROBS || EPI == EPI_LOGITS; }
 
 template <int EPI>
 hipError_t launch_slab_t(const GemmArgs& a, hipStream_t stream) {
@@ -1038,30 +1138,37 @@ hipError_t launch_any_t(const GemmArgs& a, hipStream_t stream) {
     return launch_lx_t<EPI>(a, stream);
 }
 
-template <int EPI, bool ODD>
+template <int EPI, bool ODD, bool ROWS>
 hipError_t fa_launch(const GemmArgs& a, int grid, int lds, int run_tiles, int n_runs, hipStream_t stream) {
-    static const hipError_t attr = hipFuncSetAttribute((const void*)gemm_slab_fa_kernel<EPI, ODD>,
+    static const hipError_t attr = hipFuncSetAttribute((const void*)gemm_slab_fa_kernel<EPI, ODD, ROWS>,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, slab_lds_limit());
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((gemm_slab_fa_kernel<EPI, ODD>), dim3(grid), dim3(512), lds, stream, a, run_tiles, n_runs);
+    hipLaunchKernelGGL((gemm_slab_fa_kernel<EPI, ODD, ROWS>), dim3(grid), dim3(512), lds, stream, a, run_tiles, n_runs);
     return hipGetLastError();
 }
 
-template <int EPI>
+// LDS of the fp32-operand kernel: the slab, its bias, the output staging (epilogues that stage) and gamma
+// (normalised rows)
+int fa_lds(int epi, const GemmArgs& a) {
+    const bool stg = epi == EPI_F32 || epi == EPI_LATCH || epi == EPI_PROBS || epi == EPI_LOGITS;
+    return (a.Kp / 64) * 8192 + LX_BN * 4 + (stg ? STG_BYTES : 0) + (epi == EPI_LATCH ? a.Kp * 4 : 0);
+}
+
+template <int EPI, bool ROWS>
 hipError_t launch_fa_t(const GemmArgs& a, hipStream_t stream) {
     const int nt = a.Np / LX_BN;
     const int mtiles = (a.M + 15) / 16;
     if (mtiles == 0) return hipSuccess;
     const int kc = a.Kp / 64;
-    const int lds = kc * 8192 + LX_BN * 4;
+    const int lds = fa_lds(EPI, a);
     // the runs of launch_slab_t
     const int groups = (mtiles + 7) / 8;
     const int R = std::max(1, std::min(nt >= 8 ? 32 : 16, groups * nt / 512));
     const int run_tiles = 8 * R;
     const int n_runs = (mtiles + run_tiles - 1) / run_tiles;
     const int grid = 8 * nt * ((n_runs + 7) / 8);
-    if (kc & 1) return fa_launch<EPI, true>(a, grid, lds, run_tiles, n_runs, stream);
-    return fa_launch<EPI, false>(a, grid, lds, run_tiles, n_runs, stream);
+    if (kc & 1) return fa_launch<EPI, true, ROWS>(a, grid, lds, run_tiles, n_runs, stream);
+    return fa_launch<EPI, false, ROWS>(a, grid, lds, run_tiles, n_runs, stream);
 }
 
 }  // namespace
@@ -1091,12 +1198,15 @@ hipError_t launch_gemm_lx(int epi, const GemmArgs& a, hipStream_t stream) {
 }
 
 bool gemm_fa_fits(int epi, const GemmArgs& a) {
-    if (epi != EPI_HIGHWAY && epi != EPI_RESID) return false;
-    if (a.Np % LX_BN || a.Kp % 64 || a.Kp < 128 || a.M <= 0) return false;
-    if (!a.Af || !a.amax || a.amax_n < 1 || a.amax_n > 16 || a.amax_ld < 4 || a.amax_ld < a.amax_n || (a.amax_ld & 3))
+    if (epi != EPI_HIGHWAY && epi != EPI_RESID && epi != EPI_LATCH) return false;
+    if (a.Np % LX_BN || a.Kp % 64 || a.Kp < 128 || a.M <= 0 || !a.Af || ((uintptr_t)a.Af & 15)) return false;
+    if (epi == EPI_LATCH) {
+        if (!a.ssq || !a.mxg || !a.gamma || !a.rinv || a.D <= 0 || a.lda < a.Kp || (a.lda & 3)) return false;
+        if (a.stat_n < 1 || a.stat_n > 16 || a.stat_ld < 4 || a.stat_ld < a.stat_n || (a.stat_ld & 3)) return false;
+    } else if (!a.amax || a.amax_n < 1 || a.amax_n > 16 || a.amax_ld < 4 || a.amax_ld < a.amax_n || (a.amax_ld & 3)) {
         return false;
-    if ((uintptr_t)a.Af & 15) return false;
-    if ((long long)(a.Kp / 64) * 8192 + LX_BN * 4 > slab_lds_limit()) return false;
+    }
+    if (fa_lds(epi, a) > slab_lds_limit()) return false;
     const int mode = option(OPT_GEMM_KERNEL);
     const bool many = a.M >= kSlabMinRows || (a.M >= kSlabMinRowsWideK && a.Kp >= 256);
     return mode == GEMM_SLAB || (mode == GEMM_AUTO && many);
@@ -1104,8 +1214,9 @@ bool gemm_fa_fits(int epi, const GemmArgs& a) {
 
 hipError_t launch_gemm_fa(int epi, const GemmArgs& a, hipStream_t stream) {
     if (!gemm_fa_fits(epi, a)) return hipErrorInvalidValue;
-    if (epi == EPI_HIGHWAY) return launch_fa_t<EPI_HIGHWAY>(a, stream);
-    return launch_fa_t<EPI_RESID>(a, stream);
+    if (epi == EPI_HIGHWAY) return launch_fa_t<EPI_HIGHWAY, false>(a, stream);
+    if (epi == EPI_LATCH) return launch_fa_t<EPI_LATCH, true>(a, stream);
+    return launch_fa_t<EPI_RESID, false>(a, stream);
 }
 
 hipError_t launch_gemm_c2(const GemmArgs& a, hipStream_t stream) {

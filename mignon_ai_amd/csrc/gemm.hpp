@@ -87,6 +87,21 @@ struct GemmArgs {
     // operand of a GEMM reading h as fp32)
     float* amax_out = nullptr;
     int amax_out_ld = 0;
+    // RMSNorm statistics between blocks, [m * stat_ld + tile] per row and channel tile. Producer (EPI_HIGHWAY
+    // or EPI_RESID with resid, when ssq_out is set): the sum of squares of the row's new blockIn values in
+    // the tile (ssq_out) and their largest |v * gamma_next[channel]| (mxg_out). Consumer (launch_gemm_fa with
+    // EPI_LATCH on rows): A = RMSNorm(Af rows; gamma) is formed as the rows are loaded (row stride lda
+    // floats), 1/rms from the sum of the row's stat_n partial sums of squares over D channels, the digits'
+    // scale from 1/rms times the largest partial maximum; 1/rms of each row is written to rinv.
+    float* ssq_out = nullptr;
+    float* mxg_out = nullptr;
+    const float* gamma_next = nullptr;
+    const float* ssq = nullptr;
+    const float* mxg = nullptr;
+    const float* gamma = nullptr;
+    int stat_ld = 0, stat_n = 0, D = 0;
+    long long lda = 0;
+    float* rinv = nullptr;
 };
 
 // Values of OPT_GEMM_KERNEL.
@@ -104,8 +119,9 @@ hipError_t launch_gemm_lx(int epi, const GemmArgs& a, hipStream_t stream);
 // Plain int8 GEMM of config 2 (EPI_C2).
 hipError_t launch_gemm_c2(const GemmArgs& a, hipStream_t stream);
 
-// The weight-stationary GEMM on an fp32 operand (Af, amax: see GemmArgs) for epilogues EPI_HIGHWAY and
-// EPI_RESID: each row is expanded to three base-256 digit planes as it is loaded,
+// The weight-stationary GEMM on an fp32 operand for epilogues EPI_HIGHWAY and EPI_RESID (Af in fragment
+// order, amax: see GemmArgs) and EPI_LATCH (Af rows normalised as loaded: ssq, mxg, gamma, rinv): each row
+// is expanded to three base-256 digit planes as it is loaded,
 // x ~= (amax/64)*(q0 + q1/256 + q2/65536) with x*2^22/amax rounded to an integer q below 2^22 in
 // magnitude (representation error below 1.8e-7*amax), so no separate pass writes the limb planes.
 // gemm_fa_fits: whether the shapes and the batch take it (the same batch sizes as the weight-stationary

@@ -11,7 +11,9 @@ launch counts show that the fp32 path ran (the row passes of h and of the attent
 Shapes: c5 (highway K 1024 in 16 K steps, output projection K 384 over six 64-wide heads), c3 (four heads of
 32, K 256), c1 (no attention, two rule steps), ragged token counts (rows past the batch in the last tile),
 the reference's trained orders.mgn (hidden size 160: the GLU output's padding columns meet zero weights;
-24-wide heads, so its attention output keeps the row pass), and an untied head with an odd vocabulary."""
+24-wide heads, so its attention output keeps the row pass), and an untied head with an odd vocabulary.
+With the fused scan, the RMSNorm before each later block's latch GEMM happens inside that GEMM (from
+statistics the previous block's last GEMM writes) and its row pass is gone too."""
 import numpy as np
 import pytest
 
@@ -23,11 +25,14 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture
 def slab_forced():
-    # small batches take the weight-stationary kernels (and with them the fp32 operands) only when forced
+    # small batches take the weight-stationary kernels (and with them the fp32 operands) and the fused scan
+    # (which the RMSNorm inside the latch GEMM needs) only when forced
     prev = engine_option("gemm", "slab")
+    prev_scan = engine_option("scan", "fused")
     prev_ops = engine_option("operands")
     yield
     engine_option("gemm", prev)
+    engine_option("scan", prev_scan)
     engine_option("operands", prev_ops)
 
 
@@ -44,15 +49,19 @@ def _run(data, ids, **kw):
     return out, rows
 
 
-def removed_passes(D, H, heads, steps, nattn, T):
+def removed_passes(D, H, heads, steps, nattn, T, chained=0):
     """Row passes the fp32 operands take away from one forward: h's per rule step when its padded width
     (a multiple of 64) is at least 128 (two K steps) and has at most 16 channel tiles of partial maxima; the
     attention output's per attention block where the fused attention runs (128-token sequences, heads of
-    32 or 64) and the padded state is at least 128 wide."""
+    32 or 64) and the padded state is at least 128 wide; and the RMSNorm before the latch GEMM of each of
+    the `chained` blocks whose input the previous block added into blockIn, where the fused scan runs
+    (sequence lengths a multiple of 16) and the padded state is at least 128 wide."""
     Hp, Dp = -(-H // 64) * 64, -(-D // 64) * 64
     n = steps if 128 <= Hp <= 1024 else 0
     if nattn and T == 128 and D // heads in (32, 64) and 128 <= Dp <= 384:
         n += nattn
+    if T % 16 == 0 and Dp >= 128:
+        n += chained
     return n
 
 
@@ -79,8 +88,10 @@ def _check(data, ids, removed, n_oracle=1, **kw):
 
 
 def _removed(spec, T):
+    chained = sum(1 for i in range(1, len(spec.blocks))
+                  if spec.blocks[i].steps > 0 and (spec.heads > 0 or spec.blocks[i - 1].steps > 0))
     return removed_passes(spec.D, spec.H, spec.heads, sum(b.steps for b in spec.blocks),
-                          len(spec.blocks) if spec.heads else 0, T)
+                          len(spec.blocks) if spec.heads else 0, T, chained)
 
 
 @pytest.mark.parametrize("cfg,shape", [("c5", (3, 128)), ("c3", (5, 128)), ("c3", (2, 61)), ("c1", (3, 37))])
@@ -98,7 +109,7 @@ def test_fp32_operands_real_model(slab_forced):
     with open(f"{GOLDEN}/orders.mgn", "rb") as f:
         data = f.read()
     ids = synth.token_ids(42, "fp32ops:orders", (3, 128), 2048)
-    _check(data, ids, removed_passes(96, 160, 4, 2, 2, 128), n_oracle=2, probs=True)
+    _check(data, ids, removed_passes(96, 160, 4, 2, 2, 128, 1), n_oracle=2, probs=True)
 
 
 def test_fp32_operands_untied_no_attention(slab_forced):
