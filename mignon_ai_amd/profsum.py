@@ -13,6 +13,10 @@
         run: the average shader clock over the dispatch (GPU-active cycles per XCD over the dispatch's
         duration) and the fraction of SIMD cycles the matrix core and the VALU were busy
 
+    python -m mignon_ai_amd.profsum memory OUT.md CMD  PASS.csv [...] AGENT_INFO.csv
+        per kernel from the `rocprofv3 --pmc` runs of MEMORY_PASSES (one run each): shader clock, matrix-core
+        busy and VALU co-execution, L2 and address-unit busy, L2 hit rate, L1-to-L2 read traffic and latency
+
 CMD is the command line that produced the files, recorded in the summary.
 """
 from __future__ import annotations
@@ -194,17 +198,85 @@ def clock_for(path: str, cls: str) -> dict | None:
     return best
 
 
+# memory mode: the counters of its passes (one rocprofv3 --pmc run each)
+MEMORY_PASSES = [
+    "TA_BUSY_avr TCP_TCC_READ_REQ_sum TCP_TCC_READ_REQ_LATENCY_sum",
+    "TCC_HIT_sum TCC_MISS_sum TCC_BUSY_avr",
+    "SQ_VALU_MFMA_BUSY_CYCLES SQ_VALU_MFMA_COEXEC_CYCLES GRBM_GUI_ACTIVE",
+]
+
+
+def memory(out: str, cmd: str, paths: list[str], agent_path: str) -> None:
+    """Per kernel, from the memory passes' CSVs: shader clock, matrix-core busy and how much of it had a VALU
+    instruction co-executing, L2 (TCC) busy, address unit (TA) busy, L2 hit rate, L1-to-L2 read requests
+    (128 bytes each) and their mean latency."""
+    gpu = [a for a in csv.DictReader(open(agent_path)) if a["Agent_Type"] == "GPU"][0]
+    nxcc, simds = int(gpu["Num_Xcc"]), int(gpu["Simd_Count"])
+    acc = defaultdict(lambda: defaultdict(float))
+    for p in paths:
+        per = defaultdict(dict)
+        names = {}
+        for r in csv.DictReader(open(p)):
+            d = r["Dispatch_Id"]
+            per[d][r["Counter_Name"]] = per[d].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+            per[d]["ns"] = float(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+            names[d] = _short(r["Kernel_Name"])
+        for d, v in per.items():
+            k = acc[names[d]]
+            for c, x in v.items():
+                if c == "ns":
+                    k["ns"] += x
+                    k["n"] += 1
+                else:
+                    k[c] += x
+    lines = [f"Command (from the repository root, one MI355X):", "", "```", cmd, "```", "",
+             f"Per kernel (dispatches of all passes; counters averaged per dispatch): shader clock from "
+             f"GRBM_GUI_ACTIVE per XCD ({nxcc} XCDs); matrix core busy = SQ_VALU_MFMA_BUSY_CYCLES over the "
+             f"{simds} SIMDs' cycles, and the share of those cycles with a VALU instruction co-executing "
+             "(SQ_VALU_MFMA_COEXEC_CYCLES); L2 busy = TCC_BUSY_avr and address unit busy = TA_BUSY_avr over "
+             "the XCD cycles; L2 hit rate from TCC_HIT/TCC_MISS; L1-to-L2 read requests (128 bytes each) "
+             "per dispatch in GB and their mean latency in cycles (TCP_TCC_READ_REQ_LATENCY over "
+             "TCP_TCC_READ_REQ). Kernels with at least 0.5% of the run's kernel time.", "",
+             "| kernel | avg ms | clock GHz | matrix busy | co-exec | L2 busy | TA busy | L2 hit | L1→L2 GB | latency |",
+             "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    total_ns = sum(v["ns"] for v in acc.values())
+    for k, v in sorted(acc.items(), key=lambda kv: -kv[1]["ns"]):
+        n = v["n"]
+        if n == 0 or v["ns"] < 0.005 * total_ns:
+            continue
+        ms = v["ns"] / n / 1e6
+        npass = len(paths)
+        per_pass = n / npass  # dispatches of this kernel per pass
+        cyc = v["GRBM_GUI_ACTIVE"] / per_pass / nxcc if v.get("GRBM_GUI_ACTIVE") else 0.0
+        if cyc <= 0:
+            continue
+        mf = v.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / per_pass / (cyc * simds)
+        co = v.get("SQ_VALU_MFMA_COEXEC_CYCLES", 0.0) / max(v.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0), 1.0)
+        l2 = v.get("TCC_BUSY_avr", 0.0) / per_pass / cyc
+        ta = v.get("TA_BUSY_avr", 0.0) / per_pass / cyc
+        hits, miss = v.get("TCC_HIT_sum", 0.0), v.get("TCC_MISS_sum", 0.0)
+        req = v.get("TCP_TCC_READ_REQ_sum", 0.0) / per_pass
+        lat = v.get("TCP_TCC_READ_REQ_LATENCY_sum", 0.0) / max(v.get("TCP_TCC_READ_REQ_sum", 0.0), 1.0)
+        lines.append(f"| `{k}` | {ms:.3f} | {cyc / (ms * 1e-3) / 1e9:.2f} | {100 * mf:.1f}% | {100 * co:.0f}% | "
+                     f"{100 * l2:.0f}% | {100 * ta:.0f}% | {100 * hits / max(hits + miss, 1.0):.0f}% | "
+                     f"{req * 128 / 1e9:.2f} | {lat:.0f} |")
+    _write(out, lines)
+
+
 def _write(out: str, lines: list[str]) -> None:
     with open(out, "w") as f:
         f.write("\n".join(lines) + "\n")
 
 
 def main(argv: list[str]) -> None:
-    if len(argv) < 4 or argv[0] not in ("stats", "pmc", "clock"):
+    if len(argv) < 4 or argv[0] not in ("stats", "pmc", "clock", "memory"):
         raise SystemExit(__doc__)
     mode, out, cmd, rest = argv[0], argv[1], argv[2], argv[3:]
     if mode == "stats":
         stats(out, cmd, rest[0])
+        return
+    if mode == "memory":
+        memory(out, cmd, rest[:-1], rest[-1])
         return
     if mode == "clock":
         clock(out, cmd, rest[0], rest[1])
