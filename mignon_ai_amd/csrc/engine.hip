@@ -1740,7 +1740,11 @@ void step_graphed(mg_sessions* s, const int32_t* ids_d, float* logits_d, const H
     mg_model* m = s->m;
     const int mode = option(OPT_STEP_GRAPH);
     auto& G = s->graph;
-    if (mode == 1 || m->prof.on || G.failed) {
+    // A step that is one kernel (the single-workgroup step, outside a batched decode) is launched directly
+    // unless graphs are forced: a graph launch costs more than the one kernel launch it would replace.
+    Step1Args one;
+    const bool one_kernel = mode == 0 && !hc.col && !hc.lse && !hc.logprob && step1_args(s, ids_d, logits_d, hc, one);
+    if (mode == 1 || m->prof.on || G.failed || one_kernel) {
         step_device(s, ids_d, logits_d, hc, st);
         return;
     }

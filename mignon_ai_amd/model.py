@@ -255,6 +255,11 @@ class Session:
     def __init__(self, model: Model, context_size: int = 0):
         self._s = Sessions(model, 1, context_size)
         self.V = model.vocab_size()
+        # Append's host buffers and their addresses, kept across calls (the call is latency-bound)
+        self._ids = np.empty(1, np.int32)
+        self._lg = np.empty((1, self.V), np.float32)
+        self._ptrs = (ptr(self._ids), ptr(self._lg))
+        self._step = lib().mg_sessions_step
 
     def prefill(self, tokens):
         tokens = _i32(tokens)
@@ -264,8 +269,9 @@ class Session:
         return lg[0].astype(np.float64)
 
     def append(self, token):
-        lg, _, _ = self._s.step(np.array([token], np.int32))
-        return lg[0].astype(np.float64)
+        self._ids[0] = token
+        check(self._step(self._s._h, self._ptrs[0], self._ptrs[1], None, None, 0))
+        return self._lg[0].astype(np.float64)
 
     def state_bytes(self) -> int:
         return self._s.state_bytes()
