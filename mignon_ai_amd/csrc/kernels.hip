@@ -1761,7 +1761,9 @@ __device__ __forceinline__ float s1_rms_inv(const float* x, int D, int lane) {
     return 1.0f / rms;
 }
 
-// Workgroup maximum of per-thread values (every thread gets it). red: 8 floats of LDS.
+// Workgroup maximum of per-thread values (every thread gets it). red: 8 floats of LDS, read after the one
+// barrier here; consecutive reductions alternate between two such buffers, so that a reduction's writes
+// never meet the previous one's reads (the barrier of the reduction between them orders the two).
 __device__ __forceinline__ float s1_block_max(float v, float* red, int lane, int w) {
     v = wave_max(v);
     if (lane == 0) red[w] = v;
@@ -1769,7 +1771,6 @@ __device__ __forceinline__ float s1_block_max(float v, float* red, int lane, int
     float m = red[0];
 #pragma unroll
     for (int i = 1; i < S1_THREADS / 64; i++) m = fmaxf(m, red[i]);
-    lds_barrier();  // red is reused by the next reduction
     return m;
 }
 
@@ -1908,6 +1909,12 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
     const int rkf = (rk_lds_floats(a.cap, DH) + 3) & ~3;  // per head, 16-byte aligned
     int8_t* xl = (int8_t*)(rk + a.heads * rkf);
     if (a.done && a.done[s_] >= 0) return;  // a finished session of a batched decode
+    // the two halves of red, alternating between consecutive workgroup reductions (s1_block_max)
+    int red_half = 0;
+    auto next_red = [&]() {
+        red_half ^= 1;
+        return red + 8 * red_half;
+    };
     const int pos = a.pos[s_];
     {
         int id = a.ids[s_];
@@ -1947,8 +1954,8 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
             } else {
                 for (int d = tid; d < Dp; d += S1_THREADS) nrm[d] = d < D ? cur[d] : 0.0f;
             }
-            lds_barrier();
-            const float sn = s1_limbs(nrm, D, Dp, xl, red, tid, lane, w);
+            // (no barrier: s1_limbs reads element d of nrm in the thread that wrote it)
+            const float sn = s1_limbs(nrm, D, Dp, xl, next_red(), tid, lane, w);
             lds_barrier();
             // lambda = sigmoid_clamped(n.W_sel*s + base) (stream.go:195-205)
             {
@@ -1980,7 +1987,7 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
                 ring[(long long)(pos % a.ring) * Dp + d] = nv;
                 if (pos >= dil) lv = ring[(long long)((pos - dil) % a.ring) * Dp + d];
             }
-            const float amax = s1_block_max(fmaxf(fabsf(nv), fmaxf(fabsf(lv), fabsf(gv))), red, lane, w);
+            const float amax = s1_block_max(fmaxf(fabsf(nv), fmaxf(fabsf(lv), fabsf(gv))), next_red(), lane, w);
             float sx, ix;
             limb_scale(amax, sx, ix);
             {
@@ -2015,7 +2022,7 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
                 });
             }
             lds_barrier();
-            const float sh = s1_limbs(hbuf, H, Hp, xl, red, tid, lane, w);
+            const float sh = s1_limbs(hbuf, H, Hp, xl, next_red(), tid, lane, w);
             lds_barrier();
             // cur = highway(cur, W2 h) (stream.go:222-229)
             {
@@ -2051,8 +2058,7 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
                 const float inv = bcast[0];
                 for (int d = tid; d < Dp; d += S1_THREADS) nrm[d] = d < D ? (cur[d] * inv) * ldg(B.anorm + d) : 0.0f;
             }
-            lds_barrier();
-            const float sa = s1_limbs(nrm, D, Dp, xl, red, tid, lane, w);
+            const float sa = s1_limbs(nrm, D, Dp, xl, next_red(), tid, lane, w);
             lds_barrier();
             {
                 const float sw = sa * B.sqkv;
@@ -2078,7 +2084,7 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
                 if (lane < DH) att[w * DH + lane] = o;
             }
             lds_barrier();
-            const float so_ = s1_limbs(att, D, Dp, xl, red, tid, lane, w);
+            const float so_ = s1_limbs(att, D, Dp, xl, next_red(), tid, lane, w);
             lds_barrier();
             {
                 const float sw = so_ * B.so;
@@ -2107,8 +2113,7 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
     } else {
         for (int d = tid; d < Dp; d += S1_THREADS) nrm[d] = d < D ? cur[d] : 0.0f;
     }
-    lds_barrier();
-    const float sf = s1_limbs(nrm, D, Dp, xl, red, tid, lane, w);
+    const float sf = s1_limbs(nrm, D, Dp, xl, next_red(), tid, lane, w);
     lds_barrier();
     {
         const float sw = sf * a.head_scale;
