@@ -34,7 +34,7 @@ on a bounded sample of the same workload.
 single_session_append (c5 line) and --config append: one session's Append latency beside the reference's
 published figure for that shape.
 The c5 line (the default) also carries compact objects of the other workloads measured in the same run
-(decode = c4, c1, c2, c3, score, sample, chat; --no-extras leaves them out).
+(decode = c4, c1, c2, c3, score, sample, chat; --no-extras leaves them and single_session_append out).
   copy          a device-to-device copy of --copy-mib MiB: the HBM counters' calibration (FETCH_SIZE and
                 WRITE_SIZE of this copy against its known size) and the practical bandwidth ceiling
 """
@@ -637,7 +637,7 @@ def run(args):
                                         "GEMM; the probability head's recompute not counted)"}
         out["kernel_classes"] = class_table(work, args.steps)
         out["wall_s"] = round(wall, 3)
-        if name == "c5":
+        if name == "c5" and not args.no_extras:
             # the one latency figure the reference publishes for this path, measured beside the headline
             out["single_session_append"] = append_latency(args.seed, repeats=10)
     out["cpu_baseline"] = cpu
@@ -687,7 +687,8 @@ def main():
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
-                    help="c5 only: leave out the compact objects of the other configurations")
+                    help="c5 only: leave out the compact objects of the other configurations and the Append "
+                         "latency (so that a profile of the run holds c5's own launches only)")
     ap.add_argument("--copy-mib", type=int, default=1024, help="--config copy: bytes copied each way (MiB)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--gemm", default="auto", choices=["auto", "stream", "slab"],

@@ -2129,6 +2129,11 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
         float* lo = a.logits + (long long)s_ * V;
         for (int c = tid; c < V; c += S1_THREADS) lo[c] = logit[c];
     }
+    // (a step asked for the logits alone, as Append is, needs none of the statistics below)
+    if (!(a.argmax || a.prob || a.next_ids || a.out_ids || a.out_probs)) {
+        if (tid == 0) a.pos[s_] = pos + 1;
+        return;
+    }
     // per 128-channel tile: the logits epilogue's statistics (max, sum exp(l - max), first argmax), with
     // its lane structure (lane group g4 = lane >> 4 holds channels 4g4 + 16ti + r)
     const bool want_argmax = a.argmax || a.next_ids || a.out_ids;

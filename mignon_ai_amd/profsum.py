@@ -55,7 +55,7 @@ _CLASSES = [("gemm_c2_kernel", "gemm_i8"), ("row_kernel", "row_norm_pack"), ("sc
 
 
 def kernel_class(name: str) -> str:
-    m = re.search(r"gemm_(?:slab|lx)_kernel<(\d+)", name)
+    m = re.search(r"gemm_(?:slab|lx|slab_fa)_kernel<(\d+)", name)
     if m:
         return _GEMM_EPI.get(int(m.group(1)), "")
     for key, cls in _CLASSES:
