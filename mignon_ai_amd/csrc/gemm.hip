@@ -1079,9 +1079,10 @@ hipError_t slab_launch(const GemmArgs& a, int grid, int lds, int run_tiles, int 
     return hipGetLastError();
 }
 
-// whole-tile prefetch for kc in {4, 6}; 0 when the pipelined loop is used
+// whole-tile prefetch for kc in {2, 4, 6}; 0 when the pipelined loop is used
 template <int EPI, bool STG>
 hipError_t slab_launch_full(int kc, const GemmArgs& a, int grid, int lds, int run_tiles, int n_runs, hipStream_t stream) {
+    if (kc == 2) return slab_launch<EPI, 0, STG, 2>(a, grid, lds, run_tiles, n_runs, stream);
     if (kc == 4) return slab_launch<EPI, 0, STG, 4>(a, grid, lds, run_tiles, n_runs, stream);
     return slab_launch<EPI, 0, STG, 6>(a, grid, lds, run_tiles, n_runs, stream);
 }
@@ -1107,7 +1108,7 @@ hipError_t launch_slab_t(const GemmArgs& a, hipStream_t stream) {
     const int rem = kc == 2 ? 3 : kc % 3;
     // The whole-tile prefetch holds 18-24 more registers per K step; the residual epilogue's loads (state
     // and blockIn rows) do not fit beside it without spilling.
-    const bool full = (kc == 4 || kc == 6) && EPI != EPI_RESID;
+    const bool full = (kc == 2 || kc == 4 || kc == 6) && EPI != EPI_RESID;
     if constexpr (can_stage<EPI>()) {
         if (stg && full) return slab_launch_full<EPI, true>(kc, a, grid, lds, run_tiles, n_runs, stream);
         if (stg) {
