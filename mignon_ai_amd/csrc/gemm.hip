@@ -361,16 +361,17 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
 #pragma unroll
             for (int r = 0; r < 4; r++) y[ti][r] = fmaf(limb_dot<B256>(acc, ti, r), sw, bb[r]);
             if constexpr (STG) {
-                if (orow || g.tgt) stg_put(stg, lane, ti, y[ti]);
+                if (orow) stg_put(stg, lane, ti, y[ti]);
             } else if (orow && mok) {
                 const int nv = g.nvalid - n;
                 if (nv > 0) store4(orow + n, y[ti], nv, vec);
             }
         }
-        // the target logit of each token row: from the staged tile, one lane per row; without staging,
-        // the lane holding it selects it without branches
+        // the target logit of each token row: from the staged tile, one lane per row, when the logits are
+        // staged for their stores; otherwise the lane holding it selects it without branches (cheaper than
+        // staging the tile for one value per row: c5's statistics pass 17.2 -> 16.9 ms)
         if (g.tgt) {
-            if constexpr (STG) {
+            if (STG && orow) {
                 __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the staged tile has landed
                 __builtin_amdgcn_wave_barrier();
                 const int t0 = row.tgt - n0;
