@@ -848,6 +848,12 @@ __device__ __forceinline__ void attn_scores(v4f (&s)[NKB], const float* att_lds,
     }
 }
 
+// The softmax exponential of the matrix-core attention kernels: the hardware 2^x of x*log2(e), within a
+// few ulp of e^x over the scores' range (x <= 0), where the reference-order kernels evaluate the
+// reference's FastExp polynomial bit for bit. These kernels already differ from the reference order in
+// their fp32 summation order, and this takes ~13 of the ~15 VALU instructions per score.
+__device__ __forceinline__ float attn_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+
 // out = P V over key blocks SKIP..NKB-1 (the skipped blocks' probabilities are zero: leaving them out
 // adds nothing, bit for bit).
 // Each output group's sum runs over (kb, r) in order; the groups' chains are interleaved.
@@ -986,7 +992,7 @@ __global__ __launch_bounds__(64 * G) void attention_mfma_kernel(AttnArgs a, int 
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int j = jstart + 16 * kb + 4 * kg + r;
-            const float e = (j >= lo && j <= t) ? fast_exp_ref(s[kb][r] - mx) : 0.0f;
+            const float e = (j >= lo && j <= t) ? attn_exp(s[kb][r] - mx) : 0.0f;
             s[kb][r] = e;
             sum += e;
         }
@@ -1161,7 +1167,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int j = jstart + 16 * kb + 4 * kg + r;
-                const float e = (j >= lo && j <= t) ? fast_exp_ref(s[kb][r] - mx) : 0.0f;
+                const float e = (j >= lo && j <= t) ? attn_exp(s[kb][r] - mx) : 0.0f;
                 s[kb][r] = e;
                 sum += e;
             }
