@@ -139,6 +139,13 @@ __device__ __forceinline__ void limb256_scale(float amax, float& scale, float& i
         scale = 65536.0f / inv;
     }
 }
+// The three digit-plane sums (p0, p1, p2) of a dot product over K <= 512 combined as p0 + (254 p1 + p2)/254^2
+// with the two lower planes joined exactly in integers first: |p1|, |p2| <= 127*127*512 < 2^23, so one
+// v_mad_i32_i24 forms 254 p1 + p2 (< 2^31 in magnitude), and the sum costs four instructions instead of five.
+// The result differs from the three-term form by the rounding of the two conversions only.
+__device__ __forceinline__ float limb_sum_k512(int p0, int p1, int p2) {
+    return fmaf((float)(__mul24(p1, 254) + p2), 1.0f / 64516.0f, (float)p0);
+}
 constexpr float kInvLimb256_1 = 1.0f / 256.0f;
 constexpr float kInvLimb256_2 = 1.0f / 65536.0f;
 

@@ -45,8 +45,10 @@ __device__ __forceinline__ void store4(float* dst, const float v[4], int nvalid_
 // n0 + 16ti + 4*(L >> 4) + r. Kept lean: for K = 384 the epilogue's VALU work is comparable to the
 // MFMA work of the whole tile.
 // B256: the digits are base 256 (an fp32 operand expanded as it is loaded, digits256_4).
-template <bool B256 = false>
+// K512: K is at most 512 (the head GEMMs): limb_sum_k512.
+template <bool B256 = false, bool K512 = false>
 __device__ __forceinline__ float limb_dot(const v4i (&acc)[3][8], int ti, int r) {
+    if constexpr (K512) return limb_sum_k512(acc[0][ti][r], acc[1][ti][r], acc[2][ti][r]);
     if constexpr (B256)
         return fmaf((float)acc[2][ti][r], kInvLimb256_2, fmaf((float)acc[1][ti][r], kInvLimb256_1, (float)acc[0][ti][r]));
     return fmaf((float)acc[2][ti][r], kInvLimb2, fmaf((float)acc[1][ti][r], kInvLimb1, (float)acc[0][ti][r]));
@@ -158,7 +160,7 @@ __device__ __forceinline__ void stats_out(const GemmArgs& g, int m, int n_tile, 
 
 // bias_t: the bias of this tile's 128 channels (global memory, or the workgroup's LDS copy).
 // STG: outputs of EPI_F32, EPI_LATCH, EPI_PROBS and EPI_LOGITS go through the wave's LDS region `stg`.
-template <int EPI, bool STG = false, bool B256 = false>
+template <int EPI, bool STG = false, bool B256 = false, bool K512 = false>
 __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[3][8], int mt0, int n0, int n_tile,
                                             int lane, const EpiRow& row, const float* bias_t, float* stg = nullptr) {
     const int g4 = lane >> 4;
@@ -250,7 +252,7 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
             const float bb[4] = {b.x, b.y, b.z, b.w};
             float v[4];
 #pragma unroll
-            for (int r = 0; r < 4; r++) v[r] = __builtin_amdgcn_exp2f(fmaf(limb_dot<B256>(acc, ti, r), swl, fmaf(bb[r], l2e, -lsel)));
+            for (int r = 0; r < 4; r++) v[r] = __builtin_amdgcn_exp2f(fmaf(limb_dot<B256, K512>(acc, ti, r), swl, fmaf(bb[r], l2e, -lsel)));
             if constexpr (STG) stg_put(stg, lane, ti, v);
             else store4(orow + n, v, nv, vec);
         }
@@ -359,7 +361,7 @@ __device__ __forceinline__ void lx_epilogue(const GemmArgs& g, const v4i (&acc)[
             const float4 b = *(const float4*)(bias_t + 4 * g4 + ti * 16);
             const float bb[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
-            for (int r = 0; r < 4; r++) y[ti][r] = fmaf(limb_dot<B256>(acc, ti, r), sw, bb[r]);
+            for (int r = 0; r < 4; r++) y[ti][r] = fmaf(limb_dot<B256, K512>(acc, ti, r), sw, bb[r]);
             if constexpr (STG) {
                 if (orow) stg_put(stg, lane, ti, y[ti]);
             } else if (orow && mok) {
@@ -510,6 +512,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         __syncthreads();
     }
 
+    // the head's GEMMs (logits, probabilities) over K <= 512 combine the digit planes with limb_sum_k512,
+    // in this kernel and the weight-stationary one alike
+    if constexpr (EPI == EPI_LOGITS || EPI == EPI_PROBS) {
+        if (kc <= 8) {
+            lx_epilogue<EPI, false, false, true>(g, acc, m0 + w * 16, n0, n_tile, lane, row, g.bias ? g.bias + n0 : nullptr);
+            return;
+        }
+    }
     lx_epilogue<EPI>(g, acc, m0 + w * 16, n0, n_tile, lane, row, g.bias ? g.bias + n0 : nullptr);
 }
 
@@ -599,7 +609,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             for (int ks = 0; ks < KCF; ks++)
 #pragma unroll
                 for (int l = 0; l < 3; l++) a[ks][l] = *(const v4i*)(np + ks * astep + l * 1024);
-            lx_epilogue<EPI, STG>(g, acc, tile * 16, n0, n_tile, lane, row, bias_s, stg);
+            lx_epilogue<EPI, STG, false, EPI == EPI_LOGITS || EPI == EPI_PROBS>(g, acc, tile * 16, n0, n_tile, lane,
+                                                                                row, bias_s, stg);  // K <= 384
             if (next >= t_end) break;
             tile = next;
             ap = np;
@@ -674,7 +685,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 step(ks + 1, a1, a0, NO, NO);
             }
         }
-        lx_epilogue<EPI, STG>(g, acc, tile * 16, n0, n_tile, lane, row, bias_s, stg);
+        if ((EPI == EPI_LOGITS || EPI == EPI_PROBS) && kc <= 8)
+            lx_epilogue<EPI, STG, false, true>(g, acc, tile * 16, n0, n_tile, lane, row, bias_s, stg);
+        else
+            lx_epilogue<EPI, STG>(g, acc, tile * 16, n0, n_tile, lane, row, bias_s, stg);
         if (next >= t_end) break;
         tile = next;
         ap = np;

@@ -1813,8 +1813,9 @@ __device__ __forceinline__ float s1_dot(const v4i (&acc)[3], int r) {
 // columns). After a group's last K step `epi` gets, for each unit, the combined dot products of token
 // lane & 15, channels c0 .. c0 + 3 with c0 = 16 f + 4 (lane >> 4), and the bias of those rows:
 // epi(f, v[4], b) (TS_FRAG), epi(q, vv[4], vg[4], bv, bg) (TS_PAIR), or epi(u, acc, b[GF]) (TS_TILE).
+// K512 (TS_FRAG, the head): the digit planes combined as the head GEMMs combine them (limb_sum_k512).
 enum { TS_FRAG = 0, TS_PAIR = 1, TS_TILE = 2 };
-template <int MODE, int GF, int KB, class Epi>
+template <int MODE, int GF, int KB, bool K512 = false, class Epi>
 __device__ __forceinline__ void ts_matvec(const int8_t* W, const float* bias, int np16, int kc, int nunits,
                                           const int8_t* xl, int lane, int w, Epi&& epi) {
     constexpr int UPG = MODE == TS_FRAG ? GF : MODE == TS_PAIR ? GF / 2 : 1;  // units per group
@@ -1886,7 +1887,8 @@ __device__ __forceinline__ void ts_matvec(const int8_t* W, const float* bias, in
                 if (ok[g]) {
                     float v[4];
 #pragma unroll
-                    for (int r = 0; r < 4; r++) v[r] = s1_dot(acc[g], r);
+                    for (int r = 0; r < 4; r++)
+                        v[r] = K512 ? limb_sum_k512(acc[g][0][r], acc[g][1][r], acc[g][2][r]) : s1_dot(acc[g], r);
                     epi(fr[g], v, b4[g]);
                 }
         }
@@ -2123,8 +2125,8 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
     lds_barrier();
     {
         const float sw = sf * a.head_scale;
-        ts_matvec<TS_FRAG, 4, 2>(a.headw, a.headb, Vp / 16, Dp / 64, Vp / 16, xl, lane, w,
-                                 [&](int f, const float (&v)[4], float4 b) {
+        ts_matvec<TS_FRAG, 4, 2, true>(a.headw, a.headb, Vp / 16, Dp / 64, Vp / 16, xl, lane, w,
+                                       [&](int f, const float (&v)[4], float4 b) {
             if (lane & 15) return;
             const int c0 = 16 * f + 4 * (lane >> 4);
             *(float4*)(logit + c0) = float4{fmaf(v[0], sw, b.x), fmaf(v[1], sw, b.y), fmaf(v[2], sw, b.z), fmaf(v[3], sw, b.w)};
@@ -2735,7 +2737,7 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
         for (int g = 0; g < 8; g++) {
             const float bb[4] = {b4[g].x, b4[g].y, b4[g].z, b4[g].w};
 #pragma unroll
-            for (int r = 0; r < 4; r++) y[g][r] = fmaf(s1_dot(acc[g], r), sw, bb[r]);
+            for (int r = 0; r < 4; r++) y[g][r] = fmaf(limb_sum_k512(acc[g][0][r], acc[g][1][r], acc[g][2][r]), sw, bb[r]);
         }
         const int nb = tt * LX_BN + 4 * g4;
         if (a.logits && t < ns) {
