@@ -685,8 +685,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 step(ks + 1, a1, a0, NO, NO);
             }
         }
-        if ((EPI == EPI_LOGITS || EPI == EPI_PROBS) && kc <= 8)
-            lx_epilogue<EPI, STG, false, true>(g, acc, tile * 16, n0, n_tile, lane, row, bias_s, stg);
+        constexpr bool HEAD = EPI == EPI_LOGITS || EPI == EPI_PROBS;
+        if (HEAD && kc <= 8)
+            lx_epilogue<EPI, STG, false, HEAD>(g, acc, tile * 16, n0, n_tile, lane, row, bias_s, stg);
         else
             lx_epilogue<EPI, STG>(g, acc, tile * 16, n0, n_tile, lane, row, bias_s, stg);
         if (next >= t_end) break;
