@@ -115,8 +115,12 @@ __device__ __forceinline__ void stg_flush(const GemmArgs& g, const float* stg, i
             float* dst = base + 2 * k * ldo + loff;
             if (vec) {
                 if constexpr (SK == ST_STREAM) {
+                    // The compiler does not see what an asm statement is, so it does not add the wait state
+                    // a store of more than 8 bytes needs before a VALU instruction may overwrite its data
+                    // registers: the s_nop is that wait (a schedule that reused the data registers for the
+                    // next row's address right after the store wrote address bits into the output).
                     const f4v t = {v.x, v.y, v.z, v.w};
-                    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1 nt" ::"v"(dst), "v"(t) : "memory");
+                    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1 nt\n\ts_nop 1" ::"v"(dst), "v"(t) : "memory");
                 } else if constexpr (SK == ST_NT) {
                     const f4v t = {v.x, v.y, v.z, v.w};
                     __builtin_nontemporal_store(t, (f4v*)dst);

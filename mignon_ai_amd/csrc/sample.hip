@@ -664,9 +664,11 @@ static_assert(kSumBlockLoads * (kSumRing - 2) == 56, "the ring's waits below cou
 // compiler, which cannot tell which LDS bytes such a load writes, waits for every one of them before any
 // LDS read, and the ring would then hold one block in flight instead of kSumRing. The load takes its LDS
 // address from M0, which the compiler reserves (it cannot be listed as clobbered): nothing else in this
-// file's device code uses M0, so no value of the compiler's lives there.
+// file's device code uses M0, so no value of the compiler's lives there. An LDS-DMA load may not read M0
+// in the instruction right after the SALU write of it (one wait state, which the compiler cannot add
+// inside an asm statement): the s_nop.
 __device__ __forceinline__ void lds_load16(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory");
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory");
 }
 
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
