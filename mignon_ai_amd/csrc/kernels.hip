@@ -2730,6 +2730,7 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
     const bool want_argmax = a.argmax || a.next_ids || a.out_ids;
     const int t = lane & 15, g4 = lane >> 4;
     const float sw = rsc[t] * a.head_scale;
+    // K = Dp <= 512 (tile_step_fits; its LDS takes Dp <= 320): within limb_sum_k512's bound
     ts_matvec<TS_TILE, 8, 1>(a.headw, a.headb, Vp / 16, kcD, ntiles, xl, lane, w,
                              [&](int tt, const v4i (&acc)[8][3], const float4 (&b4)[8]) {
         float y[8][4];
