@@ -410,6 +410,7 @@ def run(args):
     engine_option("attention", args.attention)
     engine_option("scan", args.scan)
     engine_option("operands", args.operands)
+    engine_option("kv_rings", args.kv_rings)
     torch.cuda.set_device(0)
     # Everything runs on one non-default stream: the engine's launches, its HIP-event kernel timing and
     # the torch events bracketing the timed region.
@@ -641,7 +642,8 @@ def run(args):
             # the one latency figure the reference publishes for this path, measured beside the headline
             out["single_session_append"] = append_latency(args.seed, repeats=10)
     out["cpu_baseline"] = cpu
-    out["kernels"] = {"gemm": args.gemm, "attention": args.attention, "scan": args.scan, "operands": args.operands}
+    out["kernels"] = {"gemm": args.gemm, "attention": args.attention, "scan": args.scan, "operands": args.operands,
+                      "kv_rings": args.kv_rings}
     return out
 
 
@@ -701,6 +703,9 @@ def main():
     ap.add_argument("--scan", default="auto", choices=["auto", "separate", "fused"],
                     help="latch scan and rule-input packing as two kernels or one (mg_engine_option); both "
                          "give identical results")
+    ap.add_argument("--kv-rings", default="auto", choices=["auto", "fp32", "packed"],
+                    help="decodes: session K/V rings as fp32 rows or packed 24-bit mantissas with a power-of-two "
+                         "scale per row (mg_engine_option)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

@@ -329,6 +329,16 @@ int mg_quantize_f32(const float* w, long long n, int8_t* q, float* scale, int fl
  *     planes as it is loaded, with the row's scale from maxima its producer writes), where the weight-
  *     stationary kernel runs them; results agree within 2e-7 of the row's largest value per operand
  *     element. Automatic is MG_OPERANDS_FP32.
+ *   MG_OPT_KV_RINGS (read when a session set is created, fixed for its life): MG_KV_FP32 keeps each
+ *     attention block's key and value rings as fp32 rows, as the reference's session does
+ *     (internal/quant/stream.go:19-35); MG_KV_PACKED keeps each (head, position) row as 24-bit mantissas
+ *     with one power-of-two scale per row (every element within 2^-24 of the row's largest magnitude of
+ *     its fp32 value, the precision the engine's limb planes give every matrix operand), 3 bytes per
+ *     element: decode attention, which reads the whole window every step, moves 3/4 of the bytes. Packed
+ *     rings apply where the fused decode attention kernel takes the model (head width a multiple of 4 up
+ *     to 64, caches of at most 64 positions, at most 16 heads); elsewhere fp32. The layered, fused and
+ *     tiled steps give bit-identical results to each other under either format. Automatic is
+ *     MG_KV_PACKED.
  * value < 0 only reads the option. Returns the previous value, or MG_ERR_INVALID. */
 #define MG_OPT_GEMM_KERNEL 0
 #define MG_OPT_ATTENTION_KERNEL 1
@@ -350,6 +360,9 @@ int mg_quantize_f32(const float* w, long long n, int8_t* q, float* scale, int fl
 #define MG_OPT_OPERANDS 5
 #define MG_OPERANDS_LIMBS 1
 #define MG_OPERANDS_FP32 2
+#define MG_OPT_KV_RINGS 6
+#define MG_KV_FP32 1
+#define MG_KV_PACKED 2
 int mg_engine_option(int option, int value);
 
 #ifdef __cplusplus

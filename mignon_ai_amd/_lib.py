@@ -24,6 +24,7 @@ MG_SCAN_SEPARATE, MG_SCAN_FUSED = 1, 2
 MG_OPT_STEP_GRAPH, MG_STEP_EAGER, MG_STEP_GRAPH = 3, 1, 2
 MG_OPT_STEP_KERNEL, MG_STEP_LAYERED, MG_STEP_FUSED, MG_STEP_TILED = 4, 1, 2, 3
 MG_OPT_OPERANDS, MG_OPERANDS_LIMBS, MG_OPERANDS_FP32 = 5, 1, 2
+MG_OPT_KV_RINGS, MG_KV_FP32, MG_KV_PACKED = 6, 1, 2
 
 _vp = ctypes.c_void_p
 _i32p = ctypes.POINTER(ctypes.c_int32)

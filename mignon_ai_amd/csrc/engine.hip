@@ -237,6 +237,10 @@ struct mg_sessions {
     mg_model* m = nullptr;
     int n = 0, window = 0;
     mg::DevBuf norm_ring, g, kring, vring, pos, next_ids, out_ids, out_probs, logits, argmax, prob;
+    // K/V ring format, fixed at creation (OPT_KV_RINGS): packed rows in kring/vring with their scales in
+    // kscale/vscale, or fp32 rows
+    bool kv_packed = false;
+    mg::DevBuf kscale, vscale;
     mg::DevBuf sample_ws;  // the sampler's exponentials and row sums
     // stop-token bookkeeping of mg_sessions_decode_greedy_until: per-session reply length, the stopped
     // count, and a ring of pinned host slots the count is copied to after each step (one event each)
@@ -277,6 +281,30 @@ struct mg_sessions {
 
 namespace mg {
 namespace {
+
+// Whether a new session set of this model keeps packed K/V rings: the decode attention of every step
+// kernel that can run on the set (attention_step_rows, step1's rk_head) reads them where the rows kernel
+// fits the model, and OPT_KV_RINGS does not ask for fp32.
+bool kv_rings_packed(const mg_model* m) {
+    if (m->nattn <= 0 || option(OPT_KV_RINGS) == 1) return false;
+    AttnStepArgs a;
+    a.S = 1; a.D = m->D; a.Dp = m->Dp; a.heads = m->heads; a.window = m->window; a.cap = m->cap;
+    return attention_step_rows_fits(a);
+}
+
+// The K/V rings of attention block ab of a set: packed words and scales, or fp32 rows.
+void ring_args(mg_sessions* s, int ab, AttnStepArgs& a) {
+    const mg_model* m = s->m;
+    const size_t rows = (size_t)ab * s->n * m->heads * m->cap;  // ring rows of the earlier blocks
+    if (s->kv_packed) {
+        const size_t words = rows * kv_row_words(m->D / m->heads);
+        a.kpack = s->kring.as<uint32_t>() + words; a.vpack = s->vring.as<uint32_t>() + words;
+        a.kscale = s->kscale.as<float>() + rows; a.vscale = s->vscale.as<float>() + rows;
+    } else {
+        const size_t floats = rows * (m->D / m->heads);
+        a.kring = s->kring.as<float>() + floats; a.vring = s->vring.as<float>() + floats;
+    }
+}
 
 template <class T>
 T* upload(mg_model* m, const std::vector<T>& h) {
@@ -888,8 +916,7 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
                 AttnStepArgs aa;
                 aa.S = M; aa.D = D; aa.Dp = Dp; aa.heads = m->heads; aa.window = m->window; aa.cap = m->cap;
                 aa.pos = c.sess->pos.as<int32_t>(); aa.qkv = w.qkv.as<float>();
-                aa.kring = c.sess->kring.as<float>() + (size_t)ab * c.B * m->cap * D;
-                aa.vring = c.sess->vring.as<float>() + (size_t)ab * c.B * m->cap * D;
+                ring_args(c.sess, ab, aa);
                 aa.att = w.att.as<float>();
                 ProfScope ps(m->prof, K_ATTN_STEP, s);
                 if (attention_step_rows_fits(aa)) {
@@ -903,9 +930,14 @@ void run_body(mg_model* m, const BodyCtx& c, hipStream_t s) {
             } else if (!fused) {
                 if (c.sess) {
                     ProfScope ps(m->prof, K_EXPORT, s);
-                    HIPCHECK(launch_export_kv(c.B, c.T, D, m->heads, m->cap, c.lens, w.qkv.as<float>(),
-                                              c.sess->kring.as<float>() + (size_t)ab * c.B * m->cap * D,
-                                              c.sess->vring.as<float>() + (size_t)ab * c.B * m->cap * D, s));
+                    AttnStepArgs r;
+                    ring_args(c.sess, ab, r);
+                    if (c.sess->kv_packed)
+                        HIPCHECK(launch_export_kv_packed(c.B, c.T, D, m->heads, m->cap, c.lens, w.qkv.as<float>(),
+                                                         r.kpack, r.vpack, r.kscale, r.vscale, s));
+                    else
+                        HIPCHECK(launch_export_kv(c.B, c.T, D, m->heads, m->cap, c.lens, w.qkv.as<float>(), r.kring,
+                                                  r.vring, s));
                 }
                 AttnArgs aa;
                 aa.B = c.B; aa.T = c.T; aa.D = D; aa.Dp = Dp; aa.heads = m->heads; aa.window = m->window; aa.cap = m->cap;
@@ -1472,6 +1504,10 @@ void clear_sessions(mg_sessions* s) {
     HIPCHECK(launch_fill_f32(s->g.as<float>(), (long long)(s->g.n / 4), 0.0f, m->stream));
     HIPCHECK(launch_fill_f32(s->kring.as<float>(), (long long)(s->kring.n / 4), 0.0f, m->stream));
     HIPCHECK(launch_fill_f32(s->vring.as<float>(), (long long)(s->vring.n / 4), 0.0f, m->stream));
+    if (s->kv_packed) {  // zero words decode to zero under any scale; the scales start at 1
+        HIPCHECK(launch_fill_f32(s->kscale.as<float>(), (long long)(s->kscale.n / 4), 1.0f, m->stream));
+        HIPCHECK(launch_fill_f32(s->vscale.as<float>(), (long long)(s->vscale.n / 4), 1.0f, m->stream));
+    }
     HIPCHECK(launch_fill_i32(s->pos.as<int32_t>(), s->n, 0, m->stream));
 }
 
@@ -1490,8 +1526,15 @@ int mg_sessions_create(mg_model* m, int n, int context, mg_sessions** out) {
         const size_t Dp = m->Dp, D = m->D;
         s->norm_ring.ensure(std::max<size_t>(16, (size_t)m->nbs * n * m->ring * Dp * 4));
         s->g.ensure(std::max<size_t>(16, (size_t)m->nbs * n * Dp * 4));
-        s->kring.ensure(std::max<size_t>(16, (size_t)m->nattn * n * m->cap * D * 4));
-        s->vring.ensure(std::max<size_t>(16, (size_t)m->nattn * n * m->cap * D * 4));
+        s->kv_packed = kv_rings_packed(m);
+        // packed: 3 bytes per element and a 4-byte scale per (head, slot) row; fp32: 4 bytes per element
+        const size_t ring_bytes = (size_t)m->nattn * n * m->cap * D * (s->kv_packed ? 3 : 4);
+        s->kring.ensure(std::max<size_t>(16, ring_bytes));
+        s->vring.ensure(std::max<size_t>(16, ring_bytes));
+        if (s->kv_packed) {
+            s->kscale.ensure(std::max<size_t>(16, (size_t)m->nattn * n * m->heads * m->cap * 4));
+            s->vscale.ensure(std::max<size_t>(16, (size_t)m->nattn * n * m->heads * m->cap * 4));
+        }
         s->pos.ensure((size_t)n * 4);
         s->next_ids.ensure((size_t)n * 4);
         clear_sessions(s.get());
@@ -1563,7 +1606,12 @@ bool step1_args_fill(mg_sessions* s, const int32_t* ids_d, float* logits_d, cons
     a.emb = m->emb; a.emb_scale = m->emb_scale; a.headw = m->headw; a.headb = m->headb; a.head_scale = m->head_scale;
     a.final_norm = m->final_norm; a.latch_base = m->latch_base;
     a.pos = s->pos.as<int32_t>(); a.g = s->g.as<float>(); a.norm_ring = s->norm_ring.as<float>();
-    a.kring = s->kring.as<float>(); a.vring = s->vring.as<float>();
+    if (s->kv_packed) {
+        a.kpack = s->kring.as<uint32_t>(); a.vpack = s->vring.as<uint32_t>();
+        a.kscale = s->kscale.as<float>(); a.vscale = s->vscale.as<float>();
+    } else {
+        a.kring = s->kring.as<float>(); a.vring = s->vring.as<float>();
+    }
     a.ids = ids_d; a.logits = logits_d; a.argmax = hc.argmax; a.prob = hc.prob; a.next_ids = hc.next_ids;
     a.out_ids = hc.out_ids; a.out_probs = hc.out_probs; a.out_ld = hc.out_ld; a.out_col = hc.out_col; a.col = hc.col;
     a.done = hc.done;
@@ -1584,8 +1632,7 @@ AttnStepArgs step_attn_args(mg_sessions* s, int ab) {
     AttnStepArgs aa;
     aa.S = s->n; aa.D = m->D; aa.Dp = m->Dp; aa.heads = m->heads; aa.window = m->window; aa.cap = m->cap;
     aa.pos = s->pos.as<int32_t>(); aa.qkv = w.qkv.as<float>();
-    aa.kring = s->kring.as<float>() + (size_t)ab * s->n * m->cap * m->D;
-    aa.vring = s->vring.as<float>() + (size_t)ab * s->n * m->cap * m->D;
+    ring_args(s, ab, aa);
     aa.xl = w.nl.as<int8_t>(); aa.xs = w.ns.as<float>();
     return aa;
 }
@@ -2085,7 +2132,10 @@ long long mg_sessions_state_bytes(const mg_sessions* s) {
 long long mg_sessions_device_bytes(const mg_sessions* s) {
     if (!s) return -1;
     const mg_model* m = s->m;
-    return (long long)m->nbs * (m->ring + 1) * m->Dp * 4 + (long long)m->nattn * 2 * m->cap * m->D * 4 + 8;
+    // packed rings: 3 bytes per element and a 4-byte scale per (head, slot) row of each ring
+    const long long rings = s->kv_packed ? (long long)m->nattn * 2 * m->cap * ((long long)m->D * 3 + m->heads * 4)
+                                         : (long long)m->nattn * 2 * m->cap * m->D * 4;
+    return (long long)m->nbs * (m->ring + 1) * m->Dp * 4 + rings + 8;
 }
 
 int mg_sessions_count(const mg_sessions* s) { return s ? s->n : -1; }

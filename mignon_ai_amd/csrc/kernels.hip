@@ -1281,8 +1281,66 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_wave_barrier();
 }
 
-// LDS floats of one head in rk_head: the values [cap][DH + 4], the query [DH], the scores [cap].
-__host__ __device__ constexpr int rk_lds_floats(int cap, int dh) { return cap * (dh + 4) + dh + cap; }
+// ------------------------------------------------------------------------------------------------
+// Packed K/V rings. A ring row (one head's key or value at one position) is held as dh/4 groups of
+// three 32-bit words, each group four 24-bit two's-complement mantissas m, with one power-of-two scale
+// s = 2^e per row: the element is m * s, exactly. e = E - 23 for the row's largest magnitude
+// amax = f * 2^E (f in [0.5, 1)), so the largest element keeps 23 significant bits and every element
+// lies within 2^-24 * amax of its fp32 value, the precision the limb planes give every matrix operand
+// relative to its row. Three bytes per element instead of four: decode attention, which streams the
+// rings, reads 3/4 of the bytes. Decoding is exact (a 24-bit integer times a power of two), so every
+// kernel that reads a packed ring sees the same fp32 values and the decode kernels stay bit-identical
+// to each other.
+// ------------------------------------------------------------------------------------------------
+struct Pk3 {
+    uint32_t x, y, z;
+};
+
+// The exponent e of a row whose largest magnitude is amax (amax * 2^-e < 2^23; e >= -120 keeps 2^e a
+// normal float, rows below 2^-97 lose their low bits).
+__device__ __forceinline__ int kv_exp(float amax) {
+    int E;
+    (void)frexpf(amax, &E);
+    return max(E - 23, -120);
+}
+
+__device__ __forceinline__ uint32_t kv_mant(float v, int e) {
+    const float r = fminf(fmaxf(rintf(ldexpf(v, -e)), -8388607.0f), 8388607.0f);
+    return (uint32_t)(int)r & 0xffffffu;
+}
+
+__device__ __forceinline__ Pk3 kv_pack(float4 v, int e) {
+    const uint32_t u0 = kv_mant(v.x, e), u1 = kv_mant(v.y, e), u2 = kv_mant(v.z, e), u3 = kv_mant(v.w, e);
+    return Pk3{u0 | (u1 << 24), (u1 >> 8) | (u2 << 16), (u2 >> 16) | (u3 << 8)};
+}
+
+// Global loads and stores of one group, as three dword accesses the compiler joins into one.
+__device__ __forceinline__ Pk3 ldg_pk3(const Pk3* p) {
+    const __attribute__((address_space(1))) uint32_t* q = (const __attribute__((address_space(1))) uint32_t*)p;
+    return Pk3{q[0], q[1], q[2]};
+}
+
+__device__ __forceinline__ void stg_pk3(Pk3* p, Pk3 v) {
+    __attribute__((address_space(1))) uint32_t* q = (__attribute__((address_space(1))) uint32_t*)p;
+    q[0] = v.x;
+    q[1] = v.y;
+    q[2] = v.z;
+}
+
+__device__ __forceinline__ float4 kv_unpack(Pk3 w, float s) {
+    const int m0 = (int)(w.x << 8) >> 8;
+    const int m1 = (int)(__builtin_amdgcn_alignbit(w.y, w.x, 24) << 8) >> 8;
+    const int m2 = (int)(__builtin_amdgcn_alignbit(w.z, w.y, 16) << 8) >> 8;
+    const int m3 = (int)w.z >> 8;
+    return float4{(float)m0 * s, (float)m1 * s, (float)m2 * s, (float)m3 * s};
+}
+
+// LDS floats of one head in rk_head, a multiple of four (16-byte aligned regions side by side): the
+// values [cap][DH + 4], the query [DH], with packed rings read from global memory (PK, not QL) the
+// current position's key [DH], the scores [cap].
+__host__ __device__ constexpr int rk_lds_floats(int cap, int dh, bool kcur = false) {
+    return (cap * (dh + 4) + dh + (kcur ? dh : 0) + cap + 3) & ~3;
+}
 
 // One (session, head) of decode attention for caches of at most 64 positions, by one wave, with each
 // lane's key row in registers: lane jj loads key lo + jj itself and scores it, so only the values (and
@@ -1291,23 +1349,28 @@ __host__ __device__ constexpr int rk_lds_floats(int cap, int dh) { return cap * 
 // query, this position's key and value, the key rows, the value rows) is issued before the first wait,
 // so a wave makes one memory round trip. `sm` (rk_lds_floats) and `inv_sh` are private to the wave.
 // Returns output element `lane` of the head (lanes < DH) and records this position's key and value in
-// the ring.
-template <int DH, bool QL = false>
+// the ring. PK: the rings are packed (kpack/kscale, vpack/vscale); the ring rows are decoded as they
+// are loaded, and the current position's key and value, which are not yet in the ring, come in fp32
+// (through LDS without QL: lanes C4..2C4-1 hold the key, 2C4..3C4-1 the value, as their `mine`).
+template <int DH, bool QL = false, bool PK = false>
 __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, int lane, float* sm, float& inv_sh) {
     constexpr int DS = DH + 4;
     constexpr int C4 = DH / 4;
     static_assert(3 * C4 <= 64, "one float4 of q, k or v per lane");
     const int cap = a.cap;
-    float* vs = sm;               // [cap][DS]
-    float* qs = vs + cap * DS;    // [DH]
-    float* es = qs + DH;          // [cap]
+    constexpr bool CUR_LANES = PK && !QL;  // the current key and value from the lanes holding them
+    float* vs = sm;                           // [cap][DS]
+    float* qs = vs + cap * DS;                // [DH]
+    float* kc = qs + DH;                      // [DH] (CUR_LANES)
+    float* es = kc + (CUR_LANES ? DH : 0);    // [cap]
     const int D = a.D;
     const int pos = a.pos[s_];
     const int lo = max(window_start(pos, a.window), pos - cap + 1);
     const int span = pos - lo + 1;  // at most cap <= 64
     const float* qkv = a.qkv + (long long)s_ * 3 * D;
-    const float* kr = a.kring + ((long long)s_ * a.heads + h) * cap * DH;
-    const float* vr = a.vring + ((long long)s_ * a.heads + h) * cap * DH;
+    const long long row0 = ((long long)s_ * a.heads + h) * cap;  // ring row of slot 0
+    const float* kr = a.kring + row0 * DH;
+    const float* vr = a.vring + row0 * DH;
     // q, k, v of this position: in LDS (QL) or global memory; the rings in global memory. Typed loads, so
     // that the compiler need not treat them as generic (flat) accesses, which it serialises.
     auto qkv4 = [&](const float* p) -> float4 {
@@ -1319,6 +1382,11 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
             return ldg((const float4*)p);
         }
     };
+    // group c of packed ring row `sl` (kpack or vpack) and that row's scale
+    auto pk4 = [&](const uint32_t* ring, const float* scl, int sl, int c) -> float4 {
+        const Pk3 w = ldg_pk3((const Pk3*)ring + (row0 + sl) * C4 + c);
+        return kv_unpack(w, ldg(scl + row0 + sl));
+    };
     // lanes 0..3*C4-1: one float4 each of this position's q, k and v (part lane / C4, chunk lane % C4)
     const int qpart = min(lane / C4, 2), qc = lane % C4;
     const float4 mine = qkv4(qkv + qpart * D + h * DH + 4 * qc);
@@ -1329,7 +1397,17 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
     float4 krow[C4];
     {
         const int jj = min(lane, span - 1);
-        if constexpr (QL) {
+        if constexpr (PK) {
+            // the ring row (the current position's slot is read too, in bounds, and its value replaced)
+#pragma unroll
+            for (int c = 0; c < C4; c++) krow[c] = pk4(a.kpack, a.kscale, slot(jj), c);
+            if constexpr (QL) {
+                if (jj == span - 1) {
+#pragma unroll
+                    for (int c = 0; c < C4; c++) krow[c] = qkv4(qkv + D + h * DH + 4 * c);
+                }
+            }
+        } else if constexpr (QL) {
             // q, k, v in LDS: the ring row and the LDS row are separate loads (the current position's
             // ring slot is read too, in bounds, and its value discarded)
             const float* kp = kr + (long long)slot(jj) * DH;
@@ -1347,8 +1425,9 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
     }
     // values: rows jj = 0..span-1 into LDS, every load issued before the first store. Lanes past the
     // end repeat the last element (the same bytes to the same address), so no store is conditional and
-    // no load can be moved next to its store.
-    const int n4 = span * C4;
+    // no load can be moved next to its store. Packed rings without QL: rows 0..span-2 from the ring, the
+    // current position's row from the lanes holding it.
+    const int n4 = (CUR_LANES ? span - 1 : span) * C4;
     for (int e0 = 0; e0 < n4; e0 += 8 * 64) {
         float4 vb[8];
         int off[8];
@@ -1356,7 +1435,12 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
         for (int u = 0; u < 8; u++) {
             const int e = min(e0 + u * 64 + lane, n4 - 1);
             const int jj = e / C4, c = e - jj * C4;
-            if constexpr (QL) {
+            if constexpr (PK) {
+                vb[u] = pk4(a.vpack, a.vscale, slot(jj), c);
+                if constexpr (QL) {
+                    if (jj == span - 1) vb[u] = qkv4(qkv + 2 * D + h * DH + 4 * c);
+                }
+            } else if constexpr (QL) {
                 vb[u] = ldg((const float4*)(vr + (long long)slot(jj) * DH + 4 * c));
                 if (jj == span - 1) vb[u] = qkv4(qkv + 2 * D + h * DH + 4 * c);
             } else {
@@ -1368,8 +1452,18 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
 #pragma unroll
         for (int u = 0; u < 8; u++) *(float4*)(vs + off[u]) = vb[u];
     }
+    if constexpr (CUR_LANES) {
+        if (qpart == 1 && lane < 2 * C4) *(float4*)(kc + 4 * qc) = mine;
+        if (qpart == 2 && lane < 3 * C4) *(float4*)(vs + (span - 1) * DS + 4 * qc) = mine;
+    }
     if (lane < C4) *(float4*)(qs + 4 * lane) = mine;
     wave_lds_sync();
+    if constexpr (CUR_LANES) {
+        if (lane == span - 1) {
+#pragma unroll
+            for (int c = 0; c < C4; c++) krow[c] = *(const float4*)(kc + 4 * c);
+        }
+    }
     float q[DH];
 #pragma unroll
     for (int i = 0; i < DH; i += 4) {
@@ -1395,21 +1489,36 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
         for (int jj = 0; jj < span; jj++) o = axpy_ref<DH>(lane, es[jj] * inv, vs[jj * DS + lane], o);
     }
     // record this position's key and value (slot pos % cap; the evicted key is outside the window)
-    if (lane >= C4 && lane < 3 * C4) {
-        float* ring = lane < 2 * C4 ? a.kring : a.vring;
-        stg((float4*)(ring + (((long long)s_ * a.heads + h) * cap + pos % cap) * DH + 4 * qc), mine);
+    if constexpr (PK) {
+        // the row's largest magnitude over the C4 lanes holding it (every lane takes part in the shuffles)
+        const float am = fmaxf(fmaxf(fabsf(mine.x), fabsf(mine.y)), fmaxf(fabsf(mine.z), fabsf(mine.w)));
+        float rm = 0.0f;
+#pragma unroll
+        for (int i = 0; i < C4; i++) rm = fmaxf(rm, __shfl(am, qpart * C4 + i, 64));
+        if (lane >= C4 && lane < 3 * C4) {
+            const int e = kv_exp(rm);
+            const long long r = row0 + pos % cap;
+            uint32_t* ring = lane < 2 * C4 ? a.kpack : a.vpack;
+            stg_pk3((Pk3*)ring + r * C4 + qc, kv_pack(mine, e));
+            if (qc == 0) stg((lane < 2 * C4 ? a.kscale : a.vscale) + r, ldexpf(1.0f, e));
+        }
+    } else {
+        if (lane >= C4 && lane < 3 * C4) {
+            float* ring = lane < 2 * C4 ? a.kring : a.vring;
+            stg((float4*)(ring + (row0 + pos % cap) * DH + 4 * qc), mine);
+        }
     }
     return o;
 }
 
-// Decode attention, one wave per (session, head), key rows in registers (rk_head).
-template <int DH>
+// Decode attention, one wave per (session, head), key rows in registers (rk_head); PK: packed rings.
+template <int DH, bool PK>
 __global__ __launch_bounds__(64) void attention_step_rk_kernel(AttnStepArgs a) {
     extern __shared__ __align__(16) float rk_smem[];
     __shared__ float rk_inv;
     const int s_ = blockIdx.x / a.heads, h = blockIdx.x % a.heads;
     const int lane = threadIdx.x;
-    const float o = rk_head<DH>(a, s_, h, lane, rk_smem, rk_inv);
+    const float o = rk_head<DH, false, PK>(a, s_, h, lane, rk_smem, rk_inv);
     if (lane < DH) a.att[(long long)s_ * a.Dp + h * DH + lane] = o;
 }
 
@@ -1417,13 +1526,14 @@ __global__ __launch_bounds__(64) void attention_step_rk_kernel(AttnStepArgs a) {
 // expansion of the attention output that the out projection reads: the row's absolute maximum over
 // all heads gives its scale, and each lane writes its element's three limbs (row_kernel's ROW_SRC
 // digits and scale, from the same values), so the output never goes through memory as fp32.
-template <int DH>
+// PK: packed rings.
+template <int DH, bool PK>
 __global__ __launch_bounds__(1024) void attention_step_rows_kernel(AttnStepArgs a) {
     extern __shared__ __align__(16) float rows_smem[];
     __shared__ float inv_sh[16], red[16];
     const int s_ = blockIdx.x, h = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (a.done && a.done[s_] >= 0) return;  // a finished session of a batched decode (the whole workgroup)
-    const float o = rk_head<DH>(a, s_, h, lane, rows_smem + h * rk_lds_floats(a.cap, DH), inv_sh[h]);
+    const float o = rk_head<DH, false, PK>(a, s_, h, lane, rows_smem + h * rk_lds_floats(a.cap, DH, PK), inv_sh[h]);
     const float mx = wave_max(lane < DH ? fabsf(o) : 0.0f);
     if (lane == 0) red[h] = mx;
     __syncthreads();
@@ -2085,10 +2195,19 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
                 sa_.S = 1; sa_.D = D; sa_.Dp = Dp; sa_.heads = a.heads; sa_.window = a.window; sa_.cap = a.cap;
                 sa_.pos = a.pos + s_;
                 sa_.qkv = qkv;
-                const long long ring0 = ((long long)ab * a.S + s_) * a.heads * a.cap * DH;
-                sa_.kring = a.kring + ring0;
-                sa_.vring = a.vring + ring0;
-                const float o = rk_head<DH, true>(sa_, 0, w, lane, rk + w * rkf, rk_inv[w]);
+                const long long rows0 = ((long long)ab * a.S + s_) * a.heads * a.cap;  // ring rows before this one's
+                float o;
+                if (a.kpack) {
+                    sa_.kpack = a.kpack + rows0 * kv_row_words(DH);
+                    sa_.vpack = a.vpack + rows0 * kv_row_words(DH);
+                    sa_.kscale = a.kscale + rows0;
+                    sa_.vscale = a.vscale + rows0;
+                    o = rk_head<DH, true, true>(sa_, 0, w, lane, rk + w * rkf, rk_inv[w]);
+                } else {
+                    sa_.kring = a.kring + rows0 * DH;
+                    sa_.vring = a.vring + rows0 * DH;
+                    o = rk_head<DH, true>(sa_, 0, w, lane, rk + w * rkf, rk_inv[w]);
+                }
                 if (lane < DH) att[w * DH + lane] = o;
             }
             lds_barrier();
@@ -2911,7 +3030,7 @@ __global__ void export_ring_kernel(int B, int T, int Dp, int ring, const int32_t
 __global__ void export_kv_kernel(int B, int T, int D, int heads, int cap, const int32_t* lens, const float* qkv,
                                  float* kr, float* vr) {
     const int b = blockIdx.x;
-    const int len = lens[b];
+    const int len = min(max(lens[b], 0), T);
     const int p0 = max(0, len - cap);
     const int dh = D / heads;
     for (int p = p0; p < len; p++)
@@ -2922,6 +3041,43 @@ __global__ void export_kv_kernel(int B, int T, int D, int heads, int cap, const 
             kr[o] = row[D + d];
             vr[o] = row[2 * D + d];
         }
+}
+
+// export_kv_kernel into packed rings: one wave per position at a time (four per workgroup, one workgroup
+// per sequence). The wave stages the position's key and value rows [k | v] in LDS with coalesced 16-byte
+// loads, finds each (head, key or value) row's exponent (kv_exp of its largest magnitude), and packs one
+// group of four per lane (kv_pack, as rk_head packs a decode step's row).
+__host__ __device__ inline int export_kv_wave_floats(int D, int heads) { return 2 * D + ((2 * heads + 3) & ~3); }
+
+__global__ __launch_bounds__(256) void export_kv_packed_kernel(int B, int T, int D, int heads, int cap,
+                                                               const int32_t* lens, const float* qkv, uint32_t* kpack,
+                                                               uint32_t* vpack, float* kscale, float* vscale) {
+    extern __shared__ __align__(16) float ex_smem[];
+    const int b = blockIdx.x, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int len = min(max(lens[b], 0), T);
+    const int p0 = max(0, len - cap);
+    const int dh = D / heads, c4 = dh / 4, nc = D / 2;  // float4 chunks of [k | v]
+    float* xw = ex_smem + w * export_kv_wave_floats(D, heads);
+    int* ew = (int*)(xw + 2 * D);  // [2 heads] row exponents: rows 0..heads-1 keys, heads..2heads-1 values
+    for (int p = p0 + w; p < len; p += 4) {
+        const float* src = qkv + ((long long)b * T + p) * 3 * D + D;  // k then v, 2D floats
+        for (int c = lane; c < nc; c += 64) *(float4*)(xw + 4 * c) = ldg((const float4*)(src + 4 * c));
+        wave_lds_sync();
+        for (int r = lane; r < 2 * heads; r += 64) {
+            float am = 0.0f;
+            for (int d = 0; d < dh; d++) am = fmaxf(am, fabsf(xw[r * dh + d]));
+            ew[r] = kv_exp(am);
+        }
+        wave_lds_sync();
+        for (int c = lane; c < nc; c += 64) {
+            const int r = c / c4, g = c - r * c4;
+            const int part = r >= heads, h = r - part * heads, e = ew[r];
+            const long long row = ((long long)b * heads + h) * cap + p % cap;
+            stg_pk3((Pk3*)(part ? vpack : kpack) + row * c4 + g, kv_pack(*(const float4*)(xw + 4 * c), e));
+            if (g == 0) stg((part ? vscale : kscale) + row, ldexpf(1.0f, e));
+        }
+        wave_lds_sync();  // the wave's buffer takes the next position
+    }
 }
 
 __global__ void set_pos_kernel(int S, const int32_t* lens, int32_t* pos, int add, int32_t* col) {
@@ -3078,11 +3234,14 @@ template <int DH>
 hipError_t attn_step_t(const AttnStepArgs& a, hipStream_t s) {
     if constexpr (DH % 4 == 0 && DH <= 64) {
         if (a.cap <= 64) {
-            const size_t lds = (size_t)rk_lds_floats(a.cap, DH) * sizeof(float);
-            hipLaunchKernelGGL(attention_step_rk_kernel<DH>, dim3(a.S * a.heads), dim3(64), lds, s, a);
+            const bool pk = a.kpack != nullptr;
+            const size_t lds = (size_t)rk_lds_floats(a.cap, DH, pk) * sizeof(float);
+            if (pk) hipLaunchKernelGGL((attention_step_rk_kernel<DH, true>), dim3(a.S * a.heads), dim3(64), lds, s, a);
+            else hipLaunchKernelGGL((attention_step_rk_kernel<DH, false>), dim3(a.S * a.heads), dim3(64), lds, s, a);
             return hipGetLastError();
         }
     }
+    if (a.kpack) return hipErrorInvalidValue;  // packed rings: the kernels above only
     if constexpr (DH % 4 == 0) {
         const size_t lds = ((size_t)2 * a.cap * (DH + 4) + a.cap) * sizeof(float);
         if (lds <= 64 * 1024) {
@@ -3097,12 +3256,18 @@ hipError_t attn_step_t(const AttnStepArgs& a, hipStream_t s) {
 template <int DH>
 hipError_t attn_step_rows_t(const AttnStepArgs& a, hipStream_t s) {
     if constexpr (DH % 4 == 0 && DH <= 64) {
-        const size_t lds = (size_t)a.heads * rk_lds_floats(a.cap, DH) * sizeof(float);
-        static const hipError_t attr = hipFuncSetAttribute((const void*)attention_step_rows_kernel<DH>,
+        const bool pk = a.kpack != nullptr;
+        const size_t lds = (size_t)a.heads * rk_lds_floats(a.cap, DH, pk) * sizeof(float);
+        static const hipError_t attr = hipFuncSetAttribute((const void*)attention_step_rows_kernel<DH, false>,
                                                            hipFuncAttributeMaxDynamicSharedMemorySize,
                                                            (int)kStepRowsMaxLds);
+        static const hipError_t attr_pk = hipFuncSetAttribute((const void*)attention_step_rows_kernel<DH, true>,
+                                                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                              (int)kStepRowsMaxLds);
         if (attr != hipSuccess) return attr;
-        hipLaunchKernelGGL(attention_step_rows_kernel<DH>, dim3(a.S), dim3(64 * a.heads), lds, s, a);
+        if (attr_pk != hipSuccess) return attr_pk;
+        if (pk) hipLaunchKernelGGL((attention_step_rows_kernel<DH, true>), dim3(a.S), dim3(64 * a.heads), lds, s, a);
+        else hipLaunchKernelGGL((attention_step_rows_kernel<DH, false>), dim3(a.S), dim3(64 * a.heads), lds, s, a);
         return hipGetLastError();
     }
     return hipErrorInvalidValue;
@@ -3247,12 +3412,15 @@ bool attention_step_rows_fits(const AttnStepArgs& a) {
         case 4: case 8: case 12: case 16: case 20: case 24: case 32: case 40: case 48: case 64: break;
         default: return false;
     }
-    return (size_t)a.heads * rk_lds_floats(a.cap, dh) * sizeof(float) <= kStepRowsMaxLds;
+    // sized for packed rings (the larger of the two layouts), so that a set's ring format, chosen by this
+    // fit, never depends on it
+    return (size_t)a.heads * rk_lds_floats(a.cap, dh, true) * sizeof(float) <= kStepRowsMaxLds;
 }
 
 hipError_t launch_attention_step_rows(const AttnStepArgs& a, hipStream_t s) {
     if (a.S <= 0) return hipSuccess;
     if (!attention_step_rows_fits(a) || !a.xl || !a.xs) return hipErrorInvalidValue;
+    if (a.kpack && (!a.vpack || !a.kscale || !a.vscale)) return hipErrorInvalidValue;
     DH_SWITCH(a.D / a.heads, attn_step_rows_t, a, s)
 }
 
@@ -3260,7 +3428,9 @@ hipError_t launch_attention_step(const AttnStepArgs& a, hipStream_t s) {
     if (a.S <= 0) return hipSuccess;
     if (a.heads <= 0 || a.D % a.heads || a.cap <= 0) return hipErrorInvalidValue;
     const int dh = a.D / a.heads;
+    if (a.kpack && (!a.vpack || !a.kscale || !a.vscale)) return hipErrorInvalidValue;
     if (dh_compiled(dh) && a.cap <= 256) DH_SWITCH(dh, attn_step_t, a, s)
+    if (a.kpack) return hipErrorInvalidValue;  // packed rings: attention_step_rk_kernel's shapes only
     AttnWaveArgs w;
     w.rows = a.S; w.D = a.D; w.Dp = a.Dp; w.heads = a.heads; w.dh = dh; w.window = a.window; w.cap = a.cap;
     w.step = true; w.qkv = a.qkv; w.pos = a.pos; w.kring = a.kring; w.vring = a.vring; w.att = a.att;
@@ -3382,6 +3552,17 @@ hipError_t launch_export_kv(int B, int T, int D, int heads, int cap, const int32
     if (B <= 0) return hipSuccess;
     if (heads <= 0 || D % heads != 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL(export_kv_kernel, dim3(B), dim3(256), 0, s, B, T, D, heads, cap, lens, qkv, kring, vring);
+    return hipGetLastError();
+}
+
+hipError_t launch_export_kv_packed(int B, int T, int D, int heads, int cap, const int32_t* lens, const float* qkv,
+                                   uint32_t* kpack, uint32_t* vpack, float* kscale, float* vscale, hipStream_t s) {
+    if (B <= 0) return hipSuccess;
+    if (heads <= 0 || D % heads != 0 || (D / heads) % 4) return hipErrorInvalidValue;
+    if (D > 1024) return hipErrorInvalidValue;
+    const size_t lds = (size_t)4 * export_kv_wave_floats(D, heads) * sizeof(float);
+    hipLaunchKernelGGL(export_kv_packed_kernel, dim3(B), dim3(256), lds, s, B, T, D, heads, cap, lens, qkv, kpack,
+                       vpack, kscale, vscale);
     return hipGetLastError();
 }
 

@@ -112,7 +112,17 @@ struct AttnStepArgs {
     int8_t* xl = nullptr;          // attention_step_rows: limbs of the output, fragment layout, K = Dp
     float* xs = nullptr;           // attention_step_rows: [S] row scales
     const int32_t* done = nullptr; // attention_step_rows: [S] or null: sessions with done[i] >= 0 are skipped
+    // Packed rings (set: kring and vring are not used). Each row (one head, one slot) is dh/4 groups of
+    // three words holding four 24-bit mantissas, with a power-of-two scale per row. Read by the kernels
+    // built on rk_head only (attention_step_rows, and attention_step_rk where launch_attention_step
+    // selects it); launch_attention_step rejects them elsewhere.
+    uint32_t* kpack = nullptr;     // [S][heads][cap][3 * dh / 4]
+    uint32_t* vpack = nullptr;     // [S][heads][cap][3 * dh / 4]
+    float* kscale = nullptr;       // [S][heads][cap]
+    float* vscale = nullptr;       // [S][heads][cap]
 };
+// Words of one packed ring row of head width dh (a multiple of 4).
+constexpr int kv_row_words(int dh) { return 3 * dh / 4; }
 hipError_t launch_attention_step(const AttnStepArgs& a, hipStream_t s);
 // Decode attention fused with the limb expansion of its output (one workgroup per session, one wave per
 // head): writes xl/xs, as the row kernel would from att, instead of att. For head widths that are a
@@ -163,8 +173,10 @@ struct Step1Args {
     const int8_t* headw = nullptr; const float* headb = nullptr; float head_scale = 0;
     const float* final_norm = nullptr; const float* latch_base = nullptr;
     // session state (the engine's layouts): pos [S]; g [nbs][S][Dp]; norm ring [nbs][S][ring][Dp];
-    // K/V rings [nattn][S][heads][cap][dh]
+    // K/V rings [nattn][S][heads][cap][dh], or packed (kpack set, AttnStepArgs' layout per attention
+    // block: words [nattn][S][heads][cap][3 dh / 4], scales [nattn][S][heads][cap])
     int32_t* pos = nullptr; float* g = nullptr; float* norm_ring = nullptr; float* kring = nullptr; float* vring = nullptr;
+    uint32_t* kpack = nullptr; uint32_t* vpack = nullptr; float* kscale = nullptr; float* vscale = nullptr;
     const int32_t* ids = nullptr;        // [S]
     float* logits = nullptr;             // [S][V] or null
     int32_t* argmax = nullptr;           // [S] or null
@@ -234,6 +246,9 @@ hipError_t launch_export_ring(int B, int T, int Dp, int ring, const int32_t* len
                               hipStream_t s);
 hipError_t launch_export_kv(int B, int T, int D, int heads, int cap, const int32_t* lens, const float* qkv,
                             float* kring, float* vring, hipStream_t s);
+// The same into packed rings (AttnStepArgs::kpack's layout; head width a multiple of 4).
+hipError_t launch_export_kv_packed(int B, int T, int D, int heads, int cap, const int32_t* lens, const float* qkv,
+                                   uint32_t* kpack, uint32_t* vpack, float* kscale, float* vscale, hipStream_t s);
 // pos[i] = (lens ? lens[i] : pos[i]) + add; with col set, also advances the decode column *col by one.
 hipError_t launch_set_pos(int S, const int32_t* lens, int32_t* pos, int add, hipStream_t s, int32_t* col = nullptr);
 hipError_t launch_fill_i32(int32_t* p, int n, int v, hipStream_t s);

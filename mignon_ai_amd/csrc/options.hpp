@@ -15,6 +15,9 @@ enum Option : int {
     OPT_OPERANDS = 5,          // batched forward: 0 automatic, 1 limb planes written by a row pass before every
                                // GEMM, 2 the GLU output and the attention output read as fp32 by the GEMMs
                                // that take them (expanded to digits as they are loaded), where they fit
+    OPT_KV_RINGS = 6,          // session K/V rings, chosen when a set is created: 0 automatic (packed where
+                               // the decode attention kernels built on rk_head take the model), 1 fp32,
+                               // 2 packed (24-bit mantissas with a power-of-two scale per row), where they fit
     OPT_COUNT
 };
 

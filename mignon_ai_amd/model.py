@@ -307,7 +307,8 @@ def quantize_f32(w):
 
 _OPTIONS = {"gemm": (0, ["auto", "stream", "slab"]), "attention": (1, ["auto", "exact", "mfma", "fused"]),
             "scan": (2, ["auto", "separate", "fused"]), "step_graph": (3, ["auto", "off", "on"]),
-            "step_kernel": (4, ["auto", "layered", "fused", "tiled"]), "operands": (5, ["auto", "limbs", "fp32"])}
+            "step_kernel": (4, ["auto", "layered", "fused", "tiled"]), "operands": (5, ["auto", "limbs", "fp32"]),
+            "kv_rings": (6, ["auto", "fp32", "packed"])}
 
 
 def sample_logits(logits, recent=None, temperature=1.0, top_k=0, top_p=1.0, rep_penalty=1.0, u=None):
@@ -339,7 +340,9 @@ def engine_option(name: str, value: str | None = None) -> str:
     "on"), "step_kernel" (decode steps: "auto", "layered", "fused": one workgroup per session, "tiled":
     one per 16 sessions) or "operands" (batched forward: "auto", "limbs": every GEMM operand's limb planes
     written by a pass of their own, "fp32": the GLU and attention outputs read as fp32 by the GEMMs that
-    take them), for the whole process. Returns the previous value (value None only reads it)."""
+    take them) or "kv_rings" (session K/V rings, fixed when a set is created: "auto" or "packed": 24-bit
+    mantissas with a power-of-two scale per row where the decode attention kernels take the model,
+    "fp32"), for the whole process. Returns the previous value (value None only reads it)."""
     opt, names = _OPTIONS[name]
     prev = lib().mg_engine_option(opt, -1 if value is None else names.index(value))
     check(prev if prev < 0 else 0)

@@ -34,6 +34,30 @@ def assert_close(got, ref, rtol=RTOL, what="values"):
     return worst
 
 
+def kv_pack(x):
+    """The packed K/V ring format (the engine's packed session rings; no reference counterpart): each row
+    x[..., :dh] (dh a multiple of 4) as dh/4 groups of three uint32 words holding four 24-bit
+    two's-complement mantissas m, and one scale 2^e per row, so that the element is m * 2^e. e = E - 23 for
+    the row's largest magnitude amax = f * 2^E (f in [0.5, 1)), at least -120; m = round half to even of
+    x * 2^-e, clamped to +-(2^23 - 1). Returns (words uint32 [..., 3 dh / 4], scales float32 [...])."""
+    x = np.asarray(x, np.float32)
+    e = np.maximum(np.frexp(np.abs(x).max(-1))[1] - 23, -120)
+    m = np.clip(np.rint(np.ldexp(x, -e[..., None])), -8388607, 8388607).astype(np.int64) & 0xFFFFFF
+    u = m.reshape(*m.shape[:-1], -1, 4)
+    w = np.stack([u[..., 0] | (u[..., 1] << 24), (u[..., 1] >> 8) | (u[..., 2] << 16),
+                  (u[..., 2] >> 16) | (u[..., 3] << 8)], -1) & 0xFFFFFFFF
+    return w.reshape(*x.shape[:-1], -1).astype(np.uint32), np.ldexp(np.float32(1), e).astype(np.float32)
+
+
+def kv_unpack(words, scales):
+    """Inverse of kv_pack: fp32 rows [..., dh] (exact: a 24-bit integer times a power of two)."""
+    w = np.asarray(words, np.int64).reshape(*np.shape(words)[:-1], -1, 3)
+    u = np.stack([w[..., 0], (w[..., 0] >> 24) | (w[..., 1] << 8), (w[..., 1] >> 16) | (w[..., 2] << 16),
+                  w[..., 2] >> 8], -1) & 0xFFFFFF
+    m = np.where(u >= 1 << 23, u - (1 << 24), u).reshape(*np.shape(words)[:-1], -1)
+    return (m.astype(np.float64) * np.asarray(scales, np.float64)[..., None]).astype(np.float32)
+
+
 @functools.lru_cache(maxsize=None)
 def model_bytes(name: str, seed: int = 1) -> bytes:
     spec = synth.CONFIGS[name]["spec"]

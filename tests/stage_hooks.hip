@@ -81,4 +81,29 @@ int mgt_attention_step(const int32_t* pos, const float* qkv, float* kring, float
     return finish(mg::launch_attention_step(a, nullptr));
 }
 
+// Decode attention on packed rings (kpack/vpack: [S][heads][cap][3 dh / 4] words, kscale/vscale:
+// [S][heads][cap]); kernel 0: launch_attention_step's choice (attention_step_rk), 2: the kernel fused
+// with the limb expansion of its output (xl, xs instead of att).
+int mgt_attention_step_packed(const int32_t* pos, const float* qkv, uint32_t* kpack, uint32_t* vpack, float* kscale,
+                              float* vscale, int S, int D, int Dp, int heads, int window, int cap, float* att,
+                              int8_t* xl, float* xs, int kernel) {
+    mg::AttnStepArgs a;
+    a.S = S; a.D = D; a.Dp = Dp; a.heads = heads; a.window = window; a.cap = cap;
+    a.pos = pos; a.qkv = qkv; a.att = att;
+    a.kpack = kpack; a.vpack = vpack; a.kscale = kscale; a.vscale = vscale;
+    if (kernel == 2) {
+        if (!mg::attention_step_rows_fits(a)) return (int)hipErrorInvalidValue;
+        a.xl = xl; a.xs = xs;
+        return finish(mg::launch_attention_step_rows(a, nullptr));
+    }
+    return finish(mg::launch_attention_step(a, nullptr));
+}
+
+// A batched prefill's K/V export into packed rings: B sequences of T rows of qkv ([B][T][3D]), the last
+// min(lens[b], cap) positions of each.
+int mgt_export_kv_packed(int B, int T, int D, int heads, int cap, const int32_t* lens, const float* qkv,
+                         uint32_t* kpack, uint32_t* vpack, float* kscale, float* vscale) {
+    return finish(mg::launch_export_kv_packed(B, T, D, heads, cap, lens, qkv, kpack, vpack, kscale, vscale, nullptr));
+}
+
 }  // extern "C"

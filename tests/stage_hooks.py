@@ -76,6 +76,8 @@ def lib():
             "mgt_latch_scan": [p, p, i, i, i, i, p],
             "mgt_attention": [p, i, i, i, i, i, i, i, p, i],
             "mgt_attention_step": [p, p, p, p, i, i, i, i, i, i, p, p, p, i],
+            "mgt_attention_step_packed": [p, p, p, p, p, p, i, i, i, i, i, i, p, p, p, i],
+            "mgt_export_kv_packed": [i, i, i, i, i, p, p, p, p, p, p],
         }
         for name, args in sig.items():
             fn = getattr(L, name)

@@ -68,10 +68,12 @@ def test_engine_option_validates():
     assert L.mg_engine_option(_lib.MG_OPT_GEMM_KERNEL, 3) == _lib.MG_ERR_INVALID
     assert L.mg_engine_option(_lib.MG_OPT_STEP_KERNEL, 4) == _lib.MG_ERR_INVALID
     assert L.mg_engine_option(_lib.MG_OPT_OPERANDS, 3) == _lib.MG_ERR_INVALID
+    assert L.mg_engine_option(_lib.MG_OPT_KV_RINGS, 3) == _lib.MG_ERR_INVALID
     for opt, val in ((_lib.MG_OPT_GEMM_KERNEL, _lib.MG_GEMM_SLAB), (_lib.MG_OPT_ATTENTION_KERNEL, _lib.MG_ATTN_EXACT),
                      (_lib.MG_OPT_SCAN_KERNEL, _lib.MG_SCAN_FUSED), (_lib.MG_OPT_STEP_GRAPH, _lib.MG_STEP_EAGER),
                      (_lib.MG_OPT_STEP_KERNEL, _lib.MG_STEP_LAYERED), (_lib.MG_OPT_STEP_KERNEL, _lib.MG_STEP_TILED),
-                     (_lib.MG_OPT_OPERANDS, _lib.MG_OPERANDS_LIMBS), (_lib.MG_OPT_OPERANDS, _lib.MG_OPERANDS_FP32)):
+                     (_lib.MG_OPT_OPERANDS, _lib.MG_OPERANDS_LIMBS), (_lib.MG_OPT_OPERANDS, _lib.MG_OPERANDS_FP32),
+                     (_lib.MG_OPT_KV_RINGS, _lib.MG_KV_FP32), (_lib.MG_OPT_KV_RINGS, _lib.MG_KV_PACKED)):
         prev = L.mg_engine_option(opt, val)
         assert prev in (0, 1, 2)
         assert L.mg_engine_option(opt, -1) == val
@@ -84,5 +86,6 @@ def test_stage_hooks_load_against_the_engine():
     import stage_hooks
 
     L = stage_hooks.lib()
-    for name in ("mgt_row", "mgt_latch_scan", "mgt_attention", "mgt_attention_step"):
+    for name in ("mgt_row", "mgt_latch_scan", "mgt_attention", "mgt_attention_step", "mgt_attention_step_packed",
+                 "mgt_export_kv_packed"):
         assert hasattr(L, name)

@@ -17,7 +17,7 @@ import pytest
 import torch
 
 import stage_hooks as H
-from helpers import assert_close
+from helpers import assert_close, kv_pack, kv_unpack
 from mignon_ai_amd import engine_option
 from oracle import oracle as O
 
@@ -223,3 +223,90 @@ def test_decode_attention_bitwise(D, heads, window, cap, kernels):
             assert np.array_equal(host(xl), host(rl)) and np.array_equal(bits(host(xs)), bits(host(rs)))
         else:
             assert np.array_equal(bits(host(att)[:, :D]), bits(want)), kernel
+
+
+PACKED_CASES = [
+    # D, heads, window, cap
+    (64, 2, 0, 32),     # dh 32
+    (256, 8, 0, 64),    # c4's shape
+    (96, 4, 6, 64),     # window 6 inside a cache of 64
+    (80, 4, 0, 48),     # dh 20: groups of a row not 16-byte aligned
+    (512, 8, 0, 64),    # dh 64
+]
+
+
+@pytest.mark.parametrize("D,heads,window,cap", PACKED_CASES)
+@pytest.mark.parametrize("kernel", [0, 2])
+def test_decode_attention_packed_rings(D, heads, window, cap, kernel):
+    """Decode attention on packed rings (attention_step_rk through launch_attention_step, and the rows
+    kernel): the output is bit-identical to the reference order over the rings' decoded values (the
+    current position's key and value in fp32), and the new row is written exactly as the host codec
+    packs it."""
+    rng = np.random.default_rng(D * cap + window + 7)
+    dh, Dp = D // heads, p64(D)
+    pos = np.array([0, 1, cap - 1, cap, cap + 5, 2 * cap + 3], np.int32)
+    S, T = len(pos), int(pos.max()) + 1
+    qkv = _qkv(rng, S, T, D)
+    # stale rows outside a span, as in a ring written before
+    kr = (rng.standard_normal((S, heads, cap, dh)) * 1e3).astype(np.float32)
+    vr = (rng.standard_normal((S, heads, cap, dh)) * 1e3).astype(np.float32)
+    want = np.empty((S, D), np.float32)
+    for i, p in enumerate(pos):
+        seq = qkv[i].copy()
+        for j in range(max(0, p - cap + 1), p):  # the ring before position p (slot j % cap)
+            kr[i, :, j % cap] = seq[j, D:2 * D].reshape(heads, dh)
+            vr[i, :, j % cap] = seq[j, 2 * D:].reshape(heads, dh)
+            # the oracle sees the values the ring holds
+            seq[j, D:2 * D] = kv_unpack(*kv_pack(seq[j, D:2 * D].reshape(heads, dh))).ravel()
+            seq[j, 2 * D:] = kv_unpack(*kv_pack(seq[j, 2 * D:].reshape(heads, dh))).ravel()
+        want[i] = O.attend_seq(seq[None, :p + 1], heads, window, cap)[0, p]
+    kw, ks = kv_pack(kr)
+    vw, vs_ = kv_pack(vr)
+    rows = np.stack([qkv[i, p] for i, p in enumerate(pos)])
+    pd, rd = dev(pos), dev(rows)
+    k, v = dev(kw.view(np.int32)), dev(vw.view(np.int32))
+    kscl, vscl = dev(ks), dev(vs_)
+    att = torch.full((S, Dp), float("nan"), device="cuda")
+    xl = torch.zeros(((S + 15) // 16) * 3 * Dp * 16, dtype=torch.int8, device="cuda")
+    xs = torch.zeros(S, device="cuda")
+    H.call("mgt_attention_step_packed", H.ptr(pd), H.ptr(rd), H.ptr(k), H.ptr(v), H.ptr(kscl), H.ptr(vscl), S, D,
+           Dp, heads, window, cap, H.ptr(att), H.ptr(xl), H.ptr(xs), kernel)
+    nk, nv = kv_pack(rows[:, D:2 * D].reshape(S, heads, dh)), kv_pack(rows[:, 2 * D:].reshape(S, heads, dh))
+    gk, gv = host(k).view(np.uint32), host(v).view(np.uint32)
+    for i, p in enumerate(pos):  # the new key and value went to slot p % cap, packed as the codec packs them
+        assert np.array_equal(gk[i, :, p % cap], nk[0][i]) and np.array_equal(host(kscl)[i, :, p % cap], nk[1][i])
+        assert np.array_equal(gv[i, :, p % cap], nv[0][i]) and np.array_equal(host(vscl)[i, :, p % cap], nv[1][i])
+    if kernel == 2:
+        rl = torch.zeros_like(xl)
+        rs = torch.zeros_like(xs)
+        wd = dev(pad_cols(want, Dp))
+        H.call("mgt_row", H.ptr(wd), S, D, Dp, None, None, H.ptr(rl), H.ptr(rs))
+        assert np.array_equal(host(xl), host(rl)) and np.array_equal(bits(host(xs)), bits(host(rs)))
+    else:
+        assert np.array_equal(bits(host(att)[:, :D]), bits(want))
+
+
+def test_export_kv_packed():
+    """A prefill's K/V export into packed rings: the last min(len, cap) positions of each sequence, each
+    (head, position) row packed as the host codec packs it; other slots untouched."""
+    rng = np.random.default_rng(11)
+    B, T, D, heads, cap = 5, 40, 96, 4, 16
+    dh = D // heads
+    qkv = _qkv(rng, B, T, D)
+    lens = np.array([1, 7, 16, 17, 40], np.int32)
+    words = rng.integers(0, 1 << 32, size=(2, B, heads, cap, 3 * dh // 4), dtype=np.uint64).astype(np.uint32)
+    scl = rng.standard_normal((2, B, heads, cap)).astype(np.float32)
+    dk, dv = dev(words[0].view(np.int32)), dev(words[1].view(np.int32))
+    dks, dvs = dev(scl[0]), dev(scl[1])
+    dl, dq = dev(lens), dev(qkv)  # referenced until the hook returns
+    H.call("mgt_export_kv_packed", B, T, D, heads, cap, H.ptr(dl), H.ptr(dq), H.ptr(dk), H.ptr(dv), H.ptr(dks),
+           H.ptr(dvs))
+    got_w = [host(dk).view(np.uint32), host(dv).view(np.uint32)]
+    got_s = [host(dks), host(dvs)]
+    for part in range(2):
+        ew, es = words[part].copy(), scl[part].copy()
+        for b in range(B):
+            for p in range(max(0, lens[b] - cap), lens[b]):
+                w, s_ = kv_pack(qkv[b, p, (1 + part) * D:(2 + part) * D].reshape(heads, dh))
+                ew[b, :, p % cap], es[b, :, p % cap] = w, s_
+        assert np.array_equal(got_w[part], ew) and np.array_equal(bits(got_s[part]), bits(es))
