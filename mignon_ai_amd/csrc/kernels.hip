@@ -1037,8 +1037,14 @@ __global__ __launch_bounds__(64 * G) void attention_mfma_kernel(AttnArgs a, int 
 // are written in after the scores. Scores, softmax and P.V then run exactly as in attention_mfma_kernel
 // with one group of G = 8 tiles, so the output is the same bit for bit, without the fp32 q/k/v round trip
 // through memory.
+// Waves per SIMD the compiler allocates registers for: two (up to 256 registers) in general; four (at most
+// 128, so that two 8-wave workgroups share a CU) for narrow heads with short windows over small models,
+// whose LDS (about 47 KiB at D = 128) leaves room for the second workgroup.
+constexpr int qkv_attn_waves(int ND, int NKB, int KC) { return ND == 2 && NKB <= 5 && KC == 2 ? 4 : 2; }
+
 template <int ND, int NKB, int KC>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void qkv_attention_kernel(
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(qkv_attn_waves(ND, NKB, KC),
+                                                                     qkv_attn_waves(ND, NKB, KC)))) void qkv_attention_kernel(
     QkvAttnArgs a, int run_seqs, int n_runs) {
     constexpr int G = 8;
     constexpr int DP = 16 * ND;               // head width
