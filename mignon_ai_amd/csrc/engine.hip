@@ -270,8 +270,12 @@ struct mg_sessions {
             ws_gen = -1;
         }
     } graph;
+    // kStepsPerGraph consecutive steps of a batched greedy decode captured as one graph (fewer graph
+    // boundaries, each of which leaves the device idle for several microseconds)
+    StepGraph graph_multi;
     ~mg_sessions() {
         graph.reset();
+        graph_multi.reset();
         for (hipEvent_t& e : stop_ev)
             if (e) (void)hipEventDestroy(e);
         if (stop_host) (void)hipHostFree(stop_host);
@@ -1783,16 +1787,22 @@ const int32_t* start_columns(mg_sessions* s, hipStream_t st) {
 // through hc.col (device memory the step advances), so one graph serves every column. The graph is
 // captured again when the workspace was reallocated, an option changed or the arguments differ; if
 // capture fails the set falls back to launching kernel by kernel.
-void step_graphed(mg_sessions* s, const int32_t* ids_d, float* logits_d, const HeadCombineArgs& hc, hipStream_t st) {
+// Steps of a batched greedy decode replayed from one graph (where the decode has no per-step host work).
+constexpr int kStepsPerGraph = 8;
+
+// `nsteps` consecutive steps (1, or kStepsPerGraph for a batched decode whose output column advances on
+// the device) replayed from one captured graph, or launched kernel by kernel where graphs are off.
+void step_graphed(mg_sessions* s, const int32_t* ids_d, float* logits_d, const HeadCombineArgs& hc, hipStream_t st,
+                  int nsteps = 1) {
     mg_model* m = s->m;
     const int mode = option(OPT_STEP_GRAPH);
-    auto& G = s->graph;
+    auto& G = nsteps == 1 ? s->graph : s->graph_multi;
     // A step that is one kernel (the single-workgroup step, outside a batched decode) is launched directly
     // unless graphs are forced: a graph launch costs more than the one kernel launch it would replace.
     Step1Args one;
     const bool one_kernel = mode == 0 && !hc.col && !hc.lse && !hc.logprob && step1_args(s, ids_d, logits_d, hc, one);
     if (mode == 1 || m->prof.on || G.failed || one_kernel) {
-        step_device(s, ids_d, logits_d, hc, st);
+        for (int i = 0; i < nsteps; i++) step_device(s, ids_d, logits_d, hc, st);
         return;
     }
     ensure_ws(m, s->n);  // before any capture: no allocation may happen inside one
@@ -1807,7 +1817,7 @@ void step_graphed(mg_sessions* s, const int32_t* ids_d, float* logits_d, const H
         bool ok = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) == hipSuccess;
         if (ok) {
             try {
-                step_device(s, ids_d, logits_d, hc, st);
+                for (int i = 0; i < nsteps; i++) step_device(s, ids_d, logits_d, hc, st);
             } catch (const Error&) {
                 ok = false;
             }
@@ -1819,7 +1829,7 @@ void step_graphed(mg_sessions* s, const int32_t* ids_d, float* logits_d, const H
             (void)hipGetLastError();
             G.reset();
             G.failed = true;
-            step_device(s, ids_d, logits_d, hc, st);
+            for (int i = 0; i < nsteps; i++) step_device(s, ids_d, logits_d, hc, st);
             return;
         }
         G.ws_gen = ws_of(m).gen;
@@ -1955,7 +1965,10 @@ int mg_sessions_decode_greedy(mg_sessions* s, const int32_t* prompts, const int3
         hc.out_ids = oi; hc.out_probs = op; hc.out_ld = max_tokens; hc.out_col = 0;
         prefill_device(s, p_d, l_d, max_len, nullptr, hc, st);
         hc.col = start_columns(s, st);
-        for (int k = 1; k < max_tokens; k++) step_graphed(s, s->next_ids.as<int32_t>(), nullptr, hc, st);
+        int k = 1;
+        for (; k + kStepsPerGraph <= max_tokens; k += kStepsPerGraph)
+            step_graphed(s, s->next_ids.as<int32_t>(), nullptr, hc, st, kStepsPerGraph);
+        for (; k < max_tokens; k++) step_graphed(s, s->next_ids.as<int32_t>(), nullptr, hc, st);
         if (!dev) {
             HIPCHECK(hipMemcpyAsync(out_ids, oi, (size_t)S * max_tokens * 4, hipMemcpyDeviceToHost, st));
             if (out_probs) HIPCHECK(hipMemcpyAsync(out_probs, op, (size_t)S * max_tokens * 8, hipMemcpyDeviceToHost, st));

@@ -65,8 +65,10 @@ def test_graph_single_session_matches_oracle(restore_graph):
 @pytest.mark.parametrize("cfg", ["c4", "c3"])
 def test_graph_decodes_equal_eager(restore_graph, cfg):
     """Batched decodes (greedy, greedy with stop tokens, sampled) replay one captured step for every column
-    (the column advances in device memory): the same tokens, probabilities and reply lengths as launching
-    each step kernel by kernel, with eager work on the model between the calls."""
+    (the column advances in device memory; the greedy decode replays eight steps per graph, then single
+    steps for the rest): the same tokens, probabilities and reply lengths as launching each step kernel by
+    kernel, with eager work on the model between the calls (a second greedy decode, of exactly two
+    eight-step graphs, after the workspace was reallocated)."""
     data = model_bytes(cfg)
     spec = synth.CONFIGS[cfg]["spec"]
     prompts = synth.token_ids(11, f"graph-dec:{cfg}", (24, 7), spec.V)
@@ -82,9 +84,12 @@ def test_graph_decodes_equal_eager(restore_graph, cfg):
         b = ss.decode_greedy_until(prompts, 30, stops, lens)
         c = ss.decode_sample(prompts, 30, list(range(24)), temperature=0.8, top_k=20, top_p=0.9, rep_penalty=1.1,
                              stops=stops, lens=lens)
-        res[mode] = (a, b, c)
-    (ea, eb, ec), (ga, gb, gc) = res["off"], res["on"]
+        m.forward_batch(synth.token_ids(13, "graph-dec:batch2", (80, 16), spec.V))
+        d = ss.decode_greedy(prompts, 17, lens)
+        res[mode] = (a, b, c, d)
+    (ea, eb, ec, ed), (ga, gb, gc, gd) = res["off"], res["on"]
     assert np.array_equal(ea[0], ga[0]) and np.array_equal(ea[1].view(np.uint64), ga[1].view(np.uint64))
+    assert np.array_equal(ed[0], gd[0]) and np.array_equal(ed[1].view(np.uint64), gd[1].view(np.uint64))
     assert np.array_equal(eb[2], gb[2]) and (eb[2] < 30).any()
     for i in range(24):
         k = eb[2][i]
