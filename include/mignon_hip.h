@@ -338,7 +338,8 @@ int mg_quantize_f32(const float* w, long long n, int8_t* q, float* scale, int fl
  *     rings apply where the fused decode attention kernel takes the model (head width a multiple of 4 up
  *     to 64, caches of at most 64 positions, at most 16 heads); elsewhere fp32. The layered, fused and
  *     tiled steps give bit-identical results to each other under either format. Automatic is
- *     MG_KV_PACKED.
+ *     MG_KV_PACKED for sets of more than 256 sessions (where decode attention streams many rings) and
+ *     MG_KV_FP32 for smaller ones (a step that is a chain of dependent phases, which decoding lengthens).
  * value < 0 only reads the option. Returns the previous value, or MG_ERR_INVALID. */
 #define MG_OPT_GEMM_KERNEL 0
 #define MG_OPT_ATTENTION_KERNEL 1

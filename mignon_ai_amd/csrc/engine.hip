@@ -286,11 +286,18 @@ struct mg_sessions {
 namespace mg {
 namespace {
 
-// Whether a new session set of this model keeps packed K/V rings: the decode attention of every step
-// kernel that can run on the set (attention_step_rows, step1's rk_head) reads them where the rows kernel
-// fits the model, and OPT_KV_RINGS does not ask for fp32.
-bool kv_rings_packed(const mg_model* m) {
-    if (m->nattn <= 0 || option(OPT_KV_RINGS) == 1) return false;
+// Sets of up to this many sessions take the one-workgroup-per-session step automatically.
+constexpr int kStep1MaxSessions = 256;
+
+// Whether a new session set of n sessions of this model keeps packed K/V rings: the decode attention of
+// every step kernel that can run on the set (attention_step_rows, step1's rk_head) reads them where the
+// rows kernel fits the model. Automatic for sets larger than the one-workgroup step takes: there decode
+// attention streams the rings of thousands of sessions and reads a quarter fewer bytes; a small set's step
+// is a chain of dependent phases, where decoding the rows only lengthens it (one session's Append 58 ->
+// 61 us with packed rings).
+bool kv_rings_packed(const mg_model* m, int n) {
+    const int opt = option(OPT_KV_RINGS);
+    if (m->nattn <= 0 || opt == 1 || (opt == 0 && n <= kStep1MaxSessions)) return false;
     AttnStepArgs a;
     a.S = 1; a.D = m->D; a.Dp = m->Dp; a.heads = m->heads; a.window = m->window; a.cap = m->cap;
     return attention_step_rows_fits(a);
@@ -1530,7 +1537,7 @@ int mg_sessions_create(mg_model* m, int n, int context, mg_sessions** out) {
         const size_t Dp = m->Dp, D = m->D;
         s->norm_ring.ensure(std::max<size_t>(16, (size_t)m->nbs * n * m->ring * Dp * 4));
         s->g.ensure(std::max<size_t>(16, (size_t)m->nbs * n * Dp * 4));
-        s->kv_packed = kv_rings_packed(m);
+        s->kv_packed = kv_rings_packed(m, n);
         // packed: 3 bytes per element and a 4-byte scale per (head, slot) row; fp32: 4 bytes per element
         const size_t ring_bytes = (size_t)m->nattn * n * m->cap * D * (s->kv_packed ? 3 : 4);
         s->kring.ensure(std::max<size_t>(16, ring_bytes));
@@ -1599,8 +1606,8 @@ void prefill_device(mg_sessions* s, const int32_t* prompts_d, const int32_t* len
     HIPCHECK(launch_set_pos(S, lens_w, s->pos.as<int32_t>(), 0, st));
 }
 
-// The one-workgroup-per-session step for this set, when the option and the shapes allow it.
-constexpr int kStep1MaxSessions = 256;  // automatic selection: sets up to this size
+// The one-workgroup-per-session step for this set, when the option and the shapes allow it (automatically
+// for sets of up to kStep1MaxSessions).
 // The arguments both single-kernel steps share.
 bool step1_args_fill(mg_sessions* s, const int32_t* ids_d, float* logits_d, const HeadCombineArgs& hc, Step1Args& a) {
     mg_model* m = s->m;

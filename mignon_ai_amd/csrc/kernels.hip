@@ -1496,11 +1496,20 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
     }
     // record this position's key and value (slot pos % cap; the evicted key is outside the window)
     if constexpr (PK) {
-        // the row's largest magnitude over the C4 lanes holding it (every lane takes part in the shuffles)
+        // the row's largest magnitude over the C4 lanes holding it (every lane takes part): for C4 a power
+        // of two the groups are aligned quads, half-rows and rows, reduced by DPP moves; else by shuffles
         const float am = fmaxf(fmaxf(fabsf(mine.x), fabsf(mine.y)), fmaxf(fabsf(mine.z), fabsf(mine.w)));
-        float rm = 0.0f;
+        float rm = am;
+        if constexpr ((C4 & (C4 - 1)) == 0) {
+            if constexpr (C4 >= 2) rm = fmaxf(rm, dpp_move<0xB1>(rm));   // quad_perm [1, 0, 3, 2]
+            if constexpr (C4 >= 4) rm = fmaxf(rm, dpp_move<0x4E>(rm));   // quad_perm [2, 3, 0, 1]
+            if constexpr (C4 >= 8) rm = fmaxf(rm, dpp_move<0x141>(rm));  // row_half_mirror
+            if constexpr (C4 >= 16) rm = fmaxf(rm, dpp_move<0x140>(rm)); // row_mirror
+        } else {
+            rm = 0.0f;
 #pragma unroll
-        for (int i = 0; i < C4; i++) rm = fmaxf(rm, __shfl(am, qpart * C4 + i, 64));
+            for (int i = 0; i < C4; i++) rm = fmaxf(rm, __shfl(am, qpart * C4 + i, 64));
+        }
         if (lane >= C4 && lane < 3 * C4) {
             const int e = kv_exp(rm);
             const long long r = row0 + pos % cap;
@@ -2011,7 +2020,9 @@ __device__ __forceinline__ void ts_matvec(const int8_t* W, const float* bias, in
     }
 }
 
-template <int DH>
+// PK: the set's K/V rings are packed (a separate instantiation, so that the fp32-ring kernel, which the
+// latency-bound small sets take, carries none of the packed path's code).
+template <int DH, bool PK>
 __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
     extern __shared__ __align__(16) float s1_smem[];
     __shared__ float red[16];
@@ -2203,7 +2214,7 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
                 sa_.qkv = qkv;
                 const long long rows0 = ((long long)ab * a.S + s_) * a.heads * a.cap;  // ring rows before this one's
                 float o;
-                if (a.kpack) {
+                if constexpr (PK) {
                     sa_.kpack = a.kpack + rows0 * kv_row_words(DH);
                     sa_.vpack = a.vpack + rows0 * kv_row_words(DH);
                     sa_.kscale = a.kscale + rows0;
@@ -3488,14 +3499,19 @@ bool step1_fits(const Step1Args& a) {
     return step1_lds_bytes(a, dh) <= 150 * 1024;
 }
 
-template <int DH>
-hipError_t step1_t(const Step1Args& a, hipStream_t s) {
+template <int DH, bool PK>
+hipError_t step1_pk_t(const Step1Args& a, hipStream_t s) {
     const size_t lds = step1_lds_bytes(a, DH);
-    static const hipError_t attr = hipFuncSetAttribute((const void*)step1_kernel<DH>,
+    static const hipError_t attr = hipFuncSetAttribute((const void*)step1_kernel<DH, PK>,
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL(step1_kernel<DH>, dim3(a.S), dim3(S1_THREADS), lds, s, a);
+    hipLaunchKernelGGL((step1_kernel<DH, PK>), dim3(a.S), dim3(S1_THREADS), lds, s, a);
     return hipGetLastError();
+}
+
+template <int DH>
+hipError_t step1_t(const Step1Args& a, hipStream_t s) {
+    return a.kpack ? step1_pk_t<DH, true>(a, s) : step1_pk_t<DH, false>(a, s);
 }
 
 bool tile_step_fits(const TileStepArgs& a) {
