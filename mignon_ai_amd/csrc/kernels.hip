@@ -3145,10 +3145,14 @@ hipError_t attn_mfma_g(const AttnArgs& a, int dh, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Eight query tiles per workgroup where sequences have at least six (fewer would leave waves idle).
+// Eight query tiles per workgroup where sequences have at least six, four from three, two for sequences of
+// one or two tiles (a wave past the sequence's last tile computes a tile that is never stored: with four
+// per workgroup, half of a 32-token prefill's waves did).
 template <int ND, int NKB>
 hipError_t attn_mfma_t(const AttnArgs& a, int dh, hipStream_t s) {
-    return (a.T + 15) / 16 >= 6 ? attn_mfma_g<ND, NKB, 8>(a, dh, s) : attn_mfma_g<ND, NKB, 4>(a, dh, s);
+    const int qtiles = (a.T + 15) / 16;
+    if (qtiles >= 6) return attn_mfma_g<ND, NKB, 8>(a, dh, s);
+    return qtiles >= 3 ? attn_mfma_g<ND, NKB, 4>(a, dh, s) : attn_mfma_g<ND, NKB, 2>(a, dh, s);
 }
 
 // Key blocks per 16-query tile: the widest span any query attends is W = min(window, cap) keys, so the
