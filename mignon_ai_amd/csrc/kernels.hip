@@ -3097,6 +3097,38 @@ __global__ __launch_bounds__(256) void export_kv_packed_kernel(int B, int T, int
     }
 }
 
+// The same where a row's C4 = dh/4 groups (a power of two up to 16) sit on an aligned quad, half-row or
+// row of lanes: one lane per group of [k | v] (a wave takes 64 groups at a time, whole rows), the row's
+// largest magnitude by DPP moves, no LDS. Same rows and bytes as export_kv_packed_kernel.
+template <int C4>
+__global__ __launch_bounds__(256) void export_kv_packed_dpp_kernel(int B, int T, int D, int heads, int cap,
+                                                                   const int32_t* lens, const float* qkv,
+                                                                   uint32_t* kpack, uint32_t* vpack, float* kscale,
+                                                                   float* vscale) {
+    const int b = blockIdx.x, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int len = min(max(lens[b], 0), T);
+    const int p0 = max(0, len - cap);
+    const int nc = D / 2;                        // groups of [k | v] per position
+    const int per = (nc + 63) / 64;              // 64-lane passes per position
+    for (int it = w; it < (len - p0) * per; it += 4) {
+        const int p = p0 + it / per, c = (it % per) * 64 + lane;
+        const bool ok = c < nc;
+        const float4 x = ldg((const float4*)(qkv + ((long long)b * T + p) * 3 * D + D + 4 * min(c, nc - 1)));
+        float m = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+        if constexpr (C4 >= 2) m = fmaxf(m, dpp_move<0xB1>(m));   // quad_perm [1, 0, 3, 2]
+        if constexpr (C4 >= 4) m = fmaxf(m, dpp_move<0x4E>(m));   // quad_perm [2, 3, 0, 1]
+        if constexpr (C4 >= 8) m = fmaxf(m, dpp_move<0x141>(m));  // row_half_mirror
+        if constexpr (C4 >= 16) m = fmaxf(m, dpp_move<0x140>(m)); // row_mirror
+        if (ok) {
+            const int r = c / C4, g = c % C4;  // row r: keys 0..heads-1, then values
+            const int part = r >= heads, h = r - part * heads, e = kv_exp(m);
+            const long long row = ((long long)b * heads + h) * cap + p % cap;
+            stg_pk3((Pk3*)(part ? vpack : kpack) + row * C4 + g, kv_pack(x, e));
+            if (g == 0) stg((part ? vscale : kscale) + row, ldexpf(1.0f, e));
+        }
+    }
+}
+
 __global__ void set_pos_kernel(int S, const int32_t* lens, int32_t* pos, int add, int32_t* col) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < S) pos[i] = (lens ? lens[i] : pos[i]) + add;
@@ -3586,6 +3618,20 @@ hipError_t launch_export_kv_packed(int B, int T, int D, int heads, int cap, cons
     if (B <= 0) return hipSuccess;
     if (heads <= 0 || D % heads != 0 || (D / heads) % 4) return hipErrorInvalidValue;
     if (D > 1024) return hipErrorInvalidValue;
+    switch (D / heads / 4) {
+#define MG_EXPORT_DPP(C)                                                                                        \
+    case C:                                                                                                     \
+        hipLaunchKernelGGL(export_kv_packed_dpp_kernel<C>, dim3(B), dim3(256), 0, s, B, T, D, heads, cap, lens, qkv, \
+                           kpack, vpack, kscale, vscale);                                                       \
+        return hipGetLastError();
+        MG_EXPORT_DPP(1)
+        MG_EXPORT_DPP(2)
+        MG_EXPORT_DPP(4)
+        MG_EXPORT_DPP(8)
+        MG_EXPORT_DPP(16)
+#undef MG_EXPORT_DPP
+        default: break;
+    }
     const size_t lds = (size_t)4 * export_kv_wave_floats(D, heads) * sizeof(float);
     hipLaunchKernelGGL(export_kv_packed_kernel, dim3(B), dim3(256), lds, s, B, T, D, heads, cap, lens, qkv, kpack,
                        vpack, kscale, vscale);

@@ -286,11 +286,14 @@ def test_decode_attention_packed_rings(D, heads, window, cap, kernel):
         assert np.array_equal(bits(host(att)[:, :D]), bits(want))
 
 
-def test_export_kv_packed():
+@pytest.mark.parametrize("D,heads", [(96, 4), (256, 8), (64, 1), (32, 2), (16, 2), (8, 2)])
+def test_export_kv_packed(D, heads):
     """A prefill's K/V export into packed rings: the last min(len, cap) positions of each sequence, each
-    (head, position) row packed as the host codec packs it; other slots untouched."""
-    rng = np.random.default_rng(11)
-    B, T, D, heads, cap = 5, 40, 96, 4, 16
+    (head, position) row packed as the host codec packs it; other slots untouched. Head widths 24 (the LDS
+    kernel) and 32, 64, 16, 8, 4 (the DPP kernel: a row's groups on an aligned half-row, row, quad, pair,
+    single lane)."""
+    rng = np.random.default_rng(11 + D)
+    B, T, cap = 5, 40, 16
     dh = D // heads
     qkv = _qkv(rng, B, T, D)
     lens = np.array([1, 7, 16, 17, 40], np.int32)
