@@ -1093,11 +1093,18 @@ struct StopTracker {
         hipLaunchKernelGGL(stop_init_kernel, dim3((S + 255) / 256), dim3(256), 0, st, S, cnt, stopped);
         HIPCHECK(hipGetLastError());
     }
+    // Without stop tokens no reply ends early: nothing to scan or copy (finish() gives every session `cut`
+    // columns); the event alone still keeps the host within kLag steps of the device, so that a
+    // cancellation takes effect at the next column.
     void scan(int col) {
+        const int slot = col % mg_sessions::kStopRing;
+        if (set.n == 0) {
+            HIPCHECK(hipEventRecord(s->stop_ev[slot], st));
+            return;
+        }
         hipLaunchKernelGGL(stop_scan_kernel, dim3((S + 255) / 256), dim3(256), 0, st, S, col, ids, max_tokens, set, cnt,
                            stopped);
         HIPCHECK(hipGetLastError());
-        const int slot = col % mg_sessions::kStopRing;
         HIPCHECK(hipMemcpyAsync(s->stop_host + slot, stopped, 4, hipMemcpyDeviceToHost, st));
         HIPCHECK(hipEventRecord(s->stop_ev[slot], st));
     }
@@ -1110,7 +1117,7 @@ struct StopTracker {
         if (c >= 0) {
             const int slot = c % mg_sessions::kStopRing;
             HIPCHECK(hipEventSynchronize(s->stop_ev[slot]));
-            if (s->stop_host[slot] >= S) return false;
+            if (set.n > 0 && s->stop_host[slot] >= S) return false;
         }
         if (cancelled()) {
             cut = k;
