@@ -2564,6 +2564,28 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
     int8_t* xl = (int8_t*)ts_smem + L.xl_off;
     const int kcD = Dp >> 6;
 
+    // A segment that starts with an out projection reads that projection's limb operand and row scales;
+    // every row's position (the ring slots of the latch updates, constant through the step) is read here
+    // too. These loads are all issued before the state rows' below, and nothing is stored before the
+    // last of them has been issued, so the segment's start costs one memory round trip.
+    constexpr int TS_AX = 3;  // 16-byte chunks of the limb operand per thread: kcD * 192 <= 1536 (Dp <= 512)
+    v4i ax[TS_AX];
+    float axs = 0.0f;
+    if (a.seg_out) {
+        const int8_t* src = a.att_xl + (long long)blockIdx.x * kcD * 3072;
+#pragma unroll
+        for (int u = 0; u < TS_AX; u++) {
+            const int c = tid + TS_THREADS * u;
+            ax[u] = c < kcD * 192 ? *(const v4i*)(src + c * 16) : v4i{0, 0, 0, 0};
+        }
+        if (tid < ns) axs = a.att_xs[s0 + tid];
+    }
+    int rpos[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int t = w + 8 * i;
+        rpos[i] = __builtin_amdgcn_readfirstlane(a.pos[s0 + (t < ns ? t : 0)]);
+    }
     // state rows (each wave its own): the embedding (quant.Model.appendPosition, ids clamped as
     // stream.go:144-146), or the previous segment's cur and blockIn; rows past the set are zero
 #pragma unroll
@@ -2600,9 +2622,12 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
     int b = a.seg_block;
     if (a.seg_out) {
         // the out projection of block b, whose attention has run: cur += att.W_o * s (attention.go:100-103)
-        const int8_t* src = a.att_xl + (long long)blockIdx.x * kcD * 3072;
-        for (int c = tid; c < kcD * 192; c += TS_THREADS) *(v4i*)(xl + c * 16) = *(const v4i*)(src + c * 16);
-        if (tid < TS_NS) rsc[tid] = tid < ns ? a.att_xs[s0 + tid] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < TS_AX; u++) {
+            const int c = tid + TS_THREADS * u;
+            if (c < kcD * 192) *(v4i*)(xl + c * 16) = ax[u];
+        }
+        if (tid < TS_NS) rsc[tid] = axs;  // zero past the set
         lds_barrier();
         const Step1Block& B = a.blocks[b];
         ts_matvec<TS_FRAG, 4, 2>(B.wo, nullptr, a.NpD / 16, kcD, a.NpD / 16, xl, lane, w, [&](int f, const float (&v)[4], float4) {
@@ -2675,7 +2700,7 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
                     const int t = w + 8 * i;
                     const bool ok = t < ns;
                     const int s = s0 + (ok ? t : 0);
-                    posr[i] = a.pos[s];
+                    posr[i] = rpos[i];
                     const float* gbase = a.g + ((long long)bs * a.S + s) * Dp;
                     const float* ring = a.norm_ring + ((long long)bs * a.S + s) * a.ring * Dp;
                     const int p = posr[i];
