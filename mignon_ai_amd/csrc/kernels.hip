@@ -1325,6 +1325,11 @@ __device__ __forceinline__ Pk3 ldg_pk3(const Pk3* p) {
     const __attribute__((address_space(1))) uint32_t* q = (const __attribute__((address_space(1))) uint32_t*)p;
     return Pk3{q[0], q[1], q[2]};
 }
+__device__ __forceinline__ Pk3 ldg_pk3_nt(const Pk3* p) {
+    typedef uint32_t u3 __attribute__((ext_vector_type(3)));
+    const u3 v = __builtin_nontemporal_load((const __attribute__((address_space(1))) u3*)p);
+    return Pk3{v.x, v.y, v.z};
+}
 
 __device__ __forceinline__ void stg_pk3(Pk3* p, Pk3 v) {
     __attribute__((address_space(1))) uint32_t* q = (__attribute__((address_space(1))) uint32_t*)p;
@@ -1358,7 +1363,12 @@ __host__ __device__ constexpr int rk_lds_floats(int cap, int dh, bool kcur = fal
 // the ring. PK: the rings are packed (kpack/kscale, vpack/vscale); the ring rows are decoded as they
 // are loaded, and the current position's key and value, which are not yet in the ring, come in fp32
 // (through LDS without QL: lanes C4..2C4-1 hold the key, 2C4..3C4-1 the value, as their `mine`).
-template <int DH, bool QL = false, bool PK = false>
+// ST (packed rings without QL, heads of at most 32): the rings are streamed, for sets whose rings are
+// larger than the caches. Key rows are then read like the value rows, consecutive lanes on consecutive
+// groups, with non-temporal loads, and reach their lanes through LDS: the loads no longer displace the
+// decode step's weights and code from the caches. With a row per lane, each cache line of the keys is
+// read by C4 loads and has to stay cached between them, which non-temporal loads do not allow.
+template <int DH, bool QL = false, bool PK = false, bool ST = false>
 __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, int lane, float* sm, float& inv_sh) {
     constexpr int DS = DH + 4;
     constexpr int C4 = DH / 4;
@@ -1393,6 +1403,11 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
         const Pk3 w = ldg_pk3((const Pk3*)ring + (row0 + sl) * C4 + c);
         return kv_unpack(w, ldg(scl + row0 + sl));
     };
+    auto pk4_nt = [&](const uint32_t* ring, const float* scl, int sl, int c) -> float4 {
+        const Pk3 w = ldg_pk3_nt((const Pk3*)ring + (row0 + sl) * C4 + c);
+        return kv_unpack(w, __builtin_nontemporal_load((const __attribute__((address_space(1))) float*)(scl + row0 + sl)));
+    };
+    constexpr bool KST = ST && CUR_LANES && C4 <= 8;
     // lanes 0..3*C4-1: one float4 each of this position's q, k and v (part lane / C4, chunk lane % C4)
     const int qpart = min(lane / C4, 2), qc = lane % C4;
     const float4 mine = qkv4(qkv + qpart * D + h * DH + 4 * qc);
@@ -1401,7 +1416,36 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
     auto slot = [&](int jj) { const int r = lo_slot + jj; return r >= cap ? r - cap : r; };
     // this lane's key row (key lo + lane; the current position's from qkv, not yet in the ring)
     float4 krow[C4];
-    {
+    if constexpr (KST) {
+        // key and value rows 0..span-2 with coalesced streaming loads (consecutive lanes on consecutive
+        // groups), every load issued before the first store; the keys pass through the value region of LDS
+        // to the lanes that score them, then the values take their place. The current position's key and
+        // value come from the lanes holding them.
+        const int nr = (span - 1) * C4;
+        float4 kb[8], vb[8];
+        int off[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int e = min(u * 64 + lane, max(nr - 1, 0));
+            const int jj = e / C4, c = e - jj * C4;
+            off[u] = jj * DS + 4 * c;
+            kb[u] = pk4_nt(a.kpack, a.kscale, slot(jj), c);
+            vb[u] = pk4_nt(a.vpack, a.vscale, slot(jj), c);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) *(float4*)(vs + off[u]) = kb[u];
+        if (qpart == 1 && lane < 2 * C4) *(float4*)(vs + (span - 1) * DS + 4 * qc) = mine;
+        wave_lds_sync();
+        {
+            const int jj = min(lane, span - 1);
+#pragma unroll
+            for (int c = 0; c < C4; c++) krow[c] = *(const float4*)(vs + jj * DS + 4 * c);
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int u = 0; u < 8; u++) *(float4*)(vs + off[u]) = vb[u];
+        if (qpart == 2 && lane < 3 * C4) *(float4*)(vs + (span - 1) * DS + 4 * qc) = mine;
+    } else {
         const int jj = min(lane, span - 1);
         if constexpr (PK) {
             // the ring row (the current position's slot is read too, in bounds, and its value replaced)
@@ -1433,7 +1477,7 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
     // end repeat the last element (the same bytes to the same address), so no store is conditional and
     // no load can be moved next to its store. Packed rings without QL: rows 0..span-2 from the ring, the
     // current position's row from the lanes holding it.
-    const int n4 = (CUR_LANES ? span - 1 : span) * C4;
+    const int n4 = KST ? 0 : (CUR_LANES ? span - 1 : span) * C4;
     for (int e0 = 0; e0 < n4; e0 += 8 * 64) {
         float4 vb[8];
         int off[8];
@@ -1458,13 +1502,13 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
 #pragma unroll
         for (int u = 0; u < 8; u++) *(float4*)(vs + off[u]) = vb[u];
     }
-    if constexpr (CUR_LANES) {
+    if constexpr (CUR_LANES && !KST) {
         if (qpart == 1 && lane < 2 * C4) *(float4*)(kc + 4 * qc) = mine;
         if (qpart == 2 && lane < 3 * C4) *(float4*)(vs + (span - 1) * DS + 4 * qc) = mine;
     }
     if (lane < C4) *(float4*)(qs + 4 * lane) = mine;
     wave_lds_sync();
-    if constexpr (CUR_LANES) {
+    if constexpr (CUR_LANES && !KST) {
         if (lane == span - 1) {
 #pragma unroll
             for (int c = 0; c < C4; c++) krow[c] = *(const float4*)(kc + 4 * c);
@@ -1541,14 +1585,14 @@ __global__ __launch_bounds__(64) void attention_step_rk_kernel(AttnStepArgs a) {
 // expansion of the attention output that the out projection reads: the row's absolute maximum over
 // all heads gives its scale, and each lane writes its element's three limbs (row_kernel's ROW_SRC
 // digits and scale, from the same values), so the output never goes through memory as fp32.
-// PK: packed rings.
-template <int DH, bool PK>
+// PK: packed rings; ST: streamed (rk_head).
+template <int DH, bool PK, bool ST = false>
 __global__ __launch_bounds__(1024) void attention_step_rows_kernel(AttnStepArgs a) {
     extern __shared__ __align__(16) float rows_smem[];
     __shared__ float inv_sh[16], red[16];
     const int s_ = blockIdx.x, h = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (a.done && a.done[s_] >= 0) return;  // a finished session of a batched decode (the whole workgroup)
-    const float o = rk_head<DH, false, PK>(a, s_, h, lane, rows_smem + h * rk_lds_floats(a.cap, DH, PK), inv_sh[h]);
+    const float o = rk_head<DH, false, PK, ST>(a, s_, h, lane, rows_smem + h * rk_lds_floats(a.cap, DH, PK), inv_sh[h]);
     const float mx = wave_max(lane < DH ? fabsf(o) : 0.0f);
     if (lane == 0) red[h] = mx;
     __syncthreads();
@@ -3331,6 +3375,16 @@ hipError_t attn_step_t(const AttnStepArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// One attention block's packed K/V rings (words and scales) in bytes: decode attention streams them,
+// without keeping them cached, from this size on, which is the Infinity Cache's (256 MiB). Below it the
+// rings of a step can stay cached until the next step reads them again (a chat set's rings, 157 MB:
+// 9.3 ms per batch with cached loads against 9.7 streamed, A/B on one box; c4's, 419 MB: 30.86 ms against
+// 29.79).
+constexpr double kStreamRingBytes = 256.0 * 1024 * 1024;
+inline double kv_ring_bytes(const AttnStepArgs& a) {
+    return 2.0 * a.S * a.heads * a.cap * (3.0 * (a.D / a.heads) + 4.0);
+}
+
 template <int DH>
 hipError_t attn_step_rows_t(const AttnStepArgs& a, hipStream_t s) {
     if constexpr (DH % 4 == 0 && DH <= 64) {
@@ -3344,8 +3398,18 @@ hipError_t attn_step_rows_t(const AttnStepArgs& a, hipStream_t s) {
                                                               (int)kStepRowsMaxLds);
         if (attr != hipSuccess) return attr;
         if (attr_pk != hipSuccess) return attr_pk;
-        if (pk) hipLaunchKernelGGL((attention_step_rows_kernel<DH, true>), dim3(a.S), dim3(64 * a.heads), lds, s, a);
-        else hipLaunchKernelGGL((attention_step_rows_kernel<DH, false>), dim3(a.S), dim3(64 * a.heads), lds, s, a);
+        const bool st = a.stream_rings > 0 || (a.stream_rings < 0 && kv_ring_bytes(a) >= kStreamRingBytes);
+        if (pk && DH <= 32 && st) {
+            static const hipError_t attr_st = hipFuncSetAttribute(
+                (const void*)attention_step_rows_kernel<DH, true, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                (int)kStepRowsMaxLds);
+            if (attr_st != hipSuccess) return attr_st;
+            hipLaunchKernelGGL((attention_step_rows_kernel<DH, true, true>), dim3(a.S), dim3(64 * a.heads), lds, s, a);
+        } else if (pk) {
+            hipLaunchKernelGGL((attention_step_rows_kernel<DH, true>), dim3(a.S), dim3(64 * a.heads), lds, s, a);
+        } else {
+            hipLaunchKernelGGL((attention_step_rows_kernel<DH, false>), dim3(a.S), dim3(64 * a.heads), lds, s, a);
+        }
         return hipGetLastError();
     }
     return hipErrorInvalidValue;

@@ -120,6 +120,9 @@ struct AttnStepArgs {
     uint32_t* vpack = nullptr;     // [S][heads][cap][3 * dh / 4]
     float* kscale = nullptr;       // [S][heads][cap]
     float* vscale = nullptr;       // [S][heads][cap]
+    // attention_step_rows on packed rings: stream them (non-temporal loads, heads of at most 32) from a
+    // ring size on (-1), never (0) or always (1)
+    int stream_rings = -1;
 };
 // Words of one packed ring row of head width dh (a multiple of 4).
 constexpr int kv_row_words(int dh) { return 3 * dh / 4; }

@@ -83,7 +83,8 @@ int mgt_attention_step(const int32_t* pos, const float* qkv, float* kring, float
 
 // Decode attention on packed rings (kpack/vpack: [S][heads][cap][3 dh / 4] words, kscale/vscale:
 // [S][heads][cap]); kernel 0: launch_attention_step's choice (attention_step_rk), 2: the kernel fused
-// with the limb expansion of its output (xl, xs instead of att).
+// with the limb expansion of its output (xl, xs instead of att), with the rings' loads chosen by their
+// size (these tests' rings are small: cached), 3: the same kernel with the rings streamed.
 int mgt_attention_step_packed(const int32_t* pos, const float* qkv, uint32_t* kpack, uint32_t* vpack, float* kscale,
                               float* vscale, int S, int D, int Dp, int heads, int window, int cap, float* att,
                               int8_t* xl, float* xs, int kernel) {
@@ -91,9 +92,10 @@ int mgt_attention_step_packed(const int32_t* pos, const float* qkv, uint32_t* kp
     a.S = S; a.D = D; a.Dp = Dp; a.heads = heads; a.window = window; a.cap = cap;
     a.pos = pos; a.qkv = qkv; a.att = att;
     a.kpack = kpack; a.vpack = vpack; a.kscale = kscale; a.vscale = vscale;
-    if (kernel == 2) {
+    if (kernel == 2 || kernel == 3) {
         if (!mg::attention_step_rows_fits(a)) return (int)hipErrorInvalidValue;
         a.xl = xl; a.xs = xs;
+        a.stream_rings = kernel == 3 ? 1 : -1;
         return finish(mg::launch_attention_step_rows(a, nullptr));
     }
     return finish(mg::launch_attention_step(a, nullptr));

@@ -236,12 +236,12 @@ PACKED_CASES = [
 
 
 @pytest.mark.parametrize("D,heads,window,cap", PACKED_CASES)
-@pytest.mark.parametrize("kernel", [0, 2])
+@pytest.mark.parametrize("kernel", [0, 2, 3])
 def test_decode_attention_packed_rings(D, heads, window, cap, kernel):
     """Decode attention on packed rings (attention_step_rk through launch_attention_step, and the rows
-    kernel): the output is bit-identical to the reference order over the rings' decoded values (the
-    current position's key and value in fp32), and the new row is written exactly as the host codec
-    packs it."""
+    kernel with cached and with streamed ring loads; the streamed form is taken for heads of up to 32):
+    the output is bit-identical to the reference order over the rings' decoded values (the current
+    position's key and value in fp32), and the new row is written exactly as the host codec packs it."""
     rng = np.random.default_rng(D * cap + window + 7)
     dh, Dp = D // heads, p64(D)
     pos = np.array([0, 1, cap - 1, cap, cap + 5, 2 * cap + 3], np.int32)
@@ -276,7 +276,7 @@ def test_decode_attention_packed_rings(D, heads, window, cap, kernel):
     for i, p in enumerate(pos):  # the new key and value went to slot p % cap, packed as the codec packs them
         assert np.array_equal(gk[i, :, p % cap], nk[0][i]) and np.array_equal(host(kscl)[i, :, p % cap], nk[1][i])
         assert np.array_equal(gv[i, :, p % cap], nv[0][i]) and np.array_equal(host(vscl)[i, :, p % cap], nv[1][i])
-    if kernel == 2:
+    if kernel >= 2:
         rl = torch.zeros_like(xl)
         rs = torch.zeros_like(xs)
         wd = dev(pad_cols(want, Dp))
