@@ -606,11 +606,18 @@ def run(args):
                     sess.decode_greedy_device(prompts, lens, G, oid, opb)
 
             # decode attention's bytes (the engine cannot state them: the spans live on the device): per
-            # session, block and appended position, the K/V ring rows of the attended span, the new K/V row
-            # and q in, the output row out
+            # session, attention block and appended position, the K/V ring rows of the attended span in,
+            # this position's q, k and v in (fp32), its K/V rows out and the output row out (limb planes and
+            # scale). A ring row of all heads is 4D bytes, or packed 3D plus a 4-byte scale per head; the
+            # set's device bytes tell which format the engine chose.
+            packed = kv_rings_packed(spec, sess.device_bytes())
+            nattn = len(spec.blocks) if spec.heads else 0
+            Dp = -(-spec.D // 64) * 64
+            row = 3 * spec.D + 4 * spec.heads if packed else 4 * spec.D  # unknown format: counted as fp32
             span = sum(min(p + 1, spec.window) for p in range(P, P + G - 1))
-            extra = {"attention_step": (args.steps * S * len(spec.blocks) *
-                                        (2 * span + (G - 1) * 4) * spec.D * 4)}
+            per_pos = 12 * spec.D + 2 * row + 3 * Dp + 4
+            extra = {"attention_step": args.steps * S * nattn * (2 * span * row + (G - 1) * per_pos)}
+            out["kv_rings_packed"] = packed
             ms, wall, ms_prof = timed(step, args.warmup, args.steps, torch, before=lambda: m.profile(True))
             prof = m.profile_read()
             out["profiled_ms_per_step"] = round(ms_prof, 4)  # the second, instrumented pass
@@ -650,6 +657,22 @@ def run(args):
 # Compact objects added to the c5 line: (key, configuration)
 EXTRAS = [("decode", "c4"), ("c1", "c1"), ("c2", "c2"), ("c3", "c3"), ("score", "score"), ("sample", "sample"),
           ("chat", "chat")]
+
+
+def kv_rings_packed(spec, device_bytes: int):
+    """Whether a session set holds its K/V rings packed, from its device bytes per session
+    (mg_sessions_device_bytes: the latch states and norm rings, nbs * (ring + 1) rows of Dp floats, plus
+    per attention block two rings of cap rows of D floats, or packed 3D bytes and a scale per head);
+    None when the figure is neither."""
+    dil = [min(b.initial_dilation * b.dilation_base ** s, 32) for b in spec.blocks for s in range(b.steps)]
+    ring = max(dil, default=0) + 1
+    Dp = -(-spec.D // 64) * 64
+    nattn = len(spec.blocks) if spec.heads else 0
+    cap = spec.window if spec.window > 0 else spec.context
+    base = sum(b.steps for b in spec.blocks) * (ring + 1) * Dp * 4 + 8
+    fp32 = base + nattn * 2 * cap * spec.D * 4
+    packed = base + nattn * 2 * cap * (3 * spec.D + 4 * spec.heads)
+    return True if device_bytes == packed else False if device_bytes == fp32 else None
 
 
 def compact(r):
