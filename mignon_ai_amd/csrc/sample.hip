@@ -505,11 +505,14 @@ __global__ __launch_bounds__(kThreads) void sample_exp_kernel(SampleArgs a) {
     double mx;
     int dummy;
     block_argmax(v, 0, red_v, red_i, mx, dummy);
+    // The exponentials (8 bytes per token: 134 MB for 4096 rows of 4096) are stored and read back
+    // (sample_sum_kernel, sample_pick_kernel) non-temporally, so that they do not displace the decode
+    // step's weights and code from the caches.
     double* e = a.scratch + (long long)row * V;
 #pragma unroll
     for (int k = 0; k < KP; k++) {
         const int i = tid + k * kThreads;
-        if (i < V) e[i] = exp(x[k] - mx);
+        if (i < V) __builtin_nontemporal_store(exp(x[k] - mx), e + i);
     }
 }
 
@@ -575,7 +578,7 @@ __global__ __launch_bounds__(64) void sample_pick_kernel(SampleArgs a) {
     for (int b = 0; b < V; b += 8 * 64) {
         double kv[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) kv[k] = e[min(b + 64 * k + lane, V - 1)] * inv;
+        for (int k = 0; k < 8; k++) kv[k] = __builtin_nontemporal_load(e + min(b + 64 * k + lane, V - 1)) * inv;
 #pragma unroll
         for (int k = 0; k < 8; k++)
             if (b + 64 * k + lane < V) m = fmax(m, kv[k]);
@@ -659,8 +662,8 @@ constexpr int kSumRing = 16;
 static_assert(kSumPairs == kSumRows, "the slot swizzle pairs every row with every column pair");
 static_assert(kSumBlockLoads * (kSumRing - 2) == 56, "the ring's waits below count 56 loads in flight");
 
-// One 16-byte load per lane from global memory straight into LDS: lane L's bytes land at LDS offset
-// lds + 16 L. Issued through inline assembly, with the waits for it written out below, because the
+// One 16-byte load per lane from global memory straight into LDS, non-temporal (the exponentials are
+// read once more, by sample_pick_kernel, and never again): lane L's bytes land at LDS offset lds + 16 L. Issued through inline assembly, with the waits for it written out below, because the
 // compiler, which cannot tell which LDS bytes such a load writes, waits for every one of them before any
 // LDS read, and the ring would then hold one block in flight instead of kSumRing. The load takes its LDS
 // address from M0, which the compiler reserves (it cannot be listed as clobbered): nothing else in this
@@ -668,7 +671,7 @@ static_assert(kSumBlockLoads * (kSumRing - 2) == 56, "the ring's waits below cou
 // in the instruction right after the SALU write of it (one wait state, which the compiler cannot add
 // inside an asm statement): the s_nop.
 __device__ __forceinline__ void lds_load16(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory");
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(g), "s"(lds) : "memory");
 }
 
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
