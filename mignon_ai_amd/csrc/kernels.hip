@@ -1403,10 +1403,6 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
         const Pk3 w = ldg_pk3((const Pk3*)ring + (row0 + sl) * C4 + c);
         return kv_unpack(w, ldg(scl + row0 + sl));
     };
-    auto pk4_nt = [&](const uint32_t* ring, const float* scl, int sl, int c) -> float4 {
-        const Pk3 w = ldg_pk3_nt((const Pk3*)ring + (row0 + sl) * C4 + c);
-        return kv_unpack(w, __builtin_nontemporal_load((const __attribute__((address_space(1))) float*)(scl + row0 + sl)));
-    };
     constexpr bool KST = ST && CUR_LANES && C4 <= 8;
     // lanes 0..3*C4-1: one float4 each of this position's q, k and v (part lane / C4, chunk lane % C4)
     const int qpart = min(lane / C4, 2), qc = lane % C4;
@@ -1422,15 +1418,26 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
         // to the lanes that score them, then the values take their place. The current position's key and
         // value come from the lanes holding them.
         const int nr = (span - 1) * C4;
-        float4 kb[8], vb[8];
-        int off[8];
+        // the row scales, lane r holding row r's, handed to the lanes of each row's groups by shuffles
+        const int jr = min(lane, max(span - 2, 0));
+        const float ksr = __builtin_nontemporal_load((const __attribute__((address_space(1))) float*)(a.kscale + row0 + slot(jr)));
+        const float vsr = __builtin_nontemporal_load((const __attribute__((address_space(1))) float*)(a.vscale + row0 + slot(jr)));
+        Pk3 kw8[8], vw8[8];
+        int off[8], rowu[8];
 #pragma unroll
         for (int u = 0; u < 8; u++) {
             const int e = min(u * 64 + lane, max(nr - 1, 0));
             const int jj = e / C4, c = e - jj * C4;
             off[u] = jj * DS + 4 * c;
-            kb[u] = pk4_nt(a.kpack, a.kscale, slot(jj), c);
-            vb[u] = pk4_nt(a.vpack, a.vscale, slot(jj), c);
+            rowu[u] = jj;
+            kw8[u] = ldg_pk3_nt((const Pk3*)a.kpack + (row0 + slot(jj)) * C4 + c);
+            vw8[u] = ldg_pk3_nt((const Pk3*)a.vpack + (row0 + slot(jj)) * C4 + c);
+        }
+        float4 kb[8], vb[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            kb[u] = kv_unpack(kw8[u], __shfl(ksr, rowu[u], 64));
+            vb[u] = kv_unpack(vw8[u], __shfl(vsr, rowu[u], 64));
         }
 #pragma unroll
         for (int u = 0; u < 8; u++) *(float4*)(vs + off[u]) = kb[u];
@@ -1523,7 +1530,8 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
     const float scale = (float)(1.0 / sqrt((double)DH));
     const float sc = dot_ref_reg4<DH>(q, krow) * scale;
     const float mx = wave_max(lane < span ? sc : -3.40282347e38f);
-    if (lane < span) es[lane] = fast_exp_ref(sc - mx);
+    const float ex = lane < span ? fast_exp_ref(sc - mx) : 0.0f;
+    if (lane < span) es[lane] = ex;
     wave_lds_sync();
     if (lane == 0) {
         float sum = 0.0f;  // nn.SoftmaxInPlaceF32's sequential sum
@@ -1532,11 +1540,13 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
         inv_sh = 1.0f / sum;
     }
     wave_lds_sync();
-    const float inv = inv_sh;
+    // p = e * (1 / sum), as SoftmaxInPlaceF32 leaves it: each lane its own key's, once
+    if (lane < span) es[lane] = ex * inv_sh;
+    wave_lds_sync();
     float o = 0.0f;
     if (lane < DH) {
 #pragma unroll 8
-        for (int jj = 0; jj < span; jj++) o = axpy_ref<DH>(lane, es[jj] * inv, vs[jj * DS + lane], o);
+        for (int jj = 0; jj < span; jj++) o = axpy_ref<DH>(lane, es[jj], vs[jj * DS + lane], o);
     }
     // record this position's key and value (slot pos % cap; the evicted key is outside the window)
     if constexpr (PK) {
