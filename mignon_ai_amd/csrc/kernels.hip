@@ -1399,9 +1399,10 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
         }
     };
     // group c of packed ring row `sl` (kpack or vpack) and that row's scale
+    // (the head's ring base is uniform over the wave; only 32-bit offsets vary over the lanes)
     auto pk4 = [&](const uint32_t* ring, const float* scl, int sl, int c) -> float4 {
-        const Pk3 w = ldg_pk3((const Pk3*)ring + (row0 + sl) * C4 + c);
-        return kv_unpack(w, ldg(scl + row0 + sl));
+        const Pk3 w = ldg_pk3(((const Pk3*)ring + row0 * C4) + (sl * C4 + c));
+        return kv_unpack(w, ldg((scl + row0) + sl));
     };
     constexpr bool KST = ST && CUR_LANES && C4 <= 8;
     // lanes 0..3*C4-1: one float4 each of this position's q, k and v (part lane / C4, chunk lane % C4)
@@ -1420,8 +1421,8 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
         const int nr = (span - 1) * C4;
         // the row scales, lane r holding row r's, handed to the lanes of each row's groups by shuffles
         const int jr = min(lane, max(span - 2, 0));
-        const float ksr = __builtin_nontemporal_load((const __attribute__((address_space(1))) float*)(a.kscale + row0 + slot(jr)));
-        const float vsr = __builtin_nontemporal_load((const __attribute__((address_space(1))) float*)(a.vscale + row0 + slot(jr)));
+        const float ksr = __builtin_nontemporal_load((const __attribute__((address_space(1))) float*)((a.kscale + row0) + slot(jr)));
+        const float vsr = __builtin_nontemporal_load((const __attribute__((address_space(1))) float*)((a.vscale + row0) + slot(jr)));
         Pk3 kw8[8], vw8[8];
         int off[8], rowu[8];
 #pragma unroll
@@ -1430,8 +1431,8 @@ __device__ __forceinline__ float rk_head(const AttnStepArgs& a, int s_, int h, i
             const int jj = e / C4, c = e - jj * C4;
             off[u] = jj * DS + 4 * c;
             rowu[u] = jj;
-            kw8[u] = ldg_pk3_nt((const Pk3*)a.kpack + (row0 + slot(jj)) * C4 + c);
-            vw8[u] = ldg_pk3_nt((const Pk3*)a.vpack + (row0 + slot(jj)) * C4 + c);
+            kw8[u] = ldg_pk3_nt(((const Pk3*)a.kpack + row0 * C4) + (slot(jj) * C4 + c));
+            vw8[u] = ldg_pk3_nt(((const Pk3*)a.vpack + row0 * C4) + (slot(jj) * C4 + c));
         }
         float4 kb[8], vb[8];
 #pragma unroll
@@ -1600,7 +1601,7 @@ template <int DH, bool PK, bool ST = false>
 __global__ __launch_bounds__(1024) void attention_step_rows_kernel(AttnStepArgs a) {
     extern __shared__ __align__(16) float rows_smem[];
     __shared__ float inv_sh[16], red[16];
-    const int s_ = blockIdx.x, h = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int s_ = blockIdx.x, h = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (a.done && a.done[s_] >= 0) return;  // a finished session of a batched decode (the whole workgroup)
     const float o = rk_head<DH, false, PK, ST>(a, s_, h, lane, rows_smem + h * rk_lds_floats(a.cap, DH, PK), inv_sh[h]);
     const float mx = wave_max(lane < DH ? fabsf(o) : 0.0f);
