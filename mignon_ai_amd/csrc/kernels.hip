@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void row_kernel(RowArgs a) {
     constexpr int RB = row_batch<NS4>();
     extern __shared__ __align__(16) int8_t row_smem[];
     int8_t* smem = row_smem;
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int D = a.D, Dp = a.Dp, C4 = Dp >> 2;
     const int m_base = blockIdx.x * ROW_TILE;
     int8_t* stage = smem;
@@ -2083,7 +2083,7 @@ __global__ __launch_bounds__(S1_THREADS) void step1_kernel(Step1Args a) {
     __shared__ float red[16];
     __shared__ float rk_inv[8];
     __shared__ float bcast[4];
-    const int s_ = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int s_ = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int D = a.D, Dp = a.Dp, H = a.H, Hp = a.Hp, V = a.V, Vp = a.Vp;
     const int ntiles = Vp / LX_BN;
     float* cur = s1_smem;
@@ -2601,7 +2601,7 @@ __global__ __launch_bounds__(TS_THREADS) void tile_step_kernel(TileStepArgs a) {
     extern __shared__ __align__(16) float ts_smem[];
     __shared__ float rsc[TS_NS];  // row scales of the current limb operand
     const int s0 = blockIdx.x * TS_NS, ns = min(TS_NS, a.S - s0);
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     if (a.done) {
         // a tile whose sessions have all finished (a batched decode's stop tokens) is skipped
         const bool run = lane < ns && a.done[s0 + lane] < 0;
